@@ -1,0 +1,398 @@
+"""Benchmark of the MI355X array-compute hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite all|headline]
+
+Prints ONE JSON line.  The headline ``value`` is the whole-job HBM
+throughput (algorithmic GB/s) of the binary-elementwise workload at 2^28
+elements -- one step = a+b and sin(a) on float32, floor_divide(a, b) and
+mod(a, b) on int32 -- with inputs resident in HBM.  ``roofline`` describes
+the step's dominant kernel, timed with HIP events on the library stream over
+the timed region.  ``cpu_baseline`` times the reference's CPU/NumPy path
+(the oracle restatement) on a bounded sample on this host.  ``configs``
+holds the other workloads (fused elementwise, reductions, scans, matmul,
+fusion chain) measured the same way.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"float32": 157.3, "float16": 2500.0, "bfloat16": 2500.0, "float64": 78.6}
+N28 = 1 << 28
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class EventTimer:
+    """Per-op kernel time from event pairs recorded on the library stream."""
+
+    def __init__(self, be):
+        self.be = be
+        self.pairs = {}
+
+    def run(self, name, fn):
+        s, e = self.be.event(), self.be.event()
+        self.be.record(s)
+        out = fn()
+        self.be.record(e)
+        self.pairs.setdefault(name, []).append((s, e))
+        return out
+
+    def ms(self, name):
+        vals = [self.be.elapsed_ms(s, e) for s, e in self.pairs[name]]
+        return statistics.mean(vals), vals
+
+    def close(self):
+        for lst in self.pairs.values():
+            for s, e in lst:
+                self.be.destroy_event(s)
+                self.be.destroy_event(e)
+        self.pairs = {}
+
+
+def _traffic_table():
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f)
+    return {}
+
+
+# --------------------------------------------------------------- C2
+def bench_c2(cp, be, steps, warmup):
+    """Headline: a+b, sin(a) (float32) and floor_divide, mod (int32), 2^28."""
+    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    t0 = time.time()
+    a_np, b_np = c2_float_inputs(N28)
+    a, b = cp.array(a_np), cp.array(b_np)
+    del a_np, b_np
+    ai_np, bi_np = c2_int_inputs(N28)
+    ai, bi = cp.array(ai_np), cp.array(bi_np)
+    del ai_np, bi_np
+    for x in (a, b, ai, bi):
+        x._ensure_gpu()
+    cp.synchronize()
+    _log(f"c2 inputs ready in {time.time() - t0:.1f}s")
+    ops = {
+        "add_f32": (lambda: a + b, 12),
+        "sin_f32": (lambda: cp.sin(a), 8),
+        "floor_divide_i32": (lambda: cp.floor_divide(ai, bi), 12),
+        "mod_i32": (lambda: cp.mod(ai, bi), 12),
+    }
+
+    def step(timer=None):
+        outs = []
+        for name, (fn, _) in ops.items():
+            if timer is None:
+                r = fn()
+                r._materialize_if_lazy()
+            else:
+                r = timer.run(name, lambda fn=fn: _mat(fn()))
+            outs.append(r)
+        return outs
+
+    for _ in range(warmup):
+        step()
+    cp.synchronize()
+    timer = EventTimer(be)
+    t = time.perf_counter()
+    for _ in range(steps):
+        step(timer)
+    cp.synchronize()
+    wall = time.perf_counter() - t
+    per_op = {}
+    for name, (_, bpe) in ops.items():
+        ms, _ = timer.ms(name)
+        per_op[name] = {"kernel_ms": round(ms, 4), "bytes": bpe * N28,
+                        "gbs": round(bpe * N28 / ms / 1e6, 1),
+                        "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    timer.close()
+    bytes_per_step = sum(bpe for _, bpe in ops.values()) * N28
+    return {"wall_s": wall, "bytes_per_step": bytes_per_step, "per_op": per_op}
+
+
+def _mat(r):
+    r._materialize_if_lazy()
+    return r
+
+
+# --------------------------------------------------------------- C1
+def bench_c1(cp, be, reps=50):
+    from macmetalpy_amd.workloads import c1_inputs
+    res = {}
+    for label, n in (("2^20", 1 << 20), ("2^28", N28)):
+        x = cp.array(c1_inputs(n))
+        x._ensure_gpu()
+        f = lambda: _mat(cp.sqrt(cp.abs(x)) + cp.exp(-x ** 2))  # noqa: E731
+        for _ in range(3):
+            f()
+        cp.synchronize()
+        timer = EventTimer(be)
+        for _ in range(reps if n < N28 else 10):
+            timer.run("c1", f)
+        cp.synchronize()
+        ms, _ = timer.ms("c1")
+        timer.close()
+        res[label] = {"kernel_ms": round(ms, 4), "gbs": round(8 * n / ms / 1e6, 1),
+                      "frac_of_peak": round(8 * n / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        del x
+    return res
+
+
+# --------------------------------------------------------------- C3
+def bench_c3(cp, be, reps=10):
+    from macmetalpy_amd.workloads import c3_matrix, c3_scan_inputs
+    A = cp.array(c3_matrix())
+    A._ensure_gpu()
+    nbytes = 4 * A.size
+    res = {}
+    cases = {
+        "sum_all": lambda: cp.sum(A), "mean_all": lambda: cp.mean(A),
+        "sum_axis1": lambda: cp.sum(A, axis=1), "mean_axis1": lambda: cp.mean(A, axis=1),
+        "argmax_axis1": lambda: cp.argmax(A, axis=1),
+        "argmax_all": lambda: cp.argmax(A, axis=None, keepdims=True),
+    }
+    for name, f in cases.items():
+        try:
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(name, f)
+            cp.synchronize()
+            ms, _ = timer.ms(name)
+            timer.close()
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1),
+                         "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        except Exception as e:  # report, keep going
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    del A
+    ci, cf = c3_scan_inputs(N28)
+    for name, arr, bpe in (("cumsum_i32_to_i64", ci, 12), ("cumsum_f32", cf, 8)):
+        try:
+            x = cp.array(arr)
+            x._ensure_gpu()
+            f = lambda: cp.cumsum(x)  # noqa: E731
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(name, f)
+            cp.synchronize()
+            ms, _ = timer.ms(name)
+            timer.close()
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
+                         "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            del x
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
+# --------------------------------------------------------------- C4
+def bench_c4(cp, be, reps=5):
+    from macmetalpy_amd.workloads import c4_inputs
+    res = {}
+    for kind, dt in (("f32", "float32"), ("f16", "float16"), ("batched", "float32")):
+        try:
+            a_np, b_np = c4_inputs(kind)
+            a, b = cp.array(a_np), cp.array(b_np)
+            a._ensure_gpu()
+            b._ensure_gpu()
+            flops = 2.0 * a_np.shape[-2] * a_np.shape[-1] * b_np.shape[-1] * (
+                a_np.shape[0] if a_np.ndim == 3 else 1)
+            del a_np, b_np
+            f = lambda: a @ b  # noqa: E731
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(kind, f)
+            cp.synchronize()
+            ms, _ = timer.ms(kind)
+            timer.close()
+            tf = flops / ms / 1e9
+            res[kind] = {"kernel_ms": round(ms, 4), "tflops": round(tf, 2),
+                         "peak_tflops": PEAK_TFLOPS[dt],
+                         "frac_of_peak": round(tf / PEAK_TFLOPS[dt], 4)}
+            del a, b
+        except Exception as e:
+            res[kind] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
+# --------------------------------------------------------------- C5
+def bench_c5(cp, be, reps=10):
+    from macmetalpy_amd.workloads import c5_inputs
+    x_np, r_np = c5_inputs()
+    x, r = cp.array(x_np), cp.array(r_np)
+    x._ensure_gpu()
+    r._ensure_gpu()
+    nbytes = 4 * x.size + 4 * r.size + 4 * x.shape[0]
+
+    def chain():
+        return cp.sum(cp.tanh(x * r + 1.0) * cp.exp(-cp.abs(x)) - cp.log1p(x * x), axis=1)
+
+    res = {}
+    for mode in ("fused", "unfused"):
+        try:
+            cp.set_config(fusion=(mode == "fused"))
+            chain()
+            cp.synchronize()
+            timer = EventTimer(be)
+            t = time.perf_counter()
+            for _ in range(reps):
+                timer.run(mode, chain)
+            cp.synchronize()
+            wall = (time.perf_counter() - t) / reps * 1e3
+            ms, _ = timer.ms(mode)
+            timer.close()
+            res[mode] = {"ms": round(ms, 4), "wall_ms": round(wall, 4)}
+        except Exception as e:
+            res[mode] = {"error": f"{type(e).__name__}: {e}"[:300]}
+        finally:
+            cp.set_config(fusion=True)
+    if "ms" in res.get("fused", {}):
+        ms = res["fused"]["ms"]
+        res["fused"].update({"gbs": round(nbytes / ms / 1e6, 1),
+                             "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)})
+        if "ms" in res.get("unfused", {}):
+            res["speedup_vs_unfused"] = round(res["unfused"]["ms"] / ms, 2)
+    return res
+
+
+# ------------------------------------------------------- CPU baseline
+def cpu_baseline(sample_log2=25, reps=10, warm=2):
+    """The reference's CPU path (NumPy ufuncs, single-threaded) on the first
+    2^sample_log2 elements of the C2 inputs; median of ``reps`` runs after
+    ``warm`` warm-ups, as the reference's bench_vs_numpy.py:30-45."""
+    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    from oracle import reference_cpu as ref
+    n = 1 << sample_log2
+    a, b = c2_float_inputs(N28)
+    a, b = a[:n].copy(), b[:n].copy()
+    ai, bi = c2_int_inputs(N28)
+    ai, bi = ai[:n].copy(), bi[:n].copy()
+    ops = [(lambda: ref.binary("add_op", a, b), 12), (lambda: ref.unary("sin_op", a), 8),
+           (lambda: ref.floor_divide(ai, bi), 12), (lambda: ref.mod(ai, bi), 12)]
+    total_bytes = sum(bpe for _, bpe in ops) * n
+    times = []
+    for i in range(warm + reps):
+        t = time.perf_counter()
+        for fn, _ in ops:
+            fn()
+        dt = time.perf_counter() - t
+        if i >= warm:
+            times.append(dt)
+    med = statistics.median(times)
+    return {"value": round(total_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": (f"a+b, sin(a) float32 and floor_divide, mod int32 on the first 2^{sample_log2} "
+                       f"elements of the 2^28 inputs; NumPy {np.__version__} single-threaded "
+                       f"ufuncs; median of {reps} after {warm} warm-ups ({med:.3f} s/step)")}
+
+
+def _env(be):
+    info = {}
+    try:
+        info.update(be.device_info())
+    except Exception:
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+        info["host_cpu"] = model
+    except OSError:
+        pass
+    info["host_nproc"] = os.cpu_count()
+    info["numpy"] = np.__version__
+    info["python"] = platform.python_version()
+    return info
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--suite", choices=["all", "headline"], default="all")
+    ap.add_argument("--cpu-sample-log2", type=int, default=25)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
+        sys.exit(2)
+
+    import macmetalpy_amd as cp
+    from macmetalpy_amd._backend import HipBackend
+    be = HipBackend()
+
+    c2 = bench_c2(cp, be, args.steps, args.warmup)
+    per_op = c2["per_op"]
+    dominant = max(per_op, key=lambda k: per_op[k]["kernel_ms"])
+    dom = per_op[dominant]
+    value = c2["bytes_per_step"] * args.steps / c2["wall_s"] / 1e9
+    kernel_names = {"add_f32": "k_binary<MMP_B_ADD,float>", "sin_f32": "k_unary<MMP_U_SIN,float>",
+                    "floor_divide_i32": "k_binary<MMP_B_FLOOR_DIVIDE,int>",
+                    "mod_i32": "k_binary<MMP_B_MOD,int>"}
+    traffic = _traffic_table().get(f"{dominant}@2^28")
+    out = {
+        "metric": "achieved HBM GB/s (fused elementwise/reduce/cumsum) + matmul TFLOPS, 1xMI355X",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["wall_s"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+i32",
+        "data": "synthetic (seeded NumPy default_rng inputs, as cp.random.seed + randn/randint)",
+        "config": {"workload": "binary elementwise 2^28: a+b, sin(a) float32 N(0,1); "
+                               "floor_divide(a,b), mod(a,b) int32 a~U[-2^30,2^30), "
+                               "b~+-U[1,1000]",
+                   "elements": N28, "bytes_per_step": c2["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "kernel": kernel_names[dominant], "op": dominant,
+                     "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": dom["bytes"],
+                     "avg_launch_ms": dom["kernel_ms"]},
+        "per_op": per_op,
+    }
+    if args.suite == "all":
+        cfgs = {}
+        for name, fn in (("c1_fused_elementwise", bench_c1), ("c3_reduce_scan", bench_c3),
+                         ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5)):
+            t = time.time()
+            try:
+                cfgs[name] = fn(cp, be)
+            except Exception as e:
+                cfgs[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+            _log(f"{name} done in {time.time() - t:.1f}s")
+        out["configs"] = cfgs
+    if not args.no_cpu:
+        t = time.time()
+        out["cpu_baseline"] = cpu_baseline(args.cpu_sample_log2)
+        _log(f"cpu baseline done in {time.time() - t:.1f}s")
+    out["env"] = _env(be)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,305 @@
+/*
+ * mmp_hip.h -- C ABI of libmmp_hip.so, the MI355X (gfx950) compute library
+ * behind macmetalpy_amd's `import macmetalpy as cp` array API.
+ *
+ * The reference drives its GPU through eleven ctypes-bound symbols of the
+ * external metalgpu dylib (src/macmetalpy/_metal_backend.py:221-263):
+ * init / deleteInstance / createBuffer / releaseBuffer / getBufferPointer /
+ * createLibrary / createLibraryFromString / setFunction / runFunction /
+ * maxThreadsPerGroup / threadExecutionWidth.  That ABI is stateful ("current
+ * library", "current function"), has no error channel and ships kernel
+ * *source* per call.  This header replaces it with typed, stateless entry
+ * points: each one names the reference call it stands in for.
+ *
+ * Conventions
+ *  - Every function returns 0 on success, a nonzero MMP_E* code on failure;
+ *    mmp_last_error() then returns a message (thread-local).
+ *  - Pointers named x/a/b/out are device pointers from mmp_alloc (or views
+ *    into them).  Strides and offsets are in ELEMENTS, like the reference's
+ *    ndarray._strides (src/macmetalpy/ndarray.py:254-260).
+ *  - All work is enqueued on one in-order HIP stream owned by the library;
+ *    mmp_sync() waits for it.  Calls are asynchronous unless noted.
+ *  - Scalars travel BY VALUE (pointer to host bytes of the given dtype); the
+ *    reference uploads them as 1-element buffers (e.g. ndarray.py:1026).
+ */
+#ifndef MMP_HIP_H
+#define MMP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define MMP_OK 0
+#define MMP_E_NODEVICE 1   /* no HIP device / mmp_init failed            */
+#define MMP_E_HIP 2        /* a HIP runtime call failed                   */
+#define MMP_E_OOM 3        /* device allocation failed                    */
+#define MMP_E_ARG 4        /* invalid argument (shape, size, null, ...)   */
+#define MMP_E_UNSUPPORTED 5 /* op / dtype combination not implemented     */
+#define MMP_E_RTC 6        /* hiprtc compile failed (log in last_error)   */
+#define MMP_E_INJECTED 7   /* failure forced by mmp_debug_fail_next       */
+
+/* ---- dtype codes (numpy dtype -> code, see macmetalpy_amd/_abi.py) ---- */
+#define MMP_BOOL 0
+#define MMP_I16 1
+#define MMP_U16 2
+#define MMP_I32 3
+#define MMP_U32 4
+#define MMP_I64 5
+#define MMP_U64 6
+#define MMP_F16 7
+#define MMP_F32 8
+#define MMP_F64 9
+#define MMP_BF16 10        /* matmul operands only */
+#define MMP_NDTYPES 11
+
+/* ---- unary elementwise ops (reference _kernels.py:84-331 names) ------- */
+#define MMP_U_NEG 0
+#define MMP_U_POSITIVE 1
+#define MMP_U_ABS 2
+#define MMP_U_SIGN 3
+#define MMP_U_SQUARE 4
+#define MMP_U_RECIPROCAL 5
+#define MMP_U_SQRT 6
+#define MMP_U_CBRT 7
+#define MMP_U_EXP 8
+#define MMP_U_EXP2 9
+#define MMP_U_EXPM1 10
+#define MMP_U_LOG 11
+#define MMP_U_LOG2 12
+#define MMP_U_LOG10 13
+#define MMP_U_LOG1P 14
+#define MMP_U_SIN 15
+#define MMP_U_COS 16
+#define MMP_U_TAN 17
+#define MMP_U_ASIN 18
+#define MMP_U_ACOS 19
+#define MMP_U_ATAN 20
+#define MMP_U_SINH 21
+#define MMP_U_COSH 22
+#define MMP_U_TANH 23
+#define MMP_U_ASINH 24
+#define MMP_U_ACOSH 25
+#define MMP_U_ATANH 26
+#define MMP_U_FLOOR 27
+#define MMP_U_CEIL 28
+#define MMP_U_RINT 29
+#define MMP_U_TRUNC 30
+#define MMP_U_DEGREES 31
+#define MMP_U_RADIANS 32
+#define MMP_NUNARY 33
+
+/* ---- binary elementwise ops (reference _kernels.py:49-82, 220-250, 335-402) */
+#define MMP_B_ADD 0
+#define MMP_B_SUB 1
+#define MMP_B_MUL 2
+#define MMP_B_DIV 3           /* true_divide (floating dtypes only)          */
+#define MMP_B_FLOOR_DIVIDE 4  /* numpy floor semantics, not truncation       */
+#define MMP_B_MOD 5           /* numpy remainder: sign of the divisor        */
+#define MMP_B_POWER 6
+#define MMP_B_MAXIMUM 7
+#define MMP_B_MINIMUM 8
+#define MMP_B_FMAX 9
+#define MMP_B_FMIN 10
+#define MMP_B_ATAN2 11
+#define MMP_B_HYPOT 12
+#define MMP_B_FMOD 13
+#define MMP_B_COPYSIGN 14
+#define MMP_B_NEXTAFTER 15
+#define MMP_B_LOGADDEXP 16
+#define MMP_B_LOGADDEXP2 17
+#define MMP_B_HEAVISIDE 18
+#define MMP_NBINARY 19
+
+/* ---- reductions and scans ---------------------------------------------- */
+#define MMP_R_SUM 0
+#define MMP_R_PROD 1
+#define MMP_R_MAX 2
+#define MMP_R_MIN 3
+#define MMP_R_MEAN 4
+#define MMP_R_ARGMAX 5
+#define MMP_R_ARGMIN 6
+#define MMP_NREDUCE 7
+
+#define MMP_S_CUMSUM 0
+#define MMP_S_CUMPROD 1
+
+/* ======================================================================== */
+/* Runtime: replaces MetalBackend (_metal_backend.py:179-372)                */
+/* ======================================================================== */
+
+/* Select and initialise a device; creates the library's stream.
+ * Replaces metalgpu `init()` (_metal_backend.py:221) called from
+ * MetalBackend.__new__ (_metal_backend.py:197-219).  Idempotent. */
+int mmp_init(int device);
+
+/* Number of visible HIP devices (0 when none; never fails for that). */
+int mmp_device_count(int *count);
+
+/* Device facts: name (gcnArchName), CU count, total HBM bytes, wave size,
+ * max threads per block.  Replaces maxThreadsPerGroup / threadExecutionWidth
+ * (_metal_backend.py:259-263). */
+int mmp_device_info(char *arch, int arch_len, int *cu_count,
+                    int64_t *total_mem, int *wave_size, int *max_threads);
+
+/* Message for the last failing call on this thread ("" if none).  The
+ * reference has no error channel (metalgpu returns void). */
+const char *mmp_last_error(void);
+
+/* Device allocation from a caching pool.  Replaces createBuffer /
+ * releaseBuffer (_metal_backend.py:225-231) and _BufferPool
+ * (_metal_backend.py:23-77).  Frees are stream-ordered: a freed block is
+ * reused only by work enqueued later on the same stream. */
+int mmp_alloc(size_t bytes, void **ptr);
+int mmp_free(void *ptr);
+/* Return all cached (free) blocks to the driver (synchronises first). */
+int mmp_empty_cache(void);
+/* Bytes currently handed out / held in the cache. */
+int mmp_memory_stats(size_t *in_use, size_t *cached);
+
+/* Host<->device copies.  The reference reads unified memory through
+ * getBufferPointer (_metal_backend.py:233-236, ndarray.py:576-618); HBM is
+ * discrete, so get()/set() become explicit copies.  h2d/d2h are synchronous
+ * with respect to the host buffer; d2d is stream-ordered. */
+int mmp_h2d(void *dst, const void *src, size_t bytes);
+int mmp_d2h(void *dst, const void *src, size_t bytes);
+int mmp_d2d(void *dst, const void *src, size_t bytes);
+
+/* Wait for all enqueued work.  Replaces MetalBackend.synchronize
+ * (_metal_backend.py:359-372: dispatch of `_sync` with wait=True). */
+int mmp_sync(void);
+
+/* Stream-ordered timing events on the library stream (benchmarks). */
+int mmp_event_create(void **ev);
+int mmp_event_record(void *ev);
+int mmp_event_elapsed_ms(void *start, void *end, float *ms);
+int mmp_event_destroy(void *ev);
+
+/* ======================================================================== */
+/* Elementwise: replaces execute_kernel(elementwise_shader, "<op>_op", n,    */
+/* [a, b, out]) from ndarray._binary_op / _unary_op (ndarray.py:960-1243)   */
+/* ======================================================================== */
+
+/* out[i] = op(x[i]) for contiguous x, out of `dtype` (MMP_U_*).
+ * Reference: ndarray._unary_op -> elementwise_shader "<op>_op"
+ * (ndarray.py:1237-1243, _kernels.py:84-331). */
+int mmp_unary(int op, int dtype, int64_t n, const void *x, void *out);
+
+/* out[i] = op(a[i], b[i]) for contiguous same-shape a, b, out (MMP_B_*).
+ * Reference: ndarray._binary_op (ndarray.py:1105-1113). */
+int mmp_binary(int op, int dtype, int64_t n, const void *a, const void *b,
+               void *out);
+
+/* Array-scalar form: scalar_side 0 => out = op(s, b[i]); 1 => op(a[i], s).
+ * `scalar` points to one host value of `dtype`.  The reference instead
+ * materialises creation.full(shape, s) on the host and uploads it
+ * (ndarray.py:995-1026). */
+int mmp_binary_scalar(int op, int dtype, int64_t n, const void *arr,
+                      const void *scalar, int scalar_side, void *out);
+
+/* Strided cast/copy: out (C-contiguous, `dst_dtype`) = (dst)x viewed with
+ * `shape` / `x_strides` (elements, may be 0 for broadcast) from x + 0.
+ * Covers astype (cast_op, _kernel_cache.py:44-58), copy (copy_buf :61-71),
+ * broadcast materialisation (broadcast_nd :74-97) and view -> contiguous
+ * (strided_copy :100-122).  ndim <= 8. */
+int mmp_copy(int src_dtype, int dst_dtype, int ndim, const int64_t *shape,
+             const void *x, const int64_t *x_strides, void *out);
+
+/* Strided write: dst view (shape, dst_strides) = (dst)src view (shape,
+ * src_strides).  Covers setitem on views (strided_write, offset_copy,
+ * scalar_write: _kernel_cache.py:125-189). ndim <= 8. */
+int mmp_copy_strided(int src_dtype, int dst_dtype, int ndim,
+                     const int64_t *shape, const void *src,
+                     const int64_t *src_strides, void *dst,
+                     const int64_t *dst_strides);
+
+/* out[i] = value for i < n (value: host bytes of dtype).  Replaces the
+ * reference's fill_scalar kernel (_kernels.py:114-118). */
+int mmp_fill(int dtype, int64_t n, const void *value, void *out);
+
+/* ======================================================================== */
+/* Reductions: replace ndarray._reduce (ndarray.py:1895-1963), _reduce_axis */
+/* (ndarray.py:2015-2066) and reductions._parallel_argmax (:314-343)        */
+/* ======================================================================== */
+
+/* Input viewed as C-contiguous (outer, len, inner); reduces the middle
+ * axis -> out (outer, inner) of `out_dtype`.  axis=None is
+ * (1, n, 1).  op: MMP_R_SUM/PROD/MAX/MIN/MEAN.  Floating sums/means
+ * accumulate in float64 and round once; integer sums accumulate in 64-bit
+ * (numpy promotes int32 sums to int64).  max/min propagate NaN. */
+int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+               int64_t inner, const void *x, void *out);
+
+/* Same view; out (outer, inner) int64 indices of the first max/min
+ * (MMP_R_ARGMAX / MMP_R_ARGMIN); a NaN counts as the extreme (first NaN
+ * wins), as np.argmax does. */
+int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len,
+                  int64_t inner, const void *x, int64_t *out);
+
+/* ======================================================================== */
+/* Scan: replaces ndarray._prefix_scan (ndarray.py:2068-2152) and the 3-pass */
+/* parallel_scan_shader (_kernels.py:1263-1360)                              */
+/* ======================================================================== */
+
+/* Inclusive scan along the middle axis of (outer, len, inner).
+ * MMP_S_CUMSUM / MMP_S_CUMPROD.  out_dtype follows numpy (int32 -> int64,
+ * float32 -> float32); floating scans carry a float64 running value. */
+int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+             int64_t inner, const void *x, void *out);
+
+/* ======================================================================== */
+/* Matmul: replaces ndarray.__matmul__ + matmul_shader (ndarray.py:1398-1450,*/
+/* _kernels.py:740-759); batched form replaces linalg_top.matmul's CPU path */
+/* (linalg_top.py:105-106)                                                  */
+/* ======================================================================== */
+
+/* C[b] = A[b] @ B[b] for b < batch; A (M,K) row stride lda, B (K,N) row
+ * stride ldb, C (M,N) row stride ldc; batch strides sA/sB/sC in elements
+ * (0 broadcasts an operand).  dtype: MMP_F32, MMP_F16, MMP_BF16, MMP_F64
+ * (float accumulation in fp32 for 16-bit inputs, fp64 for f64) or an
+ * integer dtype (exact, wrapping). */
+int mmp_matmul(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+               const void *A, int64_t lda, int64_t sA, const void *B,
+               int64_t ldb, int64_t sB, void *C, int64_t ldc, int64_t sC);
+
+/* ======================================================================== */
+/* Runtime compilation: replaces createLibraryFromString + setFunction +    */
+/* runFunction (_metal_backend.py:237-257, 313-357) for the fusion engine  */
+/* (_fusion.py:443-486) and RawKernel (raw_kernel.py:32-62)                 */
+/* ======================================================================== */
+
+/* Compile HIP C++ `src` with hiprtc for the current device's arch (gfx950)
+ * and return a kernel handle for `name`.  Cached by (src, name, options). */
+int mmp_rtc_compile(const char *src, const char *name, const char *options,
+                    void **kernel);
+
+/* Compile only (no device needed): writes the code object size to
+ * *code_size and copies it to `code` when code_cap is large enough. */
+int mmp_rtc_build(const char *src, const char *options, const char *arch,
+                  void *code, size_t code_cap, size_t *code_size);
+
+/* Launch with a grid given in BLOCKS (HIP convention). args: kernel
+ * parameter pointers, one per kernel argument. */
+int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
+                   uint32_t shared_bytes, void **args);
+
+/* Launch with a grid given in THREADS (Metal dispatchThreads convention of
+ * the reference's RawKernel, raw_kernel.py:46-59): exactly threads3[d]
+ * work-items run; the last workgroup may be partial. */
+int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3,
+                           const uint32_t *block3, uint32_t shared_bytes,
+                           void **args);
+
+/* ---- test hooks -------------------------------------------------------- */
+/* Make the next `count`-th call of kind (1 = mmp_alloc, 2 = mmp_rtc_compile,
+ * 3 = kernel launch) fail with MMP_E_INJECTED.  count 0 disables. */
+int mmp_debug_fail_next(int kind, int count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MMP_HIP_H */

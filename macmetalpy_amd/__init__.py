@@ -1,0 +1,99 @@
+"""macmetalpy_amd -- MacMetalPy's array-compute hot path on AMD MI355X.
+
+Drop-in for the reference's ``import macmetalpy as cp`` names on the hot
+path (src/macmetalpy/__init__.py:8-236): ndarray, creation, random inputs,
+elementwise ufuncs, sum/mean/max/min/prod/argmax/argmin, cumsum/cumprod,
+matmul / linalg.matmul / dot, RawKernel, set_config and synchronize.
+Unlike the reference (darwin-only, __init__.py:5-6) it imports on any host;
+device work needs libmmp_hip.so and a gfx950 GPU and raises otherwise.
+"""
+from __future__ import annotations
+
+import math as _math
+
+import numpy as _np
+
+from ._config import get_config, set_config
+from .ndarray import ndarray
+from .raw_kernel import RawKernel
+from .creation import (
+    array, asarray, empty, zeros, ones, full, arange, linspace, eye,
+    zeros_like, ones_like, empty_like, full_like, ascontiguousarray,
+)
+from .ufunc_ops import (
+    negative, positive, absolute, abs, fabs, sign, square, reciprocal, sqrt, cbrt,
+    exp, exp2, expm1, log, log2, log10, log1p, sin, cos, tan, arcsin, arccos, arctan,
+    sinh, cosh, tanh, arcsinh, arccosh, arctanh, floor, ceil, rint, trunc, degrees,
+    radians, rad2deg, deg2rad,
+    add, subtract, multiply, divide, true_divide, floor_divide, mod, remainder, power,
+    maximum, minimum, fmax, fmin, arctan2, hypot, fmod, copysign, nextafter, logaddexp,
+    logaddexp2, heaviside, float_power, divmod,
+    less, less_equal, greater, greater_equal, equal, not_equal,
+)
+from .reductions import (
+    sum, mean, prod, max, min, amax, amin, argmax, argmin, cumsum, cumprod, var, std,
+    cumulative_sum, cumulative_prod,
+)
+from .linalg_top import matmul, dot, vdot, inner
+from . import linalg
+from . import random
+
+# NumPy 2 aliases (reference __init__.py:262-272)
+acos = arccos
+acosh = arccosh
+asin = arcsin
+asinh = arcsinh
+atan = arctan
+atan2 = arctan2
+atanh = arctanh
+pow = power
+
+
+def synchronize() -> None:
+    """Block until all enqueued device work finished (reference
+    __init__.py:233-236).  Lazy (unevaluated) arrays stay lazy."""
+    from ._backend import HipBackend
+    HipBackend().synchronize()
+
+
+def materialize(*arrays) -> None:
+    """Enqueue the kernels of lazy (fused) arrays now, without waiting for
+    them; the reference evaluates lazily only on get()/reductions
+    (_fusion.materialize, ndarray.py:478-481)."""
+    for a in arrays:
+        a._materialize_if_lazy()
+
+
+def expand_dims(a, axis):
+    return asarray(a).expand_dims(axis)
+
+
+def reshape(a, shape):
+    return asarray(a).reshape(shape)
+
+
+def transpose(a, axes=None):
+    return asarray(a).transpose(axes)
+
+
+def ravel(a):
+    return asarray(a).ravel()
+
+
+float16 = _np.float16
+float32 = _np.float32
+float64 = _np.float64
+int16 = _np.int16
+int32 = _np.int32
+int64 = _np.int64
+uint16 = _np.uint16
+uint32 = _np.uint32
+uint64 = _np.uint64
+bool_ = _np.bool_
+newaxis = None
+nan = float("nan")
+inf = float("inf")
+pi = _math.pi
+e = _math.e
+
+__version__ = "0.1.0"

@@ -1,0 +1,345 @@
+"""ctypes binding of libmmp_hip.so -- the HIP counterpart of MetalBackend.
+
+Reference: src/macmetalpy/_metal_backend.py.  There, a ``MetalBackend``
+singleton loads the metalgpu dylib through ctypes (:108-118, 197-263), owns
+a buffer pool (:23-77) and exposes ``create_buffer`` / ``array_to_buffer`` /
+``execute_kernel`` / ``synchronize`` (:269-372).  ``HipBackend`` keeps those
+method names and meanings, but
+
+* buffers are device allocations (HBM is not host-visible), so reading one
+  is an explicit device-to-host copy;
+* kernels are typed C entry points (``unary``, ``binary``, ``reduce`` ...)
+  plus ``compile``/``launch`` for runtime-compiled HIP source, instead of
+  "compile this MSL text, pick a function, run it";
+* every call checks the C status and raises with the library's message.
+
+There is no CPU fallback: if the library is missing or no GPU is present
+the first device operation raises ``HipError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _abi
+
+__all__ = ["HipBackend", "DeviceBuffer", "HipError", "lib_path", "load_library"]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def lib_path() -> str:
+    return os.environ.get("MMP_HIP_LIB", os.path.join(_HERE, "libmmp_hip.so"))
+
+
+class HipError(RuntimeError):
+    """A libmmp_hip.so call failed."""
+
+
+class HipUnsupportedError(HipError, TypeError):
+    """Op/dtype combination the device library does not implement."""
+
+
+class HipArgumentError(HipError, ValueError):
+    """Invalid argument rejected by the device library."""
+
+
+class HipOutOfMemoryError(HipError, MemoryError):
+    """Device allocation failed."""
+
+
+_ERR_CLASSES = {
+    _abi.MMP_E_UNSUPPORTED: HipUnsupportedError,
+    _abi.MMP_E_ARG: HipArgumentError,
+    _abi.MMP_E_OOM: HipOutOfMemoryError,
+}
+
+_c_i64 = ctypes.c_int64
+_c_vp = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_sz = ctypes.c_size_t
+_c_u32p = ctypes.POINTER(ctypes.c_uint32)
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+_SIGNATURES = {
+    "mmp_init": [_c_int],
+    "mmp_device_count": [ctypes.POINTER(_c_int)],
+    "mmp_device_info": [ctypes.c_char_p, _c_int, ctypes.POINTER(_c_int), _c_i64p,
+                        ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)],
+    "mmp_alloc": [_c_sz, ctypes.POINTER(_c_vp)],
+    "mmp_free": [_c_vp],
+    "mmp_empty_cache": [],
+    "mmp_memory_stats": [ctypes.POINTER(_c_sz), ctypes.POINTER(_c_sz)],
+    "mmp_h2d": [_c_vp, _c_vp, _c_sz],
+    "mmp_d2h": [_c_vp, _c_vp, _c_sz],
+    "mmp_d2d": [_c_vp, _c_vp, _c_sz],
+    "mmp_sync": [],
+    "mmp_event_create": [ctypes.POINTER(_c_vp)],
+    "mmp_event_record": [_c_vp],
+    "mmp_event_elapsed_ms": [_c_vp, _c_vp, ctypes.POINTER(ctypes.c_float)],
+    "mmp_event_destroy": [_c_vp],
+    "mmp_unary": [_c_int, _c_int, _c_i64, _c_vp, _c_vp],
+    "mmp_binary": [_c_int, _c_int, _c_i64, _c_vp, _c_vp, _c_vp],
+    "mmp_binary_scalar": [_c_int, _c_int, _c_i64, _c_vp, _c_vp, _c_int, _c_vp],
+    "mmp_copy": [_c_int, _c_int, _c_int, _c_i64p, _c_vp, _c_i64p, _c_vp],
+    "mmp_copy_strided": [_c_int, _c_int, _c_int, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p],
+    "mmp_fill": [_c_int, _c_i64, _c_vp, _c_vp],
+    "mmp_reduce": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_argreduce": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_scan": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_matmul": [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
+                   _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64],
+    "mmp_rtc_compile": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_c_vp)],
+    "mmp_rtc_build": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_vp, _c_sz,
+                      ctypes.POINTER(_c_sz)],
+    "mmp_rtc_launch": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
+    "mmp_rtc_launch_threads": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
+    "mmp_debug_fail_next": [_c_int, _c_int],
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def load_library():
+    """Load libmmp_hip.so (no device needed) and declare its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        path = lib_path()
+        if not os.path.exists(path):
+            raise HipError(
+                f"{path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python -m macmetalpy_amd.csrc.build`")
+        lib = ctypes.CDLL(path)
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _c_int
+        lib.mmp_last_error.argtypes = []
+        lib.mmp_last_error.restype = ctypes.c_char_p
+        _lib = lib
+        return lib
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = _lib.mmp_last_error().decode(errors="replace")
+        raise _ERR_CLASSES.get(status, HipError)(f"{what}: {msg} (status {status})")
+
+
+def _i64_array(vals: Sequence[int]):
+    arr = (ctypes.c_int64 * max(1, len(vals)))(*vals)
+    return arr
+
+
+class DeviceBuffer:
+    """Owning handle to one device allocation (the reference's ``_Buffer``,
+    _metal_backend.py:121-165).  Freed back to the stream-ordered pool when
+    the last reference goes away."""
+
+    __slots__ = ("ptr", "nbytes", "lazy_dependents", "__weakref__")
+
+    def __init__(self, ptr: int, nbytes: int):
+        self.ptr = ptr
+        self.nbytes = nbytes
+        # lazy arrays whose expression reads this buffer (see _elementwise)
+        self.lazy_dependents = None
+
+    def __del__(self):
+        lib = _lib
+        if lib is not None and self.ptr:
+            try:
+                lib.mmp_free(self.ptr)
+            except Exception:  # interpreter shutdown
+                pass
+            self.ptr = 0
+
+    def __repr__(self):
+        return f"DeviceBuffer(0x{self.ptr:x}, {self.nbytes} bytes)"
+
+
+class HipBackend:
+    """Process-wide device context (one GPU, one stream)."""
+
+    _instance: Optional["HipBackend"] = None
+    _lock = threading.Lock()
+
+    def __new__(cls) -> "HipBackend":
+        inst = cls._instance
+        if inst is not None:
+            return inst
+        with cls._lock:
+            if cls._instance is None:
+                inst = super().__new__(cls)
+                inst._lib = load_library()
+                _check(inst._lib.mmp_init(int(os.environ.get("MMP_DEVICE", "0"))), "mmp_init")
+                cls._instance = inst
+            return cls._instance
+
+    # ------------------------------------------------------------ device
+    def device_info(self) -> dict:
+        arch = ctypes.create_string_buffer(64)
+        cus, waves, mt = _c_int(), _c_int(), _c_int()
+        mem = _c_i64()
+        _check(self._lib.mmp_device_info(arch, 64, ctypes.byref(cus), ctypes.byref(mem),
+                                         ctypes.byref(waves), ctypes.byref(mt)),
+               "mmp_device_info")
+        return {"arch": arch.value.decode(), "cu_count": cus.value,
+                "total_mem": mem.value, "wave_size": waves.value,
+                "max_threads_per_block": mt.value}
+
+    def maxThreadsPerGroup(self) -> int:  # reference name, _metal_backend.py:259
+        return self.device_info()["max_threads_per_block"]
+
+    def threadExecutionWidth(self) -> int:  # reference name, _metal_backend.py:261
+        return self.device_info()["wave_size"]
+
+    # ----------------------------------------------------------- buffers
+    def create_buffer(self, n: int, dtype) -> DeviceBuffer:
+        """Uninitialised device buffer of ``n`` elements of ``dtype``."""
+        nbytes = int(n) * np.dtype(dtype).itemsize
+        p = _c_vp()
+        _check(self._lib.mmp_alloc(max(nbytes, 1), ctypes.byref(p)), "mmp_alloc")
+        return DeviceBuffer(p.value, nbytes)
+
+    def array_to_buffer(self, arr: np.ndarray) -> DeviceBuffer:
+        """Upload a host array (made C-contiguous) into a new buffer."""
+        arr = np.ascontiguousarray(arr)
+        buf = self.create_buffer(arr.size, arr.dtype)
+        if arr.nbytes:
+            _check(self._lib.mmp_h2d(buf.ptr, arr.ctypes.data, arr.nbytes), "mmp_h2d")
+        return buf
+
+    def write_buffer(self, buf: DeviceBuffer, byte_offset: int, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes:
+            _check(self._lib.mmp_h2d(buf.ptr + byte_offset, arr.ctypes.data, arr.nbytes),
+                   "mmp_h2d")
+
+    def read_buffer(self, buf: DeviceBuffer, byte_offset: int, out: np.ndarray) -> np.ndarray:
+        """Copy ``out.nbytes`` bytes starting at ``byte_offset`` into ``out``."""
+        if out.nbytes:
+            _check(self._lib.mmp_d2h(out.ctypes.data, buf.ptr + byte_offset, out.nbytes),
+                   "mmp_d2h")
+        return out
+
+    def copy_buffer(self, dst: int, src: int, nbytes: int) -> None:
+        if nbytes:
+            _check(self._lib.mmp_d2d(dst, src, nbytes), "mmp_d2d")
+
+    def synchronize(self) -> None:
+        _check(self._lib.mmp_sync(), "mmp_sync")
+
+    def memory_stats(self) -> tuple[int, int]:
+        a, b = _c_sz(), _c_sz()
+        _check(self._lib.mmp_memory_stats(ctypes.byref(a), ctypes.byref(b)), "mmp_memory_stats")
+        return a.value, b.value
+
+    def empty_cache(self) -> None:
+        _check(self._lib.mmp_empty_cache(), "mmp_empty_cache")
+
+    # ------------------------------------------------------------ events
+    def event(self) -> int:
+        e = _c_vp()
+        _check(self._lib.mmp_event_create(ctypes.byref(e)), "mmp_event_create")
+        return e.value
+
+    def record(self, ev: int) -> None:
+        _check(self._lib.mmp_event_record(ev), "mmp_event_record")
+
+    def elapsed_ms(self, start: int, end: int) -> float:
+        ms = ctypes.c_float()
+        _check(self._lib.mmp_event_elapsed_ms(start, end, ctypes.byref(ms)),
+               "mmp_event_elapsed_ms")
+        return float(ms.value)
+
+    def destroy_event(self, ev: int) -> None:
+        _check(self._lib.mmp_event_destroy(ev), "mmp_event_destroy")
+
+    # ----------------------------------------------------------- kernels
+    def unary(self, op: int, dcode: int, n: int, x: int, out: int) -> None:
+        _check(self._lib.mmp_unary(op, dcode, n, x, out), "mmp_unary")
+
+    def binary(self, op: int, dcode: int, n: int, a: int, b: int, out: int) -> None:
+        _check(self._lib.mmp_binary(op, dcode, n, a, b, out), "mmp_binary")
+
+    def binary_scalar(self, op: int, dcode: int, n: int, arr: int, scalar: np.ndarray,
+                      scalar_side: int, out: int) -> None:
+        _check(self._lib.mmp_binary_scalar(op, dcode, n, arr, scalar.ctypes.data,
+                                           scalar_side, out), "mmp_binary_scalar")
+
+    def copy(self, src_code: int, dst_code: int, shape, x: int, x_strides, out: int) -> None:
+        nd = len(shape)
+        _check(self._lib.mmp_copy(src_code, dst_code, nd, _i64_array(shape), x,
+                                  _i64_array(x_strides), out), "mmp_copy")
+
+    def copy_strided(self, src_code: int, dst_code: int, shape, src: int, src_strides,
+                     dst: int, dst_strides) -> None:
+        nd = len(shape)
+        _check(self._lib.mmp_copy_strided(src_code, dst_code, nd, _i64_array(shape), src,
+                                          _i64_array(src_strides), dst,
+                                          _i64_array(dst_strides)), "mmp_copy_strided")
+
+    def fill(self, dcode: int, n: int, value: np.ndarray, out: int) -> None:
+        _check(self._lib.mmp_fill(dcode, n, value.ctypes.data, out), "mmp_fill")
+
+    def reduce(self, op: int, dcode: int, out_code: int, outer: int, length: int,
+               inner: int, x: int, out: int) -> None:
+        _check(self._lib.mmp_reduce(op, dcode, out_code, outer, length, inner, x, out),
+               "mmp_reduce")
+
+    def argreduce(self, op: int, dcode: int, outer: int, length: int, inner: int,
+                  x: int, out: int) -> None:
+        _check(self._lib.mmp_argreduce(op, dcode, outer, length, inner, x, out),
+               "mmp_argreduce")
+
+    def scan(self, op: int, dcode: int, out_code: int, outer: int, length: int,
+             inner: int, x: int, out: int) -> None:
+        _check(self._lib.mmp_scan(op, dcode, out_code, outer, length, inner, x, out),
+               "mmp_scan")
+
+    def matmul(self, dcode: int, batch: int, M: int, N: int, K: int,
+               A: int, lda: int, sA: int, B: int, ldb: int, sB: int,
+               C: int, ldc: int, sC: int) -> None:
+        _check(self._lib.mmp_matmul(dcode, batch, M, N, K, A, lda, sA, B, ldb, sB,
+                                    C, ldc, sC), "mmp_matmul")
+
+    # -------------------------------------------------- runtime compile
+    def compile(self, source: str, name: str, options: str = "") -> int:
+        """hiprtc-compile ``source`` and return a kernel handle (cached)."""
+        k = _c_vp()
+        _check(self._lib.mmp_rtc_compile(source.encode(), name.encode(), options.encode(),
+                                         ctypes.byref(k)), f"mmp_rtc_compile({name})")
+        return k.value
+
+    def launch(self, kernel: int, grid: Sequence[int], block: Sequence[int],
+               args: Sequence, shared: int = 0, *, threads: bool = False) -> None:
+        """Launch a compiled kernel.  ``args`` are ctypes scalars/structs in
+        kernel-parameter order.  ``threads=True`` interprets ``grid`` as the
+        total number of work-items per dimension (exact, may be ragged)."""
+        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
+        b = (ctypes.c_uint32 * 3)(*(list(block) + [1] * (3 - len(block))))
+        ptrs = (_c_vp * max(1, len(args)))(
+            *[ctypes.cast(ctypes.byref(a), _c_vp) for a in args])
+        fn = self._lib.mmp_rtc_launch_threads if threads else self._lib.mmp_rtc_launch
+        _check(fn(kernel, g, b, shared, ptrs), "mmp_rtc_launch")
+
+
+def rtc_build(source: str, options: str = "", arch: str = "gfx950") -> bytes:
+    """Compile HIP source to a code object without touching a device."""
+    lib = load_library()
+    size = _c_sz()
+    _check(lib.mmp_rtc_build(source.encode(), options.encode(), arch.encode(), None, 0,
+                             ctypes.byref(size)), "mmp_rtc_build")
+    buf = ctypes.create_string_buffer(size.value)
+    _check(lib.mmp_rtc_build(source.encode(), options.encode(), arch.encode(), buf,
+                             size.value, ctypes.byref(size)), "mmp_rtc_build")
+    return buf.raw

@@ -1,0 +1,65 @@
+"""Global configuration (reference: src/macmetalpy/_config.py:11-64).
+
+Same singleton and ``set_config`` keywords as the reference, plus two
+switches this implementation adds:
+
+* ``fusion`` -- build lazy expression DAGs and compile one kernel per DAG
+  (default True).  False evaluates op by op with precompiled kernels, the
+  "unfused" baseline of the fusion benchmark.
+* ``float64_behavior`` keeps the reference's two values.  ``"cpu_fallback"``
+  (the reference's default) keeps float64 precision; on MI355X float64 runs
+  natively on the GPU, so nothing falls back to the CPU.  ``"downcast"``
+  converts float64 inputs to float32 as the reference does.
+"""
+from __future__ import annotations
+
+import threading
+from typing import Literal
+
+__all__ = ["MacMetalConfig", "get_config", "set_config"]
+
+
+class MacMetalConfig:
+    _instance: "MacMetalConfig | None" = None
+    _lock = threading.Lock()
+
+    def __new__(cls) -> "MacMetalConfig":
+        with cls._lock:
+            if cls._instance is None:
+                inst = super().__new__(cls)
+                inst.float64_behavior = "cpu_fallback"
+                inst.warn_on_downcast = True
+                inst.default_float_dtype = "float32"
+                inst.fast_math = False
+                inst.fusion = True
+                cls._instance = inst
+            return cls._instance
+
+
+def get_config() -> MacMetalConfig:
+    return MacMetalConfig()
+
+
+def set_config(
+    *,
+    float64_behavior: Literal["downcast", "cpu_fallback"] | None = None,
+    warn_on_downcast: bool | None = None,
+    default_float_dtype: str | None = None,
+    fast_math: bool | None = None,
+    fusion: bool | None = None,
+) -> None:
+    """Update configuration values (reference: _config.py:43-64)."""
+    cfg = get_config()
+    if float64_behavior is not None:
+        if float64_behavior not in ("downcast", "cpu_fallback"):
+            raise ValueError(
+                f"float64_behavior must be 'downcast' or 'cpu_fallback', got {float64_behavior!r}")
+        cfg.float64_behavior = float64_behavior
+    if warn_on_downcast is not None:
+        cfg.warn_on_downcast = bool(warn_on_downcast)
+    if default_float_dtype is not None:
+        cfg.default_float_dtype = default_float_dtype
+    if fast_math is not None:
+        cfg.fast_math = bool(fast_math)
+    if fusion is not None:
+        cfg.fusion = bool(fusion)

@@ -1,0 +1,241 @@
+"""Elementwise dispatch: dtype resolution, lazy DAG construction, eager path.
+
+Reference: ndarray._binary_op / _unary_op (src/macmetalpy/ndarray.py:960-1243).
+The reference's order of steps is kept -- wrap scalar, resolve the result
+dtype, cast, broadcast, fusion intercept, launch -- with three changes:
+
+* no CPU path: every op runs on the GPU whatever the size (the reference
+  sends arrays below 8K/256K/4M elements to NumPy, ndarray.py:41-44);
+* the result dtype is NumPy's own type resolution for the ufunc
+  (``np.sin(int32)`` is float64, ``int32 // int32`` is int32, ...), then the
+  float64 policy; the reference's GPU kernels instead compute in the input
+  dtype;
+* with fusion on (default) every op returns a lazy array; scalars become
+  kernel arguments and broadcasts stride-0 leaves.  With fusion off, ops run
+  one by one on precompiled kernels after materialising broadcasts and
+  casts, as the reference's GPU path does.
+"""
+from __future__ import annotations
+
+import numbers
+import weakref
+
+import numpy as np
+
+from . import _abi
+from ._broadcasting import broadcast_shapes
+from ._config import get_config
+from ._dtypes import resolve_dtype, ufunc_result_dtype
+from ._fusion import (
+    _MAX_DEPTH, _MAX_LEAVES, BinaryOpNode, CastNode, InputNode, ScalarNode, UnaryOpNode,
+    materialize,
+)
+
+__all__ = ["unary", "binary", "is_scalar", "flush_lazy", "track_lazy"]
+
+
+def is_scalar(x) -> bool:
+    return isinstance(x, (numbers.Number, np.generic, bool)) and not isinstance(x, np.ndarray)
+
+
+def _ndarray():
+    from .ndarray import ndarray
+    return ndarray
+
+
+def _asarray(x):
+    from . import creation
+    return creation.asarray(x)
+
+
+# ----------------------------------------------------- lazy dependents
+def track_lazy(arr) -> None:
+    """Register lazy ``arr`` with every device buffer its DAG reads, so an
+    in-place write to one of those buffers first evaluates ``arr``."""
+    for buf in arr._fusion_node._buffers:
+        deps = buf.lazy_dependents
+        if deps is None:
+            deps = buf.lazy_dependents = weakref.WeakSet()
+        deps.add(arr)
+
+
+def flush_lazy(buffer) -> None:
+    """Evaluate pending lazy arrays that read ``buffer`` (before an in-place
+    write to it).  NumPy evaluates eagerly, so they must see the old data."""
+    if buffer is None:
+        return
+    deps = buffer.lazy_dependents
+    if not deps:
+        return
+    for arr in list(deps):
+        if arr._fusion_node is not None:
+            materialize(arr)
+    deps.clear()
+
+
+# ----------------------------------------------------------- node helpers
+def _node_of(x, dtype):
+    """Fusion node reading ndarray ``x`` as ``dtype``."""
+    node = x._fusion_node
+    if node is None:
+        x._ensure_gpu()
+        node = InputNode(x._buffer, x._shape, x._dtype, x._strides, x._offset)
+    if node._dtype != dtype:
+        node = CastNode(node, dtype)
+    return node
+
+
+def _limit(x, node, dtype, extra_depth=1):
+    """Materialise ``x`` first when fusing would exceed the depth or leaf
+    caps (reference: _MAX_DEPTH, ndarray.py:1218-1224)."""
+    if x._fusion_node is not None and (node._depth + extra_depth > _MAX_DEPTH
+                                       or node._nleaves > _MAX_LEAVES):
+        materialize(x)
+        return _node_of(x, dtype)
+    return node
+
+
+def _lazy_result(node):
+    arr = _ndarray()._lazy(node)
+    track_lazy(arr)
+    return arr
+
+
+def _empty(shape, dtype):
+    from . import creation
+    return creation.empty(shape, dtype=dtype)
+
+
+def _materialise_operand(x, shape, dtype):
+    """Unfused mode: contiguous, full-shape, result-dtype copy of ``x``
+    (the reference's astype + _gpu_broadcast_to, ndarray.py:1058-1065)."""
+    x._materialize_if_lazy()
+    if x._shape == tuple(shape) and x._dtype == dtype and x._is_device_contiguous():
+        return x
+    return x._broadcast_copy(shape, dtype)
+
+
+# ------------------------------------------------------------------ ops
+def unary(op_name: str, x):
+    x = _asarray(x)
+    ufunc = _abi.UNARY_OPS[op_name][1]
+    rdt = ufunc_result_dtype(ufunc, x._dtype)
+    if x.size == 0:
+        return _empty(x._shape, rdt)
+    if not get_config().fusion:
+        xin = _materialise_operand(x, x._shape, rdt)
+        node = UnaryOpNode(op_name, _node_of(xin, rdt), x._shape, rdt)
+        out = _lazy_result(node)
+        materialize(out)
+        return out
+    node = _limit(x, _node_of(x, rdt), rdt)
+    return _lazy_result(UnaryOpNode(op_name, node, x._shape, rdt))
+
+
+def _scalar_operand(v):
+    """Python / NumPy scalar for dtype resolution (NEP 50: Python scalars
+    are weak, NumPy scalars strong)."""
+    if isinstance(v, np.generic):
+        return v
+    if isinstance(v, bool):
+        return bool(v)
+    return v
+
+
+def binary(op_name: str, a, b):
+    nd = _ndarray()
+    a_arr = isinstance(a, nd)
+    b_arr = isinstance(b, nd)
+    if not a_arr and not is_scalar(a):
+        a = _asarray(a)
+        a_arr = True
+    if not b_arr and not is_scalar(b):
+        b = _asarray(b)
+        b_arr = True
+    if not a_arr and not b_arr:
+        a = _asarray(a)
+        a_arr = True
+    ka = a._dtype if a_arr else _scalar_operand(a)
+    kb = b._dtype if b_arr else _scalar_operand(b)
+    if op_name in _abi.COMPARE_OPS:
+        # NumPy compares in the operands' common dtype and returns bool
+        ufunc = _abi.COMPARE_OPS[op_name][0]
+        ufunc_result_dtype(ufunc, ka, kb)  # raises for invalid operands
+        odt = resolve_dtype(np.result_type(ka, kb))
+        rdt = np.dtype(np.bool_)
+    else:
+        ufunc = _abi.BINARY_OPS[op_name][1]
+        rdt = ufunc_result_dtype(ufunc, ka, kb)
+        odt = rdt
+    sa = a._shape if a_arr else ()
+    sb = b._shape if b_arr else ()
+    shape = broadcast_shapes(sa, sb)
+    size = 1
+    for s in shape:
+        size *= s
+    if size == 0:
+        return _empty(shape, rdt)
+    if op_name == "pow_op" and rdt.kind in "iu":
+        _check_int_power(b if b_arr else None, None if b_arr else b)
+
+    if not get_config().fusion:
+        an = (_node_of(_materialise_operand(a, shape, odt), odt) if a_arr
+              else ScalarNode(a, odt))
+        bn = (_node_of(_materialise_operand(b, shape, odt), odt) if b_arr
+              else ScalarNode(b, odt))
+        out = _lazy_result(BinaryOpNode(op_name, an, bn, shape, rdt))
+        materialize(out)
+        return out
+
+    an = _node_of(a, odt) if a_arr else ScalarNode(a, odt)
+    bn = _node_of(b, odt) if b_arr else ScalarNode(b, odt)
+    if a_arr:
+        an = _limit(a, an, odt)
+    if b_arr:
+        bn = _limit(b, bn, odt)
+    if an._nleaves + bn._nleaves > _MAX_LEAVES:
+        if a_arr and a._fusion_node is not None:
+            materialize(a)
+            an = _node_of(a, odt)
+        if b_arr and b._fusion_node is not None:
+            materialize(b)
+            bn = _node_of(b, odt)
+    return _lazy_result(BinaryOpNode(op_name, an, bn, shape, rdt))
+
+
+def _check_int_power(exp_arr, exp_scalar):
+    """NumPy raises for integer powers with negative integer exponents."""
+    msg = "Integers to negative integer powers are not allowed."
+    if exp_arr is None:
+        if exp_scalar < 0:
+            raise ValueError(msg)
+        return
+    if exp_arr._dtype.kind == "i" and exp_arr.size:
+        from . import reductions
+        if int(reductions.min(exp_arr)) < 0:
+            raise ValueError(msg)
+
+
+def power(a, b):
+    """``a ** b`` with NumPy's scalar-exponent shortcuts for inexact arrays:
+    ``**2`` -> square, ``**0.5`` -> sqrt, ``**-1`` -> reciprocal (NumPy's
+    fast_scalar_power), which round differently from pow()."""
+    nd = _ndarray()
+    if isinstance(a, nd) and a._dtype.kind == "f" and is_scalar(b) and not isinstance(b, np.generic):
+        if isinstance(b, int) and not isinstance(b, bool):
+            if b == 2:
+                return unary("square_op", a)
+            if b == -1:
+                return unary("reciprocal_op", a)
+        elif isinstance(b, float):
+            if b == 2.0:
+                return unary("square_op", a)
+            if b == 0.5:
+                return unary("sqrt_op", a)
+            if b == -1.0:
+                return unary("reciprocal_op", a)
+    return binary("pow_op", a, b)
+
+
+def resolve(dtype):
+    return resolve_dtype(dtype)

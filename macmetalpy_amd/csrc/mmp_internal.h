@@ -1,0 +1,60 @@
+// mmp_internal.h -- shared host-side helpers of libmmp_hip.so (not ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mmp_hip.h"
+
+namespace mmpi {
+
+// Library stream (created by mmp_init).  All kernels and copies go here.
+hipStream_t stream();
+// Ensure mmp_init ran (lazily initialising device 0); returns status.
+int ensure_init();
+// Number of compute units of the current device.
+int cu_count();
+
+// Record an error message for mmp_last_error and return `code`.
+int fail(int code, const char *fmt, ...);
+// Check a HIP status; on error record it and return MMP_E_HIP.
+int check_hip(hipError_t e, const char *what);
+// Check the last launch; returns 0 or MMP_E_HIP (also honours injection).
+int check_launch(const char *what);
+// Fault-injection counters (mmp_debug_fail_next).
+bool inject(int kind);
+
+// Per-device scratch memory owned by the library (grown on demand, never
+// shrunk).  Used for reduction partials, completion tickets and scan tile
+// descriptors.  The memory is zero-filled when first allocated; kernels
+// that use counters leave them at zero when they finish.
+void *scratch(int slot, size_t bytes, int *status);
+enum { SCRATCH_REDUCE_PARTIALS = 0, SCRATCH_REDUCE_TICKETS = 1,
+       SCRATCH_SCAN_FLAGS = 2, SCRATCH_SCAN_VALUES = 3,
+       SCRATCH_SCAN_COUNTER = 4, SCRATCH_NSLOTS = 5 };
+// Monotone call counter used to tag scan tile flags with a generation, so
+// the flag array never needs clearing between calls.
+uint32_t next_generation();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace mmpi
+
+// Dispatch a dtype code onto a C++ type.  BODY is a lambda-like block that
+// uses the type alias `T`.
+#define MMP_DISPATCH_ALL(dtype, ...)                                          \
+  switch (dtype) {                                                            \
+    case MMP_BOOL: { typedef bool T; __VA_ARGS__ }                            \
+    case MMP_I16: { typedef mmp_i16 T; __VA_ARGS__ }                          \
+    case MMP_U16: { typedef mmp_u16 T; __VA_ARGS__ }                          \
+    case MMP_I32: { typedef mmp_i32 T; __VA_ARGS__ }                          \
+    case MMP_U32: { typedef mmp_u32 T; __VA_ARGS__ }                          \
+    case MMP_I64: { typedef mmp_i64 T; __VA_ARGS__ }                          \
+    case MMP_U64: { typedef mmp_u64 T; __VA_ARGS__ }                          \
+    case MMP_F16: { typedef mmp_half T; __VA_ARGS__ }                         \
+    case MMP_F32: { typedef float T; __VA_ARGS__ }                            \
+    case MMP_F64: { typedef double T; __VA_ARGS__ }                           \
+    default:                                                                  \
+      return mmpi::fail(MMP_E_UNSUPPORTED, "unsupported dtype code %d",       \
+                        (int)(dtype));                                        \
+  }

@@ -1,0 +1,523 @@
+// mmp_ops.h -- per-element operations with NumPy semantics, for gfx950.
+//
+// One definition of every elementwise op, included both by the precompiled
+// kernels (elementwise.hip, built by hipcc) and by the kernels the fusion
+// engine generates at run time (compiled by hiprtc).  Because both paths
+// evaluate the same functions with the same compile flags
+// (-ffp-contract=off), a fused expression is bit-identical to the same
+// expression evaluated op by op.
+//
+// The semantics follow what the reference computes on its CPU/NumPy path
+// (src/macmetalpy/ndarray.py:74-111 maps every op to a numpy ufunc), NOT its
+// Metal shaders, which differ from NumPy in several places:
+//  - integer floor_divide truncates there (_kernels.py:44); here it floors;
+//  - remainder there is a - floor_divide(a, b) * b in three launches
+//    (math_ops.py:540-548); here it is one op with NumPy's sign rules;
+//  - expm1 / log1p there are exp(x)-1 / log(1+x) (_kernels.py:263, 269);
+//    here they are the accurate library functions.
+// Float16 values are widened to float, computed, and rounded back once, as
+// NumPy's float16 loops do.  Integer arithmetic wraps (two's complement).
+#pragma once
+
+#ifndef __HIPCC_RTC__
+#include <hip/hip_runtime.h>
+#endif
+
+typedef _Float16 mmp_half;
+typedef short mmp_i16;
+typedef unsigned short mmp_u16;
+typedef int mmp_i32;
+typedef unsigned int mmp_u32;
+typedef long long mmp_i64;
+typedef unsigned long long mmp_u64;
+
+#define MMP_DI __device__ __forceinline__
+
+// ---------------------------------------------------------------- traits
+template <typename T> struct mmp_t;
+template <> struct mmp_t<float> {
+  enum { is_float = 1, is_signed = 1, is_bool = 0 };
+  typedef float C;
+  typedef float U;
+};
+template <> struct mmp_t<double> {
+  enum { is_float = 1, is_signed = 1, is_bool = 0 };
+  typedef double C;
+  typedef double U;
+};
+template <> struct mmp_t<mmp_half> {
+  enum { is_float = 1, is_signed = 1, is_bool = 0 };
+  typedef float C;
+  typedef float U;
+};
+template <> struct mmp_t<mmp_i16> {
+  enum { is_float = 0, is_signed = 1, is_bool = 0 };
+  typedef mmp_i16 C;
+  typedef mmp_u16 U;
+  static constexpr mmp_i16 lowest = (mmp_i16)(-32767 - 1);
+};
+template <> struct mmp_t<mmp_u16> {
+  enum { is_float = 0, is_signed = 0, is_bool = 0 };
+  typedef mmp_u16 C;
+  typedef mmp_u16 U;
+  static constexpr mmp_u16 lowest = 0;
+};
+template <> struct mmp_t<mmp_i32> {
+  enum { is_float = 0, is_signed = 1, is_bool = 0 };
+  typedef mmp_i32 C;
+  typedef mmp_u32 U;
+  static constexpr mmp_i32 lowest = (-2147483647 - 1);
+};
+template <> struct mmp_t<mmp_u32> {
+  enum { is_float = 0, is_signed = 0, is_bool = 0 };
+  typedef mmp_u32 C;
+  typedef mmp_u32 U;
+  static constexpr mmp_u32 lowest = 0u;
+};
+template <> struct mmp_t<mmp_i64> {
+  enum { is_float = 0, is_signed = 1, is_bool = 0 };
+  typedef mmp_i64 C;
+  typedef mmp_u64 U;
+  static constexpr mmp_i64 lowest = (-9223372036854775807LL - 1);
+};
+template <> struct mmp_t<mmp_u64> {
+  enum { is_float = 0, is_signed = 0, is_bool = 0 };
+  typedef mmp_u64 C;
+  typedef mmp_u64 U;
+  static constexpr mmp_u64 lowest = 0ull;
+};
+template <> struct mmp_t<bool> {
+  enum { is_float = 0, is_signed = 0, is_bool = 1 };
+  typedef bool C;
+  typedef bool U;
+  static constexpr bool lowest = false;
+};
+
+// --------------------------------------------- float / double math overloads
+#define MMP_MATH1(name, f32, f64)                                             \
+  MMP_DI float mm_##name(float x) { return f32(x); }                          \
+  MMP_DI double mm_##name(double x) { return f64(x); }
+#define MMP_MATH2(name, f32, f64)                                             \
+  MMP_DI float mm_##name(float x, float y) { return f32(x, y); }              \
+  MMP_DI double mm_##name(double x, double y) { return f64(x, y); }
+
+MMP_MATH1(sqrt, sqrtf, sqrt)
+MMP_MATH1(cbrt, cbrtf, cbrt)
+MMP_MATH1(exp, expf, exp)
+MMP_MATH1(exp2, exp2f, exp2)
+MMP_MATH1(expm1, expm1f, expm1)
+MMP_MATH1(log, logf, log)
+MMP_MATH1(log2, log2f, log2)
+MMP_MATH1(log10, log10f, log10)
+MMP_MATH1(log1p, log1pf, log1p)
+MMP_MATH1(sin, sinf, sin)
+MMP_MATH1(cos, cosf, cos)
+MMP_MATH1(tan, tanf, tan)
+MMP_MATH1(asin, asinf, asin)
+MMP_MATH1(acos, acosf, acos)
+MMP_MATH1(atan, atanf, atan)
+MMP_MATH1(sinh, sinhf, sinh)
+MMP_MATH1(cosh, coshf, cosh)
+MMP_MATH1(tanh, tanhf, tanh)
+MMP_MATH1(asinh, asinhf, asinh)
+MMP_MATH1(acosh, acoshf, acosh)
+MMP_MATH1(atanh, atanhf, atanh)
+MMP_MATH1(floor, floorf, floor)
+MMP_MATH1(ceil, ceilf, ceil)
+MMP_MATH1(rint, rintf, rint)
+MMP_MATH1(trunc, truncf, trunc)
+MMP_MATH1(fabs, fabsf, fabs)
+MMP_MATH2(pow, powf, pow)
+MMP_MATH2(atan2, atan2f, atan2)
+MMP_MATH2(hypot, hypotf, hypot)
+MMP_MATH2(fmod, fmodf, fmod)
+MMP_MATH2(copysign, copysignf, copysign)
+MMP_MATH2(nextafter, nextafterf, nextafter)
+
+MMP_DI bool mm_isnan(float x) { return x != x; }
+MMP_DI bool mm_isnan(double x) { return x != x; }
+MMP_DI float mm_nan(float) { return __builtin_nanf(""); }
+MMP_DI double mm_nan(double) { return __builtin_nan(""); }
+
+// 180/pi and pi/180, rounded to the compute type first as
+// numpy's npy_degreesf / npy_radiansf do (x * (float)(180.0/NPY_PI)).
+MMP_DI float mm_rad2deg(float) { return (float)(180.0 / 3.14159265358979323846); }
+MMP_DI double mm_rad2deg(double) { return 180.0 / 3.14159265358979323846; }
+MMP_DI float mm_deg2rad(float) { return (float)(3.14159265358979323846 / 180.0); }
+MMP_DI double mm_deg2rad(double) { return 3.14159265358979323846 / 180.0; }
+MMP_DI float mm_ln2(float) { return 0.693147180559945309417f; }
+MMP_DI double mm_ln2(double) { return 0.693147180559945309417; }
+MMP_DI float mm_log2e(float) { return 1.442695040888963407360f; }
+MMP_DI double mm_log2e(double) { return 1.442695040888963407360; }
+
+// ------------------------------------------------------ integer helpers
+template <typename T> MMP_DI T iwrap_add(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  return (T)(U)((U)a + (U)b);
+}
+template <typename T> MMP_DI T iwrap_sub(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  return (T)(U)((U)a - (U)b);
+}
+template <typename T> MMP_DI T iwrap_mul(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  // 16-bit operands promote to int in C++; multiply in 32-bit unsigned.
+  if constexpr (sizeof(T) < 4) {
+    return (T)(U)((unsigned int)(U)a * (unsigned int)(U)b);
+  } else {
+    return (T)(U)((U)a * (U)b);
+  }
+}
+
+// =====================================================================
+// Unary ops.  C = compute type; results rounded to T once.
+// =====================================================================
+template <typename T> MMP_DI T op_neg(T x) {
+  if constexpr (mmp_t<T>::is_float) {
+    return (T)(-(typename mmp_t<T>::C)x);
+  } else {
+    return iwrap_sub((T)0, x);
+  }
+}
+template <typename T> MMP_DI T op_positive(T x) { return x; }
+template <typename T> MMP_DI T op_abs(T x) {
+  if constexpr (mmp_t<T>::is_float) {
+    return (T)mm_fabs((typename mmp_t<T>::C)x);
+  } else if constexpr (mmp_t<T>::is_signed) {
+    return x < 0 ? iwrap_sub((T)0, x) : x;  // abs(INT_MIN) == INT_MIN
+  } else {
+    return x;
+  }
+}
+template <typename T> MMP_DI T op_sign(T x) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C v = (C)x;
+    if (mm_isnan(v)) return (T)v;
+    return (T)(v > (C)0 ? (C)1 : (v < (C)0 ? (C)-1 : (C)0));
+  } else if constexpr (mmp_t<T>::is_signed) {
+    return (T)((x > 0) - (x < 0));
+  } else {
+    return (T)(x > 0 ? 1 : 0);
+  }
+}
+template <typename T> MMP_DI T op_square(T x) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)((C)x * (C)x);
+  } else {
+    return iwrap_mul(x, x);
+  }
+}
+template <typename T> MMP_DI T op_reciprocal(T x) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)((C)1 / (C)x);
+  } else {
+    // numpy's integer reciprocal evaluates 1/x; 1/0 yields the lowest value
+    if (x == 0) return mmp_t<T>::lowest;
+    if constexpr (mmp_t<T>::is_signed) {
+      return (T)(x == 1 ? 1 : (x == -1 ? -1 : 0));
+    } else {
+      return (T)(x == 1 ? 1 : 0);
+    }
+  }
+}
+
+#define MMP_FLOAT_UNARY(NAME, EXPR)                                           \
+  template <typename T> MMP_DI T op_##NAME(T x_) {                            \
+    typedef typename mmp_t<T>::C C;                                           \
+    C x = (C)x_;                                                              \
+    return (T)(EXPR);                                                         \
+  }
+
+MMP_FLOAT_UNARY(sqrt, mm_sqrt(x))
+MMP_FLOAT_UNARY(cbrt, mm_cbrt(x))
+MMP_FLOAT_UNARY(exp, mm_exp(x))
+MMP_FLOAT_UNARY(exp2, mm_exp2(x))
+MMP_FLOAT_UNARY(expm1, mm_expm1(x))
+MMP_FLOAT_UNARY(log, mm_log(x))
+MMP_FLOAT_UNARY(log2, mm_log2(x))
+MMP_FLOAT_UNARY(log10, mm_log10(x))
+MMP_FLOAT_UNARY(log1p, mm_log1p(x))
+MMP_FLOAT_UNARY(sin, mm_sin(x))
+MMP_FLOAT_UNARY(cos, mm_cos(x))
+MMP_FLOAT_UNARY(tan, mm_tan(x))
+MMP_FLOAT_UNARY(arcsin, mm_asin(x))
+MMP_FLOAT_UNARY(arccos, mm_acos(x))
+MMP_FLOAT_UNARY(arctan, mm_atan(x))
+MMP_FLOAT_UNARY(sinh, mm_sinh(x))
+MMP_FLOAT_UNARY(cosh, mm_cosh(x))
+MMP_FLOAT_UNARY(tanh, mm_tanh(x))
+MMP_FLOAT_UNARY(arcsinh, mm_asinh(x))
+MMP_FLOAT_UNARY(arccosh, mm_acosh(x))
+MMP_FLOAT_UNARY(arctanh, mm_atanh(x))
+MMP_FLOAT_UNARY(degrees, x * mm_rad2deg(x))
+MMP_FLOAT_UNARY(radians, x * mm_deg2rad(x))
+
+// floor/ceil/rint/trunc keep integer inputs unchanged (numpy returns the
+// integer dtype for floor/ceil/trunc of integers).
+#define MMP_ROUNDING_UNARY(NAME, FN)                                          \
+  template <typename T> MMP_DI T op_##NAME(T x) {                             \
+    if constexpr (mmp_t<T>::is_float) {                                       \
+      return (T)FN((typename mmp_t<T>::C)x);                                  \
+    } else {                                                                  \
+      return x;                                                               \
+    }                                                                         \
+  }
+MMP_ROUNDING_UNARY(floor, mm_floor)
+MMP_ROUNDING_UNARY(ceil, mm_ceil)
+MMP_ROUNDING_UNARY(rint, mm_rint)
+MMP_ROUNDING_UNARY(trunc, mm_trunc)
+
+// =====================================================================
+// Binary ops
+// =====================================================================
+template <typename T> MMP_DI T op_add(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)((C)a + (C)b);
+  } else if constexpr (mmp_t<T>::is_bool) {
+    return a || b;
+  } else {
+    return iwrap_add(a, b);
+  }
+}
+template <typename T> MMP_DI T op_subtract(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)((C)a - (C)b);
+  } else {
+    return iwrap_sub(a, b);
+  }
+}
+template <typename T> MMP_DI T op_multiply(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)((C)a * (C)b);
+  } else if constexpr (mmp_t<T>::is_bool) {
+    return a && b;
+  } else {
+    return iwrap_mul(a, b);
+  }
+}
+template <typename T> MMP_DI T op_true_divide(T a, T b) {
+  typedef typename mmp_t<T>::C C;
+  return (T)((C)a / (C)b);
+}
+
+// NumPy's float divmod (numpy/_core/src/npymath/npy_math_internal.h.src,
+// npy_divmod): the quotient is (a - fmod(a, b)) / b, corrected towards
+// -inf and snapped to the nearest integer; the remainder takes b's sign.
+template <typename C> MMP_DI C mm_divmod(C a, C b, C *modulus) {
+  C mod = mm_fmod(a, b);
+  if (!(b != (C)0)) {  // b == 0 (b is not NaN here)
+    *modulus = mod;
+    return a / b;
+  }
+  C div = (a - mod) / b;
+  if (mod != (C)0) {
+    if ((b < (C)0) != (mod < (C)0)) {
+      mod += b;
+      div -= (C)1;
+    }
+  } else {
+    mod = mm_copysign((C)0, b);
+  }
+  C floordiv;
+  if (div != (C)0) {
+    floordiv = mm_floor(div);
+    if (div - floordiv > (C)0.5) floordiv += (C)1;
+  } else {
+    floordiv = mm_copysign((C)0, a / b);
+  }
+  *modulus = mod;
+  return floordiv;
+}
+
+template <typename T> MMP_DI T op_floor_divide(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (!(y != (C)0) && !mm_isnan(y)) return (T)(x / y);  // npy_floor_divide
+    C m;
+    return (T)mm_divmod(x, y, &m);
+  } else {
+    if (b == 0) return (T)0;  // numpy: 0 (with a divide-by-zero warning)
+    if constexpr (mmp_t<T>::is_signed) {
+      if (b == (T)-1) return iwrap_sub((T)0, a);  // INT_MIN // -1 wraps
+      T q = (T)(a / b);
+      T r = (T)(a - q * b);
+      if (r != 0 && ((r < 0) != (b < 0))) q = (T)(q - 1);
+      return q;
+    } else {
+      return (T)(a / b);
+    }
+  }
+}
+
+template <typename T> MMP_DI T op_remainder(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (!(y != (C)0) && !mm_isnan(y)) return (T)mm_fmod(x, y);  // npy_remainder
+    C m;
+    mm_divmod(x, y, &m);
+    return (T)m;
+  } else {
+    if (b == 0) return (T)0;
+    if constexpr (mmp_t<T>::is_signed) {
+      if (b == (T)-1) return (T)0;
+      T q = (T)(a / b);
+      T r = (T)(a - q * b);
+      if (r != 0 && ((r < 0) != (b < 0))) r = (T)(r + b);
+      return r;
+    } else {
+      return (T)(a % b);
+    }
+  }
+}
+
+template <typename T> MMP_DI T op_fmod(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)mm_fmod((C)a, (C)b);
+  } else {
+    if (b == 0) return (T)0;
+    if constexpr (mmp_t<T>::is_signed) {
+      if (b == (T)-1) return (T)0;
+    }
+    return (T)(a % b);  // C semantics: sign of the dividend
+  }
+}
+
+template <typename T> MMP_DI T op_power(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    return (T)mm_pow((C)a, (C)b);
+  } else {
+    // exponentiation by squaring with wrap-around; negative exponents are
+    // rejected by the host before launch (numpy raises ValueError).
+    if constexpr (mmp_t<T>::is_signed) {
+      if (b < 0) return (T)0;
+    }
+    typedef typename mmp_t<T>::U U;
+    U base = (U)a, e = (U)b, r = (U)1;
+    while (e) {
+      if (e & (U)1) r = (U)iwrap_mul((T)r, (T)base);
+      e = (U)(e >> 1);
+      if (e) base = (U)iwrap_mul((T)base, (T)base);
+    }
+    return (T)r;
+  }
+}
+
+// maximum/minimum propagate NaN; on ties the second operand is returned,
+// matching numpy's results for (+0, -0) pairs.  fmax/fmin ignore NaN.
+template <typename T> MMP_DI T op_maximum(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (mm_isnan(x)) return a;
+    if (mm_isnan(y)) return b;
+    return x > y ? a : b;
+  } else if constexpr (mmp_t<T>::is_bool) {
+    return a || b;
+  } else {
+    return a > b ? a : b;
+  }
+}
+template <typename T> MMP_DI T op_minimum(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (mm_isnan(x)) return a;
+    if (mm_isnan(y)) return b;
+    return x < y ? a : b;
+  } else if constexpr (mmp_t<T>::is_bool) {
+    return a && b;
+  } else {
+    return a < b ? a : b;
+  }
+}
+template <typename T> MMP_DI T op_fmax(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (mm_isnan(y)) return a;
+    if (mm_isnan(x)) return b;
+    return x > y ? a : b;
+  } else {
+    return op_maximum(a, b);
+  }
+}
+template <typename T> MMP_DI T op_fmin(T a, T b) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    C x = (C)a, y = (C)b;
+    if (mm_isnan(y)) return a;
+    if (mm_isnan(x)) return b;
+    return x < y ? a : b;
+  } else {
+    return op_minimum(a, b);
+  }
+}
+
+#define MMP_FLOAT_BINARY(NAME, EXPR)                                          \
+  template <typename T> MMP_DI T op_##NAME(T a_, T b_) {                      \
+    typedef typename mmp_t<T>::C C;                                           \
+    C a = (C)a_, b = (C)b_;                                                   \
+    return (T)(EXPR);                                                         \
+  }
+MMP_FLOAT_BINARY(arctan2, mm_atan2(a, b))
+MMP_FLOAT_BINARY(hypot, mm_hypot(a, b))
+MMP_FLOAT_BINARY(copysign, mm_copysign(a, b))
+MMP_FLOAT_BINARY(nextafter, mm_nextafter(a, b))
+
+// numpy npy_logaddexp / npy_logaddexp2
+template <typename T> MMP_DI T op_logaddexp(T a_, T b_) {
+  typedef typename mmp_t<T>::C C;
+  C x = (C)a_, y = (C)b_;
+  if (x == y) return (T)(x + mm_ln2(x));
+  C d = x - y;
+  if (d > (C)0) return (T)(x + mm_log1p(mm_exp(-d)));
+  if (d <= (C)0) return (T)(y + mm_log1p(mm_exp(d)));
+  return (T)d;  // NaN
+}
+template <typename T> MMP_DI T op_logaddexp2(T a_, T b_) {
+  typedef typename mmp_t<T>::C C;
+  C x = (C)a_, y = (C)b_;
+  if (x == y) return (T)(x + (C)1);
+  C d = x - y;
+  if (d > (C)0) return (T)(x + mm_log2e(x) * mm_log1p(mm_exp2(-d)));
+  if (d <= (C)0) return (T)(y + mm_log2e(x) * mm_log1p(mm_exp2(d)));
+  return (T)d;
+}
+// numpy npy_heaviside
+template <typename T> MMP_DI T op_heaviside(T a_, T h) {
+  typedef typename mmp_t<T>::C C;
+  C x = (C)a_;
+  if (mm_isnan(x)) return (T)mm_nan(x);
+  if (x == (C)0) return h;
+  if (x < (C)0) return (T)0;
+  return (T)1;
+}
+
+// =====================================================================
+// Conversions (astype).  bool targets test != 0 (NaN -> true).
+// =====================================================================
+template <typename To, typename From> MMP_DI To mmp_convert(From v) {
+  if constexpr (mmp_t<To>::is_bool) {
+    if constexpr (mmp_t<From>::is_float) {
+      return (typename mmp_t<From>::C)v != (typename mmp_t<From>::C)0;
+    } else {
+      return v != 0;
+    }
+  } else if constexpr (mmp_t<From>::is_bool) {
+    return (To)(v ? 1 : 0);
+  } else if constexpr (sizeof(From) == 2 && mmp_t<From>::is_float) {
+    return (To)(float)v;  // half -> widen first
+  } else {
+    return (To)v;
+  }
+}

@@ -1,0 +1,499 @@
+// runtime.hip -- device, stream, caching allocator, copies, events, error
+// reporting, scratch memory and runtime compilation for libmmp_hip.so.
+//
+// Replaces MetalBackend (src/macmetalpy/_metal_backend.py:179-372) and its
+// _BufferPool (:23-77).  Differences by design:
+//  * one in-order HIP stream per process (default priority); the caching
+//    pool's frees are stream-ordered, so a freed block can be handed to the
+//    next allocation immediately -- the reference defers reuse until a
+//    synchronize() (_metal_backend.py:155-162) because Metal command buffers
+//    are not ordered against host reuse;
+//  * every call reports failures through a status code + thread-local
+//    message instead of the metalgpu ABI's silent `void`;
+//  * kernels are precompiled gfx950 code objects; only fused expressions and
+//    user RawKernels go through hiprtc, cached by source text.
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "mmp_internal.h"
+
+namespace {
+
+struct Device {
+  bool ready = false;
+  int id = -1;
+  hipStream_t stream = nullptr;
+  int cus = 0;
+  int wave = 64;
+  int max_threads = 1024;
+  int64_t total_mem = 0;
+  std::string arch;
+};
+
+Device g_dev;
+std::mutex g_mu;                 // guards g_dev init, pool, rtc cache
+thread_local std::string g_err;  // mmp_last_error
+
+// ---- caching pool --------------------------------------------------------
+// Sizes are rounded to 4 KiB below 2 MiB and to 2 MiB above; a free block
+// is reused for a request of the same rounded size (or up to 25% larger
+// for big blocks).  Minimum 4 KiB so tiny arrays never share a page with
+// another allocation.
+std::multimap<size_t, void *> g_free;         // rounded size -> block
+std::unordered_map<void *, size_t> g_live;    // block -> rounded size
+size_t g_in_use = 0, g_cached = 0;
+
+size_t round_size(size_t b) {
+  const size_t small = 4096, big = 2u << 20;
+  if (b < big) return (b + small - 1) / small * small;
+  return (b + big - 1) / big * big;
+}
+
+// ---- scratch -------------------------------------------------------------
+void *g_scratch[mmpi::SCRATCH_NSLOTS] = {};
+size_t g_scratch_size[mmpi::SCRATCH_NSLOTS] = {};
+uint32_t g_generation = 0;
+
+// ---- fault injection (mmp_debug_fail_next) -------------------------------
+int g_fail_kind = 0, g_fail_count = 0;
+
+// ---- rtc cache -----------------------------------------------------------
+struct RtcEntry {
+  hipModule_t module;
+  hipFunction_t fn;
+};
+std::unordered_map<std::string, RtcEntry> g_rtc;
+
+int init_locked(int device) {
+  if (g_dev.ready) {
+    if (device == g_dev.id) return MMP_OK;
+    return mmpi::fail(MMP_E_ARG, "already initialised on device %d", g_dev.id);
+  }
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0)
+    return mmpi::fail(MMP_E_NODEVICE, "no HIP device available (%s)",
+                      e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return mmpi::fail(MMP_E_ARG, "device %d out of range (%d devices)", device, count);
+  if (int st = mmpi::check_hip(hipSetDevice(device), "hipSetDevice")) return st;
+  hipDeviceProp_t prop;
+  if (int st = mmpi::check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"))
+    return st;
+  hipStream_t s;
+  if (int st = mmpi::check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking),
+                               "hipStreamCreateWithFlags"))
+    return st;
+  g_dev.stream = s;
+  g_dev.id = device;
+  g_dev.cus = prop.multiProcessorCount;
+  g_dev.wave = prop.warpSize;
+  g_dev.max_threads = prop.maxThreadsPerBlock;
+  g_dev.total_mem = (int64_t)prop.totalGlobalMem;
+  g_dev.arch = prop.gcnArchName;
+  g_dev.ready = true;
+  return MMP_OK;
+}
+
+void release_cached_locked() {
+  for (auto &kv : g_free) {
+    (void)hipFree(kv.second);
+  }
+  g_free.clear();
+  g_cached = 0;
+}
+
+}  // namespace
+
+// ========================================================================
+// internal helpers
+// ========================================================================
+namespace mmpi {
+
+int fail(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return MMP_OK;
+  return fail(e == hipErrorOutOfMemory ? MMP_E_OOM : MMP_E_HIP, "%s failed: %s", what,
+              hipGetErrorString(e));
+}
+
+bool inject(int kind) {
+  if (g_fail_kind != kind || g_fail_count <= 0) return false;
+  if (--g_fail_count == 0) {
+    g_fail_kind = 0;
+    return true;
+  }
+  return false;
+}
+
+int check_launch(const char *what) {
+  if (inject(3)) return fail(MMP_E_INJECTED, "%s: injected launch failure", what);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return MMP_OK;
+  return fail(MMP_E_HIP, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t stream() { return g_dev.stream; }
+
+int ensure_init() {
+  if (g_dev.ready) return MMP_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return init_locked(0);
+}
+
+int cu_count() { return g_dev.cus; }
+
+void *scratch(int slot, size_t bytes, int *status) {
+  *status = MMP_OK;
+  if (slot < 0 || slot >= SCRATCH_NSLOTS) {
+    *status = fail(MMP_E_ARG, "bad scratch slot");
+    return nullptr;
+  }
+  if (g_scratch_size[slot] >= bytes && g_scratch[slot]) return g_scratch[slot];
+  size_t want = round_size(bytes < 65536 ? 65536 : bytes);
+  // growing: wait for users of the old block before replacing it
+  if (g_scratch[slot]) {
+    if ((*status = check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize")))
+      return nullptr;
+    (void)hipFree(g_scratch[slot]);
+    g_scratch[slot] = nullptr;
+    g_scratch_size[slot] = 0;
+  }
+  void *p = nullptr;
+  if ((*status = check_hip(hipMalloc(&p, want), "hipMalloc(scratch)"))) return nullptr;
+  if ((*status = check_hip(hipMemsetAsync(p, 0, want, g_dev.stream), "hipMemsetAsync(scratch)"))) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  g_scratch[slot] = p;
+  g_scratch_size[slot] = want;
+  return p;
+}
+
+uint32_t next_generation() {
+  // 30 usable bits (flags keep 2 state bits); 0 is never used so that
+  // zero-filled scratch never matches a live generation.
+  g_generation = (g_generation + 1) & 0x3fffffffu;
+  if (g_generation == 0) g_generation = 1;
+  return g_generation;
+}
+
+}  // namespace mmpi
+
+// ========================================================================
+// C ABI
+// ========================================================================
+extern "C" {
+
+const char *mmp_last_error(void) { return g_err.c_str(); }
+
+int mmp_init(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return init_locked(device);
+}
+
+int mmp_device_count(int *count) {
+  if (!count) return mmpi::fail(MMP_E_ARG, "null count");
+  int c = 0;
+  if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+  *count = c;
+  return MMP_OK;
+}
+
+int mmp_device_info(char *arch, int arch_len, int *cu_count, int64_t *total_mem,
+                    int *wave_size, int *max_threads) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (arch && arch_len > 0) {
+    std::snprintf(arch, (size_t)arch_len, "%s", g_dev.arch.c_str());
+  }
+  if (cu_count) *cu_count = g_dev.cus;
+  if (total_mem) *total_mem = g_dev.total_mem;
+  if (wave_size) *wave_size = g_dev.wave;
+  if (max_threads) *max_threads = g_dev.max_threads;
+  return MMP_OK;
+}
+
+int mmp_alloc(size_t bytes, void **ptr) {
+  if (!ptr) return mmpi::fail(MMP_E_ARG, "null ptr");
+  *ptr = nullptr;
+  if (int st = mmpi::ensure_init()) return st;
+  if (mmpi::inject(1)) return mmpi::fail(MMP_E_INJECTED, "mmp_alloc: injected failure");
+  const size_t want = round_size(bytes ? bytes : 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_free.lower_bound(want);
+  const size_t limit = want < (64u << 20) ? want : want + want / 4;
+  if (it != g_free.end() && it->first <= limit) {
+    void *p = it->second;
+    const size_t sz = it->first;
+    g_free.erase(it);
+    g_cached -= sz;
+    g_live[p] = sz;
+    g_in_use += sz;
+    *ptr = p;
+    return MMP_OK;
+  }
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess) {
+    // give the cache back to the driver and retry once
+    (void)hipGetLastError();
+    (void)hipStreamSynchronize(g_dev.stream);
+    release_cached_locked();
+    e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return mmpi::fail(MMP_E_OOM, "mmp_alloc(%zu bytes): %s", bytes, hipGetErrorString(e));
+    }
+  }
+  g_live[p] = want;
+  g_in_use += want;
+  *ptr = p;
+  return MMP_OK;
+}
+
+int mmp_free(void *ptr) {
+  if (!ptr) return MMP_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_live.find(ptr);
+  if (it == g_live.end()) return mmpi::fail(MMP_E_ARG, "mmp_free: unknown pointer %p", ptr);
+  const size_t sz = it->second;
+  g_live.erase(it);
+  g_in_use -= sz;
+  g_free.emplace(sz, ptr);
+  g_cached += sz;
+  return MMP_OK;
+}
+
+int mmp_empty_cache(void) {
+  if (!g_dev.ready) return MMP_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+    return st;
+  release_cached_locked();
+  return MMP_OK;
+}
+
+int mmp_memory_stats(size_t *in_use, size_t *cached) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (in_use) *in_use = g_in_use;
+  if (cached) *cached = g_cached;
+  return MMP_OK;
+}
+
+int mmp_h2d(void *dst, const void *src, size_t bytes) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (bytes == 0) return MMP_OK;
+  if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
+  if (int st = mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_dev.stream),
+                               "hipMemcpyAsync(H2D)"))
+    return st;
+  return mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize");
+}
+
+int mmp_d2h(void *dst, const void *src, size_t bytes) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (bytes == 0) return MMP_OK;
+  if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
+  if (int st = mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_dev.stream),
+                               "hipMemcpyAsync(D2H)"))
+    return st;
+  return mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize");
+}
+
+int mmp_d2d(void *dst, const void *src, size_t bytes) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (bytes == 0) return MMP_OK;
+  if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
+  return mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_dev.stream),
+                         "hipMemcpyAsync(D2D)");
+}
+
+int mmp_sync(void) {
+  if (!g_dev.ready) return MMP_OK;
+  return mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize");
+}
+
+int mmp_event_create(void **ev) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (!ev) return mmpi::fail(MMP_E_ARG, "null event");
+  hipEvent_t e;
+  if (int st = mmpi::check_hip(hipEventCreate(&e), "hipEventCreate")) return st;
+  *ev = (void *)e;
+  return MMP_OK;
+}
+
+int mmp_event_record(void *ev) {
+  if (int st = mmpi::ensure_init()) return st;
+  return mmpi::check_hip(hipEventRecord((hipEvent_t)ev, g_dev.stream), "hipEventRecord");
+}
+
+int mmp_event_elapsed_ms(void *start, void *end, float *ms) {
+  if (int st = mmpi::check_hip(hipEventSynchronize((hipEvent_t)end), "hipEventSynchronize"))
+    return st;
+  return mmpi::check_hip(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end),
+                         "hipEventElapsedTime");
+}
+
+int mmp_event_destroy(void *ev) {
+  return mmpi::check_hip(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+}
+
+// ---- runtime compilation -------------------------------------------------
+// Compile `src`; when `name_expr` is given (e.g. "&kernel" for a kernel
+// without extern "C"), also return its lowered (mangled) symbol name.
+static int rtc_compile_code(const char *src, const char *options, const char *arch,
+                            std::vector<char> *code, const char *name_expr = nullptr,
+                            std::string *lowered = nullptr) {
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, src, "mmp_rtc.hip", 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS)
+    return mmpi::fail(MMP_E_RTC, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
+  if (name_expr) hiprtcAddNameExpression(prog, name_expr);
+  // split options on whitespace
+  std::vector<std::string> opts;
+  std::string a = std::string("--offload-arch=") + arch;
+  opts.push_back(a);
+  if (options) {
+    std::string cur;
+    for (const char *p = options;; ++p) {
+      if (*p == 0 || *p == ' ' || *p == '\t' || *p == '\n') {
+        if (!cur.empty()) opts.push_back(cur);
+        cur.clear();
+        if (*p == 0) break;
+      } else {
+        cur.push_back(*p);
+      }
+    }
+  }
+  std::vector<const char *> argv;
+  for (auto &s : opts) argv.push_back(s.c_str());
+  r = hiprtcCompileProgram(prog, (int)argv.size(), argv.data());
+  if (r != HIPRTC_SUCCESS) {
+    size_t lsz = 0;
+    hiprtcGetProgramLogSize(prog, &lsz);
+    std::string log(lsz + 1, '\0');
+    if (lsz) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    if (log.size() > 900) log.resize(900);
+    return mmpi::fail(MMP_E_RTC, "hiprtc compile failed: %s", log.c_str());
+  }
+  size_t csz = 0;
+  hiprtcGetCodeSize(prog, &csz);
+  code->resize(csz);
+  hiprtcGetCode(prog, code->data());
+  if (name_expr && lowered) {
+    const char *ln = nullptr;
+    if (hiprtcGetLoweredName(prog, name_expr, &ln) == HIPRTC_SUCCESS && ln) *lowered = ln;
+  }
+  hiprtcDestroyProgram(&prog);
+  return MMP_OK;
+}
+
+int mmp_rtc_build(const char *src, const char *options, const char *arch, void *code,
+                  size_t code_cap, size_t *code_size) {
+  if (!src) return mmpi::fail(MMP_E_ARG, "null source");
+  std::vector<char> buf;
+  if (int st = rtc_compile_code(src, options, arch ? arch : "gfx950", &buf)) return st;
+  if (code_size) *code_size = buf.size();
+  if (code && code_cap >= buf.size()) std::memcpy(code, buf.data(), buf.size());
+  return MMP_OK;
+}
+
+int mmp_rtc_compile(const char *src, const char *name, const char *options, void **kernel) {
+  if (!src || !name || !kernel) return mmpi::fail(MMP_E_ARG, "null argument");
+  if (int st = mmpi::ensure_init()) return st;
+  if (mmpi::inject(2)) return mmpi::fail(MMP_E_INJECTED, "mmp_rtc_compile: injected failure");
+  std::string key = std::string(name) + '\x01' + (options ? options : "") + '\x01' + src;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_rtc.find(key);
+    if (it != g_rtc.end()) {
+      *kernel = (void *)it->second.fn;
+      return MMP_OK;
+    }
+  }
+  std::string arch = g_dev.arch;
+  const size_t colon = arch.find(':');
+  if (colon != std::string::npos) arch.resize(colon);
+  std::vector<char> code;
+  if (int st = rtc_compile_code(src, options, arch.c_str(), &code)) return st;
+  hipModule_t mod;
+  if (int st = mmpi::check_hip(hipModuleLoadData(&mod, code.data()), "hipModuleLoadData"))
+    return st;
+  hipFunction_t fn;
+  hipError_t e = hipModuleGetFunction(&fn, mod, name);
+  if (e != hipSuccess) {
+    // not extern "C": recompile asking hiprtc for the mangled name
+    (void)hipGetLastError();
+    (void)hipModuleUnload(mod);
+    std::string expr = std::string("&") + name, lowered;
+    if (int st = rtc_compile_code(src, options, arch.c_str(), &code, expr.c_str(), &lowered))
+      return st;
+    if (lowered.empty())
+      return mmpi::fail(MMP_E_RTC, "kernel '%s' not found in compiled source", name);
+    if (int st = mmpi::check_hip(hipModuleLoadData(&mod, code.data()), "hipModuleLoadData"))
+      return st;
+    e = hipModuleGetFunction(&fn, mod, lowered.c_str());
+    if (e != hipSuccess) {
+      (void)hipModuleUnload(mod);
+      return mmpi::fail(MMP_E_RTC, "kernel '%s' (%s) not found in compiled source (%s)", name,
+                        lowered.c_str(), hipGetErrorString(e));
+    }
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_rtc[key] = RtcEntry{mod, fn};
+  *kernel = (void *)fn;
+  return MMP_OK;
+}
+
+int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
+                   uint32_t shared_bytes, void **args) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (!kernel || !grid3 || !block3) return mmpi::fail(MMP_E_ARG, "null argument");
+  if (grid3[0] == 0 || grid3[1] == 0 || grid3[2] == 0) return MMP_OK;
+  if (mmpi::inject(3)) return mmpi::fail(MMP_E_INJECTED, "mmp_rtc_launch: injected failure");
+  hipError_t e = hipModuleLaunchKernel((hipFunction_t)kernel, grid3[0], grid3[1], grid3[2],
+                                       block3[0], block3[1], block3[2], shared_bytes,
+                                       g_dev.stream, args, nullptr);
+  return mmpi::check_hip(e, "hipModuleLaunchKernel");
+}
+
+int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3, const uint32_t *block3,
+                           uint32_t shared_bytes, void **args) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (!kernel || !threads3 || !block3) return mmpi::fail(MMP_E_ARG, "null argument");
+  if (threads3[0] == 0 || threads3[1] == 0 || threads3[2] == 0) return MMP_OK;
+  if (mmpi::inject(3)) return mmpi::fail(MMP_E_INJECTED, "mmp_rtc_launch_threads: injected failure");
+  hipError_t e = hipExtModuleLaunchKernel((hipFunction_t)kernel, threads3[0], threads3[1],
+                                          threads3[2], block3[0], block3[1], block3[2],
+                                          shared_bytes, g_dev.stream, args, nullptr);
+  return mmpi::check_hip(e, "hipExtModuleLaunchKernel");
+}
+
+int mmp_debug_fail_next(int kind, int count) {
+  if (kind < 0 || kind > 3 || count < 0) return mmpi::fail(MMP_E_ARG, "bad injection request");
+  g_fail_kind = count > 0 ? kind : 0;
+  g_fail_count = count;
+  return MMP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,310 @@
+"""Reductions and scans (reference: src/macmetalpy/reductions.py:74-163,
+314-418, 661-681 and ndarray._reduce / _reduce_axis / _prefix_scan,
+ndarray.py:1895-2152).
+
+Result dtypes and special cases follow NumPy (the reference's CPU path):
+integer sums and cumulative sums widen to 64 bits, ``mean`` of integers is
+float64 (resolved by the float64 policy), ``argmax`` returns int64 indices
+with the first-NaN rule, empty ``max``/``argmax`` raise.  Accuracy: float
+sums, means and scans accumulate in float64 on the device and round once.
+
+When the input is a lazy expression and the reduction is ``sum``/``mean``
+over the last axis or all axes, the reduction is fused into the expression
+kernel (one pass over HBM); the reference materialises the expression and,
+for axis reductions, loses it (ndarray.py:697-702).
+"""
+from __future__ import annotations
+
+import builtins
+import warnings
+
+import numpy as np
+
+from . import _abi
+from ._backend import HipBackend
+from ._config import get_config
+from ._dtypes import dtype_code, resolve_dtype
+from .ndarray import ndarray, _normalize_axis, _prod
+
+__all__ = ["sum", "mean", "prod", "max", "min", "amax", "amin", "argmax", "argmin",
+           "cumsum", "cumprod", "var", "std", "cumulative_sum", "cumulative_prod"]
+
+_OUT_DTYPE_CACHE: dict = {}
+
+
+def _np_out_dtype(kind: str, dt: np.dtype) -> np.dtype:
+    key = (kind, dt)
+    r = _OUT_DTYPE_CACHE.get(key)
+    if r is None:
+        z = np.zeros(1, dtype=dt)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            r = {"sum": np.sum, "prod": np.prod, "mean": np.mean, "cumsum": np.cumsum,
+                 "cumprod": np.cumprod, "var": np.var}[kind](z).dtype
+        r = resolve_dtype(r)
+        _OUT_DTYPE_CACHE[key] = r
+    return r
+
+
+def _asarray(a):
+    from . import creation
+    return creation.asarray(a)
+
+
+def _axes(axis, ndim):
+    if axis is None:
+        return None
+    if isinstance(axis, (tuple, list)):
+        ax = tuple(sorted({_normalize_axis(a, ndim) for a in axis}))
+    else:
+        ax = (_normalize_axis(axis, ndim),)
+    return ax
+
+
+def _out_shape(shape, axes, keepdims):
+    if axes is None:
+        return tuple(1 for _ in shape) if keepdims else ()
+    if keepdims:
+        return tuple(1 if i in axes else s for i, s in enumerate(shape))
+    return tuple(s for i, s in enumerate(shape) if i not in axes)
+
+
+def _finish(res, out):
+    if out is None:
+        return res
+    return out._inplace(res)
+
+
+def _fused_ok(a, axes, kind, dtype):
+    if a._fusion_node is None or dtype is not None or not get_config().fusion:
+        return False
+    if kind not in ("sum", "mean"):
+        return False
+    if a._dtype.kind not in "fiub":
+        return False
+    return axes is None or axes == (a.ndim - 1,)
+
+
+def _layout(shape, axes):
+    """(outer, len, inner) of a contiguous array for reducing ``axes``,
+    or None when the reduced axes are not one contiguous run."""
+    if axes is None:
+        return 1, _prod(shape), 1
+    if list(axes) != list(range(axes[0], axes[-1] + 1)):
+        return None
+    return _prod(shape[:axes[0]]), _prod(shape[axes[0]:axes[-1] + 1]), _prod(shape[axes[-1] + 1:])
+
+
+_CODES = {"sum": _abi.REDUCE_SUM, "prod": _abi.REDUCE_PROD, "max": _abi.REDUCE_MAX,
+          "min": _abi.REDUCE_MIN, "mean": _abi.REDUCE_MEAN}
+
+
+def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
+    a = _asarray(a)
+    axes = _axes(axis, a.ndim)
+    if dtype is not None:
+        a = a.astype(dtype)
+    if kind in ("max", "min"):
+        odt = a._dtype
+    else:
+        odt = _np_out_dtype(kind, a._dtype)
+    oshape = _out_shape(a._shape, axes, keepdims)
+    red_len = _prod(a._shape) if axes is None else _prod(a._shape[i] for i in axes)
+
+    if red_len == 0 or a.size == 0:
+        return _finish(_empty_reduction(kind, oshape, odt, red_len), out)
+
+    if _fused_ok(a, axes, kind, dtype):
+        from ._fusion import CastNode, run_sum
+        node = a._fusion_node
+        if kind == "mean" and node._dtype.kind != "f":
+            node = CastNode(node, np.dtype(np.float64))
+        res = ndarray._empty_device(oshape, odt)
+        run_sum(node, axes is not None, odt, res._ptr, kind == "mean")
+        return _finish(res, out)
+
+    x = a._ensure_contiguous()
+    lay = _layout(x._shape, axes)
+    if lay is None:
+        # bring the reduced axes to the end (one strided copy), then reduce
+        keep = [i for i in range(x.ndim) if i not in axes]
+        xt = x.transpose(keep + list(axes))._contiguous_copy()
+        lay = (_prod(xt._shape[:len(keep)]), _prod(xt._shape[len(keep):]), 1)
+        x = xt
+    outer, length, inner = lay
+    res = ndarray._empty_device(oshape, odt)
+    HipBackend().reduce(_CODES[kind], dtype_code(x._dtype), dtype_code(odt), outer, length,
+                        inner, x._ptr, res._ptr)
+    return _finish(res, out)
+
+
+def _empty_reduction(kind, oshape, odt, red_len):
+    from . import creation
+    if red_len == 0:
+        if kind == "sum":
+            return creation.zeros(oshape, dtype=odt)
+        if kind == "prod":
+            return creation.ones(oshape, dtype=odt)
+        if kind == "mean":
+            warnings.warn("Mean of empty slice.", RuntimeWarning, stacklevel=3)
+            return creation.full(oshape, np.nan, dtype=odt)
+        raise ValueError(f"zero-size array to reduction operation {kind}imum which has no identity"
+                         if kind in ("max", "min") else
+                         f"zero-size array to reduction operation {kind}")
+    return creation.empty(oshape, dtype=odt)
+
+
+def sum(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
+        where=np._NoValue):
+    """Sum of elements (reference reductions.py:74-113)."""
+    if where is not np._NoValue:
+        raise NotImplementedError("sum(where=...) is not supported on the device")
+    r = _reduce(a, "sum", axis, dtype, None, keepdims)
+    if initial is not np._NoValue:
+        r = r + initial
+    return _finish(r, out)
+
+
+def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
+    """Arithmetic mean (reference reductions.py:116-163): the float64 sum
+    divided by the count in float64, rounded once to the result dtype."""
+    if where is not np._NoValue:
+        raise NotImplementedError("mean(where=...) is not supported on the device")
+    return _reduce(a, "mean", axis, dtype, out, keepdims)
+
+
+def prod(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
+         where=np._NoValue):
+    r = _reduce(a, "prod", axis, dtype, None, keepdims)
+    if initial is not np._NoValue:
+        r = r * initial
+    return _finish(r, out)
+
+
+def max(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._NoValue):
+    """Maximum; NaN propagates (NumPy)."""
+    r = _reduce(a, "max", axis, None, None, keepdims)
+    if initial is not np._NoValue:
+        from .ufunc_ops import maximum
+        r = maximum(r, initial)
+    return _finish(r, out)
+
+
+def min(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._NoValue):
+    """Minimum; NaN propagates (NumPy)."""
+    r = _reduce(a, "min", axis, None, None, keepdims)
+    if initial is not np._NoValue:
+        from .ufunc_ops import minimum
+        r = minimum(r, initial)
+    return _finish(r, out)
+
+
+amax = max
+amin = min
+
+
+def _argreduce(a, op, axis, out, keepdims):
+    a = _asarray(a)
+    name = "argmax" if op == _abi.REDUCE_ARGMAX else "argmin"
+    if a.size == 0:
+        raise ValueError(f"attempt to get {name} of an empty sequence")
+    x = a._ensure_contiguous()
+    be = HipBackend()
+    if axis is None:
+        res = ndarray._empty_device((), np.int64)
+        be.argreduce(op, dtype_code(x._dtype), 1, x.size, 1, x._ptr, res._ptr)
+        if keepdims:
+            res = res.reshape((1,) * a.ndim)
+            return _finish(res, out)
+        if out is not None:
+            return _finish(res, out)
+        return int(res.get())  # reference returns a Python int (reductions.py:407)
+    ax = _normalize_axis(axis, a.ndim)
+    outer, length, inner = _prod(x._shape[:ax]), x._shape[ax], _prod(x._shape[ax + 1:])
+    if length == 0:
+        raise ValueError(f"attempt to get {name} of an empty sequence")
+    oshape = _out_shape(x._shape, (ax,), keepdims)
+    res = ndarray._empty_device(oshape, np.int64)
+    be.argreduce(op, dtype_code(x._dtype), outer, length, inner, x._ptr, res._ptr)
+    return _finish(res, out)
+
+
+def argmax(a, axis=None, out=None, keepdims=False):
+    """Index of the first maximum (first NaN if any), int64 (reference
+    reductions.py:381-418 returns int32 and ignores NaN)."""
+    return _argreduce(a, _abi.REDUCE_ARGMAX, axis, out, keepdims)
+
+
+def argmin(a, axis=None, out=None, keepdims=False):
+    return _argreduce(a, _abi.REDUCE_ARGMIN, axis, out, keepdims)
+
+
+def _scan(a, op, kind, axis, dtype, out):
+    a = _asarray(a)
+    if dtype is not None:
+        a = a.astype(dtype)
+    odt = _np_out_dtype(kind, a._dtype)
+    x = a._ensure_contiguous()
+    if axis is None:
+        x = x.reshape(-1)
+        outer, length, inner = 1, x.size, 1
+        oshape = (x.size,)
+    else:
+        ax = _normalize_axis(axis, x.ndim)
+        outer, length, inner = _prod(x._shape[:ax]), x._shape[ax], _prod(x._shape[ax + 1:])
+        oshape = x._shape
+    res = ndarray._empty_device(oshape, odt)
+    if res.size:
+        HipBackend().scan(op, dtype_code(x._dtype), dtype_code(odt), outer, length, inner,
+                          x._ptr, res._ptr)
+    return _finish(res, out)
+
+
+def cumsum(a, axis=None, dtype=None, out=None):
+    """Inclusive prefix sum (reference reductions.py:661-681); int32 input
+    gives int64 output as in NumPy (the reference's GPU path keeps int32)."""
+    return _scan(a, _abi.SCAN_CUMSUM, "cumsum", axis, dtype, out)
+
+
+def cumprod(a, axis=None, dtype=None, out=None):
+    return _scan(a, _abi.SCAN_CUMPROD, "cumprod", axis, dtype, out)
+
+
+def cumulative_sum(x, /, *, axis=None, dtype=None, out=None, include_initial=False):
+    r = cumsum(x, axis=axis if axis is not None else (0 if _asarray(x).ndim == 1 else None),
+               dtype=dtype, out=out)
+    if include_initial:
+        raise NotImplementedError("include_initial=True is not supported")
+    return r
+
+
+def cumulative_prod(x, /, *, axis=None, dtype=None, out=None, include_initial=False):
+    if include_initial:
+        raise NotImplementedError("include_initial=True is not supported")
+    return cumprod(x, axis=axis if axis is not None else (0 if _asarray(x).ndim == 1 else None),
+                   dtype=dtype, out=out)
+
+
+def var(a, axis=None, dtype=None, out=None, ddof=0, keepdims=False):
+    """Variance as mean(|x - mean(x)|**2) * n / (n - ddof); with fusion on,
+    the deviation, square and mean run as one kernel per pass."""
+    from .ufunc_ops import square
+    a = _asarray(a)
+    if dtype is not None:
+        a = a.astype(dtype)
+    elif a._dtype.kind in "iub":
+        a = a.astype(resolve_dtype(np.float64))
+    axes = _axes(axis, a.ndim)
+    n = a.size if axes is None else _prod(a._shape[i] for i in axes)
+    m = mean(a, axis=axis, keepdims=True)
+    if axes is None:
+        m = m.reshape(())
+    v = mean(square(a - m), axis=axis, keepdims=keepdims)
+    if ddof:
+        v = v * (n / builtins.max(n - ddof, 0)) if n - ddof > 0 else v * np.inf
+    return _finish(v, out)
+
+
+def std(a, axis=None, dtype=None, out=None, ddof=0, keepdims=False):
+    from .ufunc_ops import sqrt
+    return _finish(sqrt(var(a, axis=axis, dtype=dtype, ddof=ddof, keepdims=keepdims)), out)

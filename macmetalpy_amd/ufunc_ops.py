@@ -1,0 +1,132 @@
+"""Elementwise ufunc front-ends.
+
+Reference: src/macmetalpy/math_ops.py:15-67, 335-548 and
+src/macmetalpy/ufunc_ops.py:38-348.  Each function converts its operands
+and calls the shared dispatcher (``_elementwise.unary`` / ``binary``), as the
+reference's wrappers call ``ndarray._unary_op`` / ``_binary_op``.  ``mod`` /
+``remainder`` is a single device op with NumPy's sign rule, where the
+reference composes ``x1 - floor_divide(x1, x2) * x2`` (math_ops.py:540-548).
+"""
+from __future__ import annotations
+
+from . import _elementwise as ew
+
+__all__: list[str] = []
+
+
+def _unary(name, op_name, doc):
+    def f(x, /, out=None, **kwargs):
+        r = ew.unary(op_name, x)
+        return _to_out(r, out)
+    f.__name__ = f.__qualname__ = name
+    f.__doc__ = doc
+    globals()[name] = f
+    __all__.append(name)
+    return f
+
+
+def _binary(name, op_name, doc):
+    def f(x1, x2, /, out=None, **kwargs):
+        r = ew.binary(op_name, x1, x2)
+        return _to_out(r, out)
+    f.__name__ = f.__qualname__ = name
+    f.__doc__ = doc
+    globals()[name] = f
+    __all__.append(name)
+    return f
+
+
+def _to_out(r, out):
+    if out is None:
+        return r
+    if isinstance(out, tuple):
+        out = out[0]
+    return out._inplace(r)
+
+
+for _name, _op, _doc in [
+    ("negative", "negative_op", "Element-wise negation."),
+    ("positive", "positive_op", "Element-wise +x."),
+    ("absolute", "abs_op", "Element-wise absolute value."),
+    ("abs", "abs_op", "Element-wise absolute value."),
+    ("fabs", "abs_op", "Element-wise absolute value (floats)."),
+    ("sign", "sign_op", "Element-wise sign."),
+    ("square", "square_op", "Element-wise square."),
+    ("reciprocal", "reciprocal_op", "Element-wise 1/x."),
+    ("sqrt", "sqrt_op", "Element-wise square root."),
+    ("cbrt", "cbrt_op", "Element-wise cube root."),
+    ("exp", "exp_op", "Element-wise exponential."),
+    ("exp2", "exp2_op", "Element-wise 2**x."),
+    ("expm1", "expm1_op", "Element-wise exp(x) - 1, accurate near 0."),
+    ("log", "log_op", "Element-wise natural logarithm."),
+    ("log2", "log2_op", "Element-wise base-2 logarithm."),
+    ("log10", "log10_op", "Element-wise base-10 logarithm."),
+    ("log1p", "log1p_op", "Element-wise log(1 + x), accurate near 0."),
+    ("sin", "sin_op", "Element-wise sine."),
+    ("cos", "cos_op", "Element-wise cosine."),
+    ("tan", "tan_op", "Element-wise tangent."),
+    ("arcsin", "asin_op", "Element-wise inverse sine."),
+    ("arccos", "acos_op", "Element-wise inverse cosine."),
+    ("arctan", "atan_op", "Element-wise inverse tangent."),
+    ("sinh", "sinh_op", "Element-wise hyperbolic sine."),
+    ("cosh", "cosh_op", "Element-wise hyperbolic cosine."),
+    ("tanh", "tanh_op", "Element-wise hyperbolic tangent."),
+    ("arcsinh", "asinh_op", "Element-wise inverse hyperbolic sine."),
+    ("arccosh", "acosh_op", "Element-wise inverse hyperbolic cosine."),
+    ("arctanh", "atanh_op", "Element-wise inverse hyperbolic tangent."),
+    ("floor", "floor_op", "Element-wise floor."),
+    ("ceil", "ceil_op", "Element-wise ceiling."),
+    ("rint", "rint_op", "Round to nearest integer (ties to even)."),
+    ("trunc", "trunc_op", "Element-wise truncation."),
+    ("degrees", "degrees_op", "Radians to degrees."),
+    ("radians", "radians_op", "Degrees to radians."),
+    ("rad2deg", "degrees_op", "Radians to degrees."),
+    ("deg2rad", "radians_op", "Degrees to radians."),
+]:
+    _unary(_name, _op, _doc)
+
+for _name, _op, _doc in [
+    ("add", "add_op", "Element-wise addition."),
+    ("subtract", "sub_op", "Element-wise subtraction."),
+    ("multiply", "mul_op", "Element-wise multiplication."),
+    ("divide", "div_op", "Element-wise true division."),
+    ("true_divide", "div_op", "Element-wise true division."),
+    ("floor_divide", "floor_divide_op", "Element-wise floor division (NumPy semantics)."),
+    ("mod", "mod_op", "Element-wise remainder with the sign of the divisor."),
+    ("remainder", "mod_op", "Element-wise remainder with the sign of the divisor."),
+    ("power", "pow_op", "Element-wise power."),
+    ("maximum", "max_op", "Element-wise maximum (NaN-propagating)."),
+    ("minimum", "min_op", "Element-wise minimum (NaN-propagating)."),
+    ("fmax", "fmax_op", "Element-wise maximum ignoring NaN."),
+    ("fmin", "fmin_op", "Element-wise minimum ignoring NaN."),
+    ("arctan2", "atan2_op", "Element-wise arctan(x1/x2) with quadrant."),
+    ("hypot", "hypot_op", "Element-wise sqrt(x1**2 + x2**2)."),
+    ("fmod", "fmod_op", "Element-wise C fmod (sign of the dividend)."),
+    ("copysign", "copysign_op", "Magnitude of x1 with the sign of x2."),
+    ("nextafter", "nextafter_op", "Next representable value after x1 towards x2."),
+    ("logaddexp", "logaddexp_op", "log(exp(x1) + exp(x2))."),
+    ("logaddexp2", "logaddexp2_op", "log2(2**x1 + 2**x2)."),
+    ("heaviside", "heaviside_op", "Heaviside step function."),
+    ("less", "lt_op", "Element-wise x1 < x2."),
+    ("less_equal", "le_op", "Element-wise x1 <= x2."),
+    ("greater", "gt_op", "Element-wise x1 > x2."),
+    ("greater_equal", "ge_op", "Element-wise x1 >= x2."),
+    ("equal", "eq_op", "Element-wise x1 == x2."),
+    ("not_equal", "ne_op", "Element-wise x1 != x2."),
+]:
+    _binary(_name, _op, _doc)
+
+
+def float_power(x1, x2, /, out=None, **kwargs):
+    """x1 ** x2 computed in float64 (NumPy float_power)."""
+    from . import creation
+    import numpy as np
+    a = creation.asarray(x1).astype(np.float64)
+    return _to_out(ew.binary("pow_op", a, x2), out)
+
+
+def divmod(x1, x2, /):
+    return ew.binary("floor_divide_op", x1, x2), ew.binary("mod_op", x1, x2)
+
+
+__all__ += ["float_power", "divmod"]

@@ -1,0 +1,184 @@
+"""Pin the oracle (CPU): every function is checked against mathematics or
+known answers that a plausible mistake (truncating division, wrong
+remainder sign, int32 cumsum, last-index argmax, fmod for mod, a dropped
+term in a fused expression) would violate."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle as C
+from oracle import reference_cpu as ref
+
+I32_MIN = -2 ** 31
+
+
+# ----------------------------------------------------- integer division
+def test_floor_divide_mod_brute_force_identity():
+    """All a in [-1024, 1024], b in +-[1, 1000]: a == q*b + r with r in
+    [0, b) for b > 0 and (b, 0] for b < 0, q == floor(a / b)."""
+    a = np.arange(-1024, 1025, dtype=np.int32)
+    b = np.concatenate([np.arange(1, 1001), -np.arange(1, 1001)]).astype(np.int32)
+    A, B = np.meshgrid(a, b, indexing="ij")
+    q = ref.floor_divide(A, B)
+    r = ref.mod(A, B)
+    assert q.dtype == np.int32 and r.dtype == np.int32
+    assert np.array_equal(q.astype(np.int64) * B + r, A)
+    pos = B > 0
+    assert np.all((r[pos] >= 0) & (r[pos] < B[pos]))
+    assert np.all((r[~pos] <= 0) & (r[~pos] > B[~pos]))
+    exact = np.array([[math.floor(x / y) for y in (7, -7, 1000, -1)] for x in range(-50, 51)])
+    got = ref.floor_divide(np.arange(-50, 51, dtype=np.int32)[:, None],
+                           np.array([7, -7, 1000, -1], dtype=np.int32)[None, :])
+    assert np.array_equal(got, exact)
+
+
+def test_integer_edge_cases_hand_derived():
+    a = np.array([7, -7, 7, -7, 0, I32_MIN, I32_MIN, 5, -5, 2 ** 31 - 1], np.int32)
+    b = np.array([2, 2, -2, -2, 3, -1, 1, 0, 0, -1], np.int32)
+    # floor(7/2)=3, floor(-7/2)=-4, floor(7/-2)=-4, floor(-7/-2)=3, 0,
+    # INT_MIN//-1 wraps to INT_MIN, x//0 -> 0 (NumPy), INT_MAX//-1 = -INT_MAX
+    assert ref.floor_divide(a, b).tolist() == [3, -4, -4, 3, 0, I32_MIN, I32_MIN, 0, 0, -(2 ** 31 - 1)]
+    assert ref.mod(a, b).tolist() == [1, 1, -1, -1, 0, 0, 0, 0, 0, 0]
+
+
+def test_c_restatement_agrees_with_numpy_restatement():
+    g = np.random.default_rng(11)
+    a = g.integers(-2 ** 31, 2 ** 31, 1 << 20, dtype=np.int64).astype(np.int32)
+    b = g.integers(-2000, 2000, 1 << 20, dtype=np.int32)
+    b[::97] = 0
+    b[::89] = -1
+    a[::83] = I32_MIN
+    assert np.array_equal(C.floor_divide_i32(a, b), ref.floor_divide(a, b))
+    assert np.array_equal(C.mod_i32(a, b), ref.mod(a, b))
+
+
+def test_reference_test_literals_float():
+    """Literal inputs of tests/test_math_ops.py:446-453 / test_math_ext.py:302-307
+    (mod) and test_untested_math.py:227-232 (floor_divide); answers by hand."""
+    a = np.array([-7.0, 8.0, -9.0], np.float32)
+    b = np.array([3.0, -3.0, -4.0], np.float32)
+    assert ref.mod(a, b).tolist() == [2.0, -1.0, -1.0]
+    fa = np.array([-7.0, -10.0, 7.0], np.float32)
+    fb = np.array([2.0, 3.0, -2.0], np.float32)
+    assert ref.floor_divide(fa, fb).tolist() == [-4.0, -4.0, -4.0]
+    # test_ndarray_gaps.py:667-678: 10.0 % [2,3,4] and [10,20,30] % 7.0
+    assert (np.float32(10.0) % np.array([2.0, 3.0, 4.0], np.float32)).tolist() == [0.0, 1.0, 2.0]
+    assert ref.mod(np.array([10.0, 20.0, 30.0], np.float32), np.float32(7.0)).tolist() == [3.0, 6.0, 2.0]
+
+
+def test_float_divmod_identity_and_sign():
+    g = np.random.default_rng(5)
+    a = (g.standard_normal(200000) * 1000).astype(np.float32)
+    b = (g.standard_normal(200000) * 10).astype(np.float32)
+    q = ref.floor_divide(a, b)
+    r = ref.mod(a, b)
+    assert np.all(q == np.floor(q))
+    nz = r != 0
+    assert np.all(np.sign(r[nz]) == np.sign(b[nz]))
+    assert np.all(np.abs(r) <= np.abs(b))
+    resid = np.abs(q.astype(np.float64) * b + r - a)
+    assert np.all(resid <= 4 * np.spacing(np.abs(a).astype(np.float32)) + np.abs(b) * 1e-6)
+    # mod is not C fmod: opposite signs differ
+    assert ref.mod(np.float32(-7), np.float32(3)) == 2 and np.fmod(np.float32(-7), np.float32(3)) == -1
+
+
+# ------------------------------------------------------ transcendentals
+@pytest.mark.parametrize("op,fn64,lo,hi", [
+    ("sin_op", np.sin, -10, 10), ("exp_op", np.exp, -80, 80), ("tanh_op", np.tanh, -10, 10),
+    ("log1p_op", np.log1p, -0.99, 100), ("sqrt_op", np.sqrt, 0, 1e6), ("cos_op", np.cos, -10, 10),
+    ("log_op", np.log, 1e-30, 1e30), ("expm1_op", np.expm1, -5, 5),
+])
+def test_float32_transcendentals_within_ulp_of_float64(op, fn64, lo, hi):
+    """The oracle computes the named function: float32 results within 2 ULP
+    of the float64 evaluation rounded once."""
+    x = np.random.default_rng(1).uniform(lo, hi, 100000).astype(np.float32)
+    got = ref.unary(op, x)
+    want = ref.correctly_rounded(fn64, x)
+    assert got.dtype == np.float32
+    assert int(ref.ulp_distance(got, want).max()) <= 2
+
+
+def test_ulp_distance_helper():
+    one = np.float32(1.0)
+    nxt = np.nextafter(one, np.float32(2))
+    assert ref.ulp_distance(np.array([one]), np.array([nxt]))[0] == 1
+    assert ref.ulp_distance(np.array([np.float32(-0.0)]), np.array([np.float32(0.0)]))[0] == 0
+    assert ref.ulp_distance(np.array([np.float32(np.nan)]), np.array([np.float32(np.nan)]))[0] == 0
+    assert ref.ulp_distance(np.array([-nxt]), np.array([nxt]))[0] == 2 * 0x3F800001
+
+
+# ------------------------------------------------------------ reductions
+def test_sum_closed_forms():
+    # tests/test_edge_shapes.py:367-378: sum of 1M ones is 1e6
+    assert ref.sum(np.ones(1_000_000, np.float32)) == 1e6
+    n = 100000
+    assert ref.sum_f64(np.arange(n, dtype=np.float32)) == n * (n - 1) / 2
+    assert ref.sum(np.ones(7, np.int32)).dtype == np.int64
+    assert ref.mean(np.arange(10, dtype=np.int32)) == 4.5
+    x = np.random.default_rng(2).standard_normal(1 << 16).astype(np.float32)
+    assert math.isclose(C.sum_f32(x), float(ref.sum_f64(x)), rel_tol=1e-12)
+
+
+def test_argmax_first_occurrence_and_nan():
+    x = np.array([1, 5, 3, 5, 2], np.float32)
+    assert ref.argmax(x) == 1  # first of the tied maxima
+    y = np.array([1, np.nan, 9, np.nan], np.float32)
+    assert ref.argmax(y) == 1  # first NaN wins
+    g = np.random.default_rng(3)
+    for _ in range(20):
+        v = g.integers(0, 5, 37).astype(np.float32)
+        assert ref.argmax(v) == min(i for i in range(37) if v[i] == v.max())
+        assert C.argmax_f32(v) == ref.argmax(v)
+    m = g.standard_normal((9, 13)).astype(np.float32)
+    assert np.array_equal(ref.argmax(m, axis=1), [int(np.argmax(r)) for r in m])
+
+
+def test_cumsum_int64_and_invariants():
+    x = np.random.default_rng(4).integers(-100, 100, 100001, endpoint=True, dtype=np.int32)
+    c = ref.cumsum(x)
+    assert c.dtype == np.int64
+    assert np.array_equal(np.diff(c), x[1:].astype(np.int64)) and c[0] == x[0]
+    assert c[-1] == x.astype(np.int64).sum()
+    assert np.array_equal(c, C.cumsum_i32(x))
+    assert np.array_equal(ref.cumsum(np.ones(1000, np.int32)), np.arange(1, 1001))
+    f = np.random.default_rng(4).random(1 << 16, dtype=np.float32)
+    c64 = ref.cumsum_f64(f)
+    assert c64.dtype == np.float64 and math.isclose(c64[-1], float(ref.sum_f64(f)), rel_tol=1e-12)
+
+
+# ---------------------------------------------------------------- matmul
+def test_matmul_known_answers():
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    assert ref.matmul(a, b).tolist() == [[19, 22], [43, 50]]
+    e = np.eye(5, dtype=np.float32)
+    m = np.random.default_rng(0).standard_normal((5, 5)).astype(np.float32)
+    assert np.array_equal(ref.matmul(m, e), m)
+    # tests/test_error_handling.py:107-114: 1-D @ 1-D is the inner product
+    assert ref.matmul(np.arange(3, dtype=np.float32), np.arange(3, dtype=np.float32)) == 5.0
+    t = np.random.default_rng(1).standard_normal((4, 3, 6))
+    u = np.random.default_rng(2).standard_normal((4, 6, 2))
+    loop = np.array([[[sum(t[k, i, p] * u[k, p, j] for p in range(6)) for j in range(2)]
+                      for i in range(3)] for k in range(4)])
+    assert np.allclose(ref.matmul_f64(t, u), loop, rtol=1e-12)
+    assert ref.normwise_rel_error(ref.matmul(a, b), [[19, 22], [43, 50]]) == 0.0
+
+
+# ------------------------------------------------------------- fusion
+def test_fused_elementwise_scalar_values():
+    x = np.array([0.0, 1.0, -4.0], np.float32)
+    y = ref.fused_elementwise(x)
+    expect = [1.0, 1.0 + math.exp(-1.0), 2.0 + math.exp(-16.0)]
+    assert np.allclose(y, expect, rtol=2e-7)
+
+
+def test_fusion_chain_against_python_loop():
+    g = np.random.default_rng(7)
+    x = g.standard_normal((3, 17)).astype(np.float32)
+    r = g.uniform(0.5, 2.0, (1, 17)).astype(np.float32)
+    z = ref.fusion_chain_f64(x, r)
+    loop = [sum(math.tanh(float(x[i, j]) * float(r[0, j]) + 1.0) * math.exp(-abs(float(x[i, j])))
+                - math.log1p(float(x[i, j]) ** 2) for j in range(17)) for i in range(3)]
+    assert np.allclose(z, loop, rtol=1e-5)
+    assert z.shape == (3,)

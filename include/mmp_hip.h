@@ -282,16 +282,11 @@ int mmp_rtc_build(const char *src, const char *options, const char *arch,
                   void *code, size_t code_cap, size_t *code_size);
 
 /* Launch with a grid given in BLOCKS (HIP convention). args: kernel
- * parameter pointers, one per kernel argument. */
+ * parameter pointers, one per kernel argument.  The reference's RawKernel
+ * gives a grid in threads (Metal dispatchThreads, raw_kernel.py:46-59); the
+ * Python RawKernel turns that into uniform workgroups that divide it. */
 int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
                    uint32_t shared_bytes, void **args);
-
-/* Launch with a grid given in THREADS (Metal dispatchThreads convention of
- * the reference's RawKernel, raw_kernel.py:46-59): exactly threads3[d]
- * work-items run; the last workgroup may be partial. */
-int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3,
-                           const uint32_t *block3, uint32_t shared_bytes,
-                           void **args);
 
 /* ---- test hooks -------------------------------------------------------- */
 /* Make the next `count`-th call of kind (1 = mmp_alloc, 2 = mmp_rtc_compile,

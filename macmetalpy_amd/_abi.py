@@ -136,5 +136,5 @@ EXPORTS = (
     "mmp_copy_strided", "mmp_fill",
     "mmp_reduce", "mmp_argreduce", "mmp_scan", "mmp_matmul",
     "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch",
-    "mmp_rtc_launch_threads", "mmp_debug_fail_next",
+    "mmp_debug_fail_next",
 )

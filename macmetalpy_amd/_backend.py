@@ -97,7 +97,6 @@ _SIGNATURES = {
     "mmp_rtc_build": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_vp, _c_sz,
                       ctypes.POINTER(_c_sz)],
     "mmp_rtc_launch": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
-    "mmp_rtc_launch_threads": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
     "mmp_debug_fail_next": [_c_int, _c_int],
 }
 
@@ -321,16 +320,15 @@ class HipBackend:
         return k.value
 
     def launch(self, kernel: int, grid: Sequence[int], block: Sequence[int],
-               args: Sequence, shared: int = 0, *, threads: bool = False) -> None:
-        """Launch a compiled kernel.  ``args`` are ctypes scalars/structs in
-        kernel-parameter order.  ``threads=True`` interprets ``grid`` as the
-        total number of work-items per dimension (exact, may be ragged)."""
+               args: Sequence, shared: int = 0) -> None:
+        """Launch a compiled kernel on the library stream; ``grid`` counts
+        workgroups, ``args`` are ctypes scalars/structs in kernel-parameter
+        order."""
         g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
         b = (ctypes.c_uint32 * 3)(*(list(block) + [1] * (3 - len(block))))
         ptrs = (_c_vp * max(1, len(args)))(
             *[ctypes.cast(ctypes.byref(a), _c_vp) for a in args])
-        fn = self._lib.mmp_rtc_launch_threads if threads else self._lib.mmp_rtc_launch
-        _check(fn(kernel, g, b, shared, ptrs), "mmp_rtc_launch")
+        _check(self._lib.mmp_rtc_launch(kernel, g, b, shared, ptrs), "mmp_rtc_launch")
 
 
 def rtc_build(source: str, options: str = "", arch: str = "gfx950") -> bytes:

@@ -51,12 +51,22 @@ def _asarray(x):
 # ----------------------------------------------------- lazy dependents
 def track_lazy(arr) -> None:
     """Register lazy ``arr`` with every device buffer its DAG reads, so an
-    in-place write to one of those buffers first evaluates ``arr``."""
+    in-place write to one of those buffers first evaluates ``arr``.  Entries
+    are weak and removed when ``arr`` dies or is evaluated (``untrack``)."""
+    key = id(arr)
     for buf in arr._fusion_node._buffers:
         deps = buf.lazy_dependents
         if deps is None:
-            deps = buf.lazy_dependents = weakref.WeakSet()
-        deps.add(arr)
+            deps = buf.lazy_dependents = {}
+        deps[key] = weakref.ref(arr, lambda _r, d=deps, k=key: d.pop(k, None))
+
+
+def untrack_lazy(arr, node) -> None:
+    key = id(arr)
+    for buf in node._buffers:
+        deps = buf.lazy_dependents
+        if deps:
+            deps.pop(key, None)
 
 
 def flush_lazy(buffer) -> None:
@@ -67,8 +77,9 @@ def flush_lazy(buffer) -> None:
     deps = buffer.lazy_dependents
     if not deps:
         return
-    for arr in list(deps):
-        if arr._fusion_node is not None:
+    for ref in list(deps.values()):
+        arr = ref()
+        if arr is not None and arr._fusion_node is not None:
             materialize(arr)
     deps.clear()
 

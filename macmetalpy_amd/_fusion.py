@@ -634,6 +634,8 @@ def materialize(arr) -> None:
     be = HipBackend()
     buf = be.create_buffer(arr.size, arr._dtype)
     materialize_node(node, buf.ptr)
+    from ._elementwise import untrack_lazy
+    untrack_lazy(arr, node)
     arr._buffer = buf
     arr._fusion_node = None
     arr._np_data = None

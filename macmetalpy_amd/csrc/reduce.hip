@@ -1,0 +1,633 @@
+// reduce.hip -- sum / mean / prod / max / min and argmax / argmin.
+//
+// Replaces the reference's multi-pass Metal reductions: reduce_sum & co.
+// (_kernels.py:422-565; one pass per factor of 8192, re-launched from
+// Python, ndarray.py:1927-1946), the one-thread-per-row axis kernels
+// (_kernels.py:1062-1146) and the two-pass argmax whose second pass is a
+// single thread (_kernels.py:1189-1243).
+//
+// The input is viewed as C-contiguous (outer, len, inner) and the middle
+// axis is reduced.
+//  * inner == 1 (contiguous rows, includes axis=None as one row): each row
+//    is split over S workgroups so that the launch has >= ~2048 of them;
+//    a workgroup streams its slice with 128-bit loads, reduces in
+//    registers, across the wave64 with butterfly shuffles and across the 4
+//    waves through LDS.  With S > 1 the partials go to scratch and the last
+//    workgroup of the row to arrive (atomic ticket) combines them in index
+//    order -- one launch, deterministic result.
+//  * inner > 1 (strided axis): one thread per output column, coalesced
+//    across the column index, the reduced axis optionally split over S
+//    workgroups with the same ticket scheme.
+// Floating sums/means/products accumulate in float64 and round once
+// (accuracy bar: 1e-5 relative to a float64-accumulated reference); integer
+// sums widen to 64 bits as NumPy does.  HBM-bound: algorithmic bytes =
+// sizeof(T) per input element (+ outputs).
+#include "mmp_ops.h"
+#include "mmp_internal.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+constexpr long long kMinPerBlock = 16384;  // elements per workgroup slice
+constexpr long long kTargetBlocks = 2048;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <typename T> union Pack {
+  u32x4 v;
+  T e[16 / sizeof(T)];
+};
+
+// --------------------------------------------------------------- ops
+template <typename T> struct AccOf {  // accumulator for sum / prod / mean
+  typedef typename mmp_t<T>::C C;
+  typedef double type;
+};
+template <> struct AccOf<mmp_i16> { typedef mmp_i64 type; };
+template <> struct AccOf<mmp_i32> { typedef mmp_i64 type; };
+template <> struct AccOf<mmp_i64> { typedef mmp_i64 type; };
+template <> struct AccOf<bool> { typedef mmp_i64 type; };
+template <> struct AccOf<mmp_u16> { typedef mmp_u64 type; };
+template <> struct AccOf<mmp_u32> { typedef mmp_u64 type; };
+template <> struct AccOf<mmp_u64> { typedef mmp_u64 type; };
+
+// Reduction policies: identity, element map, combine, finalize.
+template <int OP, typename T> struct Red;
+
+template <typename T> struct Red<MMP_R_SUM, T> {
+  typedef typename AccOf<T>::type A;
+  static __device__ __forceinline__ A ident() { return (A)0; }
+  static __device__ __forceinline__ A map(T v) {
+    if constexpr (mmp_t<T>::is_float) return (A)(typename mmp_t<T>::C)v;
+    else return (A)v;
+  }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) return a + b;
+    else return (A)((mmp_u64)a + (mmp_u64)b);
+  }
+};
+template <typename T> struct Red<MMP_R_MEAN, T> : Red<MMP_R_SUM, T> {
+  typedef double A;
+  static __device__ __forceinline__ A ident() { return 0.0; }
+  static __device__ __forceinline__ A map(T v) {
+    if constexpr (mmp_t<T>::is_float) return (double)(typename mmp_t<T>::C)v;
+    else return (double)v;
+  }
+  static __device__ __forceinline__ A comb(A a, A b) { return a + b; }
+};
+template <typename T> struct Red<MMP_R_PROD, T> {
+  typedef typename AccOf<T>::type A;
+  static __device__ __forceinline__ A ident() { return (A)1; }
+  static __device__ __forceinline__ A map(T v) {
+    if constexpr (mmp_t<T>::is_float) return (A)(typename mmp_t<T>::C)v;
+    else return (A)v;
+  }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) return a * b;
+    else return (A)((mmp_u64)a * (mmp_u64)b);
+  }
+};
+// max / min in the compute type; NaN propagates; ties keep the first
+template <typename T> struct Red<MMP_R_MAX, T> {
+  typedef typename mmp_t<T>::C A;
+  static __device__ __forceinline__ A ident() {
+    if constexpr (mmp_t<T>::is_float) return -__builtin_huge_valf();
+    else return (A)mmp_t<T>::lowest;
+  }
+  static __device__ __forceinline__ A map(T v) { return (A)v; }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) {
+      if (a != a) return a;
+      if (b != b) return b;
+    }
+    return b > a ? b : a;
+  }
+};
+template <typename T> struct Red<MMP_R_MIN, T> {
+  typedef typename mmp_t<T>::C A;
+  static __device__ __forceinline__ A ident() {
+    if constexpr (mmp_t<T>::is_float) return __builtin_huge_valf();
+    else if constexpr (mmp_t<T>::is_bool) return (A)1;
+    else return (A)~(typename mmp_t<T>::U)mmp_t<T>::lowest;
+  }
+  static __device__ __forceinline__ A map(T v) { return (A)v; }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) {
+      if (a != a) return a;
+      if (b != b) return b;
+    }
+    return b < a ? b : a;
+  }
+};
+
+// argmax / argmin pair; "better" = NaN first, then extreme value, then
+// smaller index.
+template <typename C> struct ArgPair {
+  C v;
+  long long i;
+};
+template <int OP, typename T> struct Arg {
+  typedef typename mmp_t<T>::C C;
+  typedef ArgPair<C> A;
+  static __device__ __forceinline__ A ident() {
+    A a;
+    if constexpr (mmp_t<T>::is_float) a.v = OP == MMP_R_ARGMAX ? -__builtin_huge_valf() : __builtin_huge_valf();
+    else if constexpr (OP == MMP_R_ARGMAX) a.v = (C)mmp_t<T>::lowest;
+    else if constexpr (mmp_t<T>::is_bool) a.v = (C)1;
+    else a.v = (C)~(typename mmp_t<T>::U)mmp_t<T>::lowest;
+    a.i = 0x7fffffffffffffffLL;
+    return a;
+  }
+  static __device__ __forceinline__ bool better(const A &x, const A &y) {  // x before y?
+    if constexpr (mmp_t<T>::is_float) {
+      const bool xn = x.v != x.v, yn = y.v != y.v;
+      if (xn || yn) return xn && (!yn || x.i < y.i);
+    }
+    if (x.v == y.v) return x.i < y.i;
+    return OP == MMP_R_ARGMAX ? x.v > y.v : x.v < y.v;
+  }
+  static __device__ __forceinline__ A comb(const A &x, const A &y) { return better(y, x) ? y : x; }
+};
+
+// --------------------------------------------------- wave / block reduce
+template <typename A> __device__ __forceinline__ A shfl_xor(A v, int m) {
+  if constexpr (sizeof(A) == 8) {
+    unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+    lo = __shfl_xor(lo, m, 64);
+    hi = __shfl_xor(hi, m, 64);
+    return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
+  } else if constexpr (sizeof(A) == 4) {
+    return __builtin_bit_cast(A, __shfl_xor(__builtin_bit_cast(unsigned, v), m, 64));
+  } else {
+    return (A)__shfl_xor((int)v, m, 64);
+  }
+}
+
+template <typename R, typename A> __device__ __forceinline__ A wave_reduce(A v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = R::comb(v, shfl_xor(v, m));
+  return v;
+}
+template <typename R, typename C> __device__ __forceinline__ ArgPair<C> wave_reduce_arg(ArgPair<C> v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    ArgPair<C> o;
+    o.v = shfl_xor(v.v, m);
+    o.i = shfl_xor(v.i, m);
+    v = R::comb(v, o);
+  }
+  return v;
+}
+
+// Block-wide reduce; the result is valid in thread 0.
+template <typename R, typename A> __device__ A block_reduce(A v, A *lds) {
+  if constexpr (sizeof(A) == 16) {
+    v = wave_reduce_arg<R>(v);
+  } else {
+    v = wave_reduce<R>(v);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[w] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) v = R::comb(v, lds[k]);
+  }
+  return v;
+}
+
+// Slice reduction over contiguous [p, p + n), element index base `i0`
+// (used by argmax).  Called by all threads of the block.
+template <typename R, typename T>
+__device__ __forceinline__ typename R::A slice_reduce(const T *__restrict__ p, long long n,
+                                                      long long i0) {
+  typedef typename R::A A;
+  constexpr int V = 16 / sizeof(T);
+  A acc0 = R::ident(), acc1 = R::ident();
+  const unsigned tid = threadIdx.x;
+  // head until 16-byte alignment
+  long long head = (long long)(((16 - ((uintptr_t)p & 15u)) & 15u) / sizeof(T));
+  if (((uintptr_t)p % sizeof(T)) != 0) head = n;  // cannot vectorise
+  if (head > n) head = n;
+  for (long long i = tid; i < head; i += kBlock) acc0 = R::comb(acc0, R::map(p[i]));
+  const long long nvec = (n - head) / V;
+  const u32x4 *pv = reinterpret_cast<const u32x4 *>(p + head);
+  long long j = tid;
+  for (; j + 3 * kBlock < nvec; j += 4 * kBlock) {
+    Pack<T> q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        if (e & 1) acc1 = R::comb(acc1, R::map(q[u].e[e]));
+        else acc0 = R::comb(acc0, R::map(q[u].e[e]));
+      }
+    }
+  }
+  for (; j < nvec; j += kBlock) {
+    Pack<T> q;
+    q.v = __builtin_nontemporal_load(pv + j);
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc0 = R::comb(acc0, R::map(q.e[e]));
+  }
+  for (long long i = head + nvec * V + tid; i < n; i += kBlock) acc0 = R::comb(acc0, R::map(p[i]));
+  (void)i0;
+  return R::comb(acc0, acc1);
+}
+
+// argmax slice: same traversal, carrying indices
+template <typename R, typename T>
+__device__ __forceinline__ typename R::A slice_argreduce(const T *__restrict__ p, long long n,
+                                                         long long i0) {
+  typedef typename R::A A;
+  typedef typename mmp_t<T>::C C;
+  constexpr int V = 16 / sizeof(T);
+  A best = R::ident();
+  const unsigned tid = threadIdx.x;
+  long long head = (long long)(((16 - ((uintptr_t)p & 15u)) & 15u) / sizeof(T));
+  if (((uintptr_t)p % sizeof(T)) != 0) head = n;
+  if (head > n) head = n;
+  for (long long i = tid; i < head; i += kBlock) best = R::comb(best, A{(C)p[i], i0 + i});
+  const long long nvec = (n - head) / V;
+  const u32x4 *pv = reinterpret_cast<const u32x4 *>(p + head);
+  long long j = tid;
+  for (; j + 3 * kBlock < nvec; j += 4 * kBlock) {
+    Pack<T> q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long ib = i0 + head + (j + u * kBlock) * V;
+#pragma unroll
+      for (int e = 0; e < V; ++e) best = R::comb(best, A{(C)q[u].e[e], ib + e});
+    }
+  }
+  for (; j < nvec; j += kBlock) {
+    Pack<T> q;
+    q.v = __builtin_nontemporal_load(pv + j);
+    const long long ib = i0 + head + j * V;
+#pragma unroll
+    for (int e = 0; e < V; ++e) best = R::comb(best, A{(C)q.e[e], ib + e});
+  }
+  for (long long i = head + nvec * V + tid; i < n; i += kBlock)
+    best = R::comb(best, A{(C)p[i], i0 + i});
+  return best;
+}
+
+// ------------------------------------------------------ finalizers
+template <int OP, typename T, typename To, typename A>
+__device__ __forceinline__ To finalize(A a, long long len) {
+  if constexpr (OP == MMP_R_MEAN) {
+    return mmp_convert<To, double>(a / (double)len);
+  } else if constexpr (OP == MMP_R_MAX || OP == MMP_R_MIN) {
+    if constexpr (sizeof(T) == 2 && mmp_t<T>::is_float) return mmp_convert<To, T>((T)a);
+    else return mmp_convert<To, A>(a);
+  } else {
+    return mmp_convert<To, A>(a);
+  }
+}
+
+// Partials are written and read with agent-scope atomics so that the last
+// workgroup of a row never reads a stale cache line of another XCD's L2.
+// (Sub-word accumulators -- max/min of 16-bit and bool types -- use plain
+// accesses ordered by the agent-scope fences around the ticket.)
+template <typename A> __device__ __forceinline__ void put_partial(A *p, const A &v) {
+  if constexpr (sizeof(A) % 8 == 0) {
+    const unsigned long long *src = reinterpret_cast<const unsigned long long *>(&v);
+    unsigned long long *dst = reinterpret_cast<unsigned long long *>(p);
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(A) / 8); ++k)
+      __hip_atomic_store(dst + k, src[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (sizeof(A) == 4) {
+    __hip_atomic_store(reinterpret_cast<unsigned *>(p), __builtin_bit_cast(unsigned, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;
+  }
+}
+template <typename A> __device__ __forceinline__ A get_partial(const A *p) {
+  if constexpr (sizeof(A) % 8 == 0) {
+    A v;
+    unsigned long long *dst = reinterpret_cast<unsigned long long *>(&v);
+    const unsigned long long *src = reinterpret_cast<const unsigned long long *>(p);
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(A) / 8); ++k)
+      dst[k] = __hip_atomic_load(src + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+  } else if constexpr (sizeof(A) == 4) {
+    return __builtin_bit_cast(A, __hip_atomic_load(reinterpret_cast<const unsigned *>(p),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  } else {
+    return *p;
+  }
+}
+
+// Last-arrival combine.  Returns true in the block that must finish the
+// row; its thread 0 then holds the combined value in `out`.
+template <typename R>
+__device__ bool last_block_combine(typename R::A v, typename R::A *partials, unsigned *ticket,
+                                   int S, int s, typename R::A *out, typename R::A *lds) {
+  __shared__ int is_last;
+  if (threadIdx.x == 0) {
+    put_partial(partials + s, v);
+    __threadfence();
+    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == (unsigned)(S - 1));
+  }
+  __syncthreads();
+  if (!is_last) return false;
+  __threadfence();
+  typename R::A acc = R::ident();
+  // fixed order: thread k combines partials k, k+256, ... then the tree
+  for (int k = threadIdx.x; k < S; k += kBlock) acc = R::comb(acc, get_partial(partials + k));
+  __syncthreads();
+  acc = block_reduce<R>(acc, lds);
+  if (threadIdx.x == 0) {
+    *out = acc;
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
+// ---------------------------------------------------------- kernels
+// Rows: grid = rows * S; block (row, s) reduces slice s of its row.
+template <int OP, typename T, typename To>
+__global__ __launch_bounds__(kBlock) void k_reduce_rows(const T *__restrict__ x, To *__restrict__ out,
+                                                       long long len, int S,
+                                                       typename Red<OP, T>::A *partials,
+                                                       unsigned *tickets) {
+  typedef Red<OP, T> R;
+  typedef typename R::A A;
+  __shared__ A lds[kWaves];
+  const long long row = blockIdx.x / S;
+  const int s = (int)(blockIdx.x - row * S);
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  A v = R::ident();
+  if (b0 < b1) v = slice_reduce<R, T>(x + row * len + b0, b1 - b0, b0);
+  v = block_reduce<R>(v, lds);
+  if (S == 1) {
+    if (threadIdx.x == 0) out[row] = finalize<OP, T, To>(v, len);
+    return;
+  }
+  A total;
+  __syncthreads();
+  if (last_block_combine<R>(v, partials + row * S, tickets + row, S, s, &total, lds) &&
+      threadIdx.x == 0)
+    out[row] = finalize<OP, T, To>(total, len);
+}
+
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void k_argreduce_rows(const T *__restrict__ x,
+                                                          long long *__restrict__ out,
+                                                          long long len, int S,
+                                                          typename Arg<OP, T>::A *partials,
+                                                          unsigned *tickets) {
+  typedef Arg<OP, T> R;
+  typedef typename R::A A;
+  __shared__ A lds[kWaves];
+  const long long row = blockIdx.x / S;
+  const int s = (int)(blockIdx.x - row * S);
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  A v = R::ident();
+  if (b0 < b1) v = slice_argreduce<R, T>(x + row * len + b0, b1 - b0, b0);
+  v = block_reduce<R>(v, lds);
+  if (S == 1) {
+    if (threadIdx.x == 0) out[row] = v.i;
+    return;
+  }
+  A total;
+  __syncthreads();
+  if (last_block_combine<R>(v, partials + row * S, tickets + row, S, s, &total, lds) &&
+      threadIdx.x == 0)
+    out[row] = total.i;
+}
+
+// Strided axis: grid (ceil(inner / 256), outer, S); thread = column.
+template <int OP, typename T, typename To>
+__global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x, To *__restrict__ out,
+                                                       long long len, long long inner, int S,
+                                                       typename Red<OP, T>::A *partials,
+                                                       unsigned *tickets) {
+  typedef Red<OP, T> R;
+  typedef typename R::A A;
+  const long long o = blockIdx.y;
+  const int s = blockIdx.z;
+  const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  A v = R::ident();
+  if (c < inner) {
+    const T *p = x + o * len * inner + c;
+    for (long long l = b0; l < b1; ++l) v = R::comb(v, R::map(p[l * inner]));
+  }
+  if (S == 1) {
+    if (c < inner) out[o * inner + c] = finalize<OP, T, To>(v, len);
+    return;
+  }
+  // partial per (o, c, s); ticket per (o, column block)
+  const long long cb = blockIdx.x, ncb = gridDim.x;
+  A *mine = partials + ((o * ncb + cb) * S + s) * kBlock;
+  if (c < inner) put_partial(mine + threadIdx.x, v);
+  __shared__ int is_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const unsigned t = __hip_atomic_fetch_add(tickets + o * ncb + cb, 1u, __ATOMIC_ACQ_REL,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == (unsigned)(S - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (c < inner) {
+    A acc = R::ident();
+    const A *base = partials + (o * ncb + cb) * S * kBlock + threadIdx.x;
+    for (int k = 0; k < S; ++k) acc = R::comb(acc, get_partial(base + k * kBlock));
+    out[o * inner + c] = finalize<OP, T, To>(acc, len);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void k_argreduce_cols(const T *__restrict__ x,
+                                                          long long *__restrict__ out,
+                                                          long long len, long long inner) {
+  typedef Arg<OP, T> R;
+  typedef typename R::A A;
+  typedef typename mmp_t<T>::C C;
+  const long long o = blockIdx.y;
+  const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= inner) return;
+  const T *p = x + o * len * inner + c;
+  A v = R::ident();
+  for (long long l = 0; l < len; ++l) v = R::comb(v, A{(C)p[l * inner], l});
+  out[o * inner + c] = v.i;
+}
+
+// ------------------------------------------------------------ launch
+int choose_splits(long long rows, long long len) {
+  long long want = (kTargetBlocks + rows - 1) / rows;
+  long long maxs = (len + kMinPerBlock - 1) / kMinPerBlock;
+  long long s = want < maxs ? want : maxs;
+  if (s < 1) s = 1;
+  if (s > 4096) s = 4096;
+  return (int)s;
+}
+
+template <int OP, typename T, typename To>
+int launch_reduce(long long outer, long long len, long long inner, const void *x, void *out) {
+  typedef typename Red<OP, T>::A A;
+  int st = MMP_OK;
+  if (inner == 1) {
+    const int S = choose_splits(outer, len);
+    A *partials = nullptr;
+    unsigned *tickets = nullptr;
+    if (S > 1) {
+      partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS, sizeof(A) * outer * S, &st);
+      if (st) return st;
+      tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer, &st);
+      if (st) return st;
+    }
+    const long long grid = outer * S;
+    if (grid > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "reduction grid too large");
+    hipLaunchKernelGGL((k_reduce_rows<OP, T, To>), dim3((unsigned)grid), dim3(kBlock), 0,
+                       mmpi::stream(), (const T *)x, (To *)out, len, S, partials, tickets);
+    return mmpi::check_launch("mmp_reduce(rows)");
+  }
+  const long long ncb = mmpi::ceil_div(inner, kBlock);
+  if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided reduction: outer extent %lld > 65535", outer);
+  long long want = (kTargetBlocks + outer * ncb - 1) / (outer * ncb);
+  long long maxs = len / 64 > 0 ? len / 64 : 1;
+  int S = (int)(want < maxs ? want : maxs);
+  if (S < 1) S = 1;
+  if (S > 1024) S = 1024;
+  A *partials = nullptr;
+  unsigned *tickets = nullptr;
+  if (S > 1) {
+    partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS,
+                                  sizeof(A) * outer * ncb * S * kBlock, &st);
+    if (st) return st;
+    tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer * ncb, &st);
+    if (st) return st;
+  }
+  hipLaunchKernelGGL((k_reduce_cols<OP, T, To>), dim3((unsigned)ncb, (unsigned)outer, (unsigned)S),
+                     dim3(kBlock), 0, mmpi::stream(), (const T *)x, (To *)out, len, inner, S,
+                     partials, tickets);
+  return mmpi::check_launch("mmp_reduce(cols)");
+}
+
+template <int OP, typename T>
+int launch_argreduce(long long outer, long long len, long long inner, const void *x, long long *out) {
+  typedef typename Arg<OP, T>::A A;
+  int st = MMP_OK;
+  if (inner == 1) {
+    const int S = choose_splits(outer, len);
+    A *partials = nullptr;
+    unsigned *tickets = nullptr;
+    if (S > 1) {
+      partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS, sizeof(A) * outer * S, &st);
+      if (st) return st;
+      tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer, &st);
+      if (st) return st;
+    }
+    const long long grid = outer * S;
+    if (grid > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "reduction grid too large");
+    hipLaunchKernelGGL((k_argreduce_rows<OP, T>), dim3((unsigned)grid), dim3(kBlock), 0,
+                       mmpi::stream(), (const T *)x, out, len, S, partials, tickets);
+    return mmpi::check_launch("mmp_argreduce(rows)");
+  }
+  if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided argreduce: outer extent %lld > 65535", outer);
+  hipLaunchKernelGGL((k_argreduce_cols<OP, T>),
+                     dim3((unsigned)mmpi::ceil_div(inner, kBlock), (unsigned)outer), dim3(kBlock), 0,
+                     mmpi::stream(), (const T *)x, out, len, inner);
+  return mmpi::check_launch("mmp_argreduce(cols)");
+}
+
+// Output dtypes NumPy's rules produce: max/min keep the dtype; sums and
+// products of floats give a float (float64 partials may round to float32 /
+// float16), of signed ints and bool int64, of unsigned ints uint64; means
+// give a float.
+template <int OP, typename T, typename To> constexpr bool out_ok() {
+  constexpr bool to_float = mmp_t<To>::is_float;
+  if (OP == MMP_R_MAX || OP == MMP_R_MIN) return __is_same(T, To);
+  if (OP == MMP_R_MEAN) return to_float;
+  if (mmp_t<T>::is_float) return to_float;
+  if (mmp_t<T>::is_signed || mmp_t<T>::is_bool) return __is_same(To, mmp_i64);
+  return __is_same(To, mmp_u64);
+}
+
+template <int OP, typename T, typename To>
+int reduce_to(long long outer, long long len, long long inner, const void *x, void *out) {
+  if constexpr (!out_ok<OP, T, To>()) {
+    return mmpi::fail(MMP_E_UNSUPPORTED, "reduction op %d: unsupported output dtype", OP);
+  } else {
+    return launch_reduce<OP, T, To>(outer, len, inner, x, out);
+  }
+}
+
+template <int OP, typename T>
+int reduce_out(int out_dtype, long long outer, long long len, long long inner, const void *x,
+               void *out) {
+  switch (out_dtype) {
+    case MMP_F32: return reduce_to<OP, T, float>(outer, len, inner, x, out);
+    case MMP_F64: return reduce_to<OP, T, double>(outer, len, inner, x, out);
+    case MMP_F16: return reduce_to<OP, T, mmp_half>(outer, len, inner, x, out);
+    case MMP_I64: return reduce_to<OP, T, mmp_i64>(outer, len, inner, x, out);
+    case MMP_U64: return reduce_to<OP, T, mmp_u64>(outer, len, inner, x, out);
+    case MMP_I32: return reduce_to<OP, T, mmp_i32>(outer, len, inner, x, out);
+    case MMP_U32: return reduce_to<OP, T, mmp_u32>(outer, len, inner, x, out);
+    case MMP_I16: return reduce_to<OP, T, mmp_i16>(outer, len, inner, x, out);
+    case MMP_U16: return reduce_to<OP, T, mmp_u16>(outer, len, inner, x, out);
+    case MMP_BOOL: return reduce_to<OP, T, bool>(outer, len, inner, x, out);
+    default: return mmpi::fail(MMP_E_UNSUPPORTED, "reduction output dtype %d", out_dtype);
+  }
+}
+
+int check_view(long long outer, long long len, long long inner, const void *x, const void *out) {
+  if (outer < 0 || len < 0 || inner < 0) return mmpi::fail(MMP_E_ARG, "negative extent");
+  if (len == 0) return mmpi::fail(MMP_E_ARG, "reduction over an empty axis");
+  if (outer * inner > 0 && (!x || !out)) return mmpi::fail(MMP_E_ARG, "null pointer");
+  return MMP_OK;
+}
+
+}  // namespace
+
+extern "C" int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+                          int64_t inner, const void *x, void *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_view(outer, len, inner, x, out)) return st;
+  if (outer * inner == 0) return MMP_OK;
+  MMP_DISPATCH_ALL(dtype, {
+    switch (op) {
+      case MMP_R_SUM: return reduce_out<MMP_R_SUM, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_PROD: return reduce_out<MMP_R_PROD, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_MAX: return reduce_out<MMP_R_MAX, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_MIN: return reduce_out<MMP_R_MIN, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_MEAN: return reduce_out<MMP_R_MEAN, T>(out_dtype, outer, len, inner, x, out);
+      default: return mmpi::fail(MMP_E_ARG, "unknown reduction op %d", op);
+    }
+  })
+}
+
+extern "C" int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len, int64_t inner,
+                             const void *x, int64_t *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_view(outer, len, inner, x, out)) return st;
+  if (outer * inner == 0) return MMP_OK;
+  MMP_DISPATCH_ALL(dtype, {
+    if (op == MMP_R_ARGMAX)
+      return launch_argreduce<MMP_R_ARGMAX, T>(outer, len, inner, x, (long long *)out);
+    if (op == MMP_R_ARGMIN)
+      return launch_argreduce<MMP_R_ARGMIN, T>(outer, len, inner, x, (long long *)out);
+    return mmpi::fail(MMP_E_ARG, "unknown arg-reduction op %d", op);
+  })
+}

@@ -12,7 +12,6 @@
 //    message instead of the metalgpu ABI's silent `void`;
 //  * kernels are precompiled gfx950 code objects; only fused expressions and
 //    user RawKernels go through hiprtc, cached by source text.
-#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
@@ -475,18 +474,6 @@ int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
                                        block3[0], block3[1], block3[2], shared_bytes,
                                        g_dev.stream, args, nullptr);
   return mmpi::check_hip(e, "hipModuleLaunchKernel");
-}
-
-int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3, const uint32_t *block3,
-                           uint32_t shared_bytes, void **args) {
-  if (int st = mmpi::ensure_init()) return st;
-  if (!kernel || !threads3 || !block3) return mmpi::fail(MMP_E_ARG, "null argument");
-  if (threads3[0] == 0 || threads3[1] == 0 || threads3[2] == 0) return MMP_OK;
-  if (mmpi::inject(3)) return mmpi::fail(MMP_E_INJECTED, "mmp_rtc_launch_threads: injected failure");
-  hipError_t e = hipExtModuleLaunchKernel((hipFunction_t)kernel, threads3[0], threads3[1],
-                                          threads3[2], block3[0], block3[1], block3[2],
-                                          shared_bytes, g_dev.stream, args, nullptr);
-  return mmpi::check_hip(e, "hipExtModuleLaunchKernel");
 }
 
 int mmp_debug_fail_next(int kind, int count) {

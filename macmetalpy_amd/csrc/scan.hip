@@ -1,0 +1,310 @@
+// scan.hip -- cumsum / cumprod.
+//
+// Replaces the reference's three-pass Metal scan (_kernels.py:1263-1360,
+// driven by ndarray._prefix_scan ndarray.py:2068-2152): block-local serial
+// scans, then ONE thread scanning all block totals, then a propagation pass.
+//
+// Here a contiguous scan (any number of rows of length len) is a single
+// pass of decoupled look-back:
+//  * workgroups take tile ids from an atomic counter in launch order, so a
+//    tile only ever waits for tiles that are already running (AMD gives no
+//    forward-progress guarantee to workgroups that have not started);
+//  * a tile (256 threads x 16 elements) is staged through LDS with 128-bit
+//    loads, scanned serially per thread in the accumulator type, then across
+//    the wave64 with shuffles and across the 4 waves through LDS;
+//  * thread 0 publishes the tile aggregate, walks back over predecessors'
+//    published aggregates / inclusive prefixes (agent-scope acquire /
+//    release), then publishes its own inclusive prefix;
+//  * tile flags carry a per-call generation number, so the flag array is
+//    never cleared between calls; waits are bounded and a timeout is
+//    recorded instead of hanging.
+// Accumulators: int64 for integers (int32 -> int64 output as NumPy),
+// float64 for floats (rounded once per output element).  HBM-bound:
+// sizeof(in) + sizeof(out) bytes per element.
+// Strided scans (inner > 1) run one thread per column, coalesced across
+// columns.
+#include "mmp_ops.h"
+#include "mmp_internal.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kItems = 16;
+constexpr int kTile = kBlock * kItems;
+constexpr int kPad = kTile / kItems;   // one pad word per thread row in LDS
+constexpr long long kSpinLimit = 1ll << 26;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct ScanAcc { typedef double type; };
+template <> struct ScanAcc<mmp_i16> { typedef mmp_i64 type; };
+template <> struct ScanAcc<mmp_i32> { typedef mmp_i64 type; };
+template <> struct ScanAcc<mmp_i64> { typedef mmp_i64 type; };
+template <> struct ScanAcc<bool> { typedef mmp_i64 type; };
+template <> struct ScanAcc<mmp_u16> { typedef mmp_u64 type; };
+template <> struct ScanAcc<mmp_u32> { typedef mmp_u64 type; };
+template <> struct ScanAcc<mmp_u64> { typedef mmp_u64 type; };
+
+template <int OP, typename T> struct ScanOp {
+  typedef typename ScanAcc<T>::type A;
+  static __device__ __forceinline__ A ident() { return OP == MMP_S_CUMSUM ? (A)0 : (A)1; }
+  static __device__ __forceinline__ A map(T v) {
+    if constexpr (mmp_t<T>::is_float) return (A)(typename mmp_t<T>::C)v;
+    else return (A)v;
+  }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) {
+      return OP == MMP_S_CUMSUM ? a + b : a * b;
+    } else {
+      return OP == MMP_S_CUMSUM ? (A)((mmp_u64)a + (mmp_u64)b) : (A)((mmp_u64)a * (mmp_u64)b);
+    }
+  }
+};
+
+__device__ __forceinline__ int padded(int i) { return i + i / kItems; }
+
+template <typename A> __device__ __forceinline__ A shfl_up64(A v, int d) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  unsigned lo = __shfl_up((unsigned)u, d, 64), hi = __shfl_up((unsigned)(u >> 32), d, 64);
+  return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
+}
+
+template <typename A> __device__ __forceinline__ void store_agent(A *p, A v, int order) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  if (order == __ATOMIC_RELEASE)
+    __hip_atomic_store((unsigned long long *)p, u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    __hip_atomic_store((unsigned long long *)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename A> __device__ __forceinline__ A load_agent(const A *p) {
+  return __builtin_bit_cast(A, __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+}
+
+struct ScanScratch {
+  unsigned *counter;   // tile ticket (left at 0 by the last tile)
+  unsigned *flags;     // per tile: generation << 2 | state (1 aggregate, 2 inclusive)
+  void *aggr;          // per tile aggregate
+  void *incl;          // per tile inclusive prefix
+  unsigned *timeout;   // set to 1 if a look-back wait ran out
+};
+
+template <int OP, typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, To *__restrict__ y,
+                                                     long long len, long long tiles_per_row,
+                                                     long long ntiles, ScanScratch sc,
+                                                     unsigned gen) {
+  typedef ScanOp<OP, Ti> S;
+  typedef typename S::A A;
+  constexpr int kStage = (sizeof(Ti) > sizeof(To) ? sizeof(Ti) : sizeof(To));
+  __shared__ __attribute__((aligned(16))) unsigned char stage[(kTile + kPad) * kStage];
+  __shared__ A wsum[kBlock / 64];
+  __shared__ A s_prefix;
+  __shared__ unsigned s_tile;
+  Ti *sx = reinterpret_cast<Ti *>(stage);
+  To *sy = reinterpret_cast<To *>(stage);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  if (tid == 0) {
+    const unsigned t = __hip_atomic_fetch_add(sc.counter, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    s_tile = t;
+    // every other workgroup has already drawn its id: re-arm for the next call
+    if ((long long)t == ntiles - 1)
+      __hip_atomic_store(sc.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const long long tile = s_tile;
+  const long long row = tile / tiles_per_row;
+  const long long t = tile - row * tiles_per_row;
+  const long long base = t * kTile;
+  const long long rem = len - base;
+  const int n = rem < kTile ? (int)rem : kTile;
+  const Ti *xr = x + row * len + base;
+  To *yr = y + row * len + base;
+
+  // 1. stage the tile (128-bit loads when whole and aligned)
+  constexpr int VI = 16 / sizeof(Ti);
+  if (n == kTile && ((uintptr_t)xr & 15u) == 0) {
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(xr);
+#pragma unroll
+    for (int k = 0; k < kTile / VI / kBlock; ++k) {
+      const int vi = k * kBlock + tid;
+      union { u32x4 v; Ti e[VI]; } q;
+      q.v = __builtin_nontemporal_load(xv + vi);
+#pragma unroll
+      for (int e = 0; e < VI; ++e) sx[padded(vi * VI + e)] = q.e[e];
+    }
+  } else {
+    for (int i = tid; i < n; i += kBlock) sx[padded(i)] = xr[i];
+  }
+  __syncthreads();
+
+  // 2. per-thread serial scan of 16 consecutive elements
+  A v[kItems];
+  A run = S::ident();
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const int i = tid * kItems + j;
+    const A val = i < n ? S::map(sx[padded(i)]) : S::ident();
+    run = S::comb(run, val);
+    v[j] = run;
+  }
+  // 3. block scan of thread totals: wave64 shuffles, then wave totals
+  A inc = run;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const A o = shfl_up64(inc, d);
+    if (lane >= d) inc = S::comb(o, inc);
+  }
+  A excl = shfl_up64(inc, 1);
+  if (lane == 0) excl = S::ident();
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  A wpre = S::ident(), total = S::ident();
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) {
+    if (w < wave) wpre = S::comb(wpre, wsum[w]);
+    total = S::comb(total, wsum[w]);
+  }
+
+  // 4. decoupled look-back (thread 0)
+  if (tid == 0) {
+    A prefix = S::ident();
+    A *aggr = reinterpret_cast<A *>(sc.aggr);
+    A *incl = reinterpret_cast<A *>(sc.incl);
+    if (t > 0) {
+      store_agent(aggr + tile, total, __ATOMIC_RELAXED);
+      __hip_atomic_store(sc.flags + tile, (gen << 2) | 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      long long j = tile - 1;
+      long long spins = 0;
+      while (true) {
+        const unsigned f = __hip_atomic_load(sc.flags + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        if ((f >> 2) != gen) {
+          if (++spins > kSpinLimit) {
+            __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        if ((f & 3u) == 2u) {
+          prefix = S::comb(load_agent(incl + j), prefix);
+          break;
+        }
+        prefix = S::comb(load_agent(aggr + j), prefix);
+        --j;  // the row's first tile always publishes an inclusive prefix
+      }
+    }
+    store_agent(incl + tile, S::comb(prefix, total), __ATOMIC_RELAXED);
+    __hip_atomic_store(sc.flags + tile, (gen << 2) | 2u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    s_prefix = prefix;
+  }
+  __syncthreads();  // also: every thread has read its inputs from `stage`
+
+  // 5. outputs through LDS, then coalesced stores
+  const A pre = S::comb(s_prefix, S::comb(wpre, excl));
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const int i = tid * kItems + j;
+    if (i < n) sy[padded(i)] = mmp_convert<To, A>(S::comb(pre, v[j]));
+  }
+  __syncthreads();
+  constexpr int VO = 16 / sizeof(To);
+  if (n == kTile && ((uintptr_t)yr & 15u) == 0) {
+    u32x4 *yv = reinterpret_cast<u32x4 *>(yr);
+#pragma unroll
+    for (int k = 0; k < kTile / VO / kBlock; ++k) {
+      const int vi = k * kBlock + tid;
+      union { u32x4 v; To e[VO]; } q;
+#pragma unroll
+      for (int e = 0; e < VO; ++e) q.e[e] = sy[padded(vi * VO + e)];
+      __builtin_nontemporal_store(q.v, yv + vi);
+    }
+  } else {
+    for (int i = tid; i < n; i += kBlock) yr[i] = sy[padded(i)];
+  }
+}
+
+// Strided axis: one thread per column, serial along the axis.
+template <int OP, typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_scan_cols(const Ti *__restrict__ x, To *__restrict__ y,
+                                                     long long len, long long inner) {
+  typedef ScanOp<OP, Ti> S;
+  const long long o = blockIdx.y;
+  const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= inner) return;
+  const long long off = o * len * inner + c;
+  typename S::A acc = S::ident();
+  for (long long l = 0; l < len; ++l) {
+    acc = S::comb(acc, S::map(x[off + l * inner]));
+    y[off + l * inner] = mmp_convert<To, typename S::A>(acc);
+  }
+}
+
+template <int OP, typename Ti, typename To> constexpr bool scan_out_ok() {
+  if (mmp_t<Ti>::is_float) return __is_same(Ti, To);
+  if (mmp_t<Ti>::is_signed || mmp_t<Ti>::is_bool) return __is_same(To, mmp_i64);
+  return __is_same(To, mmp_u64);
+}
+
+template <int OP, typename Ti, typename To>
+int launch_scan(long long outer, long long len, long long inner, const void *x, void *y) {
+  if constexpr (!scan_out_ok<OP, Ti, To>()) {
+    return mmpi::fail(MMP_E_UNSUPPORTED, "scan: unsupported output dtype");
+  } else {
+    typedef typename ScanOp<OP, Ti>::A A;
+    if (inner == 1) {
+      const long long tpr = mmpi::ceil_div(len, kTile);
+      const long long ntiles = outer * tpr;
+      if (ntiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "scan too large");
+      int st = MMP_OK;
+      ScanScratch sc;
+      sc.counter = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st);
+      if (st) return st;
+      sc.timeout = sc.counter + 1;
+      sc.flags = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_FLAGS, 4 * ntiles, &st);
+      if (st) return st;
+      char *vals = (char *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES, 2 * sizeof(A) * ntiles, &st);
+      if (st) return st;
+      sc.aggr = vals;
+      sc.incl = vals + sizeof(A) * ntiles;
+      const unsigned gen = mmpi::next_generation();
+      hipLaunchKernelGGL((k_scan_rows<OP, Ti, To>), dim3((unsigned)ntiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);
+      return mmpi::check_launch("mmp_scan(rows)");
+    }
+    if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided scan: outer extent %lld > 65535", outer);
+    hipLaunchKernelGGL((k_scan_cols<OP, Ti, To>),
+                       dim3((unsigned)mmpi::ceil_div(inner, kBlock), (unsigned)outer), dim3(kBlock),
+                       0, mmpi::stream(), (const Ti *)x, (To *)y, len, inner);
+    return mmpi::check_launch("mmp_scan(cols)");
+  }
+}
+
+template <int OP, typename Ti>
+int scan_out(int out_dtype, long long outer, long long len, long long inner, const void *x, void *y) {
+  switch (out_dtype) {
+    case MMP_F32: return launch_scan<OP, Ti, float>(outer, len, inner, x, y);
+    case MMP_F64: return launch_scan<OP, Ti, double>(outer, len, inner, x, y);
+    case MMP_F16: return launch_scan<OP, Ti, mmp_half>(outer, len, inner, x, y);
+    case MMP_I64: return launch_scan<OP, Ti, mmp_i64>(outer, len, inner, x, y);
+    case MMP_U64: return launch_scan<OP, Ti, mmp_u64>(outer, len, inner, x, y);
+    default: return mmpi::fail(MMP_E_UNSUPPORTED, "scan output dtype %d", out_dtype);
+  }
+}
+
+}  // namespace
+
+extern "C" int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+                        int64_t inner, const void *x, void *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (outer < 0 || len < 0 || inner < 0) return mmpi::fail(MMP_E_ARG, "negative extent");
+  if (outer * len * inner == 0) return MMP_OK;
+  if (!x || !out) return mmpi::fail(MMP_E_ARG, "null pointer");
+  MMP_DISPATCH_ALL(dtype, {
+    if (op == MMP_S_CUMSUM) return scan_out<MMP_S_CUMSUM, T>(out_dtype, outer, len, inner, x, out);
+    if (op == MMP_S_CUMPROD) return scan_out<MMP_S_CUMPROD, T>(out_dtype, outer, len, inner, x, out);
+    return mmpi::fail(MMP_E_ARG, "unknown scan op %d", op);
+  })
+}

@@ -5,9 +5,15 @@ shape: ``grid`` is the TOTAL number of threads (int or 1-3 tuple), as in
 Metal's ``dispatchThreads``, and ``args`` are arrays bound in order.  The
 source is HIP C++ (compiled by hiprtc for gfx950) instead of MSL; the
 kernel reads its index as ``blockIdx.x * blockDim.x + threadIdx.x`` and,
-because exactly ``grid`` threads are launched (the last workgroup may be
-partial), needs no bounds check.  Scalars (NumPy scalar objects) may be
-passed by value after the arrays.
+because exactly ``grid`` threads are launched, needs no bounds check.
+
+Exactness with uniform workgroups: the workgroup extent in each dimension
+is the largest divisor of the thread count that fits the block budget
+(256 threads), so the grid is a whole number of workgroups and HIP's
+``blockDim`` keeps its usual meaning.  Thread counts with a divisor that is
+a multiple of 64 fill whole wave64s; a prime count runs one thread per
+workgroup (correct, slow).  Scalars (NumPy scalar objects, Python
+int/float) may be passed by value.
 """
 from __future__ import annotations
 
@@ -30,7 +36,28 @@ _CTYPES = {
     np.dtype(np.bool_): ctypes.c_bool,
 }
 
-_BLOCKS = {1: (256, 1, 1), 2: (16, 16, 1), 3: (8, 8, 4)}
+_BUDGET = 256
+
+
+def _largest_divisor(n: int, limit: int) -> int:
+    """Largest d <= limit dividing n, preferring multiples of 64."""
+    limit = max(1, min(limit, n))
+    best = 1
+    for d in range(limit, 0, -1):
+        if n % d == 0:
+            if d % 64 == 0:
+                return d
+            if best == 1:
+                best = d
+    return best
+
+
+def block_for_grid(grid) -> tuple:
+    """Uniform workgroup extents dividing ``grid`` exactly (x first)."""
+    bx = _largest_divisor(grid[0], _BUDGET)
+    by = _largest_divisor(grid[1], _BUDGET // bx) if len(grid) > 1 else 1
+    bz = _largest_divisor(grid[2], _BUDGET // (bx * by)) if len(grid) > 2 else 1
+    return (bx, by, bz)
 
 
 class RawKernel:
@@ -57,10 +84,10 @@ class RawKernel:
         grid = tuple(int(g) for g in grid)
         if not 1 <= len(grid) <= 3:
             raise ValueError("grid tuple must have 1-3 elements")
-        dims = len(grid)
-        while dims > 1 and grid[dims - 1] == 1:
-            dims -= 1
-        block = _BLOCKS[dims]
+        if any(g <= 0 for g in grid):
+            return
+        block = block_for_grid(grid)
+        blocks = tuple(g // b for g, b in zip(grid, block))
         cargs = []
         arrays = []
         for a in args:
@@ -78,4 +105,4 @@ class RawKernel:
                 raise TypeError(f"unsupported RawKernel argument type {type(a).__name__}")
         for a in arrays:  # the kernel may write any of them
             ew.flush_lazy(a._buffer)
-        HipBackend().launch(self.kernel, grid, block, cargs, shared_mem, threads=True)
+        HipBackend().launch(self.kernel, blocks, block, cargs, shared_mem)

@@ -139,12 +139,28 @@ MMP_DI bool mm_isnan(double x) { return x != x; }
 MMP_DI float mm_nan(float) { return __builtin_nanf(""); }
 MMP_DI double mm_nan(double) { return __builtin_nan(""); }
 
-// 180/pi and pi/180, rounded to the compute type first as
-// numpy's npy_degreesf / npy_radiansf do (x * (float)(180.0/NPY_PI)).
-MMP_DI float mm_rad2deg(float) { return (float)(180.0 / 3.14159265358979323846); }
+// 180/pi and pi/180 as NumPy's float32 loops use them: the quotient of the
+// float32 constants, evaluated in float32 (180.0f / NPY_PIf); in double for
+// float64.
+MMP_DI float mm_rad2deg(float) { return 180.0f / 3.14159265358979323846f; }
 MMP_DI double mm_rad2deg(double) { return 180.0 / 3.14159265358979323846; }
-MMP_DI float mm_deg2rad(float) { return (float)(3.14159265358979323846 / 180.0); }
+MMP_DI float mm_deg2rad(float) { return 3.14159265358979323846f / 180.0f; }
 MMP_DI double mm_deg2rad(double) { return 3.14159265358979323846 / 180.0; }
+
+// float32 functions evaluated through float64 and rounded once.  Used where
+// the float32 device library is more than 2 ULP away from NumPy's results
+// (exp2, log10, arcsin, arccos, arctan2); the float64 path is within
+// 0.5 ULP (+ the float64 error) of the correctly rounded value.
+MMP_DI float mm_exp2_acc(float x) { return (float)exp2((double)x); }
+MMP_DI double mm_exp2_acc(double x) { return exp2(x); }
+MMP_DI float mm_log10_acc(float x) { return (float)log10((double)x); }
+MMP_DI double mm_log10_acc(double x) { return log10(x); }
+MMP_DI float mm_asin_acc(float x) { return (float)asin((double)x); }
+MMP_DI double mm_asin_acc(double x) { return asin(x); }
+MMP_DI float mm_acos_acc(float x) { return (float)acos((double)x); }
+MMP_DI double mm_acos_acc(double x) { return acos(x); }
+MMP_DI float mm_atan2_acc(float y, float x) { return (float)atan2((double)y, (double)x); }
+MMP_DI double mm_atan2_acc(double y, double x) { return atan2(y, x); }
 MMP_DI float mm_ln2(float) { return 0.693147180559945309417f; }
 MMP_DI double mm_ln2(double) { return 0.693147180559945309417; }
 MMP_DI float mm_log2e(float) { return 1.442695040888963407360f; }
@@ -234,17 +250,17 @@ template <typename T> MMP_DI T op_reciprocal(T x) {
 MMP_FLOAT_UNARY(sqrt, mm_sqrt(x))
 MMP_FLOAT_UNARY(cbrt, mm_cbrt(x))
 MMP_FLOAT_UNARY(exp, mm_exp(x))
-MMP_FLOAT_UNARY(exp2, mm_exp2(x))
+MMP_FLOAT_UNARY(exp2, mm_exp2_acc(x))
 MMP_FLOAT_UNARY(expm1, mm_expm1(x))
 MMP_FLOAT_UNARY(log, mm_log(x))
 MMP_FLOAT_UNARY(log2, mm_log2(x))
-MMP_FLOAT_UNARY(log10, mm_log10(x))
+MMP_FLOAT_UNARY(log10, mm_log10_acc(x))
 MMP_FLOAT_UNARY(log1p, mm_log1p(x))
 MMP_FLOAT_UNARY(sin, mm_sin(x))
 MMP_FLOAT_UNARY(cos, mm_cos(x))
 MMP_FLOAT_UNARY(tan, mm_tan(x))
-MMP_FLOAT_UNARY(arcsin, mm_asin(x))
-MMP_FLOAT_UNARY(arccos, mm_acos(x))
+MMP_FLOAT_UNARY(arcsin, mm_asin_acc(x))
+MMP_FLOAT_UNARY(arccos, mm_acos_acc(x))
 MMP_FLOAT_UNARY(arctan, mm_atan(x))
 MMP_FLOAT_UNARY(sinh, mm_sinh(x))
 MMP_FLOAT_UNARY(cosh, mm_cosh(x))
@@ -412,14 +428,16 @@ template <typename T> MMP_DI T op_power(T a, T b) {
   }
 }
 
-// maximum/minimum propagate NaN; on ties the second operand is returned,
-// matching numpy's results for (+0, -0) pairs.  fmax/fmin ignore NaN.
+// maximum/minimum propagate NaN; fmax/fmin ignore NaN.  On ties (+0 vs -0)
+// numpy's float32/float64 loops return the second operand and its float16
+// loops (npy_half_ge / npy_half_le) the first; both are reproduced.
 template <typename T> MMP_DI T op_maximum(T a, T b) {
   if constexpr (mmp_t<T>::is_float) {
     typedef typename mmp_t<T>::C C;
     C x = (C)a, y = (C)b;
     if (mm_isnan(x)) return a;
     if (mm_isnan(y)) return b;
+    if constexpr (sizeof(T) == 2) return x >= y ? a : b;
     return x > y ? a : b;
   } else if constexpr (mmp_t<T>::is_bool) {
     return a || b;
@@ -433,6 +451,7 @@ template <typename T> MMP_DI T op_minimum(T a, T b) {
     C x = (C)a, y = (C)b;
     if (mm_isnan(x)) return a;
     if (mm_isnan(y)) return b;
+    if constexpr (sizeof(T) == 2) return x <= y ? a : b;
     return x < y ? a : b;
   } else if constexpr (mmp_t<T>::is_bool) {
     return a && b;
@@ -446,6 +465,7 @@ template <typename T> MMP_DI T op_fmax(T a, T b) {
     C x = (C)a, y = (C)b;
     if (mm_isnan(y)) return a;
     if (mm_isnan(x)) return b;
+    if constexpr (sizeof(T) == 2) return x >= y ? a : b;
     return x > y ? a : b;
   } else {
     return op_maximum(a, b);
@@ -457,6 +477,7 @@ template <typename T> MMP_DI T op_fmin(T a, T b) {
     C x = (C)a, y = (C)b;
     if (mm_isnan(y)) return a;
     if (mm_isnan(x)) return b;
+    if constexpr (sizeof(T) == 2) return x <= y ? a : b;
     return x < y ? a : b;
   } else {
     return op_minimum(a, b);
@@ -469,10 +490,33 @@ template <typename T> MMP_DI T op_fmin(T a, T b) {
     C a = (C)a_, b = (C)b_;                                                   \
     return (T)(EXPR);                                                         \
   }
-MMP_FLOAT_BINARY(arctan2, mm_atan2(a, b))
+MMP_FLOAT_BINARY(arctan2, mm_atan2_acc(a, b))
 MMP_FLOAT_BINARY(hypot, mm_hypot(a, b))
 MMP_FLOAT_BINARY(copysign, mm_copysign(a, b))
-MMP_FLOAT_BINARY(nextafter, mm_nextafter(a, b))
+
+// nextafter steps in the representation of T itself; for float16 that is
+// the half-precision bit pattern (numpy npy_half_nextafter), not float's.
+template <typename T> MMP_DI T op_nextafter(T a_, T b_) {
+  if constexpr (sizeof(T) == 2) {
+    const unsigned short x = __builtin_bit_cast(unsigned short, a_);
+    const unsigned short y = __builtin_bit_cast(unsigned short, b_);
+    const float fx = (float)a_, fy = (float)b_;
+    if (fx != fx || fy != fy) return (T)__builtin_nanf("");
+    if (fx == fy) return b_;
+    unsigned short r;
+    if ((x & 0x7fffu) == 0) {
+      r = (unsigned short)((y & 0x8000u) | 1u);  // smallest subnormal towards y
+    } else if ((fx < fy) == !(x & 0x8000u)) {
+      r = (unsigned short)(x + 1u);  // away from zero
+    } else {
+      r = (unsigned short)(x - 1u);
+    }
+    return __builtin_bit_cast(T, r);
+  } else {
+    typedef typename mmp_t<T>::C C;
+    return (T)mm_nextafter((C)a_, (C)b_);
+  }
+}
 
 // numpy npy_logaddexp / npy_logaddexp2
 template <typename T> MMP_DI T op_logaddexp(T a_, T b_) {

@@ -29,8 +29,20 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
-constexpr long long kMinPerBlock = 16384;  // elements per workgroup slice
-constexpr long long kTargetBlocks = 2048;
+// Split policy (tuning constants, overridable at build time for sweeps):
+// at least kMinPerBlock elements per workgroup, about kTargetBlocks
+// workgroups per launch, at most kMaxSplits workgroups per row.
+#ifndef MMP_REDUCE_TARGET_BLOCKS
+#define MMP_REDUCE_TARGET_BLOCKS 2048
+#endif
+#ifndef MMP_REDUCE_UNROLL
+#define MMP_REDUCE_UNROLL 4
+#endif
+constexpr long long kMinPerBlock = 16384;
+constexpr long long kTargetBlocks = MMP_REDUCE_TARGET_BLOCKS;
+constexpr long long kMaxSplits = 16384;
+constexpr int kUnroll = MMP_REDUCE_UNROLL;   // 16-byte loads in flight per thread
+constexpr long long kSpinLimit = 1ll << 26;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 template <typename T> union Pack {
@@ -214,12 +226,12 @@ __device__ __forceinline__ typename R::A slice_reduce(const T *__restrict__ p, l
   const long long nvec = (n - head) / V;
   const u32x4 *pv = reinterpret_cast<const u32x4 *>(p + head);
   long long j = tid;
-  for (; j + 3 * kBlock < nvec; j += 4 * kBlock) {
-    Pack<T> q[4];
+  for (; j + (kUnroll - 1) * kBlock < nvec; j += kUnroll * kBlock) {
+    Pack<T> q[kUnroll];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
+    for (int u = 0; u < kUnroll; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         if (e & 1) acc1 = R::comb(acc1, R::map(q[u].e[e]));
@@ -254,12 +266,12 @@ __device__ __forceinline__ typename R::A slice_argreduce(const T *__restrict__ p
   const long long nvec = (n - head) / V;
   const u32x4 *pv = reinterpret_cast<const u32x4 *>(p + head);
   long long j = tid;
-  for (; j + 3 * kBlock < nvec; j += 4 * kBlock) {
-    Pack<T> q[4];
+  for (; j + (kUnroll - 1) * kBlock < nvec; j += kUnroll * kBlock) {
+    Pack<T> q[kUnroll];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
+    for (int u = 0; u < kUnroll; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kUnroll; ++u) {
       const long long ib = i0 + head + (j + u * kBlock) * V;
 #pragma unroll
       for (int e = 0; e < V; ++e) best = R::comb(best, A{(C)q[u].e[e], ib + e});
@@ -290,59 +302,110 @@ __device__ __forceinline__ To finalize(A a, long long len) {
   }
 }
 
-// Partials are written and read with agent-scope atomics so that the last
-// workgroup of a row never reads a stale cache line of another XCD's L2.
-// (Sub-word accumulators -- max/min of 16-bit and bool types -- use plain
-// accesses ordered by the agent-scope fences around the ticket.)
-template <typename A> __device__ __forceinline__ void put_partial(A *p, const A &v) {
-  if constexpr (sizeof(A) % 8 == 0) {
-    const unsigned long long *src = reinterpret_cast<const unsigned long long *>(&v);
-    unsigned long long *dst = reinterpret_cast<unsigned long long *>(p);
+// ------------------------------------------------ cross-workgroup words
+// Workgroups of one row exchange their partials through scratch words that
+// validate themselves: every 64-bit word holds a 32-bit call tag in its high
+// half and 32 payload bits in its low half, and is written / read with
+// RELAXED agent-scope atomics.  The reader spins until the tag matches the
+// current call.  No release/acquire fence is needed -- on multi-XCD CDNA an
+// agent-scope fence writes back / invalidates the whole L2 of the XCD, which
+// costs far more than the partial itself.
+template <typename A> constexpr int words_of() { return (int)((sizeof(A) + 3) / 4); }
+
+template <typename A>
+__device__ __forceinline__ void put_tagged(unsigned long long *slot, const A &v, unsigned tag) {
+  constexpr int W = words_of<A>();
+  unsigned buf[W] = {};
+  __builtin_memcpy(buf, &v, sizeof(A));
 #pragma unroll
-    for (int k = 0; k < (int)(sizeof(A) / 8); ++k)
-      __hip_atomic_store(dst + k, src[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else if constexpr (sizeof(A) == 4) {
-    __hip_atomic_store(reinterpret_cast<unsigned *>(p), __builtin_bit_cast(unsigned, v),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    *p = v;
-  }
-}
-template <typename A> __device__ __forceinline__ A get_partial(const A *p) {
-  if constexpr (sizeof(A) % 8 == 0) {
-    A v;
-    unsigned long long *dst = reinterpret_cast<unsigned long long *>(&v);
-    const unsigned long long *src = reinterpret_cast<const unsigned long long *>(p);
-#pragma unroll
-    for (int k = 0; k < (int)(sizeof(A) / 8); ++k)
-      dst[k] = __hip_atomic_load(src + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return v;
-  } else if constexpr (sizeof(A) == 4) {
-    return __builtin_bit_cast(A, __hip_atomic_load(reinterpret_cast<const unsigned *>(p),
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  } else {
-    return *p;
-  }
+  for (int k = 0; k < W; ++k)
+    __hip_atomic_store(slot + k, ((unsigned long long)tag << 32) | buf[k], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Last-arrival combine.  Returns true in the block that must finish the
-// row; its thread 0 then holds the combined value in `out`.
+// Spins (bounded) until every word of the slot carries `tag`.
+template <typename A>
+__device__ __forceinline__ A get_tagged(const unsigned long long *slot, unsigned tag,
+                                        unsigned *timeout) {
+  constexpr int W = words_of<A>();
+  unsigned buf[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    unsigned long long w;
+    long long spins = 0;
+    while (((w = __hip_atomic_load(slot + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
+           tag) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    buf[k] = (unsigned)w;
+  }
+  A v;
+  __builtin_memcpy(&v, buf, sizeof(A));
+  return v;
+}
+
+struct ReduceScratch {
+  unsigned long long *words;  // tagged partial words
+  unsigned *tickets;          // arrival counters (left at 0)
+  unsigned *timeout;          // set to 1 if a wait ran out
+  unsigned tag;               // this call's generation
+};
+
+// Last-arrival combine of the S partials of one row.  Returns true in the
+// workgroup that finishes the row; its thread 0 then holds the result in
+// *out.  Partials are combined in index order (deterministic).
 template <typename R>
-__device__ bool last_block_combine(typename R::A v, typename R::A *partials, unsigned *ticket,
-                                   int S, int s, typename R::A *out, typename R::A *lds) {
+__device__ bool last_block_combine(typename R::A v, unsigned long long *words, unsigned *ticket,
+                                   int S, int s, const ReduceScratch &sc, typename R::A *out,
+                                   typename R::A *lds) {
+  typedef typename R::A A;
+  constexpr int W = words_of<A>();
   __shared__ int is_last;
   if (threadIdx.x == 0) {
-    put_partial(partials + s, v);
-    __threadfence();
-    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    put_tagged(words + (long long)s * W, v, sc.tag);
+    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = (t == (unsigned)(S - 1));
   }
   __syncthreads();
   if (!is_last) return false;
-  __threadfence();
-  typename R::A acc = R::ident();
-  // fixed order: thread k combines partials k, k+256, ... then the tree
-  for (int k = threadIdx.x; k < S; k += kBlock) acc = R::comb(acc, get_partial(partials + k));
+  // Issue the loads of kBatch partials before validating any of them, so
+  // the last workgroup pays the atomic-load latency once per batch.
+  constexpr int kBatch = 8;
+  A acc = R::ident();
+  for (int k0 = threadIdx.x; k0 < S; k0 += kBlock * kBatch) {
+    unsigned long long w[kBatch][W];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = k0 + b * kBlock;
+#pragma unroll
+      for (int j = 0; j < W; ++j)
+        w[b][j] = k < S ? __hip_atomic_load(words + (long long)k * W + j, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT)
+                        : 0ull;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = k0 + b * kBlock;
+      if (k >= S) break;
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < W; ++j) ok = ok && (unsigned)(w[b][j] >> 32) == sc.tag;
+      A part;
+      if (ok) {
+        unsigned buf[W];
+#pragma unroll
+        for (int j = 0; j < W; ++j) buf[j] = (unsigned)w[b][j];
+        __builtin_memcpy(&part, buf, sizeof(A));
+      } else {
+        part = get_tagged<A>(words + (long long)k * W, sc.tag, sc.timeout);
+      }
+      acc = R::comb(acc, part);
+    }
+  }
   __syncthreads();
   acc = block_reduce<R>(acc, lds);
   if (threadIdx.x == 0) {
@@ -353,12 +416,10 @@ __device__ bool last_block_combine(typename R::A v, typename R::A *partials, uns
 }
 
 // ---------------------------------------------------------- kernels
-// Rows: grid = rows * S; block (row, s) reduces slice s of its row.
+// Rows: grid = rows * S; workgroup (row, s) reduces slice s of its row.
 template <int OP, typename T, typename To>
 __global__ __launch_bounds__(kBlock) void k_reduce_rows(const T *__restrict__ x, To *__restrict__ out,
-                                                       long long len, int S,
-                                                       typename Red<OP, T>::A *partials,
-                                                       unsigned *tickets) {
+                                                       long long len, int S, ReduceScratch sc) {
   typedef Red<OP, T> R;
   typedef typename R::A A;
   __shared__ A lds[kWaves];
@@ -376,7 +437,8 @@ __global__ __launch_bounds__(kBlock) void k_reduce_rows(const T *__restrict__ x,
   }
   A total;
   __syncthreads();
-  if (last_block_combine<R>(v, partials + row * S, tickets + row, S, s, &total, lds) &&
+  if (last_block_combine<R>(v, sc.words + row * S * words_of<A>(), sc.tickets + row, S, s, sc,
+                            &total, lds) &&
       threadIdx.x == 0)
     out[row] = finalize<OP, T, To>(total, len);
 }
@@ -384,9 +446,7 @@ __global__ __launch_bounds__(kBlock) void k_reduce_rows(const T *__restrict__ x,
 template <int OP, typename T>
 __global__ __launch_bounds__(kBlock) void k_argreduce_rows(const T *__restrict__ x,
                                                           long long *__restrict__ out,
-                                                          long long len, int S,
-                                                          typename Arg<OP, T>::A *partials,
-                                                          unsigned *tickets) {
+                                                          long long len, int S, ReduceScratch sc) {
   typedef Arg<OP, T> R;
   typedef typename R::A A;
   __shared__ A lds[kWaves];
@@ -404,7 +464,8 @@ __global__ __launch_bounds__(kBlock) void k_argreduce_rows(const T *__restrict__
   }
   A total;
   __syncthreads();
-  if (last_block_combine<R>(v, partials + row * S, tickets + row, S, s, &total, lds) &&
+  if (last_block_combine<R>(v, sc.words + row * S * words_of<A>(), sc.tickets + row, S, s, sc,
+                            &total, lds) &&
       threadIdx.x == 0)
     out[row] = total.i;
 }
@@ -413,10 +474,10 @@ __global__ __launch_bounds__(kBlock) void k_argreduce_rows(const T *__restrict__
 template <int OP, typename T, typename To>
 __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x, To *__restrict__ out,
                                                        long long len, long long inner, int S,
-                                                       typename Red<OP, T>::A *partials,
-                                                       unsigned *tickets) {
+                                                       ReduceScratch sc) {
   typedef Red<OP, T> R;
   typedef typename R::A A;
+  constexpr int W = words_of<A>();
   const long long o = blockIdx.y;
   const int s = blockIdx.z;
   const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
@@ -432,29 +493,26 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x,
     if (c < inner) out[o * inner + c] = finalize<OP, T, To>(v, len);
     return;
   }
-  // partial per (o, c, s); ticket per (o, column block)
+  // one tagged partial per (o, column block, s, thread); ticket per (o, cb)
   const long long cb = blockIdx.x, ncb = gridDim.x;
-  A *mine = partials + ((o * ncb + cb) * S + s) * kBlock;
-  if (c < inner) put_partial(mine + threadIdx.x, v);
+  unsigned long long *grp = sc.words + (o * ncb + cb) * (long long)S * kBlock * W;
+  put_tagged(grp + ((long long)s * kBlock + threadIdx.x) * W, v, sc.tag);
   __shared__ int is_last;
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned t = __hip_atomic_fetch_add(tickets + o * ncb + cb, 1u, __ATOMIC_ACQ_REL,
+    const unsigned t = __hip_atomic_fetch_add(sc.tickets + o * ncb + cb, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
     is_last = (t == (unsigned)(S - 1));
   }
   __syncthreads();
   if (!is_last) return;
-  __threadfence();
-  if (c < inner) {
-    A acc = R::ident();
-    const A *base = partials + (o * ncb + cb) * S * kBlock + threadIdx.x;
-    for (int k = 0; k < S; ++k) acc = R::comb(acc, get_partial(base + k * kBlock));
-    out[o * inner + c] = finalize<OP, T, To>(acc, len);
-  }
+  A acc = R::ident();
+  for (int k = 0; k < S; ++k)
+    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.tag,
+                                     sc.timeout));
+  if (c < inner) out[o * inner + c] = finalize<OP, T, To>(acc, len);
   if (threadIdx.x == 0)
-    __hip_atomic_store(tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int OP, typename T>
@@ -479,28 +537,38 @@ int choose_splits(long long rows, long long len) {
   long long maxs = (len + kMinPerBlock - 1) / kMinPerBlock;
   long long s = want < maxs ? want : maxs;
   if (s < 1) s = 1;
-  if (s > 4096) s = 4096;
+  if (s > kMaxSplits) s = kMaxSplits;
   return (int)s;
+}
+
+// Scratch for `count` tagged partials of type A plus `nticket` tickets.
+template <typename A>
+int reduce_scratch(long long count, long long nticket, ReduceScratch *sc) {
+  int st = MMP_OK;
+  sc->words = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS,
+                                                  8ull * words_of<A>() * count, &st);
+  if (st) return st;
+  sc->tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4ull * nticket, &st);
+  if (st) return st;
+  sc->timeout = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st) + 2;
+  if (st) return st;
+  sc->tag = mmpi::next_generation();
+  return MMP_OK;
 }
 
 template <int OP, typename T, typename To>
 int launch_reduce(long long outer, long long len, long long inner, const void *x, void *out) {
   typedef typename Red<OP, T>::A A;
-  int st = MMP_OK;
+  ReduceScratch sc{};
   if (inner == 1) {
     const int S = choose_splits(outer, len);
-    A *partials = nullptr;
-    unsigned *tickets = nullptr;
     if (S > 1) {
-      partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS, sizeof(A) * outer * S, &st);
-      if (st) return st;
-      tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer, &st);
-      if (st) return st;
+      if (int st = reduce_scratch<A>(outer * S, outer, &sc)) return st;
     }
     const long long grid = outer * S;
     if (grid > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "reduction grid too large");
     hipLaunchKernelGGL((k_reduce_rows<OP, T, To>), dim3((unsigned)grid), dim3(kBlock), 0,
-                       mmpi::stream(), (const T *)x, (To *)out, len, S, partials, tickets);
+                       mmpi::stream(), (const T *)x, (To *)out, len, S, sc);
     return mmpi::check_launch("mmp_reduce(rows)");
   }
   const long long ncb = mmpi::ceil_div(inner, kBlock);
@@ -510,39 +578,27 @@ int launch_reduce(long long outer, long long len, long long inner, const void *x
   int S = (int)(want < maxs ? want : maxs);
   if (S < 1) S = 1;
   if (S > 1024) S = 1024;
-  A *partials = nullptr;
-  unsigned *tickets = nullptr;
   if (S > 1) {
-    partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS,
-                                  sizeof(A) * outer * ncb * S * kBlock, &st);
-    if (st) return st;
-    tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer * ncb, &st);
-    if (st) return st;
+    if (int st = reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)) return st;
   }
   hipLaunchKernelGGL((k_reduce_cols<OP, T, To>), dim3((unsigned)ncb, (unsigned)outer, (unsigned)S),
-                     dim3(kBlock), 0, mmpi::stream(), (const T *)x, (To *)out, len, inner, S,
-                     partials, tickets);
+                     dim3(kBlock), 0, mmpi::stream(), (const T *)x, (To *)out, len, inner, S, sc);
   return mmpi::check_launch("mmp_reduce(cols)");
 }
 
 template <int OP, typename T>
 int launch_argreduce(long long outer, long long len, long long inner, const void *x, long long *out) {
   typedef typename Arg<OP, T>::A A;
-  int st = MMP_OK;
+  ReduceScratch sc{};
   if (inner == 1) {
     const int S = choose_splits(outer, len);
-    A *partials = nullptr;
-    unsigned *tickets = nullptr;
     if (S > 1) {
-      partials = (A *)mmpi::scratch(mmpi::SCRATCH_REDUCE_PARTIALS, sizeof(A) * outer * S, &st);
-      if (st) return st;
-      tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4 * outer, &st);
-      if (st) return st;
+      if (int st = reduce_scratch<A>(outer * S, outer, &sc)) return st;
     }
     const long long grid = outer * S;
     if (grid > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "reduction grid too large");
     hipLaunchKernelGGL((k_argreduce_rows<OP, T>), dim3((unsigned)grid), dim3(kBlock), 0,
-                       mmpi::stream(), (const T *)x, out, len, S, partials, tickets);
+                       mmpi::stream(), (const T *)x, out, len, S, sc);
     return mmpi::check_launch("mmp_argreduce(rows)");
   }
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided argreduce: outer extent %lld > 65535", outer);

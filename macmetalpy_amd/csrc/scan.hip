@@ -13,11 +13,11 @@
 //    loads, scanned serially per thread in the accumulator type, then across
 //    the wave64 with shuffles and across the 4 waves through LDS;
 //  * thread 0 publishes the tile aggregate, walks back over predecessors'
-//    published aggregates / inclusive prefixes (agent-scope acquire /
-//    release), then publishes its own inclusive prefix;
-//  * tile flags carry a per-call generation number, so the flag array is
-//    never cleared between calls; waits are bounded and a timeout is
-//    recorded instead of hanging.
+//    published aggregates / inclusive prefixes, then publishes its own
+//    inclusive prefix;
+//  * descriptors carry a per-call generation tag, so they are never
+//    cleared between calls; waits are bounded and a timeout is recorded
+//    instead of hanging.
 // Accumulators: int64 for integers (int32 -> int64 output as NumPy),
 // float64 for floats (rounded once per output element).  HBM-bound:
 // sizeof(in) + sizeof(out) bytes per element.
@@ -69,24 +69,24 @@ template <typename A> __device__ __forceinline__ A shfl_up64(A v, int d) {
   return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
 }
 
-template <typename A> __device__ __forceinline__ void store_agent(A *p, A v, int order) {
-  unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-  if (order == __ATOMIC_RELEASE)
-    __hip_atomic_store((unsigned long long *)p, u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-  else
-    __hip_atomic_store((unsigned long long *)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename A> __device__ __forceinline__ A load_agent(const A *p) {
-  return __builtin_bit_cast(A, __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT));
+// Tile descriptors are two 64-bit words, each = (tag << 32) | 32 payload
+// bits, tag = generation << 2 | state (1 aggregate, 2 inclusive prefix).
+// They are written and read with RELAXED agent-scope atomics; a reader only
+// accepts a descriptor whose two tags agree and carry this call's
+// generation.  No release/acquire fences: on multi-XCD CDNA those write
+// back / invalidate the whole L2 and would serialise the look-back.
+template <typename A>
+__device__ __forceinline__ void publish(unsigned long long *d, A v, unsigned tag) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const unsigned long long hi = (unsigned long long)tag << 32;
+  __hip_atomic_store(d, hi | (u & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(d + 1, hi | (u >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct ScanScratch {
-  unsigned *counter;   // tile ticket (left at 0 by the last tile)
-  unsigned *flags;     // per tile: generation << 2 | state (1 aggregate, 2 inclusive)
-  void *aggr;          // per tile aggregate
-  void *incl;          // per tile inclusive prefix
-  unsigned *timeout;   // set to 1 if a look-back wait ran out
+  unsigned *counter;          // tile ticket (left at 0 by the last tile)
+  unsigned long long *desc;   // 2 words per tile
+  unsigned *timeout;          // set to 1 if a look-back wait ran out
 };
 
 template <int OP, typename Ti, typename To>
@@ -171,16 +171,16 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
   // 4. decoupled look-back (thread 0)
   if (tid == 0) {
     A prefix = S::ident();
-    A *aggr = reinterpret_cast<A *>(sc.aggr);
-    A *incl = reinterpret_cast<A *>(sc.incl);
+    unsigned long long *d = sc.desc;
     if (t > 0) {
-      store_agent(aggr + tile, total, __ATOMIC_RELAXED);
-      __hip_atomic_store(sc.flags + tile, (gen << 2) | 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      publish(d + 2 * tile, total, (gen << 2) | 1u);
       long long j = tile - 1;
       long long spins = 0;
       while (true) {
-        const unsigned f = __hip_atomic_load(sc.flags + j, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        if ((f >> 2) != gen) {
+        const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
+        if (t0 != t1 || (t0 >> 2) != gen) {
           if (++spins > kSpinLimit) {
             __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
@@ -188,16 +188,13 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
           __builtin_amdgcn_s_sleep(1);
           continue;
         }
-        if ((f & 3u) == 2u) {
-          prefix = S::comb(load_agent(incl + j), prefix);
-          break;
-        }
-        prefix = S::comb(load_agent(aggr + j), prefix);
+        const A val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
+        prefix = S::comb(val, prefix);
+        if ((t0 & 3u) == 2u) break;
         --j;  // the row's first tile always publishes an inclusive prefix
       }
     }
-    store_agent(incl + tile, S::comb(prefix, total), __ATOMIC_RELAXED);
-    __hip_atomic_store(sc.flags + tile, (gen << 2) | 2u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
     s_prefix = prefix;
   }
   __syncthreads();  // also: every thread has read its inputs from `stage`
@@ -263,12 +260,8 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
       sc.counter = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st);
       if (st) return st;
       sc.timeout = sc.counter + 1;
-      sc.flags = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_FLAGS, 4 * ntiles, &st);
+      sc.desc = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES, 16ull * ntiles, &st);
       if (st) return st;
-      char *vals = (char *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES, 2 * sizeof(A) * ntiles, &st);
-      if (st) return st;
-      sc.aggr = vals;
-      sc.incl = vals + sizeof(A) * ntiles;
       const unsigned gen = mmpi::next_generation();
       hipLaunchKernelGGL((k_scan_rows<OP, Ti, To>), dim3((unsigned)ntiles), dim3(kBlock), 0,
                          mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);

@@ -324,6 +324,32 @@ def _env(be):
     return info
 
 
+ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32")
+
+
+def run_only(cp, be, name, steps):
+    """One op of the headline workload, `steps` launches (for counter
+    profiling); copy_f32 is a plain strided-copy kernel of 2^28 floats
+    (1 GiB read + 1 GiB written) used to calibrate the byte counters."""
+    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    if name in ("add_f32", "sin_f32", "copy_f32"):
+        a, b = (cp.array(x) for x in c2_float_inputs(N28))
+    else:
+        a, b = (cp.array(x) for x in c2_int_inputs(N28))
+    a._ensure_gpu()
+    b._ensure_gpu()
+    fn = {"add_f32": lambda: a + b, "sin_f32": lambda: cp.sin(a),
+          "floor_divide_i32": lambda: cp.floor_divide(a, b), "mod_i32": lambda: cp.mod(a, b),
+          "copy_f32": lambda: a.copy()}[name]
+    timer = EventTimer(be)
+    for _ in range(steps):
+        timer.run(name, lambda: _mat(fn()))
+    cp.synchronize()
+    ms, _ = timer.ms(name)
+    timer.close()
+    print(json.dumps({"only": name, "steps": steps, "kernel_ms": round(ms, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +358,8 @@ def main():
     ap.add_argument("--suite", choices=["all", "headline"], default="all")
     ap.add_argument("--cpu-sample-log2", type=int, default=25)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=ONLY_OPS, default=None,
+                    help="run one headline op `--steps` times and exit (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -341,6 +369,9 @@ def main():
     import macmetalpy_amd as cp
     from macmetalpy_amd._backend import HipBackend
     be = HipBackend()
+    if args.only:
+        run_only(cp, be, args.only, args.steps)
+        return
 
     c2 = bench_c2(cp, be, args.steps, args.warmup)
     per_op = c2["per_op"]

@@ -502,7 +502,7 @@ template <typename T> MMP_DI T op_nextafter(T a_, T b_) {
     const unsigned short y = __builtin_bit_cast(unsigned short, b_);
     const float fx = (float)a_, fy = (float)b_;
     if (fx != fx || fy != fy) return (T)__builtin_nanf("");
-    if (fx == fy) return b_;
+    if (fx == fy) return a_;  // npy_half_nextafter keeps x (also for -0 vs +0)
     unsigned short r;
     if ((x & 0x7fffu) == 0) {
       r = (unsigned short)((y & 0x8000u) | 1u);  // smallest subnormal towards y

@@ -33,10 +33,10 @@ constexpr int kWaves = kBlock / 64;
 // at least kMinPerBlock elements per workgroup, about kTargetBlocks
 // workgroups per launch, at most kMaxSplits workgroups per row.
 #ifndef MMP_REDUCE_TARGET_BLOCKS
-#define MMP_REDUCE_TARGET_BLOCKS 2048
+#define MMP_REDUCE_TARGET_BLOCKS 1024
 #endif
 #ifndef MMP_REDUCE_UNROLL
-#define MMP_REDUCE_UNROLL 4
+#define MMP_REDUCE_UNROLL 8
 #endif
 constexpr long long kMinPerBlock = 16384;
 constexpr long long kTargetBlocks = MMP_REDUCE_TARGET_BLOCKS;

@@ -68,15 +68,30 @@ def test_exact_unary(op, dtype):
     _bits_equal(_dev_unary(op, x), ref.unary(op, x))
 
 
+# float32 ops evaluated through float64 on the device (<= 1 ULP of exact);
+# NumPy's own float32 results for these are up to 3 ULP from exact.
+VIA_F64 = {"exp2_op", "log10_op", "asin_op", "acos_op", "atan2_op"}
+
+
+def _check_f32_ulp(op, got, want_np, want_cr, check_cr=True):
+    d_np = ref.ulp_distance(got, want_np)
+    d_cr = ref.ulp_distance(got, want_cr)
+    if op in VIA_F64:
+        assert int(d_cr.max()) <= 1
+        np_err = ref.ulp_distance(want_np, want_cr)
+        assert np.all(d_np <= np.maximum(2, np_err + 1))
+    else:
+        assert int(d_np.max()) <= 2
+        if check_cr:
+            assert int(d_cr.max()) <= 2
+
+
 @pytest.mark.parametrize("op,fn64,dom", TRANSCENDENTAL)
 def test_transcendental_f32_ulp(op, fn64, dom):
     x = np.random.default_rng(1).uniform(*dom, 200000).astype(np.float32)
     x = np.concatenate([x, SPECIALS32])
     got = _dev_unary(op, x)
-    want_np = ref.unary(op, x)
-    want_cr = ref.correctly_rounded(fn64, x)
-    assert int(ref.ulp_distance(got, want_np).max()) <= 2
-    assert int(ref.ulp_distance(got, want_cr).max()) <= 2
+    _check_f32_ulp(op, got, ref.unary(op, x), ref.correctly_rounded(fn64, x))
 
 
 @pytest.mark.parametrize("op,fn64,dom", TRANSCENDENTAL[:12])
@@ -109,7 +124,11 @@ def test_binary_transcendental_f32(op):
     b = (g.standard_normal(100000) * 3).astype(np.float32)
     got = _dev_binary(op, a, b)
     want = ref.binary(op, a, b)
-    assert int(ref.ulp_distance(got, want).max()) <= 2
+    fn64 = {"pow_op": np.power, "atan2_op": np.arctan2, "hypot_op": np.hypot,
+            "logaddexp_op": np.logaddexp, "logaddexp2_op": np.logaddexp2}[op]
+    with np.errstate(all="ignore"):
+        cr = fn64(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    _check_f32_ulp(op, got, want, cr, check_cr=False)
 
 
 INT_EDGE = np.array([0, 1, -1, 2, -2, 7, -7, 100, -100, 2 ** 31 - 1, -2 ** 31,

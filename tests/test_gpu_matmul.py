@@ -1,0 +1,110 @@
+"""Matmul on the GPU (MFMA) against the oracle.  Bars (normwise, against a
+float64 product of the same inputs): 1e-4 for float32, 1e-2 for float16,
+1e-12 for float64; integer products bit-exact (wrapping, as NumPy)."""
+import numpy as np
+import pytest
+
+import macmetalpy_amd as cp
+from macmetalpy_amd.workloads import c4_inputs
+from oracle import reference_cpu as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float32: 1e-4, np.float16: 1e-2, np.float64: 1e-12}
+
+
+def _check(a, b, got, dtype):
+    want = ref.matmul_f64(a, b)
+    assert got.dtype == np.dtype(dtype)
+    assert got.shape == want.shape
+    err = ref.normwise_rel_error(got, want)
+    assert err <= TOL[dtype], err
+    # elementwise: |C - C_ref| <= tol * (|A| @ |B|)
+    bound = np.matmul(np.abs(np.asarray(a, np.float64)), np.abs(np.asarray(b, np.float64)))
+    assert np.all(np.abs(got.astype(np.float64) - want) <= TOL[dtype] * bound + 1e-30)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.float64])
+@pytest.mark.parametrize("mnk", [(128, 128, 64), (256, 384, 128), (65, 130, 47), (1, 1, 1),
+                                 (300, 5, 700), (7, 257, 3)])
+def test_matmul_2d(dtype, mnk):
+    m, n, k = mnk
+    g = np.random.default_rng(m * 7 + n)
+    a = (g.standard_normal((m, k)) / np.sqrt(k)).astype(dtype)
+    b = (g.standard_normal((k, n)) / np.sqrt(k)).astype(dtype)
+    got = (cp.array(a) @ cp.array(b)).get()
+    _check(a, b, got, dtype)
+
+
+def test_matmul_mfma_layout_known_answer():
+    """Integer-valued operands make every product exact in fp32, so the
+    MFMA fragment layout (row / column / k mapping) must reproduce NumPy
+    exactly."""
+    g = np.random.default_rng(0)
+    for dtype in (np.float32, np.float16, np.float64):
+        a = g.integers(-3, 4, (128, 64)).astype(dtype)
+        b = g.integers(-3, 4, (64, 128)).astype(dtype)
+        got = (cp.array(a) @ cp.array(b)).get()
+        assert np.array_equal(got.astype(np.float64), a.astype(np.float64) @ b.astype(np.float64)), dtype
+    e = np.eye(128, dtype=np.float32)
+    m = g.standard_normal((128, 128)).astype(np.float32)
+    assert np.array_equal((cp.array(m) @ cp.array(e)).get(), m)
+    assert np.array_equal((cp.array(e) @ cp.array(m)).get(), m)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64, np.int16, np.uint32])
+def test_matmul_integer_exact(dtype):
+    g = np.random.default_rng(1)
+    a = g.integers(-1000 if np.dtype(dtype).kind == "i" else 0, 1000, (70, 300)).astype(dtype)
+    b = g.integers(-1000 if np.dtype(dtype).kind == "i" else 0, 1000, (300, 45)).astype(dtype)
+    got = (cp.array(a) @ cp.array(b)).get()
+    want = np.matmul(a, b)
+    assert got.dtype == want.dtype and np.array_equal(got, want)
+
+
+def test_matmul_batched_broadcast_and_1d():
+    g = np.random.default_rng(2)
+    a = g.standard_normal((3, 128, 96)).astype(np.float32)
+    b = g.standard_normal((3, 96, 64)).astype(np.float32)
+    _check(a, b, cp.matmul(cp.array(a), cp.array(b)).get(), np.float32)
+    _check(a, b, (cp.array(a) @ cp.array(b)).get(), np.float32)    # 3-D @ (NumPy semantics)
+    b2 = g.standard_normal((96, 64)).astype(np.float32)              # broadcast B
+    _check(a, b2, cp.matmul(cp.array(a), cp.array(b2)).get(), np.float32)
+    a4 = g.standard_normal((2, 1, 40, 30)).astype(np.float32)
+    b4 = g.standard_normal((3, 30, 20)).astype(np.float32)
+    got = cp.matmul(cp.array(a4), cp.array(b4)).get()
+    assert got.shape == (2, 3, 40, 20)
+    assert ref.normwise_rel_error(got, ref.matmul_f64(a4, b4)) <= 1e-4
+    v = g.standard_normal(96).astype(np.float32)
+    m = g.standard_normal((96, 50)).astype(np.float32)
+    assert ref.normwise_rel_error((cp.array(v) @ cp.array(m)).get(), v.astype(np.float64) @ m) <= 1e-5
+    assert ref.normwise_rel_error((cp.array(m.T) @ cp.array(v)).get(), m.T.astype(np.float64) @ v) <= 1e-5
+    # tests/test_error_handling.py:107-114: 1-D @ 1-D inner product
+    x = np.arange(3, dtype=np.float32)
+    assert float((cp.array(x) @ cp.array(x)).get()) == 5.0
+    assert ref.normwise_rel_error(cp.linalg.matmul(cp.array(m.T), cp.array(m)).get(),
+                                  m.T.astype(np.float64) @ m) <= 1e-4
+    assert ref.normwise_rel_error(cp.dot(cp.array(m.T), cp.array(m)).get(),
+                                  m.T.astype(np.float64) @ m) <= 1e-4
+
+
+def test_matmul_shape_mismatch_message():
+    # tests/test_error_handling.py:100-105
+    with pytest.raises(ValueError, match="shape mismatch"):
+        cp.zeros((2, 3), dtype=cp.float32) @ cp.zeros((4, 5), dtype=cp.float32)
+
+
+@pytest.mark.parametrize("kind,dtype", [("f32", np.float32), ("f16", np.float16),
+                                        ("batched", np.float32)])
+def test_c4_full_size_sampled(kind, dtype):
+    a, b = c4_inputs(kind)
+    got = (cp.array(a) @ cp.array(b)).get()
+    assert got.dtype == np.dtype(dtype)
+    rows = np.random.default_rng(3).choice(a.shape[-2], 64, replace=False)
+    if a.ndim == 3:
+        for bi in (0, 31, 63):
+            want = ref.matmul_f64(a[bi][rows], b[bi])
+            assert ref.normwise_rel_error(got[bi][rows], want) <= TOL[dtype]
+    else:
+        want = ref.matmul_f64(a[rows], b)
+        assert ref.normwise_rel_error(got[rows], want) <= TOL[dtype]

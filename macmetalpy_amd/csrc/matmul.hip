@@ -183,18 +183,23 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm16(const T *__restrict__ A,
 }
 
 // ------------------------------------------------------ fp32 / fp64
+// Output element r of lane group g (= lane / 16) holds tile row
+// 4*g + r for the fp32 MFMA but g + 4*r for the fp64 one (measured on
+// gfx950 with a single-wave probe); the column is lane % 16 for both.
 template <typename T> struct Mfma4;
 template <> struct Mfma4<float> {
   typedef f4 acc_t;
   static __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
+  static __device__ __forceinline__ int out_row(int g, int r) { return 4 * g + r; }
 };
 template <> struct Mfma4<double> {
   typedef d4 acc_t;
   static __device__ __forceinline__ d4 mfma(double a, double b, d4 c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
+  static __device__ __forceinline__ int out_row(int g, int r) { return g + 4 * r; }
 };
 
 template <typename T, bool EDGE>
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm4(const T *__restrict__ A, co
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + i * 16 + g * 4 + r;
+        const int row = m0 + wm * 64 + i * 16 + Mfma4<T>::out_row(g, r);
         const int col = n0 + wn * 64 + j * 16 + fr;
         if (!EDGE || (row < M && col < N)) Cb[(long long)row * ldc + col] = acc[i][j][r];
       }

@@ -9,12 +9,13 @@
 //  * workgroups take tile ids from an atomic counter in launch order, so a
 //    tile only ever waits for tiles that are already running (AMD gives no
 //    forward-progress guarantee to workgroups that have not started);
-//  * a tile (256 threads x 16 elements) is staged through LDS with 128-bit
-//    loads, scanned serially per thread in the accumulator type, then across
-//    the wave64 with shuffles and across the 4 waves through LDS;
-//  * thread 0 publishes the tile aggregate, walks back over predecessors'
-//    published aggregates / inclusive prefixes, then publishes its own
-//    inclusive prefix;
+//  * a tile (16384 elements: 4 sub-tiles of 256 threads x 16 consecutive
+//    elements) is staged through LDS with 128-bit loads into registers,
+//    scanned serially per thread in the accumulator type, then across the
+//    wave64 with shuffles and across the 4 waves through LDS;
+//  * wave 0 publishes the tile aggregate, reads the 64 nearest
+//    predecessors' descriptors at once and combines aggregates up to the
+//    nearest inclusive prefix, then publishes its own inclusive prefix;
 //  * descriptors carry a per-call generation tag, so they are never
 //    cleared between calls; waits are bounded and a timeout is recorded
 //    instead of hanging.
@@ -29,10 +30,15 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kItems = 16;
-constexpr int kTile = kBlock * kItems;
-constexpr int kPad = kTile / kItems;   // one pad word per thread row in LDS
+constexpr int kItems = 16;                // consecutive elements per thread per sub-tile
+constexpr int kSubTile = kBlock * kItems; // 4096 elements staged through LDS at a time
+constexpr int kPad = kSubTile / kItems;   // one pad word per thread row in LDS
 constexpr long long kSpinLimit = 1ll << 26;
+// A tile (one ticket, one look-back) is kSub sub-tiles: 16384 elements for
+// 1-, 2- and 4-byte inputs, 8192 for 8-byte inputs (register budget).  A
+// same-address atomic ticket costs ~11 ns per workgroup on MI355X and the
+// tickets serialise, so tiles must be large.
+template <typename Ti> constexpr int sub_tiles() { return sizeof(Ti) >= 8 ? 2 : 4; }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -62,6 +68,12 @@ template <int OP, typename T> struct ScanOp {
 };
 
 __device__ __forceinline__ int padded(int i) { return i + i / kItems; }
+
+template <typename A> __device__ __forceinline__ A shfl_xor64(A v, int m) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  unsigned lo = __shfl_xor((unsigned)u, m, 64), hi = __shfl_xor((unsigned)(u >> 32), m, 64);
+  return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
+}
 
 template <typename A> __device__ __forceinline__ A shfl_up64(A v, int d) {
   unsigned long long u = __builtin_bit_cast(unsigned long long, v);
@@ -96,9 +108,11 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
                                                      unsigned gen) {
   typedef ScanOp<OP, Ti> S;
   typedef typename S::A A;
+  constexpr int Q = sub_tiles<Ti>();
+  constexpr int kTile = Q * kSubTile;
   constexpr int kStage = (sizeof(Ti) > sizeof(To) ? sizeof(Ti) : sizeof(To));
-  __shared__ __attribute__((aligned(16))) unsigned char stage[(kTile + kPad) * kStage];
-  __shared__ A wsum[kBlock / 64];
+  __shared__ __attribute__((aligned(16))) unsigned char stage[(kSubTile + kPad) * kStage];
+  __shared__ A wsum[Q][kBlock / 64];
   __shared__ A s_prefix;
   __shared__ unsigned s_tile;
   Ti *sx = reinterpret_cast<Ti *>(stage);
@@ -123,103 +137,152 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
   const Ti *xr = x + row * len + base;
   To *yr = y + row * len + base;
 
-  // 1. stage the tile (128-bit loads when whole and aligned)
+  // 1. stage each sub-tile through LDS (128-bit loads when whole and
+  //    aligned); each thread keeps its 16 consecutive inputs in registers
   constexpr int VI = 16 / sizeof(Ti);
-  if (n == kTile && ((uintptr_t)xr & 15u) == 0) {
-    const u32x4 *xv = reinterpret_cast<const u32x4 *>(xr);
+  Ti xin[Q][kItems];
 #pragma unroll
-    for (int k = 0; k < kTile / VI / kBlock; ++k) {
-      const int vi = k * kBlock + tid;
-      union { u32x4 v; Ti e[VI]; } q;
-      q.v = __builtin_nontemporal_load(xv + vi);
+  for (int q = 0; q < Q; ++q) {
+    const int qb = q * kSubTile;
+    const int qn = n - qb < 0 ? 0 : (n - qb < kSubTile ? n - qb : kSubTile);
+    if (q) __syncthreads();
+    if (qn == kSubTile && ((uintptr_t)(xr + qb) & 15u) == 0) {
+      const u32x4 *xv = reinterpret_cast<const u32x4 *>(xr + qb);
 #pragma unroll
-      for (int e = 0; e < VI; ++e) sx[padded(vi * VI + e)] = q.e[e];
+      for (int k = 0; k < kSubTile / VI / kBlock; ++k) {
+        const int vi = k * kBlock + tid;
+        union { u32x4 v; Ti e[VI]; } u;
+        u.v = __builtin_nontemporal_load(xv + vi);
+#pragma unroll
+        for (int e = 0; e < VI; ++e) sx[padded(vi * VI + e)] = u.e[e];
+      }
+    } else {
+      for (int i = tid; i < qn; i += kBlock) sx[padded(i)] = xr[qb + i];
     }
-  } else {
-    for (int i = tid; i < n; i += kBlock) sx[padded(i)] = xr[i];
-  }
-  __syncthreads();
-
-  // 2. per-thread serial scan of 16 consecutive elements
-  A v[kItems];
-  A run = S::ident();
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const int i = tid * kItems + j;
-    const A val = i < n ? S::map(sx[padded(i)]) : S::ident();
-    run = S::comb(run, val);
-    v[j] = run;
-  }
-  // 3. block scan of thread totals: wave64 shuffles, then wave totals
-  A inc = run;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const A o = shfl_up64(inc, d);
-    if (lane >= d) inc = S::comb(o, inc);
-  }
-  A excl = shfl_up64(inc, 1);
-  if (lane == 0) excl = S::ident();
-  if (lane == 63) wsum[wave] = inc;
-  __syncthreads();
-  A wpre = S::ident(), total = S::ident();
-#pragma unroll
-  for (int w = 0; w < kBlock / 64; ++w) {
-    if (w < wave) wpre = S::comb(wpre, wsum[w]);
-    total = S::comb(total, wsum[w]);
+    for (int j = 0; j < kItems; ++j) {
+      const int i = tid * kItems + j;
+      xin[q][j] = i < qn ? sx[padded(i)] : (Ti)0;
+    }
   }
 
-  // 4. decoupled look-back (thread 0)
-  if (tid == 0) {
+  // 2. per-thread totals of each sub-tile, block scans across threads
+  //    (wave64 shuffles, then the 4 wave totals through LDS)
+  A excl[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int qn = n - q * kSubTile;
+    A run = S::ident();
+#pragma unroll
+    for (int j = 0; j < kItems; ++j)
+      if (tid * kItems + j < qn) run = S::comb(run, S::map(xin[q][j]));
+    A inc = run;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const A o = shfl_up64(inc, d);
+      if (lane >= d) inc = S::comb(o, inc);
+    }
+    A ex = shfl_up64(inc, 1);
+    if (lane == 0) ex = S::ident();
+    excl[q] = ex;
+    if (lane == 63) wsum[q][wave] = inc;
+  }
+  __syncthreads();
+  A total = S::ident();
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    A wpre = S::ident(), qtot = S::ident();
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) {
+      if (w < wave) wpre = S::comb(wpre, wsum[q][w]);
+      qtot = S::comb(qtot, wsum[q][w]);
+    }
+    excl[q] = S::comb(total, S::comb(wpre, excl[q]));  // prefix within the tile
+    total = S::comb(total, qtot);
+  }
+
+  // 3. decoupled look-back by wave 0: its 64 lanes read the descriptors of
+  //    the 64 nearest predecessors at once (lane 0 = tile - 1).  The window
+  //    is usable when every lane nearer than the nearest inclusive prefix
+  //    holds a valid aggregate; otherwise it is re-read (bounded).  Tiles
+  //    before the row's first tile count as an inclusive identity.
+  if (wave == 0) {
     A prefix = S::ident();
     unsigned long long *d = sc.desc;
     if (t > 0) {
-      publish(d + 2 * tile, total, (gen << 2) | 1u);
-      long long j = tile - 1;
+      if (lane == 0) publish(d + 2 * tile, total, (gen << 2) | 1u);
+      const long long first = tile - t;  // first tile of this row
+      long long top = tile - 1;
       long long spins = 0;
       while (true) {
-        const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
-        if (t0 != t1 || (t0 >> 2) != gen) {
+        const long long j = top - lane;
+        unsigned state = 2u;
+        A val = S::ident();
+        if (j >= first) {
+          const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
+          state = (t0 == t1 && (t0 >> 2) == gen) ? (t0 & 3u) : 0u;
+          val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
+        }
+        const unsigned long long incl = __ballot(state == 2u);
+        const unsigned long long bad = __ballot(state == 0u);
+        const int p = incl ? __ffsll((long long)incl) - 1 : 64;  // nearest inclusive lane
+        const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
+        if (bad & nearer) {
           if (++spins > kSpinLimit) {
-            __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
           __builtin_amdgcn_s_sleep(1);
           continue;
         }
-        const A val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
-        prefix = S::comb(val, prefix);
-        if ((t0 & 3u) == 2u) break;
-        --j;  // the row's first tile always publishes an inclusive prefix
+        A part = lane <= p ? val : S::ident();
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
+        prefix = S::comb(part, prefix);
+        if (p < 64) break;
+        top -= 64;
       }
     }
-    publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
-    s_prefix = prefix;
-  }
-  __syncthreads();  // also: every thread has read its inputs from `stage`
-
-  // 5. outputs through LDS, then coalesced stores
-  const A pre = S::comb(s_prefix, S::comb(wpre, excl));
-#pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const int i = tid * kItems + j;
-    if (i < n) sy[padded(i)] = mmp_convert<To, A>(S::comb(pre, v[j]));
+    if (lane == 0) {
+      publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
+      s_prefix = prefix;
+    }
   }
   __syncthreads();
+
+  // 4. outputs per sub-tile through LDS, then coalesced stores
   constexpr int VO = 16 / sizeof(To);
-  if (n == kTile && ((uintptr_t)yr & 15u) == 0) {
-    u32x4 *yv = reinterpret_cast<u32x4 *>(yr);
 #pragma unroll
-    for (int k = 0; k < kTile / VO / kBlock; ++k) {
-      const int vi = k * kBlock + tid;
-      union { u32x4 v; To e[VO]; } q;
+  for (int q = 0; q < Q; ++q) {
+    const int qb = q * kSubTile;
+    const int qn = n - qb < 0 ? 0 : (n - qb < kSubTile ? n - qb : kSubTile);
+    A run = S::comb(s_prefix, excl[q]);
 #pragma unroll
-      for (int e = 0; e < VO; ++e) q.e[e] = sy[padded(vi * VO + e)];
-      __builtin_nontemporal_store(q.v, yv + vi);
+    for (int j = 0; j < kItems; ++j) {
+      const int i = tid * kItems + j;
+      if (i < qn) {
+        run = S::comb(run, S::map(xin[q][j]));
+        sy[padded(i)] = mmp_convert<To, A>(run);
+      }
     }
-  } else {
-    for (int i = tid; i < n; i += kBlock) yr[i] = sy[padded(i)];
+    __syncthreads();
+    if (qn == kSubTile && ((uintptr_t)(yr + qb) & 15u) == 0) {
+      u32x4 *yv = reinterpret_cast<u32x4 *>(yr + qb);
+#pragma unroll
+      for (int k = 0; k < kSubTile / VO / kBlock; ++k) {
+        const int vi = k * kBlock + tid;
+        union { u32x4 v; To e[VO]; } u;
+#pragma unroll
+        for (int e = 0; e < VO; ++e) u.e[e] = sy[padded(vi * VO + e)];
+        __builtin_nontemporal_store(u.v, yv + vi);
+      }
+    } else {
+      for (int i = tid; i < qn; i += kBlock) yr[qb + i] = sy[padded(i)];
+    }
+    __syncthreads();
   }
 }
 
@@ -252,7 +315,7 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
   } else {
     typedef typename ScanOp<OP, Ti>::A A;
     if (inner == 1) {
-      const long long tpr = mmpi::ceil_div(len, kTile);
+      const long long tpr = mmpi::ceil_div(len, (long long)sub_tiles<Ti>() * kSubTile);
       const long long ntiles = outer * tpr;
       if (ntiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "scan too large");
       int st = MMP_OK;

@@ -182,6 +182,245 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm16(const T *__restrict__ A,
       }
 }
 
+// ------------------------------------------- 16-bit inputs, large tiles
+// 256 x 256 output tile per workgroup for operands whose extents divide
+// the tile and whose rows are 16-byte aligned.  WM x WN waves (2 x 4 by
+// default: eight waves, two per SIMD, each owning a 128 x 64 sub-tile with
+// its 128 fp32 accumulators in VGPRs); one workgroup per CU.  Per 64-deep
+// k slab a workgroup moves 64 KiB L2 -> LDS for 256 x 256 x 64 MACs, half
+// the L2 traffic per flop of a 128 x 128 tile.
+//  * Loading (eight waves): waves 0-3 fetch B, waves 4-7 fetch A, every
+//    thread as eight 16-byte row pieces.  A is stored unchanged
+//    (k-contiguous); a B thread owns an 8(k) x 8(n) block and transposes it
+//    in registers (v_perm) into eight k-contiguous columns.  Eight
+//    consecutive lanes cover one 128 B row segment in HBM and one LDS row.
+//  * LDS: two buffers of 256 rows x 128 B for each operand, 16-byte chunks
+//    XOR-swizzled per row (see swz below): conflict-free fragment reads and
+//    stores.
+//  * Pipeline per slab kt: store slab kt + 1 (already in registers) to the
+//    idle buffer, issue the global loads of slab kt + 2, run slab kt's
+//    MFMAs with the loads spread between them, one barrier.
+//  * The MFMA is issued as C^T = B^T A^T (operands swapped), so a lane's
+//    four accumulators are four consecutive columns of one C row: the
+//    epilogue writes 8 B per lane per 16 x 16 tile.
+//  * Workgroup ids are remapped so that the tiles one XCD runs together
+//    (ids are dealt round-robin over the eight XCDs) form 4-row groups:
+//    concurrent workgroups on an XCD share A and B panels in its L2.
+// Measured at 8192^3 float16 on MI355X: 0.85 PF/s (1.31 ms).  The same loop
+// without global loads reaches 1.4 PF/s and a register-fed MFMA loop with
+// random operands 1.6 PF/s (operand-dependent power limits the clock), so
+// the remaining gap is the global->LDS path.
+#ifndef MMP_GEMM16_SPLIT
+#define MMP_GEMM16_SPLIT 1
+#endif
+#ifndef MMP_GEMM16_INTERLEAVE
+#define MMP_GEMM16_INTERLEAVE 1
+#endif
+
+template <int BW> struct BRow;
+template <> struct BRow<8> { typedef u32x4 type; };
+template <> struct BRow<4> { typedef u32x2 type; };
+
+template <typename T, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm16_big(
+    const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
+    long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
+    int tiles_m, int tiles_n) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TB = 256, BK = 64, LDK = BK;
+  constexpr int TM = TB / WM, TN = TB / WN;   // wave tile
+  constexpr int I = TM / 16, J = TN / 16;     // 16 x 16 MFMA tiles per wave
+  constexpr int AV = TB * (BK / 8) / NT;      // A vectors per thread
+  constexpr int BW = TB * BK / (NT * 8);      // B block width (n)
+  static_assert(BW == 4 || BW == 8, "B block width");
+  typedef typename Half16<T>::vec V;
+  typedef typename BRow<BW>::type BR;
+  __shared__ __attribute__((aligned(16))) unsigned short As[2][TB * LDK];
+  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][TB * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // XCD-aware, 4-row grouped tile order
+  const int nblk = tiles_m * tiles_n;
+  int b = blockIdx.x;
+  if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
+  constexpr int GM = 4;
+  const int group = b / (GM * tiles_n), first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = b - group * GM * tiles_n;
+  const int tm = first_m + rem % gm, tn = rem / gm;
+
+  const long long bz = blockIdx.y;
+  const int m0 = tm * TB, n0 = tn * TB;
+  const unsigned short *Ag = reinterpret_cast<const unsigned short *>(A + bz * sA) +
+                             (long long)m0 * lda;
+  const unsigned short *Bg = reinterpret_cast<const unsigned short *>(B + bz * sB) + n0;
+
+  u32x4 ra[AV];
+  BR rb[8];
+  const int a_row = tid >> 3, a_kv = tid & 7;
+  const int b_k8 = tid & 7, b_nb = tid >> 3;
+  // LDS rows are 128 B (64 k); 16-byte chunk c of row r is stored at
+  // chunk c ^ ((r >> 1) & 7).  Measured on gfx950: ds_read_b128 serves
+  // 16 lanes per cycle (lanes sharing bits 1 and 5 of the lane id) and
+  // conflicts when two of them hit the same 16 B slot modulo 512 B; with
+  // this swizzle the fragment reads (16 rows x 2 chunks per lane group)
+  // and the row-contiguous stores are conflict-free, where a 144 B row
+  // pitch gave 2-way conflicts on every fragment read.
+  auto swz = [](int r) { return (r >> 1) & 7; };
+  const int a_swz = swz(a_row);
+
+  // With eight waves, the first four load B and the last four load A, each
+  // thread as eight 16-byte row pieces (a B thread owns an 8(k) x 8(n)
+  // block, an A thread eight row segments): every global load is 16 bytes
+  // wide and each wave issues eight, instead of twelve half of which move
+  // only 8 bytes per lane.  The role test is uniform per wave.
+  constexpr bool SPLIT = NT == 512 && MMP_GEMM16_SPLIT;
+  const bool b_role = tid < 256;
+  const int t2 = tid & 255;
+  const int s_k8 = t2 & 7, s_nb = t2 >> 3;     // B role: 8 x 8 block
+  const int s_row = t2 >> 3, s_kv = t2 & 7;    // A role: rows s_row + 32p
+  const int s_swz = swz(s_row);
+  u32x4 rs[8];
+  auto load_split = [&](int k0) {
+    if (b_role) {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        rs[kk] = *reinterpret_cast<const u32x4 *>(Bg + (long long)(k0 + s_k8 * 8 + kk) * ldb + s_nb * 8);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        rs[p] = *reinterpret_cast<const u32x4 *>(Ag + (long long)(s_row + 32 * p) * lda + k0 + s_kv * 8);
+    }
+  };
+  auto store_split = [&](int buf) {
+    if (b_role) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 w;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          w[d] = __builtin_amdgcn_perm(rs[2 * d + 1][c >> 1], rs[2 * d][c >> 1], sel);
+        *reinterpret_cast<u32x4 *>(&Bs[buf][(s_nb * 8 + c) * LDK + (s_k8 ^ swz(s_nb * 8 + c)) * 8]) = w;
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        *reinterpret_cast<u32x4 *>(&As[buf][(s_row + 32 * p) * LDK + (s_kv ^ s_swz) * 8]) = rs[p];
+    }
+  };
+
+  auto load = [&](int k0) {
+    if constexpr (SPLIT) {
+      load_split(k0);
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < AV; ++p)
+      ra[p] = *reinterpret_cast<const u32x4 *>(Ag + (long long)(a_row + (NT / 8) * p) * lda +
+                                               k0 + a_kv * 8);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      rb[kk] = *reinterpret_cast<const BR *>(Bg + (long long)(k0 + b_k8 * 8 + kk) * ldb +
+                                             b_nb * BW);
+  };
+  auto store = [&](int buf) {
+    if constexpr (SPLIT) {
+      store_split(buf);
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < AV; ++p)
+      *reinterpret_cast<u32x4 *>(&As[buf][(a_row + (NT / 8) * p) * LDK + (a_kv ^ a_swz) * 8]) = ra[p];
+    // column c of the 8 x BW block: half c of each of the eight rows
+#pragma unroll
+    for (int c = 0; c < BW; ++c) {
+      const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 w;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        w[d] = __builtin_amdgcn_perm(rb[2 * d + 1][c >> 1], rb[2 * d][c >> 1], sel);
+      *reinterpret_cast<u32x4 *>(&Bs[buf][(b_nb * BW + c) * LDK + (b_k8 ^ swz(b_nb * BW + c)) * 8]) = w;
+    }
+  };
+
+  f4 acc[I][J];
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / BK;
+  const int fr = lane & 15;
+  // fragment chunk offsets (halves) of sub-steps 0 and 1 for this lane
+  const int fch[2] = {(((lane >> 4) + 0) ^ swz(fr)) * 8, (((lane >> 4) + 4) ^ swz(fr)) * 8};
+  auto mfmas = [&](int cur) {
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      V af[I], bf[J];
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        af[i] = *reinterpret_cast<const V *>(&As[cur][(wm * TM + i * 16 + fr) * LDK + fch[s]]);
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        bf[j] = *reinterpret_cast<const V *>(&Bs[cur][(wn * TN + j * 16 + fr) * LDK + fch[s]]);
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) acc[i][j] = Half16<T>::mfma(bf[j], af[i], acc[i][j]);
+    }
+  };
+
+  // Pipeline: slab kt + 1 sits in registers when step kt begins.  The step
+  // writes it to the idle LDS buffer, refills the registers with slab
+  // kt + 2 (clamped to the last slab; the surplus copy is never read) and
+  // then runs slab kt's MFMAs from the other buffer, so the LDS stores and
+  // the global-load latency overlap the MFMAs instead of separating them;
+  // one barrier per slab.  Straight-line steps let the scheduler interleave
+  // loads, LDS traffic and MFMAs.
+  load(0);
+  store(0);
+  load(min(1, nk - 1) * BK);
+  __syncthreads();
+  constexpr int NLOAD = SPLIT ? 8 : AV + 8;  // global loads per thread per slab
+  constexpr int NMFMA = 2 * I * J;          // MFMAs per wave per slab
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    store(cur ^ 1);
+    load(min(kt + 2, nk - 1) * BK);
+    mfmas(cur);
+#if MMP_GEMM16_INTERLEAVE
+    // spread the global loads over the MFMA stream: a wave that issues all
+    // of them back to back stalls on the full address queue and starves
+    // the matrix core
+#pragma unroll
+    for (int g = 0; g < NLOAD; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // 1 VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NLOAD, 0);    // MFMAs
+    }
+#endif
+    __syncthreads();
+  }
+
+  // epilogue: accumulator r of lane l is C[row l % 16][col 4 * (l / 16) + r]
+  T *Cb = C + bz * sC;
+  const int cr = lane & 15, cc = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int row = m0 + wm * TM + i * 16 + cr;
+      const int col = n0 + wn * TN + j * 16 + cc;
+      unsigned short h[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h[r] = __builtin_bit_cast(unsigned short, from_f32<T>(acc[i][j][r]));
+      *reinterpret_cast<u32x2 *>(Cb + (long long)row * ldc + col) =
+          u32x2{h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16)};
+    }
+}
+
 // ------------------------------------------------------ fp32 / fp64
 // Output element r of lane group g (= lane / 16) holds tile row
 // 4*g + r for the fp32 MFMA but g + 4*r for the fp64 one (measured on
@@ -351,9 +590,36 @@ __global__ __launch_bounds__(kBlock) void k_gemm_int(const T *__restrict__ A, co
 // -------------------------------------------------------------- launch
 inline bool al(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
+// Large-tile kernel: 2 = 2 x 4 waves of 128 x 64 (default), 1 = 2 x 2
+// waves of 128 x 128 (slower: the compiler shuffles its 256 accumulators
+// between register files), 0 = off.  Used once the product has at least
+// MMP_GEMM16_BIG_MIN_TILES 256 x 256 tiles (fewer leave CUs idle).
+#ifndef MMP_GEMM16_BIG
+#define MMP_GEMM16_BIG 2
+#endif
+#ifndef MMP_GEMM16_BIG_MIN_TILES
+#define MMP_GEMM16_BIG_MIN_TILES 128
+#endif
+
 template <typename T>
 int launch16(long long batch, int M, int N, int K, const void *A, long long lda, long long sA,
              const void *B, long long ldb, long long sB, void *C, long long ldc, long long sC) {
+  if (MMP_GEMM16_BIG && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && lda % 8 == 0 &&
+      ldb % 8 == 0 && ldc % 4 == 0 && sA % 8 == 0 && sB % 8 == 0 && sC % 4 == 0 && al(A, 16) &&
+      al(B, 16) && al(C, 8) &&
+      (long long)(M / 256) * (N / 256) * batch >= MMP_GEMM16_BIG_MIN_TILES) {
+    const int tm = M / 256, tn = N / 256;
+    dim3 grid((unsigned)(tm * tn), (unsigned)batch);
+    if (MMP_GEMM16_BIG == 2)
+      hipLaunchKernelGGL((k_gemm16_big<T, 2, 4>), grid, dim3(512), 0, mmpi::stream(),
+                         (const T *)A, (const T *)B, (T *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
+                         tm, tn);
+    else
+      hipLaunchKernelGGL((k_gemm16_big<T, 2, 2>), grid, dim3(256), 0, mmpi::stream(),
+                         (const T *)A, (const T *)B, (T *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
+                         tm, tn);
+    return mmpi::check_launch("mmp_matmul(mfma16 256x256)");
+  }
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const bool fast = M % BM == 0 && N % BN == 0 && K % 64 == 0 && lda % 8 == 0 && ldb % 4 == 0 &&
                     sA % 8 == 0 && sB % 4 == 0 && al(A, 16) && al(B, 8);

@@ -52,6 +52,22 @@ def test_matmul_mfma_layout_known_answer():
     assert np.array_equal((cp.array(e) @ cp.array(m)).get(), m)
 
 
+@pytest.mark.parametrize("batch,m,n,k", [(1, 2048, 4096, 320), (2, 2048, 2048, 192)])
+def test_matmul_f16_large_tile_exact(batch, m, n, k):
+    """Products with at least 128 tiles of 256 x 256 take the large-tile
+    float16 kernel (split A/B loading, swizzled LDS, swapped-operand
+    epilogue, XCD tile remap; an odd number of 64-deep slabs for k = 320).
+    Operands in {-1, 0, 1} make every sum an integer of magnitude <= k, exact
+    in fp32 and in the float16 output, so the whole result must equal
+    NumPy's."""
+    g = np.random.default_rng(k)
+    a = g.integers(-1, 2, (batch, m, k)).astype(np.float16)
+    b = g.integers(-1, 2, (batch, k, n)).astype(np.float16)
+    got = (cp.array(a) @ cp.array(b)).get()
+    want = np.matmul(a.astype(np.float32), b.astype(np.float32))
+    assert got.dtype == np.float16 and np.array_equal(got.astype(np.float32), want)
+
+
 @pytest.mark.parametrize("dtype", [np.int32, np.int64, np.int16, np.uint32])
 def test_matmul_integer_exact(dtype):
     g = np.random.default_rng(1)

@@ -10,15 +10,20 @@
 //    tile only ever waits for tiles that are already running (AMD gives no
 //    forward-progress guarantee to workgroups that have not started);
 //  * a tile (16384 elements: 4 sub-tiles of 256 threads x 16 consecutive
-//    elements) is staged through LDS with 128-bit loads into registers,
-//    scanned serially per thread in the accumulator type, then across the
-//    wave64 with shuffles and across the 4 waves through LDS;
-//  * wave 0 publishes the tile aggregate, reads the 64 nearest
-//    predecessors' descriptors at once and combines aggregates up to the
-//    nearest inclusive prefix, then publishes its own inclusive prefix;
+//    elements) is loaded with 128-bit loads, all issued up front, and
+//    redistributed through LDS into registers, scanned serially per thread
+//    in the accumulator type, then across the wave64 with shuffles and
+//    across the 4 waves through LDS;
+//  * wave 0 publishes the tile aggregate, reads the 8 nearest predecessors'
+//    descriptors at once and combines aggregates up to the nearest
+//    inclusive prefix, then publishes its own inclusive prefix;
 //  * descriptors carry a per-call generation tag, so they are never
 //    cleared between calls; waits are bounded and a timeout is recorded
-//    instead of hanging.
+//    instead of hanging;
+//  * rows whose byte length is a multiple of 16 (and 16-byte aligned
+//    operands) run their whole tiles through a guard-free kernel and each
+//    row's partial tail through a second small launch; other layouts run a
+//    guarded kernel.
 // Accumulators: int64 for integers (int32 -> int64 output as NumPy),
 // float64 for floats (rounded once per output element).  HBM-bound:
 // sizeof(in) + sizeof(out) bytes per element.
@@ -101,11 +106,116 @@ struct ScanScratch {
   unsigned *timeout;          // set to 1 if a look-back wait ran out
 };
 
-template <int OP, typename Ti, typename To>
-__global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, To *__restrict__ y,
-                                                     long long len, long long tiles_per_row,
-                                                     long long ntiles, ScanScratch sc,
-                                                     unsigned gen) {
+template <bool B> struct Bool { static constexpr bool value = B; };
+
+// An empty asm "redefinition": the value is only available where this is
+// executed.  Used on the inputs in the output pass, so that the compiler
+// neither hoists that pass's running sums above the barriers (which keeps
+// all 64 wide accumulators of a thread live at once) nor keeps the widened
+// inputs of the totals pass alive for it; either costs half the occupancy.
+template <typename T> __device__ __forceinline__ T opaque(T v) {
+  if constexpr (sizeof(T) == 4 || sizeof(T) == 8) {
+    asm volatile("" : "+v"(v));
+    return v;
+  } else if constexpr (sizeof(T) == 2) {
+    unsigned u = (unsigned)__builtin_bit_cast(unsigned short, v);
+    asm volatile("" : "+v"(u));
+    return __builtin_bit_cast(T, (unsigned short)u);
+  } else {
+    unsigned u = (unsigned)__builtin_bit_cast(unsigned char, v);
+    asm volatile("" : "+v"(u));
+    return __builtin_bit_cast(T, (unsigned char)u);
+  }
+}
+
+// Decoupled look-back by wave 0: lanes 0..kLook-1 read the descriptors of
+// the kLook (8) nearest predecessors at once (lane 0 = tile - 1).  The window is
+// usable when every lane nearer than the nearest inclusive prefix holds a
+// valid aggregate; otherwise it is re-read (bounded).  Tiles before the
+// row's first tile count as an inclusive identity.  Returns the exclusive
+// prefix of `tile` (lane 0's value is the one used).  The descriptor reads
+// are agent-scope loads that contend with the other tiles' publications;
+// measured on MI355X at 2^28 elements, int32 -> int64: 64 tiles per round
+// 0.72 ms, 32: 0.64, 16: 0.60, 8: 0.58, 4: 0.57 (float32 best at 8), and
+// 256 per round 1.03 ms.
+#ifndef MMP_SCAN_LOOK
+#define MMP_SCAN_LOOK 8
+#endif
+constexpr int kLook = MMP_SCAN_LOOK;
+
+template <typename S>
+__device__ typename S::A look_back(const ScanScratch &sc, long long tile, long long t,
+                                   typename S::A total, unsigned gen, int lane) {
+  typedef typename S::A A;
+  A prefix = S::ident();
+  unsigned long long *d = sc.desc;
+  if (t > 0) {
+    if (lane == 0) publish(d + 2 * tile, total, (gen << 2) | 1u);
+    const long long first = tile - t;  // first tile of this row
+    const unsigned long long in_window = kLook >= 64 ? ~0ull : ((1ull << kLook) - 1);
+    long long top = tile - 1;
+    long long spins = 0;
+    while (true) {
+      const long long j = top - lane;
+      unsigned state = 2u;
+      A val = S::ident();
+      if (lane < kLook && j >= first) {
+        const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
+        state = (t0 == t1 && (t0 >> 2) == gen) ? (t0 & 3u) : 0u;
+        val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
+      }
+      const unsigned long long incl = __ballot(state == 2u) & in_window;
+      const unsigned long long bad = __ballot(state == 0u) & in_window;
+      const int p = incl ? __ffsll((long long)incl) - 1 : kLook;  // nearest inclusive lane
+      const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
+      if (bad & nearer) {
+        if (++spins > kSpinLimit) {
+          if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        continue;
+      }
+      A part = lane <= p && lane < kLook ? val : S::ident();
+#pragma unroll
+      for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
+      prefix = S::comb(part, prefix);
+      if (p < kLook) break;
+      top -= kLook;
+    }
+  }
+  if (lane == 0) publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
+  return prefix;
+}
+
+// Prefix for a row's tail (MODE 2): the inclusive descriptor of the row's
+// last whole tile, published by the preceding launch on the same stream.
+template <typename S>
+__device__ typename S::A tail_prefix(const ScanScratch &sc, long long pred, unsigned gen) {
+  const unsigned long long w0 = __hip_atomic_load(sc.desc + 2 * pred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long w1 = __hip_atomic_load(sc.desc + 2 * pred + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
+  if (!(t0 == t1 && t0 == ((gen << 2) | 2u)))
+    __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(typename S::A, (w0 & 0xffffffffull) | (w1 << 32));
+}
+
+// MODE 0: whole, 16-byte aligned tiles only (grid = rows x whole tiles per
+//         row), guard-free streaming body, look-back.
+// MODE 1: any layout (grid = rows x ceil tiles per row), guarded body,
+//         look-back.
+// MODE 2: the partial last tile of each row after a MODE 0 launch (grid =
+//         rows); its prefix is the inclusive descriptor MODE 0 published for
+//         the row's last whole tile.
+// MODE 0 is compiled for at least two workgroups per CU (measured best:
+// more concurrent tiles lengthen every look-back); keeping the guarded
+// paths out of it keeps its registers down.
+template <int OP, typename Ti, typename To, int MODE>
+__global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
+    const Ti *__restrict__ x, To *__restrict__ y, long long len, long long tiles_per_row,
+    long long ntiles, ScanScratch sc, unsigned gen) {
   typedef ScanOp<OP, Ti> S;
   typedef typename S::A A;
   constexpr int Q = sub_tiles<Ti>();
@@ -119,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
   To *sy = reinterpret_cast<To *>(stage);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  if (tid == 0) {
+  if (MODE != 2 && tid == 0) {
     const unsigned t = __hip_atomic_fetch_add(sc.counter, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
     s_tile = t;
@@ -127,9 +237,10 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
     if ((long long)t == ntiles - 1)
       __hip_atomic_store(sc.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  const long long tile = s_tile;
-  const long long row = tile / tiles_per_row;
+  if (MODE != 2) __syncthreads();
+  // MODE 2: tile = the row's tail, one past its last whole tile
+  const long long tile = MODE == 2 ? (long long)blockIdx.x * tiles_per_row + tiles_per_row : s_tile;
+  const long long row = MODE == 2 ? (long long)blockIdx.x : tile / tiles_per_row;
   const long long t = tile - row * tiles_per_row;
   const long long base = t * kTile;
   const long long rem = len - base;
@@ -137,153 +248,136 @@ __global__ __launch_bounds__(kBlock) void k_scan_rows(const Ti *__restrict__ x, 
   const Ti *xr = x + row * len + base;
   To *yr = y + row * len + base;
 
-  // 1. stage each sub-tile through LDS (128-bit loads when whole and
-  //    aligned); each thread keeps its 16 consecutive inputs in registers
-  constexpr int VI = 16 / sizeof(Ti);
-  Ti xin[Q][kItems];
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int qb = q * kSubTile;
-    const int qn = n - qb < 0 ? 0 : (n - qb < kSubTile ? n - qb : kSubTile);
-    if (q) __syncthreads();
-    if (qn == kSubTile && ((uintptr_t)(xr + qb) & 15u) == 0) {
-      const u32x4 *xv = reinterpret_cast<const u32x4 *>(xr + qb);
-#pragma unroll
-      for (int k = 0; k < kSubTile / VI / kBlock; ++k) {
-        const int vi = k * kBlock + tid;
-        union { u32x4 v; Ti e[VI]; } u;
-        u.v = __builtin_nontemporal_load(xv + vi);
-#pragma unroll
-        for (int e = 0; e < VI; ++e) sx[padded(vi * VI + e)] = u.e[e];
-      }
-    } else {
-      for (int i = tid; i < qn; i += kBlock) sx[padded(i)] = xr[qb + i];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kItems; ++j) {
-      const int i = tid * kItems + j;
-      xin[q][j] = i < qn ? sx[padded(i)] : (Ti)0;
-    }
-  }
+  // The tile body is instantiated twice: FULL (a whole tile with 16-byte
+  // aligned input and output: 128-bit loads and stores, no per-element
+  // guards) and the guarded general case (a row's last tile, unaligned
+  // views).  Only the first is on the streaming path.
+  auto body = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    constexpr int VI = 16 / sizeof(Ti);
+    constexpr int NV = kSubTile / VI / kBlock;  // 16-byte input vectors per thread per sub-tile
+    auto count = [&](int q) {  // valid elements of sub-tile q
+      if constexpr (FULL) return kSubTile;
+      const int r = n - q * kSubTile;
+      return r < 0 ? 0 : (r < kSubTile ? r : kSubTile);
+    };
 
-  // 2. per-thread totals of each sub-tile, block scans across threads
-  //    (wave64 shuffles, then the 4 wave totals through LDS)
-  A excl[Q];
+    // 1. inputs: all of the tile's 128-bit loads are issued first (a whole
+    //    tile in flight per workgroup), then each sub-tile is redistributed
+    //    through LDS so that a thread holds 16 consecutive elements
+    u32x4 raw[FULL ? Q : 1][FULL ? NV : 1];
+    if constexpr (FULL) {
+      const u32x4 *xv = reinterpret_cast<const u32x4 *>(xr);
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int qn = n - q * kSubTile;
-    A run = S::ident();
+      for (int q = 0; q < Q; ++q)
 #pragma unroll
-    for (int j = 0; j < kItems; ++j)
-      if (tid * kItems + j < qn) run = S::comb(run, S::map(xin[q][j]));
-    A inc = run;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const A o = shfl_up64(inc, d);
-      if (lane >= d) inc = S::comb(o, inc);
+        for (int k = 0; k < NV; ++k)
+          raw[q][k] = __builtin_nontemporal_load(xv + q * (kSubTile / VI) + k * kBlock + tid);
     }
-    A ex = shfl_up64(inc, 1);
-    if (lane == 0) ex = S::ident();
-    excl[q] = ex;
-    if (lane == 63) wsum[q][wave] = inc;
-  }
-  __syncthreads();
-  A total = S::ident();
+    Ti xin[Q][kItems];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    A wpre = S::ident(), qtot = S::ident();
+    for (int q = 0; q < Q; ++q) {
+      if (q) __syncthreads();
+      if constexpr (FULL) {
 #pragma unroll
-    for (int w = 0; w < kBlock / 64; ++w) {
-      if (w < wave) wpre = S::comb(wpre, wsum[q][w]);
-      qtot = S::comb(qtot, wsum[q][w]);
-    }
-    excl[q] = S::comb(total, S::comb(wpre, excl[q]));  // prefix within the tile
-    total = S::comb(total, qtot);
-  }
-
-  // 3. decoupled look-back by wave 0: its 64 lanes read the descriptors of
-  //    the 64 nearest predecessors at once (lane 0 = tile - 1).  The window
-  //    is usable when every lane nearer than the nearest inclusive prefix
-  //    holds a valid aggregate; otherwise it is re-read (bounded).  Tiles
-  //    before the row's first tile count as an inclusive identity.
-  if (wave == 0) {
-    A prefix = S::ident();
-    unsigned long long *d = sc.desc;
-    if (t > 0) {
-      if (lane == 0) publish(d + 2 * tile, total, (gen << 2) | 1u);
-      const long long first = tile - t;  // first tile of this row
-      long long top = tile - 1;
-      long long spins = 0;
-      while (true) {
-        const long long j = top - lane;
-        unsigned state = 2u;
-        A val = S::ident();
-        if (j >= first) {
-          const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
-          state = (t0 == t1 && (t0 >> 2) == gen) ? (t0 & 3u) : 0u;
-          val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
+        for (int k = 0; k < NV; ++k) {
+          const int vi = k * kBlock + tid;
+          union { u32x4 v; Ti e[VI]; } u;
+          u.v = raw[q][k];
+#pragma unroll
+          for (int e = 0; e < VI; ++e) sx[padded(vi * VI + e)] = u.e[e];
         }
-        const unsigned long long incl = __ballot(state == 2u);
-        const unsigned long long bad = __ballot(state == 0u);
-        const int p = incl ? __ffsll((long long)incl) - 1 : 64;  // nearest inclusive lane
-        const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
-        if (bad & nearer) {
-          if (++spins > kSpinLimit) {
-            if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-          continue;
-        }
-        A part = lane <= p ? val : S::ident();
+      } else {
+        const int qn = count(q);
+        for (int i = tid; i < qn; i += kBlock) sx[padded(i)] = xr[q * kSubTile + i];
+      }
+      __syncthreads();
 #pragma unroll
-        for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
-        prefix = S::comb(part, prefix);
-        if (p < 64) break;
-        top -= 64;
+      for (int j = 0; j < kItems; ++j) {
+        const int i = tid * kItems + j;
+        xin[q][j] = (FULL || i < count(q)) ? sx[padded(i)] : (Ti)0;
       }
     }
-    if (lane == 0) {
-      publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
-      s_prefix = prefix;
-    }
-  }
-  __syncthreads();
 
-  // 4. outputs per sub-tile through LDS, then coalesced stores
-  constexpr int VO = 16 / sizeof(To);
+    // 2. per-thread totals of each sub-tile, block scans across threads
+    //    (wave64 shuffles, then the 4 wave totals through LDS)
+    A excl[Q];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int qb = q * kSubTile;
-    const int qn = n - qb < 0 ? 0 : (n - qb < kSubTile ? n - qb : kSubTile);
-    A run = S::comb(s_prefix, excl[q]);
+    for (int q = 0; q < Q; ++q) {
+      A run = S::ident();
 #pragma unroll
-    for (int j = 0; j < kItems; ++j) {
-      const int i = tid * kItems + j;
-      if (i < qn) {
-        run = S::comb(run, S::map(xin[q][j]));
-        sy[padded(i)] = mmp_convert<To, A>(run);
+      for (int j = 0; j < kItems; ++j)
+        if (FULL || tid * kItems + j < count(q)) run = S::comb(run, S::map(xin[q][j]));
+      A inc = run;
+#pragma unroll
+      for (int dd = 1; dd < 64; dd <<= 1) {
+        const A o = shfl_up64(inc, dd);
+        if (lane >= dd) inc = S::comb(o, inc);
       }
+      A ex = shfl_up64(inc, 1);
+      if (lane == 0) ex = S::ident();
+      excl[q] = ex;
+      if (lane == 63) wsum[q][wave] = inc;
     }
     __syncthreads();
-    if (qn == kSubTile && ((uintptr_t)(yr + qb) & 15u) == 0) {
-      u32x4 *yv = reinterpret_cast<u32x4 *>(yr + qb);
+    A total = S::ident();
 #pragma unroll
-      for (int k = 0; k < kSubTile / VO / kBlock; ++k) {
-        const int vi = k * kBlock + tid;
-        union { u32x4 v; To e[VO]; } u;
+    for (int q = 0; q < Q; ++q) {
+      A wpre = S::ident(), qtot = S::ident();
 #pragma unroll
-        for (int e = 0; e < VO; ++e) u.e[e] = sy[padded(vi * VO + e)];
-        __builtin_nontemporal_store(u.v, yv + vi);
+      for (int w = 0; w < kBlock / 64; ++w) {
+        if (w < wave) wpre = S::comb(wpre, wsum[q][w]);
+        qtot = S::comb(qtot, wsum[q][w]);
       }
-    } else {
-      for (int i = tid; i < qn; i += kBlock) yr[qb + i] = sy[padded(i)];
+      excl[q] = S::comb(total, S::comb(wpre, excl[q]));  // prefix within the tile
+      total = S::comb(total, qtot);
+    }
+
+    // 3. look-back (wave 0), prefix to every thread through LDS
+    if constexpr (MODE == 2) {
+      if (tid == 0) s_prefix = t > 0 ? tail_prefix<S>(sc, tile - 1, gen) : S::ident();
+    } else if (wave == 0) {
+      const A prefix = look_back<S>(sc, tile, t, total, gen, lane);
+      if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();
-  }
+
+    // 4. outputs per sub-tile through LDS, then coalesced stores
+    constexpr int VO = 16 / sizeof(To);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int qn = count(q);
+      A run = S::comb(s_prefix, excl[q]);
+#pragma unroll
+      for (int j = 0; j < kItems; ++j) {
+        const int i = tid * kItems + j;
+        if (FULL || i < qn) {
+          run = S::comb(run, S::map(opaque(xin[q][j])));
+          sy[padded(i)] = mmp_convert<To, A>(run);
+        }
+      }
+      __syncthreads();
+      if constexpr (FULL) {
+        u32x4 *yv = reinterpret_cast<u32x4 *>(yr + q * kSubTile);
+#pragma unroll
+        for (int k = 0; k < kSubTile / VO / kBlock; ++k) {
+          const int vi = k * kBlock + tid;
+          union { u32x4 v; To e[VO]; } u;
+#pragma unroll
+          for (int e = 0; e < VO; ++e) u.e[e] = sy[padded(vi * VO + e)];
+          __builtin_nontemporal_store(u.v, yv + vi);
+        }
+      } else {
+        for (int i = tid; i < qn; i += kBlock) yr[q * kSubTile + i] = sy[padded(i)];
+      }
+      __syncthreads();
+    }
+  };
+
+  if constexpr (MODE == 0)
+    body(Bool<true>());
+  else
+    body(Bool<false>());
 }
 
 // Strided axis: one thread per column, serial along the axis.
@@ -315,20 +409,40 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
   } else {
     typedef typename ScanOp<OP, Ti>::A A;
     if (inner == 1) {
-      const long long tpr = mmpi::ceil_div(len, (long long)sub_tiles<Ti>() * kSubTile);
+      constexpr long long kTile = (long long)sub_tiles<Ti>() * kSubTile;
+      // streaming layout: every row starts 16-byte aligned in input and output
+      const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0 &&
+                       (len * (long long)sizeof(Ti)) % 16 == 0 &&
+                       (len * (long long)sizeof(To)) % 16 == 0;
+      const long long tpr = vec ? len / kTile : mmpi::ceil_div(len, kTile);
       const long long ntiles = outer * tpr;
-      if (ntiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "scan too large");
+      if (ntiles > 0x7fffffffLL || outer > 0x7fffffffLL)
+        return mmpi::fail(MMP_E_ARG, "scan too large");
       int st = MMP_OK;
       ScanScratch sc;
       sc.counter = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st);
       if (st) return st;
       sc.timeout = sc.counter + 1;
-      sc.desc = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES, 16ull * ntiles, &st);
+      sc.desc = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES,
+                                                      16ull * (ntiles > 0 ? ntiles : 1), &st);
       if (st) return st;
       const unsigned gen = mmpi::next_generation();
-      hipLaunchKernelGGL((k_scan_rows<OP, Ti, To>), dim3((unsigned)ntiles), dim3(kBlock), 0,
-                         mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);
-      return mmpi::check_launch("mmp_scan(rows)");
+      if (!vec) {
+        hipLaunchKernelGGL((k_scan_rows<OP, Ti, To, 1>), dim3((unsigned)ntiles), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);
+        return mmpi::check_launch("mmp_scan(rows)");
+      }
+      if (ntiles > 0) {
+        hipLaunchKernelGGL((k_scan_rows<OP, Ti, To, 0>), dim3((unsigned)ntiles), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);
+        if (int e = mmpi::check_launch("mmp_scan(rows)")) return e;
+      }
+      if (len % kTile) {
+        hipLaunchKernelGGL((k_scan_rows<OP, Ti, To, 2>), dim3((unsigned)outer), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);
+        return mmpi::check_launch("mmp_scan(row tails)");
+      }
+      return MMP_OK;
     }
     if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided scan: outer extent %lld > 65535", outer);
     hipLaunchKernelGGL((k_scan_cols<OP, Ti, To>),

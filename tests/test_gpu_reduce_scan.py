@@ -162,6 +162,31 @@ def test_cumsum_axes(shape, axis):
     assert _rel_err(gf, want) <= RTOL
 
 
+@pytest.mark.parametrize("dtype", [np.int32, np.int16, np.int64, np.uint32, np.float32,
+                                   np.float64, np.bool_])
+@pytest.mark.parametrize("shape", [(16384 * 3,), (16384 * 4 + 4000,), (3, 40000), (2, 32768)])
+def test_cumsum_whole_tiles_and_tails(dtype, shape):
+    """Rows whose byte length is a multiple of 16 take the streaming kernel
+    for their whole tiles (16384 elements, 8192 for 8-byte types) and a
+    second launch for each row's partial tail, which starts from the
+    inclusive prefix the first launch published for the row's last whole
+    tile."""
+    g = np.random.default_rng(len(shape) * 31 + shape[-1])
+    if dtype == np.bool_:
+        x = g.random(shape) < 0.5
+    elif np.dtype(dtype).kind == "f":
+        x = g.random(shape).astype(dtype)
+    else:
+        x = g.integers(0, 100, shape).astype(dtype)
+    got = cp.cumsum(cp.array(x), axis=-1).get()
+    if np.dtype(dtype).kind == "f":
+        want = np.cumsum(x.astype(np.float64), axis=-1).astype(dtype)
+        assert got.dtype == np.dtype(dtype) and _rel_err(got, want) <= RTOL
+    else:
+        want = np.cumsum(x, axis=-1)
+        assert got.dtype == want.dtype and np.array_equal(got, want)
+
+
 def test_cumprod_small():
     x = np.random.default_rng(9).integers(1, 3, 40).astype(np.int32)
     assert np.array_equal(cp.cumprod(cp.array(x)).get(), np.cumprod(x))

@@ -288,6 +288,16 @@ int mmp_rtc_build(const char *src, const char *options, const char *arch,
 int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
                    uint32_t shared_bytes, void **args);
 
+/* ---- device-side wait status ------------------------------------------ */
+/* Split reductions and scans combine results across workgroups with
+ * bounded waits; a wait that runs out records a flag and lets the kernel
+ * finish instead of hanging.  Waits for the library stream, stores the
+ * flags raised since the last call in *flags (bit 0: scan look-back,
+ * bit 1: reduction combine) and clears them.  Non-zero means a result
+ * produced since the last call may be wrong.  No counterpart in the
+ * reference (its Metal scan and reductions use separate passes). */
+int mmp_wait_status(uint32_t *flags);
+
 /* ---- test hooks -------------------------------------------------------- */
 /* Make the next `count`-th call of kind (1 = mmp_alloc, 2 = mmp_rtc_compile,
  * 3 = kernel launch) fail with MMP_E_INJECTED.  count 0 disables. */

@@ -136,5 +136,6 @@ EXPORTS = (
     "mmp_copy_strided", "mmp_fill",
     "mmp_reduce", "mmp_argreduce", "mmp_scan", "mmp_matmul",
     "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch",
+    "mmp_wait_status",
     "mmp_debug_fail_next",
 )

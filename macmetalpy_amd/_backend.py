@@ -97,6 +97,7 @@ _SIGNATURES = {
     "mmp_rtc_build": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_vp, _c_sz,
                       ctypes.POINTER(_c_sz)],
     "mmp_rtc_launch": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
+    "mmp_wait_status": [ctypes.POINTER(ctypes.c_uint32)],
     "mmp_debug_fail_next": [_c_int, _c_int],
 }
 
@@ -236,6 +237,14 @@ class HipBackend:
 
     def synchronize(self) -> None:
         _check(self._lib.mmp_sync(), "mmp_sync")
+
+    def wait_status(self) -> int:
+        """Flags of device-side bounded waits that ran out since the last
+        call (bit 0 scan look-back, bit 1 reduction combine), then cleared.
+        Non-zero means a scan or reduction result may be wrong."""
+        f = ctypes.c_uint32()
+        _check(self._lib.mmp_wait_status(ctypes.byref(f)), "mmp_wait_status")
+        return f.value
 
     def memory_stats(self) -> tuple[int, int]:
         a, b = _c_sz(), _c_sz()

@@ -476,6 +476,26 @@ int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
   return mmpi::check_hip(e, "hipModuleLaunchKernel");
 }
 
+int mmp_wait_status(uint32_t *flags) {
+  if (!flags) return mmpi::fail(MMP_E_ARG, "null pointer");
+  *flags = 0;
+  if (int st = mmpi::ensure_init()) return st;
+  // words: [0] scan ticket, [1] scan look-back timeout, [2] reduction timeout
+  unsigned *w = static_cast<unsigned *>(g_scratch[mmpi::SCRATCH_SCAN_COUNTER]);
+  if (!w) return MMP_OK;
+  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+    return st;
+  unsigned h[3] = {0, 0, 0};
+  if (int st = mmpi::check_hip(hipMemcpy(h, w, sizeof h, hipMemcpyDeviceToHost), "hipMemcpy"))
+    return st;
+  *flags = (h[1] ? 1u : 0u) | (h[2] ? 2u : 0u);
+  if (*flags) {
+    if (int st = mmpi::check_hip(hipMemset(w + 1, 0, 2 * sizeof(unsigned)), "hipMemset"))
+      return st;
+  }
+  return MMP_OK;
+}
+
 int mmp_debug_fail_next(int kind, int count) {
   if (kind < 0 || kind > 3 || count < 0) return mmpi::fail(MMP_E_ARG, "bad injection request");
   g_fail_kind = count > 0 ? kind : 0;

@@ -25,3 +25,15 @@ def _reset_config():
     set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True)
     yield
     set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True)
+
+
+@pytest.fixture(autouse=True)
+def _no_device_wait_timeouts(request):
+    """After every GPU test: no split reduction or scan may have run out of
+    its bounded cross-workgroup wait (that would make its result suspect)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    from macmetalpy_amd._backend import HipBackend
+    flags = HipBackend().wait_status()
+    assert flags == 0, f"device-side wait ran out during this test (flags {flags:#x})"

@@ -324,23 +324,32 @@ def _env(be):
     return info
 
 
-ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32")
+ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
+            "cumsum_f32", "matmul_f16")
 
 
 def run_only(cp, be, name, steps):
-    """One op of the headline workload, `steps` launches (for counter
+    """One op of a benchmark workload, `steps` launches (for counter
     profiling); copy_f32 is a plain strided-copy kernel of 2^28 floats
     (1 GiB read + 1 GiB written) used to calibrate the byte counters."""
-    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    from macmetalpy_amd.workloads import (c2_float_inputs, c2_int_inputs, c3_scan_inputs,
+                                          c4_inputs)
     if name in ("add_f32", "sin_f32", "copy_f32"):
         a, b = (cp.array(x) for x in c2_float_inputs(N28))
-    else:
+    elif name in ("floor_divide_i32", "mod_i32"):
         a, b = (cp.array(x) for x in c2_int_inputs(N28))
+    elif name in ("cumsum_i32", "cumsum_f32"):
+        ci, cf = c3_scan_inputs()
+        a = b = cp.array(ci if name == "cumsum_i32" else cf)
+        del ci, cf
+    else:  # matmul_f16
+        a, b = (cp.array(x) for x in c4_inputs("f16"))
     a._ensure_gpu()
     b._ensure_gpu()
     fn = {"add_f32": lambda: a + b, "sin_f32": lambda: cp.sin(a),
           "floor_divide_i32": lambda: cp.floor_divide(a, b), "mod_i32": lambda: cp.mod(a, b),
-          "copy_f32": lambda: a.copy()}[name]
+          "copy_f32": lambda: a.copy(), "cumsum_i32": lambda: cp.cumsum(a),
+          "cumsum_f32": lambda: cp.cumsum(a), "matmul_f16": lambda: a @ b}[name]
     timer = EventTimer(be)
     for _ in range(steps):
         timer.run(name, lambda: _mat(fn()))

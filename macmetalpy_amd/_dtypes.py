@@ -78,6 +78,12 @@ def ufunc_result_dtype(ufunc: np.ufunc, *operands) -> np.dtype:
     key = None
     if all(isinstance(o, np.dtype) for o in operands):
         key = (ufunc, operands)
+    elif all(isinstance(o, np.dtype) and o.kind == "f" or type(o) in (int, float, bool)
+             for o in operands) and any(isinstance(o, np.dtype) for o in operands):
+        # Python scalars are weak (NEP 50): with a floating array operand the
+        # result depends on the scalars' types only, never on their values
+        key = (ufunc, tuple(o if isinstance(o, np.dtype) else type(o) for o in operands))
+    if key is not None:
         hit = _UFUNC_CACHE.get(key)
         if hit is not None:
             return hit

@@ -38,14 +38,27 @@ def is_scalar(x) -> bool:
     return isinstance(x, (numbers.Number, np.generic, bool)) and not isinstance(x, np.ndarray)
 
 
+_mods = {}
+
+
 def _ndarray():
-    from .ndarray import ndarray
-    return ndarray
+    cls = _mods.get("ndarray")
+    if cls is None:  # imported lazily: ndarray imports this module
+        from .ndarray import ndarray as cls
+        _mods["ndarray"] = cls
+    return cls
+
+
+def _creation():
+    mod = _mods.get("creation")
+    if mod is None:
+        from . import creation as mod
+        _mods["creation"] = mod
+    return mod
 
 
 def _asarray(x):
-    from . import creation
-    return creation.asarray(x)
+    return _creation().asarray(x)
 
 
 # ----------------------------------------------------- lazy dependents
@@ -113,8 +126,7 @@ def _lazy_result(node):
 
 
 def _empty(shape, dtype):
-    from . import creation
-    return creation.empty(shape, dtype=dtype)
+    return _creation().empty(shape, dtype=dtype)
 
 
 def _materialise_operand(x, shape, dtype):

@@ -451,6 +451,25 @@ def _kernel_for(src: str) -> int:
     return k
 
 
+# Kernels by program structure: the generated source is a function of the
+# SSA steps (op names and operand indices), the value dtypes, the leaves'
+# dtypes and stride classes, the number of outer dimensions, the output
+# dtype, the vector flag and the mode -- so a repeated expression skips
+# source generation (about 30 us of Python per call) as well as compilation.
+_struct_cache: dict = {}
+
+
+def _kernel_for_program(prog, kinds, nouter, out_dtype, vec, mode) -> int:
+    key = (tuple(prog.steps), tuple(prog.dtypes), tuple(a._dtype for a in prog.arrays),
+           tuple(kinds), nouter, out_dtype, vec, mode)
+    k = _struct_cache.get(key)
+    if k is None:
+        k = _kernel_for(generate_source(prog, kinds, nouter, out_dtype, vec, mode))
+        with _cache_lock:
+            _struct_cache[key] = k
+    return k
+
+
 def _leaf_ptr(node: InputNode) -> int:
     return node._buffer.ptr + node._offset * node._dtype.itemsize
 
@@ -525,8 +544,7 @@ def run_map(root: FusionNode, out_buffer, out_ptr: int) -> None:
     cshape, outer, cols, leaf_str, kinds = _plan(prog, shape, keep_last=False)
     out_dtype = root._dtype
     vec = _vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, out_dtype.itemsize, "map")
-    src = generate_source(prog, kinds, len(outer), out_dtype, vec, "map")
-    kern = _kernel_for(src)
+    kern = _kernel_for_program(prog, kinds, len(outer), out_dtype, vec, "map")
     tile = _BLOCK * _ELEMS * _UNROLL
     colblocks = -(-cols // tile)
     P = _param_struct(len(prog.arrays), len(prog.scalars), len(outer))
@@ -561,9 +579,8 @@ def run_sum(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean: bo
     colblocks = max(1, min(want, -(-cols // 4096)))
     final_direct = axis_last and colblocks == 1
     P = _param_struct(len(prog.arrays), len(prog.scalars), len(outer))
-    src = generate_source(prog, kinds, len(outer), out_dtype if final_direct else acc_dt,
-                          False, "sum")
-    kern = _kernel_for(src)
+    kern = _kernel_for_program(prog, kinds, len(outer), out_dtype if final_direct else acc_dt,
+                               False, "sum")
     if final_direct:
         p, rows = _fill_params(prog, P, outer, cols, leaf_str, out_ptr, 1, scale)
         be.launch(kern, (rows, 1, 1), (_BLOCK, 1, 1), [p])

@@ -159,6 +159,12 @@ template <int OP, typename T> struct Arg {
     return OP == MMP_R_ARGMAX ? x.v > y.v : x.v < y.v;
   }
   static __device__ __forceinline__ A comb(const A &x, const A &y) { return better(y, x) ? y : x; }
+  // v (visited later) replaces the running best b of one thread's sequence
+  static __device__ __forceinline__ bool seq_better(C v, C b) {
+    bool r = OP == MMP_R_ARGMAX ? v > b : v < b;
+    if constexpr (mmp_t<T>::is_float) r |= (v != v) & (b == b);
+    return r;
+  }
 };
 
 // --------------------------------------------------- wave / block reduce
@@ -250,43 +256,63 @@ __device__ __forceinline__ typename R::A slice_reduce(const T *__restrict__ p, l
   return R::comb(acc0, acc1);
 }
 
-// argmax slice: same traversal, carrying indices
+// argmax slice: same traversal, carrying indices.  Each thread visits its
+// elements in increasing index order, so within a thread a strict
+// comparison keeps the first occurrence of the extreme and no index
+// comparison is needed; indices are 32-bit offsets into the slice.  A NaN
+// replaces a non-NaN best (the first NaN wins, as NumPy), and the first
+// visited element always replaces the "nothing yet" state (so a row whose
+// extreme equals the identity, e.g. all -inf, still reports index 0).
+// Ties across threads are resolved by R::comb (smaller index).
 template <typename R, typename T>
 __device__ __forceinline__ typename R::A slice_argreduce(const T *__restrict__ p, long long n,
                                                          long long i0) {
   typedef typename R::A A;
   typedef typename mmp_t<T>::C C;
   constexpr int V = 16 / sizeof(T);
-  A best = R::ident();
+  constexpr unsigned kNone = 0xffffffffu;
+  if (n >= (long long)kNone) {  // offsets would not fit in 32 bits: generic path
+    A best = R::ident();
+    for (long long i = threadIdx.x; i < n; i += kBlock) best = R::comb(best, A{(C)p[i], i0 + i});
+    return best;
+  }
+  C bv = R::ident().v;
+  unsigned bi = kNone;
+  auto visit = [&](C v, unsigned off) {
+    bool upd = R::seq_better(v, bv) | (bi == kNone);
+    bv = upd ? v : bv;
+    bi = upd ? off : bi;
+  };
   const unsigned tid = threadIdx.x;
-  long long head = (long long)(((16 - ((uintptr_t)p & 15u)) & 15u) / sizeof(T));
-  if (((uintptr_t)p % sizeof(T)) != 0) head = n;
-  if (head > n) head = n;
-  for (long long i = tid; i < head; i += kBlock) best = R::comb(best, A{(C)p[i], i0 + i});
-  const long long nvec = (n - head) / V;
+  const unsigned un = (unsigned)n;
+  unsigned head = (unsigned)(((16 - ((uintptr_t)p & 15u)) & 15u) / sizeof(T));
+  if (((uintptr_t)p % sizeof(T)) != 0) head = un;
+  if (head > un) head = un;
+  for (unsigned i = tid; i < head; i += kBlock) visit((C)p[i], i);
+  const unsigned nvec = (un - head) / V;
   const u32x4 *pv = reinterpret_cast<const u32x4 *>(p + head);
-  long long j = tid;
+  unsigned j = tid;
   for (; j + (kUnroll - 1) * kBlock < nvec; j += kUnroll * kBlock) {
     Pack<T> q[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) q[u].v = __builtin_nontemporal_load(pv + j + u * kBlock);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const long long ib = i0 + head + (j + u * kBlock) * V;
+      const unsigned ib = head + (j + u * kBlock) * V;
 #pragma unroll
-      for (int e = 0; e < V; ++e) best = R::comb(best, A{(C)q[u].e[e], ib + e});
+      for (int e = 0; e < V; ++e) visit((C)q[u].e[e], ib + e);
     }
   }
   for (; j < nvec; j += kBlock) {
     Pack<T> q;
     q.v = __builtin_nontemporal_load(pv + j);
-    const long long ib = i0 + head + j * V;
+    const unsigned ib = head + j * V;
 #pragma unroll
-    for (int e = 0; e < V; ++e) best = R::comb(best, A{(C)q.e[e], ib + e});
+    for (int e = 0; e < V; ++e) visit((C)q.e[e], ib + e);
   }
-  for (long long i = head + nvec * V + tid; i < n; i += kBlock)
-    best = R::comb(best, A{(C)p[i], i0 + i});
-  return best;
+  for (unsigned i = head + nvec * V + tid; i < un; i += kBlock) visit((C)p[i], i);
+  if (bi == kNone) return R::ident();
+  return A{bv, i0 + (long long)bi};
 }
 
 // ------------------------------------------------------ finalizers

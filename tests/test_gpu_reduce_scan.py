@@ -95,6 +95,45 @@ def test_nan_rules_and_ties():
     assert cp.argmax(cp.array(big)) == 17 == C.argmax_f32(big)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.float64, np.int32, np.int64,
+                                   np.uint32, np.int16, np.bool_])
+def test_argmax_argmin_extremes_and_first_occurrence(dtype):
+    """Rows whose extreme equals the reduction's identity (all -inf / +inf,
+    all INT_MIN / INT_MAX, all False) must still report index 0; ties
+    between elements that different threads visit resolve to the smaller
+    index; the first NaN wins in float rows."""
+    g = np.random.default_rng(11)
+    rows, cols = 9, 70001
+    if np.dtype(dtype).kind == "f":
+        m = g.standard_normal((rows, cols)).astype(dtype)
+        m[0] = -np.inf
+        m[1] = np.inf
+        m[2, [50000, 7, 30000]] = np.nan
+        m[3, [60000, 1234]] = np.inf
+    elif dtype == np.bool_:
+        m = g.random((rows, cols)) < 0.5
+        m[0] = False
+        m[1] = True
+    else:
+        info = np.iinfo(dtype)
+        m = g.integers(info.min // 2 if info.min else 0, info.max // 2, (rows, cols)).astype(dtype)
+        m[0] = info.min
+        m[1] = info.max
+        m[3, [60000, 1234]] = info.max
+        m[4, [65000, 4321]] = info.min
+    M = cp.array(m)
+    for axis in (1, None):
+        want_max = np.argmax(m, axis=axis)
+        want_min = np.argmin(m, axis=axis)
+        got_max = cp.argmax(M, axis=axis)
+        got_min = cp.argmin(M, axis=axis)
+        if axis is None:
+            assert got_max == int(want_max) and got_min == int(want_min)
+        else:
+            assert np.array_equal(got_max.get(), want_max)
+            assert np.array_equal(got_min.get(), want_min)
+
+
 def test_reference_known_answers():
     # tests/test_edge_shapes.py:367-378: sum of 1M ones
     assert float(cp.sum(cp.ones(1_000_000, dtype=np.float32)).get()) == 1e6

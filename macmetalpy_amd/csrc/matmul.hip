@@ -18,6 +18,9 @@
 //    are k-contiguous; B arrives n-contiguous from HBM and is transposed in
 //    registers (each thread owns an 8(k) x 4(n) block) before the LDS store.
 //    Accumulation in fp32 (the reference accumulates float16 in half).
+//    Products with 256-divisible extents, 16-byte aligned rows and at least
+//    128 output tiles of 256 x 256 use k_gemm16_dma instead (256 x 256
+//    tiles, operands copied global -> LDS without passing through VGPRs).
 //  * float32 / float64: v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64.  The
 //    k slot a lane feeds is permuted (MFMA step t, lane group g consumes
 //    k = KG*g + t), so a lane's A values for a whole slab are contiguous in
@@ -182,66 +185,60 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm16(const T *__restrict__ A,
       }
 }
 
-// ------------------------------------------- 16-bit inputs, large tiles
+// ---------------------------- 16-bit inputs, large tiles, global -> LDS DMA
 // 256 x 256 output tile per workgroup for operands whose extents divide
-// the tile and whose rows are 16-byte aligned.  WM x WN waves (2 x 4 by
-// default: eight waves, two per SIMD, each owning a 128 x 64 sub-tile with
-// its 128 fp32 accumulators in VGPRs); one workgroup per CU.  Per 64-deep
-// k slab a workgroup moves 64 KiB L2 -> LDS for 256 x 256 x 64 MACs, half
-// the L2 traffic per flop of a 128 x 128 tile.
-//  * Loading (eight waves): waves 0-3 fetch B, waves 4-7 fetch A, every
-//    thread as eight 16-byte row pieces.  A is stored unchanged
-//    (k-contiguous); a B thread owns an 8(k) x 8(n) block and transposes it
-//    in registers (v_perm) into eight k-contiguous columns.  Eight
-//    consecutive lanes cover one 128 B row segment in HBM and one LDS row.
-//  * LDS: two buffers of 256 rows x 128 B for each operand, 16-byte chunks
-//    XOR-swizzled per row (see swz below): conflict-free fragment reads and
-//    stores.
-//  * Pipeline per slab kt: store slab kt + 1 (already in registers) to the
-//    idle buffer, issue the global loads of slab kt + 2, run slab kt's
-//    MFMAs with the loads spread between them, one barrier.
+// the tile and whose rows are 16-byte aligned.  Eight waves (2 x 4, two per
+// SIMD), each owning a 128 x 64 sub-tile with its 128 fp32 accumulators in
+// VGPRs; one workgroup per CU.  Per 64-deep k slab a workgroup moves 64 KiB
+// L2 -> LDS for 256 x 256 x 64 MACs.  Every operand byte goes HBM/L2 -> LDS
+// with global_load_lds_dwordx4 (lane L of a wave's load lands at 16 B x L of
+// the destination), so there is no register staging, no ds_write and no
+// register transposition:
+//  * Loading: waves 0-3 fill B, waves 4-7 fill A, eight 1 KiB loads per
+//    wave per slab.
+//  * A stage: 256 rows x 128 B (k-contiguous, as in HBM), 16-byte chunk c
+//    of row r at c ^ ((r >> 1) & 7); a load instruction fills 8 rows, each
+//    lane fetching the global chunk that belongs at its landing slot.
+//  * B stage: 64 k-rows x 512 B (n-contiguous, as in HBM), 16-byte chunk c
+//    of row k at c ^ fb(k), fb(k) = 2 * ((k & 3) | ((k >> 3) & 3) << 2), so
+//    that the 16 rows one transposed read touches fall in distinct 32 B
+//    slots.  B fragments come from ds_read_b64_tr_b16 (measured on gfx950:
+//    within each 16-lane group, result element j of lane 4a + b is element
+//    b of the 8 bytes addressed by lane a + 4j): two reads give a lane the
+//    8 consecutive k of one column that the MFMA operand needs.  Both
+//    layouts read without LDS bank conflicts (SQ_LDS_BANK_CONFLICT = 0).
+//  * Two stages as separate LDS arrays, k loop unrolled by two, so the
+//    compiler can tell that the MFMA reads of one stage never alias the
+//    loads in flight into the other; slab kt + 1 is loaded while slab kt
+//    runs, and the barrier at the end of each slab waits for this wave's
+//    loads (vmcnt) before publishing the stage.
 //  * The MFMA is issued as C^T = B^T A^T (operands swapped), so a lane's
 //    four accumulators are four consecutive columns of one C row: the
 //    epilogue writes 8 B per lane per 16 x 16 tile.
 //  * Workgroup ids are remapped so that the tiles one XCD runs together
 //    (ids are dealt round-robin over the eight XCDs) form 4-row groups:
 //    concurrent workgroups on an XCD share A and B panels in its L2.
-// Measured at 8192^3 float16 on MI355X: 0.85 PF/s (1.31 ms).  The same loop
-// without global loads reaches 1.4 PF/s and a register-fed MFMA loop with
-// random operands 1.6 PF/s (operand-dependent power limits the clock), so
-// the remaining gap is the global->LDS path.
-#ifndef MMP_GEMM16_SPLIT
-#define MMP_GEMM16_SPLIT 1
-#endif
-#ifndef MMP_GEMM16_INTERLEAVE
-#define MMP_GEMM16_INTERLEAVE 1
-#endif
+// Measured at 8192^3 float16 on MI355X: 1.13 PF/s (0.97 ms); torch.matmul
+// (hipBLASLt) on the same device 1.22 PF/s.  Register-staged loading
+// (global -> VGPR -> ds_write, B transposed with v_perm) reached 0.88 PF/s;
+// a four-stage 32-deep variant of this kernel 1.10 PF/s (twice the
+// barriers).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-template <int BW> struct BRow;
-template <> struct BRow<8> { typedef u32x4 type; };
-template <> struct BRow<4> { typedef u32x2 type; };
-
-template <typename T, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm16_big(
+template <typename T>
+__global__ __launch_bounds__(512, 1) void k_gemm16_dma(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
     int tiles_m, int tiles_n) {
-  constexpr int NT = 64 * WM * WN;
-  constexpr int TB = 256, BK = 64, LDK = BK;
-  constexpr int TM = TB / WM, TN = TB / WN;   // wave tile
-  constexpr int I = TM / 16, J = TN / 16;     // 16 x 16 MFMA tiles per wave
-  constexpr int AV = TB * (BK / 8) / NT;      // A vectors per thread
-  constexpr int BW = TB * BK / (NT * 8);      // B block width (n)
-  static_assert(BW == 4 || BW == 8, "B block width");
+  constexpr int WN = 4, TB = 256, BK = 64;
+  constexpr int TM = 128, TN = 64, I = TM / 16, J = TN / 16;
   typedef typename Half16<T>::vec V;
-  typedef typename BRow<BW>::type BR;
-  __shared__ __attribute__((aligned(16))) unsigned short As[2][TB * LDK];
-  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][TB * LDK];
+  __shared__ __attribute__((aligned(16))) unsigned short As0[TB * BK], As1[TB * BK];
+  __shared__ __attribute__((aligned(16))) unsigned short Bs0[BK * TB], Bs1[BK * TB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // XCD-aware, 4-row grouped tile order
   const int nblk = tiles_m * tiles_n;
   int b = blockIdx.x;
   if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
@@ -257,93 +254,32 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm16_big(
                              (long long)m0 * lda;
   const unsigned short *Bg = reinterpret_cast<const unsigned short *>(B + bz * sB) + n0;
 
-  u32x4 ra[AV];
-  BR rb[8];
-  const int a_row = tid >> 3, a_kv = tid & 7;
-  const int b_k8 = tid & 7, b_nb = tid >> 3;
-  // LDS rows are 128 B (64 k); 16-byte chunk c of row r is stored at
-  // chunk c ^ ((r >> 1) & 7).  Measured on gfx950: ds_read_b128 serves
-  // 16 lanes per cycle (lanes sharing bits 1 and 5 of the lane id) and
-  // conflicts when two of them hit the same 16 B slot modulo 512 B; with
-  // this swizzle the fragment reads (16 rows x 2 chunks per lane group)
-  // and the row-contiguous stores are conflict-free, where a 144 B row
-  // pitch gave 2-way conflicts on every fragment read.
   auto swz = [](int r) { return (r >> 1) & 7; };
-  const int a_swz = swz(a_row);
+  auto fb = [](int k) { return 2 * ((k & 3) | (((k >> 3) & 3) << 2)); };
 
-  // With eight waves, the first four load B and the last four load A, each
-  // thread as eight 16-byte row pieces (a B thread owns an 8(k) x 8(n)
-  // block, an A thread eight row segments): every global load is 16 bytes
-  // wide and each wave issues eight, instead of twelve half of which move
-  // only 8 bytes per lane.  The role test is uniform per wave.
-  constexpr bool SPLIT = NT == 512 && MMP_GEMM16_SPLIT;
-  const bool b_role = tid < 256;
-  const int t2 = tid & 255;
-  const int s_k8 = t2 & 7, s_nb = t2 >> 3;     // B role: 8 x 8 block
-  const int s_row = t2 >> 3, s_kv = t2 & 7;    // A role: rows s_row + 32p
-  const int s_swz = swz(s_row);
-  u32x4 rs[8];
-  auto load_split = [&](int k0) {
+  // Loads: waves 0-3 fill B (each wave 8 instructions x 2 rows of 512 B),
+  // waves 4-7 fill A (each wave 8 instructions x 8 rows of 128 B).  Per
+  // lane, the global offset (halves) of instruction p for slab k0 = 0.
+  const bool b_role = wave < 4;
+  const int w4 = wave & 3;
+  long long goff[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int inst = w4 * 8 + p;              // 0..31 within the stage
     if (b_role) {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        rs[kk] = *reinterpret_cast<const u32x4 *>(Bg + (long long)(k0 + s_k8 * 8 + kk) * ldb + s_nb * 8);
+      const int row = inst * 2 + (lane >> 5), slot = lane & 31;
+      goff[p] = (long long)row * ldb + (slot ^ fb(row)) * 8;
     } else {
-#pragma unroll
-      for (int p = 0; p < 8; ++p)
-        rs[p] = *reinterpret_cast<const u32x4 *>(Ag + (long long)(s_row + 32 * p) * lda + k0 + s_kv * 8);
+      const int row = inst * 8 + (lane >> 3), slot = lane & 7;
+      goff[p] = (long long)row * lda + (slot ^ swz(row)) * 8;
     }
-  };
-  auto store_split = [&](int buf) {
-    if (b_role) {
+  }
+  auto issue = [&](unsigned short *As_, unsigned short *Bs_, int k0) {
+    const unsigned short *g = b_role ? Bg + (long long)k0 * ldb : Ag + k0;
+    unsigned short *dst = b_role ? Bs_ : As_;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 w;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          w[d] = __builtin_amdgcn_perm(rs[2 * d + 1][c >> 1], rs[2 * d][c >> 1], sel);
-        *reinterpret_cast<u32x4 *>(&Bs[buf][(s_nb * 8 + c) * LDK + (s_k8 ^ swz(s_nb * 8 + c)) * 8]) = w;
-      }
-    } else {
-#pragma unroll
-      for (int p = 0; p < 8; ++p)
-        *reinterpret_cast<u32x4 *>(&As[buf][(s_row + 32 * p) * LDK + (s_kv ^ s_swz) * 8]) = rs[p];
-    }
-  };
-
-  auto load = [&](int k0) {
-    if constexpr (SPLIT) {
-      load_split(k0);
-      return;
-    }
-#pragma unroll
-    for (int p = 0; p < AV; ++p)
-      ra[p] = *reinterpret_cast<const u32x4 *>(Ag + (long long)(a_row + (NT / 8) * p) * lda +
-                                               k0 + a_kv * 8);
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      rb[kk] = *reinterpret_cast<const BR *>(Bg + (long long)(k0 + b_k8 * 8 + kk) * ldb +
-                                             b_nb * BW);
-  };
-  auto store = [&](int buf) {
-    if constexpr (SPLIT) {
-      store_split(buf);
-      return;
-    }
-#pragma unroll
-    for (int p = 0; p < AV; ++p)
-      *reinterpret_cast<u32x4 *>(&As[buf][(a_row + (NT / 8) * p) * LDK + (a_kv ^ a_swz) * 8]) = ra[p];
-    // column c of the 8 x BW block: half c of each of the eight rows
-#pragma unroll
-    for (int c = 0; c < BW; ++c) {
-      const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
-      u32x4 w;
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        w[d] = __builtin_amdgcn_perm(rb[2 * d + 1][c >> 1], rb[2 * d][c >> 1], sel);
-      *reinterpret_cast<u32x4 *>(&Bs[buf][(b_nb * BW + c) * LDK + (b_k8 ^ swz(b_nb * BW + c)) * 8]) = w;
-    }
+    for (int p = 0; p < 8; ++p)
+      __builtin_amdgcn_global_load_lds(g + goff[p], dst + (w4 * 8 + p) * 512, 16, 0, 0);
   };
 
   f4 acc[I][J];
@@ -352,20 +288,31 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm16_big(
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = K / BK;
-  const int fr = lane & 15;
-  // fragment chunk offsets (halves) of sub-steps 0 and 1 for this lane
-  const int fch[2] = {(((lane >> 4) + 0) ^ swz(fr)) * 8, (((lane >> 4) + 4) ^ swz(fr)) * 8};
-  auto mfmas = [&](int cur) {
+  const int fr = lane & 15, grp = lane >> 4;
+  const int fch[2] = {((grp + 0) ^ swz(fr)) * 8, ((grp + 4) ^ swz(fr)) * 8};
+  auto mfmas = [&](const unsigned short *As_, const unsigned short *Bs_) {
 #pragma unroll
     for (int s = 0; s < BK / 32; ++s) {
       V af[I], bf[J];
 #pragma unroll
       for (int i = 0; i < I; ++i)
-        af[i] = *reinterpret_cast<const V *>(&As[cur][(wm * TM + i * 16 + fr) * LDK + fch[s]]);
+        af[i] = *reinterpret_cast<const V *>(&As_[(wm * TM + i * 16 + fr) * BK + fch[s]]);
 #pragma unroll
-      for (int j = 0; j < J; ++j)
-        bf[j] = *reinterpret_cast<const V *>(&Bs[cur][(wn * TN + j * 16 + fr) * LDK + fch[s]]);
+      for (int j = 0; j < J; ++j) {
+        // lane (group grp, index q) addresses k row 32s + 8grp + q/4 (+4),
+        // columns 4 (q % 4) .. +3 of the 16-column tile
+        const int q = fr;
+        const int col = wn * TN + j * 16 + 4 * (q & 3);
+        const int k1 = s * 32 + grp * 8 + (q >> 2), k2 = k1 + 4;
+        const int c8 = col >> 3, w = col & 7;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(Bs_ + k1 * TB + ((c8 ^ fb(k1)) << 3) + w));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(Bs_ + k2 * TB + ((c8 ^ fb(k2)) << 3) + w));
+        typedef short s16x8 __attribute__((ext_vector_type(8)));
+        const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        bf[j] = __builtin_bit_cast(V, v8);
+      }
 #pragma unroll
       for (int i = 0; i < I; ++i)
 #pragma unroll
@@ -373,38 +320,20 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm16_big(
     }
   };
 
-  // Pipeline: slab kt + 1 sits in registers when step kt begins.  The step
-  // writes it to the idle LDS buffer, refills the registers with slab
-  // kt + 2 (clamped to the last slab; the surplus copy is never read) and
-  // then runs slab kt's MFMAs from the other buffer, so the LDS stores and
-  // the global-load latency overlap the MFMAs instead of separating them;
-  // one barrier per slab.  Straight-line steps let the scheduler interleave
-  // loads, LDS traffic and MFMAs.
-  load(0);
-  store(0);
-  load(min(1, nk - 1) * BK);
+  const int nk = K / BK;
+  issue(As0, Bs0, 0);
   __syncthreads();
-  constexpr int NLOAD = SPLIT ? 8 : AV + 8;  // global loads per thread per slab
-  constexpr int NMFMA = 2 * I * J;          // MFMAs per wave per slab
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    store(cur ^ 1);
-    load(min(kt + 2, nk - 1) * BK);
-    mfmas(cur);
-#if MMP_GEMM16_INTERLEAVE
-    // spread the global loads over the MFMA stream: a wave that issues all
-    // of them back to back stalls on the full address queue and starves
-    // the matrix core
-#pragma unroll
-    for (int g = 0; g < NLOAD; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // 1 VMEM read
-      __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NLOAD, 0);    // MFMAs
-    }
-#endif
+  for (int kt = 0; kt < nk; kt += 2) {
+    if (kt + 1 < nk) issue(As1, Bs1, (kt + 1) * BK);
+    mfmas(As0, Bs0);
     __syncthreads();
+    if (kt + 1 < nk) {
+      if (kt + 2 < nk) issue(As0, Bs0, (kt + 2) * BK);
+      mfmas(As1, Bs1);
+      __syncthreads();
+    }
   }
 
-  // epilogue: accumulator r of lane l is C[row l % 16][col 4 * (l / 16) + r]
   T *Cb = C + bz * sC;
   const int cr = lane & 15, cc = (lane >> 4) * 4;
 #pragma unroll
@@ -590,13 +519,8 @@ __global__ __launch_bounds__(kBlock) void k_gemm_int(const T *__restrict__ A, co
 // -------------------------------------------------------------- launch
 inline bool al(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
-// Large-tile kernel: 2 = 2 x 4 waves of 128 x 64 (default), 1 = 2 x 2
-// waves of 128 x 128 (slower: the compiler shuffles its 256 accumulators
-// between register files), 0 = off.  Used once the product has at least
-// MMP_GEMM16_BIG_MIN_TILES 256 x 256 tiles (fewer leave CUs idle).
-#ifndef MMP_GEMM16_BIG
-#define MMP_GEMM16_BIG 2
-#endif
+// The 256 x 256 kernel is used once the product has at least
+// MMP_GEMM16_BIG_MIN_TILES tiles (fewer leave CUs idle).
 #ifndef MMP_GEMM16_BIG_MIN_TILES
 #define MMP_GEMM16_BIG_MIN_TILES 128
 #endif
@@ -604,20 +528,13 @@ inline bool al(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 template <typename T>
 int launch16(long long batch, int M, int N, int K, const void *A, long long lda, long long sA,
              const void *B, long long ldb, long long sB, void *C, long long ldc, long long sC) {
-  if (MMP_GEMM16_BIG && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && lda % 8 == 0 &&
-      ldb % 8 == 0 && ldc % 4 == 0 && sA % 8 == 0 && sB % 8 == 0 && sC % 4 == 0 && al(A, 16) &&
-      al(B, 16) && al(C, 8) &&
-      (long long)(M / 256) * (N / 256) * batch >= MMP_GEMM16_BIG_MIN_TILES) {
+  if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+      ldc % 4 == 0 && sA % 8 == 0 && sB % 8 == 0 && sC % 4 == 0 && al(A, 16) && al(B, 16) &&
+      al(C, 8) && (long long)(M / 256) * (N / 256) * batch >= MMP_GEMM16_BIG_MIN_TILES) {
     const int tm = M / 256, tn = N / 256;
-    dim3 grid((unsigned)(tm * tn), (unsigned)batch);
-    if (MMP_GEMM16_BIG == 2)
-      hipLaunchKernelGGL((k_gemm16_big<T, 2, 4>), grid, dim3(512), 0, mmpi::stream(),
-                         (const T *)A, (const T *)B, (T *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
-                         tm, tn);
-    else
-      hipLaunchKernelGGL((k_gemm16_big<T, 2, 2>), grid, dim3(256), 0, mmpi::stream(),
-                         (const T *)A, (const T *)B, (T *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
-                         tm, tn);
+    hipLaunchKernelGGL((k_gemm16_dma<T>), dim3((unsigned)(tm * tn), (unsigned)batch), dim3(512), 0,
+                       mmpi::stream(), (const T *)A, (const T *)B, (T *)C, M, N, K, lda, ldb,
+                       ldc, sA, sB, sC, tm, tn);
     return mmpi::check_launch("mmp_matmul(mfma16 256x256)");
   }
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;

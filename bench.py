@@ -204,7 +204,7 @@ def bench_c3(cp, be, reps=10):
 
 
 # --------------------------------------------------------------- C4
-def bench_c4(cp, be, reps=5):
+def bench_c4(cp, be, reps=20, warm=10):
     from macmetalpy_amd.workloads import c4_inputs
     res = {}
     for kind, dt in (("f32", "float32"), ("f16", "float16"), ("batched", "float32")):
@@ -217,7 +217,10 @@ def bench_c4(cp, be, reps=5):
                 a_np.shape[0] if a_np.ndim == 3 else 1)
             del a_np, b_np
             f = lambda: a @ b  # noqa: E731
-            f()
+            # the matrix cores' clock settles over the first few ms of
+            # sustained MFMA work: time steady state, mean of `reps` launches
+            for _ in range(warm):
+                f()
             cp.synchronize()
             timer = EventTimer(be)
             for _ in range(reps):

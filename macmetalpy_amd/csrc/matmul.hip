@@ -218,8 +218,8 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm16(const T *__restrict__ A,
 //  * Workgroup ids are remapped so that the tiles one XCD runs together
 //    (ids are dealt round-robin over the eight XCDs) form 4-row groups:
 //    concurrent workgroups on an XCD share A and B panels in its L2.
-// Measured at 8192^3 float16 on MI355X: 1.13 PF/s (0.97 ms); torch.matmul
-// (hipBLASLt) on the same device 1.22 PF/s.  Register-staged loading
+// Measured at 8192^3 float16 on MI355X: 1.17-1.18 PF/s (0.93-0.94 ms);
+// torch.matmul (hipBLASLt) on the same device 1.22 PF/s.  Register-staged loading
 // (global -> VGPR -> ds_write, B transposed with v_perm) reached 0.88 PF/s;
 // a four-stage 32-deep variant of this kernel 1.10 PF/s (twice the
 // barriers).
@@ -321,15 +321,31 @@ __global__ __launch_bounds__(512, 1) void k_gemm16_dma(
   };
 
   const int nk = K / BK;
+  // Instruction order within a slab: the 16 LDS reads of the first 32-deep
+  // half, then its MFMAs with the second half's 16 reads placed one after
+  // every other MFMA, then the second half's MFMAs.  Left to itself the
+  // compiler reads two A fragments at a time and waits for them right
+  // before their MFMAs; this order keeps a half-slab of reads in flight
+  // (1.07 -> 1.17 PF/s at 8192^3).
+  auto sched = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+#pragma unroll
+    for (int m = 0; m < 64; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (m < 32 && (m & 1)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
   issue(As0, Bs0, 0);
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 2) {
     if (kt + 1 < nk) issue(As1, Bs1, (kt + 1) * BK);
     mfmas(As0, Bs0);
+    sched();
     __syncthreads();
     if (kt + 1 < nk) {
       if (kt + 2 < nk) issue(As0, Bs0, (kt + 2) * BK);
       mfmas(As1, Bs1);
+      sched();
       __syncthreads();
     }
   }

@@ -238,6 +238,43 @@ def bench_c4(cp, be, reps=20, warm=10):
     return res
 
 
+# ------------------------------- bitwise / logical / where / clip / any
+def bench_logic(cp, be, reps=10):
+    """Bitwise, predicate, where, clip and any/count_nonzero at 2^28 elements
+    on the C2 inputs; bytes are each op's algorithmic HBM bytes (operands
+    read once, result written once; bool results 1 B)."""
+    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    a, b = (cp.array(x) for x in c2_float_inputs(N28))
+    ia, ib = (cp.array(x) for x in c2_int_inputs(N28))
+    for x in (a, b, ia, ib):
+        x._ensure_gpu()
+    cases = {
+        "bitwise_and_i32": (lambda: _mat(ia & ib), 12),
+        "right_shift_i32": (lambda: _mat(ia >> 3), 8),
+        "isnan_f32": (lambda: _mat(cp.isnan(a)), 5),
+        "where_f32": (lambda: _mat(cp.where(a > 0, a, b)), 12),
+        "clip_f32": (lambda: _mat(cp.clip(a, -1.0, 1.0)), 8),
+        "any_f32": (lambda: cp.any(a > 3.0), 4),
+        "count_nonzero_f32": (lambda: cp.count_nonzero(a > 0, axis=0), 4),
+    }
+    res = {}
+    for name, (f, bpe) in cases.items():
+        try:
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(name, f)
+            cp.synchronize()
+            ms, _ = timer.ms(name)
+            timer.close()
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
+                         "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
 # --------------------------------------------------------------- C5
 def bench_c5(cp, be, reps=10):
     from macmetalpy_amd.workloads import c5_inputs
@@ -421,7 +458,8 @@ def main():
     if args.suite == "all":
         cfgs = {}
         for name, fn in (("c1_fused_elementwise", bench_c1), ("c3_reduce_scan", bench_c3),
-                         ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5)):
+                         ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5),
+                         ("logic_where_clip_2p28", bench_logic)):
             t = time.time()
             try:
                 cfgs[name] = fn(cp, be)

@@ -2,7 +2,9 @@
 
 Drop-in for the reference's ``import macmetalpy as cp`` names on the hot
 path (src/macmetalpy/__init__.py:8-236): ndarray, creation, random inputs,
-elementwise ufuncs, sum/mean/max/min/prod/argmax/argmin, cumsum/cumprod,
+elementwise ufuncs (arithmetic, transcendental, comparison, bitwise,
+logical, predicates), where / clip, sum/mean/max/min/prod/argmax/argmin,
+any/all/count_nonzero, cumsum/cumprod,
 matmul / linalg.matmul / dot, RawKernel, set_config and synchronize.
 Unlike the reference (darwin-only, __init__.py:5-6) it imports on any host;
 device work needs libmmp_hip.so and a gfx950 GPU and raises otherwise.
@@ -29,10 +31,14 @@ from .ufunc_ops import (
     maximum, minimum, fmax, fmin, arctan2, hypot, fmod, copysign, nextafter, logaddexp,
     logaddexp2, heaviside, float_power, divmod,
     less, less_equal, greater, greater_equal, equal, not_equal,
+    invert, bitwise_not, bitwise_invert, bitwise_and, bitwise_or, bitwise_xor, left_shift,
+    right_shift, bitwise_left_shift, bitwise_right_shift, logical_and, logical_or,
+    logical_xor, logical_not, isnan, isinf, isfinite, signbit,
 )
+from .math_ops import where, clip, count_nonzero
 from .reductions import (
-    sum, mean, prod, max, min, amax, amin, argmax, argmin, cumsum, cumprod, var, std,
-    cumulative_sum, cumulative_prod,
+    sum, mean, prod, max, min, amax, amin, argmax, argmin, any, all, cumsum, cumprod, var,
+    std, cumulative_sum, cumulative_prod,
 )
 from .linalg_top import matmul, dot, vdot, inner
 from . import linalg

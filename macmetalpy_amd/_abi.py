@@ -121,6 +121,40 @@ COMPARE_OPS: dict[str, tuple[np.ufunc, str]] = {
     "ne_op": (np.not_equal, "!="),
 }
 
+# Ops the fusion engine generates kernels for, with no precompiled entry
+# point (reference: bitwise_ops.py:58-93, logic_ops.py:45-63,
+# math_ops.py:558-578, ufunc_ops.py:352): op_name -> (numpy ufunc,
+# mmp_ops.h function).
+EXPR_UNARY_OPS: dict[str, tuple[np.ufunc, str]] = {
+    "invert_op": (np.invert, "op_invert"),
+    "logical_not_op": (np.logical_not, "op_logical_not"),
+    "isnan_op": (np.isnan, "op_isnan"),
+    "isinf_op": (np.isinf, "op_isinf"),
+    "isfinite_op": (np.isfinite, "op_isfinite"),
+    "signbit_op": (np.signbit, "op_signbit"),
+}
+EXPR_BINARY_OPS: dict[str, tuple[np.ufunc, str]] = {
+    "bit_and_op": (np.bitwise_and, "op_bitwise_and"),
+    "bit_or_op": (np.bitwise_or, "op_bitwise_or"),
+    "bit_xor_op": (np.bitwise_xor, "op_bitwise_xor"),
+    "lshift_op": (np.left_shift, "op_left_shift"),
+    "rshift_op": (np.right_shift, "op_right_shift"),
+    "logical_and_op": (np.logical_and, "op_logical_and"),
+    "logical_or_op": (np.logical_or, "op_logical_or"),
+    "logical_xor_op": (np.logical_xor, "op_logical_xor"),
+}
+# Ops with a bool result that read their operands in the operands' own
+# (common) dtype, like the comparisons.
+BOOL_RESULT_OPS = frozenset({"logical_not_op", "isnan_op", "isinf_op", "isfinite_op",
+                             "signbit_op", "logical_and_op", "logical_or_op",
+                             "logical_xor_op"})
+
+# op_name -> mmp_ops.h function, for every unary / binary op
+UNARY_FN = {k: v[2] for k, v in UNARY_OPS.items()}
+UNARY_FN.update({k: v[1] for k, v in EXPR_UNARY_OPS.items()})
+BINARY_FN = {k: v[2] for k, v in BINARY_OPS.items()}
+BINARY_FN.update({k: v[1] for k, v in EXPR_BINARY_OPS.items()})
+
 REDUCE_SUM, REDUCE_PROD, REDUCE_MAX, REDUCE_MIN, REDUCE_MEAN = 0, 1, 2, 3, 4
 REDUCE_ARGMAX, REDUCE_ARGMIN = 5, 6
 SCAN_CUMSUM, SCAN_CUMPROD = 0, 1

@@ -28,10 +28,10 @@ from ._config import get_config
 from ._dtypes import resolve_dtype, ufunc_result_dtype
 from ._fusion import (
     _MAX_DEPTH, _MAX_LEAVES, BinaryOpNode, CastNode, InputNode, ScalarNode, UnaryOpNode,
-    materialize,
+    WhereNode, materialize,
 )
 
-__all__ = ["unary", "binary", "is_scalar", "flush_lazy", "track_lazy"]
+__all__ = ["unary", "binary", "where", "is_scalar", "flush_lazy", "track_lazy"]
 
 
 def is_scalar(x) -> bool:
@@ -141,17 +141,20 @@ def _materialise_operand(x, shape, dtype):
 # ------------------------------------------------------------------ ops
 def unary(op_name: str, x):
     x = _asarray(x)
-    ufunc = _abi.UNARY_OPS[op_name][1]
+    ent = _abi.UNARY_OPS.get(op_name)
+    ufunc = ent[1] if ent is not None else _abi.EXPR_UNARY_OPS[op_name][0]
     rdt = ufunc_result_dtype(ufunc, x._dtype)
+    # predicates read the operand as it is; other ops compute in the result dtype
+    idt = x._dtype if op_name in _abi.BOOL_RESULT_OPS else rdt
     if x.size == 0:
         return _empty(x._shape, rdt)
     if not get_config().fusion:
-        xin = _materialise_operand(x, x._shape, rdt)
-        node = UnaryOpNode(op_name, _node_of(xin, rdt), x._shape, rdt)
+        xin = _materialise_operand(x, x._shape, idt)
+        node = UnaryOpNode(op_name, _node_of(xin, idt), x._shape, rdt)
         out = _lazy_result(node)
         materialize(out)
         return out
-    node = _limit(x, _node_of(x, rdt), rdt)
+    node = _limit(x, _node_of(x, idt), idt)
     return _lazy_result(UnaryOpNode(op_name, node, x._shape, rdt))
 
 
@@ -180,14 +183,16 @@ def binary(op_name: str, a, b):
         a_arr = True
     ka = a._dtype if a_arr else _scalar_operand(a)
     kb = b._dtype if b_arr else _scalar_operand(b)
-    if op_name in _abi.COMPARE_OPS:
-        # NumPy compares in the operands' common dtype and returns bool
-        ufunc = _abi.COMPARE_OPS[op_name][0]
+    if op_name in _abi.COMPARE_OPS or op_name in _abi.BOOL_RESULT_OPS:
+        # NumPy compares (and tests truth) in the operands' common dtype and
+        # returns bool
+        ufunc = (_abi.COMPARE_OPS.get(op_name) or _abi.EXPR_BINARY_OPS[op_name])[0]
         ufunc_result_dtype(ufunc, ka, kb)  # raises for invalid operands
         odt = resolve_dtype(np.result_type(ka, kb))
         rdt = np.dtype(np.bool_)
     else:
-        ufunc = _abi.BINARY_OPS[op_name][1]
+        ent = _abi.BINARY_OPS.get(op_name)
+        ufunc = ent[1] if ent is not None else _abi.EXPR_BINARY_OPS[op_name][0]
         rdt = ufunc_result_dtype(ufunc, ka, kb)
         odt = rdt
     sa = a._shape if a_arr else ()
@@ -224,6 +229,55 @@ def binary(op_name: str, a, b):
             materialize(b)
             bn = _node_of(b, odt)
     return _lazy_result(BinaryOpNode(op_name, an, bn, shape, rdt))
+
+
+def where(cond, x, y):
+    """``x`` where ``cond`` is true, else ``y``, broadcast together
+    (reference math_ops.py:106-155).  The result dtype is NumPy's
+    ``result_type(x, y)`` (Python scalars weak); ``cond`` is read as its
+    truth value.  Lazy like the other elementwise ops."""
+    nd = _ndarray()
+    cond = cond if isinstance(cond, nd) else _asarray(cond)
+    ops = []
+    for v in (x, y):
+        if not isinstance(v, nd) and not is_scalar(v):
+            v = _asarray(v)
+        ops.append(v)
+    x, y = ops
+    x_arr, y_arr = isinstance(x, nd), isinstance(y, nd)
+    kx = x._dtype if x_arr else _scalar_operand(x)
+    ky = y._dtype if y_arr else _scalar_operand(y)
+    rdt = resolve_dtype(np.result_type(kx, ky))
+    shape = broadcast_shapes(cond._shape, x._shape if x_arr else (), y._shape if y_arr else ())
+    size = 1
+    for s in shape:
+        size *= s
+    if size == 0:
+        return _empty(shape, rdt)
+    bdt = np.dtype(np.bool_)
+    unfused = not get_config().fusion
+
+    def leaf(v, is_arr, dt):
+        if not is_arr:
+            return ScalarNode(v, dt)
+        if unfused:
+            return _node_of(_materialise_operand(v, shape, dt), dt)
+        return _limit(v, _node_of(v, dt), dt)
+
+    cn = leaf(cond, True, bdt)
+    xn = leaf(x, x_arr, rdt)
+    yn = leaf(y, y_arr, rdt)
+    if cn._nleaves + xn._nleaves + yn._nleaves > _MAX_LEAVES:
+        for v, is_arr in ((cond, True), (x, x_arr), (y, y_arr)):
+            if is_arr and v._fusion_node is not None:
+                materialize(v)
+        cn = leaf(cond, True, bdt)
+        xn = leaf(x, x_arr, rdt)
+        yn = leaf(y, y_arr, rdt)
+    out = _lazy_result(WhereNode(cn, xn, yn, shape, rdt))
+    if unfused:
+        materialize(out)
+    return out
 
 
 def _check_int_power(exp_arr, exp_scalar):

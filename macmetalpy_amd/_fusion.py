@@ -41,7 +41,7 @@ from ._dtypes import ctype_name, dtype_code
 
 __all__ = [
     "FusionNode", "InputNode", "ScalarNode", "UnaryOpNode", "BinaryOpNode", "CastNode",
-    "materialize", "materialize_reduce", "generate_source", "_MAX_DEPTH", "RTC_OPTIONS",
+    "WhereNode", "materialize", "materialize_reduce", "generate_source", "_MAX_DEPTH", "RTC_OPTIONS",
 ]
 
 _MAX_DEPTH = 16
@@ -147,6 +147,22 @@ class BinaryOpNode(FusionNode):
         self._nleaves = lhs._nleaves + rhs._nleaves
 
 
+class WhereNode(FusionNode):
+    """``cond ? x : y`` (reference where_shader, _kernels.py:984-1000);
+    ``cond`` is a bool node, ``x`` and ``y`` have the result dtype."""
+    __slots__ = ("_cond", "_x", "_y")
+
+    def __init__(self, cond, x, y, shape, dtype):
+        self._cond = cond
+        self._x = x
+        self._y = y
+        self._shape = tuple(shape)
+        self._dtype = np.dtype(dtype)
+        self._depth = max(cond._depth, x._depth, y._depth) + 1
+        self._buffers = _merge_buffers(cond, x, y)
+        self._nleaves = cond._nleaves + x._nleaves + y._nleaves
+
+
 # ---------------------------------------------------------- DAG analysis
 def _c_contig_strides(shape):
     st, acc = [], 1
@@ -198,6 +214,9 @@ class _Program:
             step = ("unary", node._op_name, self._visit(node._input))
         elif isinstance(node, BinaryOpNode):
             step = ("binary", node._op_name, self._visit(node._lhs), self._visit(node._rhs))
+        elif isinstance(node, WhereNode):
+            step = ("where", self._visit(node._cond), self._visit(node._x),
+                    self._visit(node._y))
         else:
             raise TypeError(f"unknown fusion node {type(node).__name__}")
         self.steps.append(step)
@@ -274,9 +293,11 @@ _BITS_T = {1: "unsigned char", 2: "unsigned short", 4: "unsigned int", 8: "unsig
 
 
 def _acc_type(dtype):
+    """Accumulator of a fused sum: float64, uint64 for unsigned inputs,
+    else int64 (NumPy sums bool and signed integers as int64)."""
     if dtype.kind == "f":
         return "double", np.dtype(np.float64)
-    if dtype.kind in "ub":
+    if dtype.kind == "u":
         return "mmp_u64", np.dtype(np.uint64)
     return "mmp_i64", np.dtype(np.int64)
 
@@ -320,11 +341,13 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode):
                 src_t = ctype_name(prog.dtypes[step[1]])
                 rhs = f"mmp_convert<{t}, {src_t}>(t{step[1]})"
             elif kind == "unary":
-                rhs = f"{_abi.UNARY_OPS[step[1]][2]}(t{step[2]})"
+                rhs = f"{_abi.UNARY_FN[step[1]]}(t{step[2]})"
+            elif kind == "where":
+                rhs = f"(t{step[1]} ? t{step[2]} : t{step[3]})"
             elif step[1] in _abi.COMPARE_OPS:
                 rhs = f"(t{step[2]} {_abi.COMPARE_OPS[step[1]][1]} t{step[3]})"
             else:
-                rhs = f"{_abi.BINARY_OPS[step[1]][2]}(t{step[2]}, t{step[3]})"
+                rhs = f"{_abi.BINARY_FN[step[1]]}(t{step[2]}, t{step[3]})"
             out.append(f"{indent}const {t} t{i} = {rhs};")
         return out
 
@@ -595,7 +618,8 @@ def run_sum(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean: bo
 
 
 def is_precompiled_unary(node) -> bool:
-    return (isinstance(node, UnaryOpNode) and isinstance(node._input, InputNode)
+    return (isinstance(node, UnaryOpNode) and node._op_name in _abi.UNARY_OPS
+            and isinstance(node._input, InputNode)
             and node._input._dtype == node._dtype
             and node._input._shape == node._shape
             and node._input._strides == _c_contig_strides(node._shape))

@@ -548,6 +548,70 @@ template <typename T> MMP_DI T op_heaviside(T a_, T h) {
 }
 
 // =====================================================================
+// Bitwise, shift, logical and predicate ops (the reference's boolean_shader,
+// bool_logic_shader and predicate_shader, _kernels.py:870-1049, which work
+// on int32 / uchar buffers; here every NumPy integer dtype, with NumPy's
+// result dtypes).  Used by generated kernels only.
+// =====================================================================
+template <typename T> MMP_DI T op_bitwise_and(T a, T b) {
+  if constexpr (mmp_t<T>::is_bool) return a && b;
+  else return (T)(a & b);
+}
+template <typename T> MMP_DI T op_bitwise_or(T a, T b) {
+  if constexpr (mmp_t<T>::is_bool) return a || b;
+  else return (T)(a | b);
+}
+template <typename T> MMP_DI T op_bitwise_xor(T a, T b) {
+  if constexpr (mmp_t<T>::is_bool) return a != b;
+  else return (T)(a ^ b);
+}
+template <typename T> MMP_DI T op_invert(T a) {
+  if constexpr (mmp_t<T>::is_bool) return !a;
+  else return (T)~a;
+}
+// numpy npy_lshift / npy_rshift: a count outside [0, bits) -- negative
+// counts included, read as unsigned -- shifts everything out: 0, or -1 for
+// a negative value shifted right.
+template <typename T> MMP_DI T op_left_shift(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  if ((U)b < (U)(8 * sizeof(T))) return (T)((U)a << (U)b);
+  return (T)0;
+}
+template <typename T> MMP_DI T op_right_shift(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  if ((U)b < (U)(8 * sizeof(T))) return (T)(a >> b);
+  if constexpr (mmp_t<T>::is_signed) return a < (T)0 ? (T)-1 : (T)0;
+  return (T)0;
+}
+// truth value: nonzero (NaN is true), as NumPy's logical loops test it
+template <typename T> MMP_DI bool mmp_truth(T v) {
+  if constexpr (mmp_t<T>::is_float) return (typename mmp_t<T>::C)v != (typename mmp_t<T>::C)0;
+  else return v != (T)0;
+}
+template <typename T> MMP_DI bool op_logical_and(T a, T b) { return mmp_truth(a) && mmp_truth(b); }
+template <typename T> MMP_DI bool op_logical_or(T a, T b) { return mmp_truth(a) || mmp_truth(b); }
+template <typename T> MMP_DI bool op_logical_xor(T a, T b) { return mmp_truth(a) != mmp_truth(b); }
+template <typename T> MMP_DI bool op_logical_not(T a) { return !mmp_truth(a); }
+template <typename T> MMP_DI bool op_isnan(T a) {
+  if constexpr (mmp_t<T>::is_float) return __builtin_isnan((typename mmp_t<T>::C)a);
+  else return false;
+}
+template <typename T> MMP_DI bool op_isinf(T a) {
+  if constexpr (mmp_t<T>::is_float) return __builtin_isinf((typename mmp_t<T>::C)a);
+  else return false;
+}
+template <typename T> MMP_DI bool op_isfinite(T a) {
+  if constexpr (mmp_t<T>::is_float) return __builtin_isfinite((typename mmp_t<T>::C)a);
+  else return true;
+}
+// sign bit of the representation: true for -0.0 and negative NaNs
+template <typename T> MMP_DI bool op_signbit(T a) {
+  if constexpr (mmp_t<T>::is_float) return __builtin_signbit((typename mmp_t<T>::C)a);
+  else if constexpr (mmp_t<T>::is_signed) return a < (T)0;
+  else return false;
+}
+
+// =====================================================================
 // Conversions (astype).  bool targets test != 0 (NaN -> true).
 // =====================================================================
 template <typename To, typename From> MMP_DI To mmp_convert(From v) {

@@ -462,6 +462,18 @@ class ndarray:
     def __pos__(self): return ew.unary("positive_op", self)
     def __abs__(self): return ew.unary("abs_op", self)
 
+    def __and__(self, o): return ew.binary("bit_and_op", self, o)
+    def __rand__(self, o): return ew.binary("bit_and_op", o, self)
+    def __or__(self, o): return ew.binary("bit_or_op", self, o)
+    def __ror__(self, o): return ew.binary("bit_or_op", o, self)
+    def __xor__(self, o): return ew.binary("bit_xor_op", self, o)
+    def __rxor__(self, o): return ew.binary("bit_xor_op", o, self)
+    def __lshift__(self, o): return ew.binary("lshift_op", self, o)
+    def __rlshift__(self, o): return ew.binary("lshift_op", o, self)
+    def __rshift__(self, o): return ew.binary("rshift_op", self, o)
+    def __rrshift__(self, o): return ew.binary("rshift_op", o, self)
+    def __invert__(self): return ew.unary("invert_op", self)
+
     def __divmod__(self, o):
         return self // o, self % o
 
@@ -495,6 +507,11 @@ class ndarray:
     def __ifloordiv__(self, o): return self._inplace(self.__floordiv__(o))
     def __imod__(self, o): return self._inplace(self.__mod__(o))
     def __ipow__(self, o): return self._inplace(self.__pow__(o))
+    def __iand__(self, o): return self._inplace(self.__and__(o))
+    def __ior__(self, o): return self._inplace(self.__or__(o))
+    def __ixor__(self, o): return self._inplace(self.__xor__(o))
+    def __ilshift__(self, o): return self._inplace(self.__lshift__(o))
+    def __irshift__(self, o): return self._inplace(self.__rshift__(o))
 
     # ----------------------------------------------------- reductions
     def sum(self, axis=None, dtype=None, out=None, keepdims=False):
@@ -516,6 +533,18 @@ class ndarray:
     def min(self, axis=None, out=None, keepdims=False):
         from . import reductions
         return reductions.min(self, axis=axis, out=out, keepdims=keepdims)
+
+    def any(self, axis=None, out=None, keepdims=False):
+        from . import reductions
+        return reductions.any(self, axis=axis, out=out, keepdims=keepdims)
+
+    def all(self, axis=None, out=None, keepdims=False):
+        from . import reductions
+        return reductions.all(self, axis=axis, out=out, keepdims=keepdims)
+
+    def clip(self, min=None, max=None, out=None):
+        from . import math_ops
+        return math_ops.clip(self, min, max, out=out)
 
     def argmax(self, axis=None, out=None, keepdims=False):
         from . import reductions

@@ -26,7 +26,7 @@ from ._config import get_config
 from ._dtypes import dtype_code, resolve_dtype
 from .ndarray import ndarray, _normalize_axis, _prod
 
-__all__ = ["sum", "mean", "prod", "max", "min", "amax", "amin", "argmax", "argmin",
+__all__ = ["sum", "mean", "prod", "max", "min", "amax", "amin", "argmax", "argmin", "any", "all",
            "cumsum", "cumprod", "var", "std", "cumulative_sum", "cumulative_prod"]
 
 _OUT_DTYPE_CACHE: dict = {}
@@ -201,6 +201,29 @@ def min(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._N
 
 amax = max
 amin = min
+
+
+def any(a, axis=None, out=None, keepdims=False, where=np._NoValue):
+    """True where any element along ``axis`` is nonzero (reference
+    reductions.py:248-278).  One fused pass counts ``a != 0`` (NaN counts as
+    true); an empty reduction is False.  Returns a bool ndarray (0-d for
+    axis=None), as the reference does."""
+    if where is not np._NoValue:
+        raise NotImplementedError("any(where=...) is not supported on the device")
+    a = _asarray(a)
+    r = _reduce(a != 0, "sum", axis, None, None, keepdims) > 0
+    return _finish(r, out)
+
+
+def all(a, axis=None, out=None, keepdims=False, where=np._NoValue):
+    """True where every element along ``axis`` is nonzero (reference
+    reductions.py:281-311); counts ``a == 0`` in one fused pass; an empty
+    reduction is True."""
+    if where is not np._NoValue:
+        raise NotImplementedError("all(where=...) is not supported on the device")
+    a = _asarray(a)
+    r = _reduce(a == 0, "sum", axis, None, None, keepdims) == 0
+    return _finish(r, out)
 
 
 def _argreduce(a, op, axis, out, keepdims):

@@ -117,6 +117,37 @@ for _name, _op, _doc in [
     _binary(_name, _op, _doc)
 
 
+# Bitwise, logical and predicate ufuncs (reference bitwise_ops.py:58-93,
+# logic_ops.py:45-63, math_ops.py:558-578, ufunc_ops.py:352).  The reference
+# computes bitwise ops in int32 and returns int32; here they keep NumPy's
+# dtypes (int64 stays int64, bool stays bool).
+for _name, _op, _doc in [
+    ("invert", "invert_op", "Bitwise NOT (logical NOT for bool)."),
+    ("bitwise_not", "invert_op", "Bitwise NOT (logical NOT for bool)."),
+    ("bitwise_invert", "invert_op", "Bitwise NOT (logical NOT for bool)."),
+    ("logical_not", "logical_not_op", "Truth value of NOT x."),
+    ("isnan", "isnan_op", "True where x is NaN."),
+    ("isinf", "isinf_op", "True where x is +inf or -inf."),
+    ("isfinite", "isfinite_op", "True where x is neither infinite nor NaN."),
+    ("signbit", "signbit_op", "True where the sign bit is set (-0.0 included)."),
+]:
+    _unary(_name, _op, _doc)
+
+for _name, _op, _doc in [
+    ("bitwise_and", "bit_and_op", "Element-wise bitwise AND."),
+    ("bitwise_or", "bit_or_op", "Element-wise bitwise OR."),
+    ("bitwise_xor", "bit_xor_op", "Element-wise bitwise XOR."),
+    ("left_shift", "lshift_op", "Shift bits left (counts outside [0, bits) give 0)."),
+    ("bitwise_left_shift", "lshift_op", "Shift bits left."),
+    ("right_shift", "rshift_op", "Arithmetic shift right (sign-filling for signed types)."),
+    ("bitwise_right_shift", "rshift_op", "Arithmetic shift right."),
+    ("logical_and", "logical_and_op", "Truth value of x1 AND x2."),
+    ("logical_or", "logical_or_op", "Truth value of x1 OR x2."),
+    ("logical_xor", "logical_xor_op", "Truth value of x1 XOR x2."),
+]:
+    _binary(_name, _op, _doc)
+
+
 def float_power(x1, x2, /, out=None, **kwargs):
     """x1 ** x2 computed in float64 (NumPy float_power)."""
     from . import creation

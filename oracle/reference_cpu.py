@@ -37,6 +37,47 @@ BINARY = {
 }
 
 
+# Bitwise, logical and predicate ops: the reference's CPU branches call these
+# NumPy ufuncs (bitwise_ops.py:24-30 _BITWISE_NP and :70-93,
+# logic_ops.py:45-63, math_ops.py:558-578, ufunc_ops.py:352).
+UNARY.update({
+    "invert_op": np.invert, "logical_not_op": np.logical_not, "isnan_op": np.isnan,
+    "isinf_op": np.isinf, "isfinite_op": np.isfinite, "signbit_op": np.signbit,
+})
+BINARY.update({
+    "bit_and_op": np.bitwise_and, "bit_or_op": np.bitwise_or, "bit_xor_op": np.bitwise_xor,
+    "lshift_op": np.left_shift, "rshift_op": np.right_shift,
+    "logical_and_op": np.logical_and, "logical_or_op": np.logical_or,
+    "logical_xor_op": np.logical_xor,
+})
+
+
+def where(cond, x, y):
+    """math_ops.where CPU branch (math_ops.py:124-130): np.where."""
+    return np.where(cond, x, y)
+
+
+def clip(a, lo, hi):
+    """math_ops.clip CPU branch (math_ops.py:180-190): np.clip."""
+    with np.errstate(all="ignore"):
+        return np.clip(a, lo, hi)
+
+
+def any_(a, axis=None, keepdims=False):
+    """reductions.any CPU branch (reductions.py:255-268): np.any."""
+    return np.any(a, axis=axis, keepdims=keepdims)
+
+
+def all_(a, axis=None, keepdims=False):
+    """reductions.all CPU branch (reductions.py:288-301): np.all."""
+    return np.all(a, axis=axis, keepdims=keepdims)
+
+
+def count_nonzero(a, axis=None, keepdims=False):
+    """math_ops.count_nonzero (math_ops.py:693): np.count_nonzero."""
+    return np.count_nonzero(a, axis=axis, keepdims=keepdims)
+
+
 def unary(op_name: str, x: np.ndarray) -> np.ndarray:
     with np.errstate(all="ignore"):
         return UNARY[op_name](x)

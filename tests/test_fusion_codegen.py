@@ -86,3 +86,53 @@ def test_strided_leaf_disables_vector_path():
     root = F.UnaryOpNode("sin_op", x, (100, 64), np.float32)
     prog, cshape, kinds, vec, src = _compile(root)
     assert kinds == ["s"] and not vec
+
+
+_INT_DTYPES = [np.bool_, np.int16, np.uint16, np.int32, np.uint32, np.int64, np.uint64]
+_ALL_DTYPES = _INT_DTYPES + [np.float16, np.float32, np.float64]
+
+
+@pytest.mark.parametrize("dtype", _INT_DTYPES)
+def test_bitwise_and_shift_ops_compile(dtype):
+    shp = (4, 256)
+    a = _leaf(shp, dtype)
+    b = _leaf(shp, dtype, ptr=0x30000)
+    root = F.BinaryOpNode("bit_xor_op", F.BinaryOpNode("bit_and_op", a, b, shp, dtype),
+                          F.BinaryOpNode("bit_or_op", a, F.UnaryOpNode("invert_op", b, shp, dtype),
+                                         shp, dtype), shp, dtype)
+    if dtype is not np.bool_:  # numpy shifts bool as int8
+        root = F.BinaryOpNode("rshift_op", F.BinaryOpNode("lshift_op", root, b, shp, dtype), a,
+                              shp, dtype)
+    prog, cshape, kinds, vec, src = _compile(root)
+    assert vec and len(prog.arrays) == 2
+    for fn in ("op_bitwise_and", "op_bitwise_or", "op_bitwise_xor", "op_invert"):
+        assert fn in src
+
+
+@pytest.mark.parametrize("dtype", _ALL_DTYPES)
+def test_predicates_logical_and_where_compile(dtype):
+    shp = (3, 512)
+    x = _leaf(shp, dtype)
+    y = _leaf((1, 512), dtype, ptr=0x30000)
+    bool_ = np.dtype(np.bool_)
+    preds = [F.UnaryOpNode(op, x, shp, bool_)
+             for op in ("isnan_op", "isinf_op", "isfinite_op", "signbit_op", "logical_not_op")]
+    c = preds[0]
+    for p in preds[1:]:
+        c = F.BinaryOpNode("logical_xor_op", c, p, shp, bool_)
+    c = F.BinaryOpNode("logical_or_op", F.BinaryOpNode("logical_and_op", x, y, shp, bool_), c,
+                       shp, bool_)
+    root = F.WhereNode(c, x, F.ScalarNode(1, dtype), shp, dtype)
+    prog, cshape, kinds, vec, src = _compile(root)
+    assert kinds == ["c", "c"] and cshape == [3, 512]  # y's rows are stride 0
+    assert "? t" in src and "op_isnan" in src
+
+
+def test_where_cond_cast_and_mixed_leaves():
+    shp = (1000,)
+    cond = F.CastNode(_leaf(shp, np.float32), np.bool_)
+    x = _leaf(shp, np.int64, ptr=0x30000)
+    root = F.WhereNode(cond, x, F.ScalarNode(-1, np.int64), shp, np.int64)
+    prog, cshape, kinds, vec, src = _compile(root)
+    assert len(prog.arrays) == 2 and len(prog.scalars) == 1
+    assert "mmp_convert<bool, float>" in src

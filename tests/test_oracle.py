@@ -182,3 +182,99 @@ def test_fusion_chain_against_python_loop():
                 - math.log1p(float(x[i, j]) ** 2) for j in range(17)) for i in range(3)]
     assert np.allclose(z, loop, rtol=1e-5)
     assert z.shape == (3,)
+
+
+# ------------------------------------------- bitwise / logical / predicates
+def _wrap(v, dtype):
+    """Python int -> dtype's two's-complement value."""
+    bits = np.dtype(dtype).itemsize * 8
+    v &= (1 << bits) - 1
+    if np.issubdtype(dtype, np.signedinteger) and v >= 1 << (bits - 1):
+        v -= 1 << bits
+    return v
+
+
+@pytest.mark.parametrize("dtype", [np.int16, np.uint16, np.int32, np.uint32, np.int64, np.uint64])
+def test_shift_and_bitwise_closed_forms(dtype):
+    """Shifts: counts in [0, bits) shift (left wraps, right is arithmetic
+    for signed types); any other count -- negative ones included -- gives 0
+    (or -1 for a negative value shifted right).  Checked against Python's
+    unbounded integers over every count in [-3, bits + 3)."""
+    info = np.iinfo(dtype)
+    bits = info.bits
+    vals = sorted({info.min, info.min + 1, -7 if info.min < 0 else 7, -1 if info.min < 0 else 1,
+                   0, 1, 5, info.max - 1, info.max, int(info.max // 3)})
+    counts = list(range(-3, bits + 3))
+    if info.min == 0:
+        counts = [c for c in counts if c >= 0]
+    a = np.array([v for v in vals for _ in counts], dtype=dtype)
+    b = np.array([c for _ in vals for c in counts], dtype=dtype)
+    left = ref.binary("lshift_op", a, b)
+    right = ref.binary("rshift_op", a, b)
+    for x, c, l, r in zip(a.tolist(), b.tolist(), left.tolist(), right.tolist()):
+        inside = 0 <= c < bits
+        assert l == (_wrap(x << c, dtype) if inside else 0), (x, c)
+        assert r == ((x >> c) if inside else (-1 if x < 0 else 0)), (x, c)
+    x = a[:: len(counts)]
+    y = x[::-1].copy()
+    mask = (1 << bits) - 1
+    for op, f in (("bit_and_op", lambda p, q: p & q), ("bit_or_op", lambda p, q: p | q),
+                  ("bit_xor_op", lambda p, q: p ^ q)):
+        got = ref.binary(op, x, y).tolist()
+        assert got == [_wrap(f(p & mask, q & mask), dtype) for p, q in zip(x.tolist(), y.tolist())]
+    assert ref.unary("invert_op", x).tolist() == [_wrap(~p, dtype) for p in x.tolist()]
+
+
+def test_predicates_and_truth_values_hand_derived():
+    specials = [np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -2.5]
+    # (isnan, isinf, isfinite, signbit, logical_not) per value
+    expect = [(1, 0, 0, 0, 0), (1, 0, 0, 1, 0), (0, 1, 0, 0, 0), (0, 1, 0, 1, 0),
+              (0, 0, 1, 0, 1), (0, 0, 1, 1, 1), (0, 0, 1, 0, 0), (0, 0, 1, 1, 0)]
+    for dt in (np.float16, np.float32, np.float64):
+        x = np.array(specials, dtype=dt)
+        x[1] = -np.abs(x[1])  # a NaN with the sign bit set
+        for k, op in enumerate(("isnan_op", "isinf_op", "isfinite_op", "signbit_op",
+                                "logical_not_op")):
+            assert ref.unary(op, x).astype(int).tolist() == [e[k] for e in expect], (dt, op)
+    i = np.array([-3, 0, 7], dtype=np.int32)
+    assert ref.unary("isnan_op", i).tolist() == [False] * 3
+    assert ref.unary("isfinite_op", i).tolist() == [True] * 3
+    assert ref.unary("signbit_op", i).tolist() == [True, False, False]
+    # truth table (NaN is true, -0.0 false), mixed operand dtypes
+    p = np.array([0.0, -0.0, np.nan, 2.0, 0.0, 3.0], dtype=np.float32)
+    q = np.array([0, 1, 0, 5, 7, 0], dtype=np.int16)
+    tp = [False, False, True, True, False, True]
+    tq = [False, True, False, True, True, False]
+    assert ref.binary("logical_and_op", p, q).tolist() == [u and v for u, v in zip(tp, tq)]
+    assert ref.binary("logical_or_op", p, q).tolist() == [u or v for u, v in zip(tp, tq)]
+    assert ref.binary("logical_xor_op", p, q).tolist() == [u != v for u, v in zip(tp, tq)]
+
+
+def test_where_clip_any_all_count_against_python():
+    rng = np.random.default_rng(11)
+    c = rng.random(50) < 0.4
+    x = rng.standard_normal(50).astype(np.float32)
+    y = np.float32(-9.5)
+    got = ref.where(c, x, y)
+    assert got.dtype == np.float32
+    assert got.tolist() == [xi if ci else -9.5 for ci, xi in zip(c.tolist(), x.tolist())]
+    # clip = min(max(a, lo), hi) with NaN propagating from any operand; lo > hi gives hi
+    a = np.array([-2.0, 0.5, 3.0, np.nan], dtype=np.float32)
+    assert ref.clip(a, -1.0, 1.0).tolist()[:3] == [-1.0, 0.5, 1.0]
+    assert np.isnan(ref.clip(a, -1.0, 1.0)[3])
+    assert ref.clip(a[:3], 2.0, 1.0).tolist() == [1.0, 1.0, 1.0]
+    assert np.isnan(ref.clip(a[:3], np.nan, 1.0)).all()
+    assert ref.clip(np.arange(5, dtype=np.int32), 1, 3).tolist() == [1, 1, 2, 3, 3]
+    m = np.array([[0.0, np.nan, 0.0], [0.0, 0.0, 0.0], [1.0, -0.0, 2.0]], dtype=np.float32)
+    rows = m.tolist()
+
+    def truth(v):
+        return v != 0 or v != v
+
+    assert ref.any_(m, axis=1).tolist() == [any(truth(v) for v in r) for r in rows]
+    assert ref.all_(m, axis=1).tolist() == [all(truth(v) for v in r) for r in rows]
+    assert ref.count_nonzero(m, axis=0).tolist() == [
+        sum(truth(r[j]) for r in rows) for j in range(3)]
+    assert ref.count_nonzero(m) == 3
+    assert ref.any_(np.zeros((2, 0)), axis=1).tolist() == [False, False]
+    assert ref.all_(np.zeros((2, 0)), axis=1).tolist() == [True, True]

@@ -430,13 +430,40 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode):
         L.append("}")
     else:  # row-sum epilogue
         L.append(f"  {acc_ct} acc = 0;")
-        L.append("  const long long per = (cols + p.colblocks - 1) / p.colblocks;")
+        if vec:
+            # column ranges are multiples of 4 elements, so every 16-byte
+            # (or narrower) vector load of a contiguous leaf is aligned
+            L.append("  const long long per = ((cols + p.colblocks - 1) / p.colblocks + 3) & ~3LL;")
+        else:
+            L.append("  const long long per = (cols + p.colblocks - 1) / p.colblocks;")
         L.append("  const long long c0 = cb * per;")
         L.append("  const long long c1 = c0 + per < cols ? c0 + per : cols;")
-        L.append(f"  for (long long c = c0 + threadIdx.x; c < c1; c += {_BLOCK}) {{")
-        L.extend(expr_lines(lambda k: scalar_load(k, "c"), "    "))
-        L.append(f"    acc += ({acc_ct}){res};")
-        L.append("  }")
+        if vec:
+            for k in range(nin):
+                if kinds[k] == "b":
+                    L.append(f"  const {ct[k]} bc{k} = in{k}[ro{k}];")
+            L.append("  #pragma unroll 4")
+            L.append(f"  for (long long c = c0 + threadIdx.x * {_ELEMS}; c < c1; "
+                     f"c += {_BLOCK * _ELEMS}) {{")
+            for k in range(nin):
+                if kinds[k] == "c":
+                    L.append(f"    const {vtypes[ct[k]]} l{k} = __builtin_nontemporal_load("
+                             f"(const {vtypes[ct[k]]}*)(in{k} + ro{k} + c));")
+            L.append(f"    #pragma unroll\n    for (int e = 0; e < {_ELEMS}; ++e) {{")
+
+            def vload_sum(k):
+                if kinds[k] == "c":
+                    return f"({ct[k]})l{k}[e]"
+                return f"bc{k}"
+            L.extend(expr_lines(vload_sum, "      "))
+            L.append(f"      acc += ({acc_ct}){res};")
+            L.append("    }")
+            L.append("  }")
+        else:
+            L.append(f"  for (long long c = c0 + threadIdx.x; c < c1; c += {_BLOCK}) {{")
+            L.extend(expr_lines(lambda k: scalar_load(k, "c"), "    "))
+            L.append(f"    acc += ({acc_ct}){res};")
+            L.append("  }")
         L.append("  // wave64 butterfly, then one value per wave through LDS")
         L.append("  #pragma unroll\n  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);")
         L.append(f"  __shared__ {acc_ct} red[{_BLOCK // 64}];")
@@ -544,9 +571,11 @@ def _fill_params(prog, P, outer, cols, leaf_str, out_ptr, colblocks, scale):
 
 
 def _vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, out_itemsize, mode):
-    if mode != "map" or cols % _ELEMS:
+    """Whether every leaf can be read (and, for 'map', the output written)
+    4 elements at a time with aligned vector accesses."""
+    if cols % _ELEMS:
         return False
-    if out_ptr % (_ELEMS * out_itemsize):
+    if mode == "map" and out_ptr % (_ELEMS * out_itemsize):
         return False
     for k, a in enumerate(prog.arrays):
         if kinds[k] == "s":
@@ -602,8 +631,9 @@ def run_sum(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean: bo
     colblocks = max(1, min(want, -(-cols // 4096)))
     final_direct = axis_last and colblocks == 1
     P = _param_struct(len(prog.arrays), len(prog.scalars), len(outer))
+    vec = _vec_ok(prog, kinds, leaf_str, outer, cols, 0, 0, "sum")
     kern = _kernel_for_program(prog, kinds, len(outer), out_dtype if final_direct else acc_dt,
-                               False, "sum")
+                               vec, "sum")
     if final_direct:
         p, rows = _fill_params(prog, P, outer, cols, leaf_str, out_ptr, 1, scale)
         be.launch(kern, (rows, 1, 1), (_BLOCK, 1, 1), [p])

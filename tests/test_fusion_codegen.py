@@ -136,3 +136,18 @@ def test_where_cond_cast_and_mixed_leaves():
     prog, cshape, kinds, vec, src = _compile(root)
     assert len(prog.arrays) == 2 and len(prog.scalars) == 1
     assert "mmp_convert<bool, float>" in src
+
+
+def test_vectorised_sum_epilogue_compiles():
+    shp = (64, 1024)
+    x = _leaf(shp, np.float32)
+    r = _leaf((1, 1024), np.float32, ptr=0x30000)
+    root = F.BinaryOpNode("gt_op", F.BinaryOpNode("mul_op", x, r, shp, np.float32),
+                          F.ScalarNode(0.5, np.float32), shp, np.bool_)
+    prog, cshape, kinds, vec, src = _compile(root, mode="sum", keep_last=True, vec=True)
+    assert vec and "__builtin_nontemporal_load" in src and "& ~3LL" in src
+    # an odd row length keeps the scalar loop
+    y = _leaf((64, 1023), np.float32)
+    prog, cshape, kinds, vec, src = _compile(F.UnaryOpNode("abs_op", y, (64, 1023), np.float32),
+                                             mode="sum", keep_last=True, vec=True)
+    assert not vec

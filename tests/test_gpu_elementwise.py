@@ -292,3 +292,23 @@ def test_empty_and_tiny():
     assert float((one * one).get()[0]) == 4.0
     z = cp.array(np.float32(3.0))
     assert float((z + 1).get()) == 4.0
+
+
+def test_log1p_f32_dense_sweep_and_specials():
+    """float32 log1p (own implementation: exact range reduction plus a
+    fitted polynomial) over every 61st bit pattern of (-1, +inf): at most
+    1 ULP from the correctly rounded value, and NumPy's special values."""
+    pos = np.arange(0, 0x7F800000, 61, dtype=np.int64).astype(np.uint32).view(np.float32)
+    neg = np.arange(0x80000000, 0xBF800000, 61, dtype=np.int64).astype(np.uint32).view(np.float32)
+    for x in (pos, neg):
+        got = _dev_unary("log1p_op", x)
+        d = ref.ulp_distance(got, ref.correctly_rounded(np.log1p, x))
+        assert int(d.max()) <= 1, x[int(np.argmax(d))]
+    sp = np.array([-1.0, -1.5, -np.inf, np.nan, np.inf, 0.0, -0.0, 1e-30, -1e-30, 1e-45,
+                   -0.99999994, 3.4e38], np.float32)
+    got = _dev_unary("log1p_op", sp)
+    with np.errstate(all="ignore"):
+        want = np.log1p(sp)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))

@@ -38,7 +38,7 @@ BINARY = {
 
 
 # Bitwise, logical and predicate ops: the reference's CPU branches call these
-# NumPy ufuncs (bitwise_ops.py:24-30 _BITWISE_NP and :70-93,
+# NumPy ufuncs (bitwise_ops.py:27-31 _BITWISE_NP and :70-93,
 # logic_ops.py:45-63, math_ops.py:558-578, ufunc_ops.py:352).
 UNARY.update({
     "invert_op": np.invert, "logical_not_op": np.logical_not, "isnan_op": np.isnan,

@@ -275,6 +275,40 @@ def bench_logic(cp, be, reps=10):
     return res
 
 
+# ------------------------------------------------------ NaN reductions
+def bench_nan(cp, be, reps=10):
+    """NaN-skipping reductions on the C3 matrix (16384 x 16384 float32)
+    with 1 % of the elements set to NaN; 4 B/elem read."""
+    from macmetalpy_amd.workloads import c3_matrix
+    m = c3_matrix()
+    m.reshape(-1)[::97] = np.nan
+    A = cp.array(m)
+    del m
+    A._ensure_gpu()
+    nbytes = 4 * A.size
+    cases = {
+        "nansum_all": lambda: cp.nansum(A), "nanmean_axis1": lambda: cp.nanmean(A, axis=1),
+        "nanmax_axis1": lambda: cp.nanmax(A, axis=1),
+        "nanargmax_axis1": lambda: cp.nanargmax(A, axis=1),
+    }
+    res = {}
+    for name, f in cases.items():
+        try:
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(name, f)
+            cp.synchronize()
+            ms, _ = timer.ms(name)
+            timer.close()
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1),
+                         "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
 # --------------------------------------------------------------- C5
 def bench_c5(cp, be, reps=10):
     from macmetalpy_amd.workloads import c5_inputs
@@ -459,7 +493,8 @@ def main():
         cfgs = {}
         for name, fn in (("c1_fused_elementwise", bench_c1), ("c3_reduce_scan", bench_c3),
                          ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5),
-                         ("logic_where_clip_2p28", bench_logic)):
+                         ("logic_where_clip_2p28", bench_logic),
+                         ("nan_reductions_16384sq", bench_nan)):
             t = time.time()
             try:
                 cfgs[name] = fn(cp, be)

@@ -122,7 +122,19 @@ extern "C" {
 #define MMP_R_MEAN 4
 #define MMP_R_ARGMAX 5
 #define MMP_R_ARGMIN 6
-#define MMP_NREDUCE 7
+/* NaN-ignoring variants (the reference's nan_reduction_shader and
+ * nan_ops.nansum/nanprod/nanmax/nanmin/nanmean/nanargmax/nanargmin,
+ * _kernels.py:599-732, nan_ops.py:112-612).  A slice with no non-NaN
+ * element gives NaN for max/min/mean, 0 for sum, 1 for prod and, for the
+ * arg ops, the index INT64_MAX (numpy raises "All-NaN slice"). */
+#define MMP_R_NANSUM 7
+#define MMP_R_NANPROD 8
+#define MMP_R_NANMAX 9
+#define MMP_R_NANMIN 10
+#define MMP_R_NANMEAN 11
+#define MMP_R_NANARGMAX 12
+#define MMP_R_NANARGMIN 13
+#define MMP_NREDUCE 14
 
 #define MMP_S_CUMSUM 0
 #define MMP_S_CUMPROD 1
@@ -227,15 +239,17 @@ int mmp_fill(int dtype, int64_t n, const void *value, void *out);
 
 /* Input viewed as C-contiguous (outer, len, inner); reduces the middle
  * axis -> out (outer, inner) of `out_dtype`.  axis=None is
- * (1, n, 1).  op: MMP_R_SUM/PROD/MAX/MIN/MEAN.  Floating sums/means
- * accumulate in float64 and round once; integer sums accumulate in 64-bit
- * (numpy promotes int32 sums to int64).  max/min propagate NaN. */
+ * (1, n, 1).  op: MMP_R_SUM/PROD/MAX/MIN/MEAN and their MMP_R_NAN*
+ * variants.  Floating sums/means accumulate in float64 and round once;
+ * integer sums accumulate in 64-bit (numpy promotes int32 sums to int64).
+ * max/min propagate NaN; the NaN variants skip it. */
 int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
                int64_t inner, const void *x, void *out);
 
 /* Same view; out (outer, inner) int64 indices of the first max/min
  * (MMP_R_ARGMAX / MMP_R_ARGMIN); a NaN counts as the extreme (first NaN
- * wins), as np.argmax does. */
+ * wins), as np.argmax does.  MMP_R_NANARGMAX / MMP_R_NANARGMIN skip NaNs
+ * (np.nanargmax); an all-NaN slice gives INT64_MAX. */
 int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len,
                   int64_t inner, const void *x, int64_t *out);
 

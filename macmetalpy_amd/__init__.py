@@ -4,7 +4,8 @@ Drop-in for the reference's ``import macmetalpy as cp`` names on the hot
 path (src/macmetalpy/__init__.py:8-236): ndarray, creation, random inputs,
 elementwise ufuncs (arithmetic, transcendental, comparison, bitwise,
 logical, predicates), where / clip, sum/mean/max/min/prod/argmax/argmin,
-any/all/count_nonzero, cumsum/cumprod,
+any/all/count_nonzero, NaN-aware reductions (nansum, nanmax, nanargmax, ...),
+cumsum/cumprod,
 matmul / linalg.matmul / dot, RawKernel, set_config and synchronize.
 Unlike the reference (darwin-only, __init__.py:5-6) it imports on any host;
 device work needs libmmp_hip.so and a gfx950 GPU and raises otherwise.
@@ -39,6 +40,10 @@ from .math_ops import where, clip, count_nonzero
 from .reductions import (
     sum, mean, prod, max, min, amax, amin, argmax, argmin, any, all, cumsum, cumprod, var,
     std, cumulative_sum, cumulative_prod,
+)
+from .nan_ops import (
+    nansum, nanprod, nanmax, nanmin, nanmean, nanvar, nanstd, nanargmax, nanargmin,
+    nancumsum, nancumprod,
 )
 from .linalg_top import matmul, dot, vdot, inner
 from . import linalg

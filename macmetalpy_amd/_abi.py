@@ -157,6 +157,9 @@ BINARY_FN.update({k: v[1] for k, v in EXPR_BINARY_OPS.items()})
 
 REDUCE_SUM, REDUCE_PROD, REDUCE_MAX, REDUCE_MIN, REDUCE_MEAN = 0, 1, 2, 3, 4
 REDUCE_ARGMAX, REDUCE_ARGMIN = 5, 6
+REDUCE_NANSUM, REDUCE_NANPROD, REDUCE_NANMAX, REDUCE_NANMIN, REDUCE_NANMEAN = 7, 8, 9, 10, 11
+REDUCE_NANARGMAX, REDUCE_NANARGMIN = 12, 13
+ARG_NONE = 0x7FFFFFFFFFFFFFFF  # index a NaN arg-reduction reports for an all-NaN slice
 SCAN_CUMSUM, SCAN_CUMPROD = 0, 1
 
 # Exported C symbols (kept in sync with include/mmp_hip.h by a test).

@@ -132,8 +132,61 @@ template <typename T> struct Red<MMP_R_MIN, T> {
   }
 };
 
+// NaN-ignoring variants (numpy nansum / nanprod / nanmax / nanmin /
+// nanmean): a NaN element maps to the identity.  nanmax / nanmin start from
+// NaN and replace it by the first non-NaN value, so an all-NaN slice stays
+// NaN; nanmean carries (sum, count) and an empty count gives 0/0 = NaN.
+template <typename T> MMP_DI bool is_nan_elem(T v) {
+  if constexpr (mmp_t<T>::is_float) return (typename mmp_t<T>::C)v != (typename mmp_t<T>::C)v;
+  else return false;
+}
+template <typename T> struct Red<MMP_R_NANSUM, T> : Red<MMP_R_SUM, T> {
+  typedef typename Red<MMP_R_SUM, T>::A A;
+  static __device__ __forceinline__ A map(T v) {
+    return is_nan_elem(v) ? (A)0 : Red<MMP_R_SUM, T>::map(v);
+  }
+};
+template <typename T> struct Red<MMP_R_NANPROD, T> : Red<MMP_R_PROD, T> {
+  typedef typename Red<MMP_R_PROD, T>::A A;
+  static __device__ __forceinline__ A map(T v) {
+    return is_nan_elem(v) ? (A)1 : Red<MMP_R_PROD, T>::map(v);
+  }
+};
+template <int OP, typename T> struct RedNanExt {  // OP: MMP_R_MAX or MMP_R_MIN
+  typedef typename mmp_t<T>::C A;
+  static __device__ __forceinline__ A ident() {
+    if constexpr (mmp_t<T>::is_float) return (A)__builtin_nanf("");
+    else return Red<OP, T>::ident();
+  }
+  static __device__ __forceinline__ A map(T v) { return (A)v; }
+  static __device__ __forceinline__ A comb(A a, A b) {
+    if constexpr (mmp_t<T>::is_float) {
+      if (a != a) return b;
+      if (b != b) return a;
+    }
+    if constexpr (OP == MMP_R_MAX) return b > a ? b : a;
+    else return b < a ? b : a;
+  }
+};
+template <typename T> struct Red<MMP_R_NANMAX, T> : RedNanExt<MMP_R_MAX, T> {};
+template <typename T> struct Red<MMP_R_NANMIN, T> : RedNanExt<MMP_R_MIN, T> {};
+struct MeanAcc {
+  double s, n;
+};
+template <typename T> struct Red<MMP_R_NANMEAN, T> {
+  typedef MeanAcc A;
+  static __device__ __forceinline__ A ident() { return A{0.0, 0.0}; }
+  static __device__ __forceinline__ A map(T v) {
+    if (is_nan_elem(v)) return A{0.0, 0.0};
+    if constexpr (mmp_t<T>::is_float) return A{(double)(typename mmp_t<T>::C)v, 1.0};
+    else return A{(double)v, 1.0};
+  }
+  static __device__ __forceinline__ A comb(A a, A b) { return A{a.s + b.s, a.n + b.n}; }
+};
+
 // argmax / argmin pair; "better" = NaN first, then extreme value, then
-// smaller index.
+// smaller index.  The NaN-ignoring variants never take a NaN: an all-NaN
+// slice keeps the identity's index (INT64_MAX).
 template <typename C> struct ArgPair {
   C v;
   long long i;
@@ -141,10 +194,12 @@ template <typename C> struct ArgPair {
 template <int OP, typename T> struct Arg {
   typedef typename mmp_t<T>::C C;
   typedef ArgPair<C> A;
+  static constexpr bool kMax = OP == MMP_R_ARGMAX || OP == MMP_R_NANARGMAX;
+  static constexpr bool kSkipNaN = OP == MMP_R_NANARGMAX || OP == MMP_R_NANARGMIN;
   static __device__ __forceinline__ A ident() {
     A a;
-    if constexpr (mmp_t<T>::is_float) a.v = OP == MMP_R_ARGMAX ? -__builtin_huge_valf() : __builtin_huge_valf();
-    else if constexpr (OP == MMP_R_ARGMAX) a.v = (C)mmp_t<T>::lowest;
+    if constexpr (mmp_t<T>::is_float) a.v = kMax ? -__builtin_huge_valf() : __builtin_huge_valf();
+    else if constexpr (kMax) a.v = (C)mmp_t<T>::lowest;
     else if constexpr (mmp_t<T>::is_bool) a.v = (C)1;
     else a.v = (C)~(typename mmp_t<T>::U)mmp_t<T>::lowest;
     a.i = 0x7fffffffffffffffLL;
@@ -153,23 +208,38 @@ template <int OP, typename T> struct Arg {
   static __device__ __forceinline__ bool better(const A &x, const A &y) {  // x before y?
     if constexpr (mmp_t<T>::is_float) {
       const bool xn = x.v != x.v, yn = y.v != y.v;
-      if (xn || yn) return xn && (!yn || x.i < y.i);
+      if constexpr (kSkipNaN) {
+        if (xn) return false;
+        if (yn) return true;
+      } else {
+        if (xn || yn) return xn && (!yn || x.i < y.i);
+      }
     }
     if (x.v == y.v) return x.i < y.i;
-    return OP == MMP_R_ARGMAX ? x.v > y.v : x.v < y.v;
+    return kMax ? x.v > y.v : x.v < y.v;
   }
   static __device__ __forceinline__ A comb(const A &x, const A &y) { return better(y, x) ? y : x; }
   // v (visited later) replaces the running best b of one thread's sequence
   static __device__ __forceinline__ bool seq_better(C v, C b) {
-    bool r = OP == MMP_R_ARGMAX ? v > b : v < b;
-    if constexpr (mmp_t<T>::is_float) r |= (v != v) & (b == b);
+    bool r = kMax ? v > b : v < b;
+    if constexpr (mmp_t<T>::is_float && !kSkipNaN) r |= (v != v) & (b == b);
     return r;
+  }
+  // whether an element may become the running best at all
+  static __device__ __forceinline__ bool eligible(C v) {
+    if constexpr (mmp_t<T>::is_float && kSkipNaN) return v == v;
+    else return true;
   }
 };
 
 // --------------------------------------------------- wave / block reduce
 template <typename A> __device__ __forceinline__ A shfl_xor(A v, int m) {
-  if constexpr (sizeof(A) == 8) {
+  if constexpr (sizeof(A) == 16) {
+    u32x4 w = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = __shfl_xor(w[k], m, 64);
+    return __builtin_bit_cast(A, w);
+  } else if constexpr (sizeof(A) == 8) {
     unsigned long long u = __builtin_bit_cast(unsigned long long, v);
     unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
     lo = __shfl_xor(lo, m, 64);
@@ -198,9 +268,12 @@ template <typename R, typename C> __device__ __forceinline__ ArgPair<C> wave_red
   return v;
 }
 
+template <typename A> struct IsArgPair { static constexpr bool value = false; };
+template <typename C> struct IsArgPair<ArgPair<C>> { static constexpr bool value = true; };
+
 // Block-wide reduce; the result is valid in thread 0.
 template <typename R, typename A> __device__ A block_reduce(A v, A *lds) {
-  if constexpr (sizeof(A) == 16) {
+  if constexpr (IsArgPair<A>::value) {
     v = wave_reduce_arg<R>(v);
   } else {
     v = wave_reduce<R>(v);
@@ -279,7 +352,7 @@ __device__ __forceinline__ typename R::A slice_argreduce(const T *__restrict__ p
   C bv = R::ident().v;
   unsigned bi = kNone;
   auto visit = [&](C v, unsigned off) {
-    bool upd = R::seq_better(v, bv) | (bi == kNone);
+    bool upd = (R::seq_better(v, bv) | (bi == kNone)) & R::eligible(v);
     bv = upd ? v : bv;
     bi = upd ? off : bi;
   };
@@ -320,7 +393,10 @@ template <int OP, typename T, typename To, typename A>
 __device__ __forceinline__ To finalize(A a, long long len) {
   if constexpr (OP == MMP_R_MEAN) {
     return mmp_convert<To, double>(a / (double)len);
-  } else if constexpr (OP == MMP_R_MAX || OP == MMP_R_MIN) {
+  } else if constexpr (OP == MMP_R_NANMEAN) {
+    return mmp_convert<To, double>(a.s / a.n);
+  } else if constexpr (OP == MMP_R_MAX || OP == MMP_R_MIN || OP == MMP_R_NANMAX ||
+                       OP == MMP_R_NANMIN) {
     if constexpr (sizeof(T) == 2 && mmp_t<T>::is_float) return mmp_convert<To, T>((T)a);
     else return mmp_convert<To, A>(a);
   } else {
@@ -640,8 +716,9 @@ int launch_argreduce(long long outer, long long len, long long inner, const void
 // give a float.
 template <int OP, typename T, typename To> constexpr bool out_ok() {
   constexpr bool to_float = mmp_t<To>::is_float;
-  if (OP == MMP_R_MAX || OP == MMP_R_MIN) return __is_same(T, To);
-  if (OP == MMP_R_MEAN) return to_float;
+  if (OP == MMP_R_MAX || OP == MMP_R_MIN || OP == MMP_R_NANMAX || OP == MMP_R_NANMIN)
+    return __is_same(T, To);
+  if (OP == MMP_R_MEAN || OP == MMP_R_NANMEAN) return to_float;
   if (mmp_t<T>::is_float) return to_float;
   if (mmp_t<T>::is_signed || mmp_t<T>::is_bool) return __is_same(To, mmp_i64);
   return __is_same(To, mmp_u64);
@@ -695,6 +772,11 @@ extern "C" int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64
       case MMP_R_MAX: return reduce_out<MMP_R_MAX, T>(out_dtype, outer, len, inner, x, out);
       case MMP_R_MIN: return reduce_out<MMP_R_MIN, T>(out_dtype, outer, len, inner, x, out);
       case MMP_R_MEAN: return reduce_out<MMP_R_MEAN, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_NANSUM: return reduce_out<MMP_R_NANSUM, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_NANPROD: return reduce_out<MMP_R_NANPROD, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_NANMAX: return reduce_out<MMP_R_NANMAX, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_NANMIN: return reduce_out<MMP_R_NANMIN, T>(out_dtype, outer, len, inner, x, out);
+      case MMP_R_NANMEAN: return reduce_out<MMP_R_NANMEAN, T>(out_dtype, outer, len, inner, x, out);
       default: return mmpi::fail(MMP_E_ARG, "unknown reduction op %d", op);
     }
   })
@@ -710,6 +792,10 @@ extern "C" int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len, int6
       return launch_argreduce<MMP_R_ARGMAX, T>(outer, len, inner, x, (long long *)out);
     if (op == MMP_R_ARGMIN)
       return launch_argreduce<MMP_R_ARGMIN, T>(outer, len, inner, x, (long long *)out);
+    if (op == MMP_R_NANARGMAX)
+      return launch_argreduce<MMP_R_NANARGMAX, T>(outer, len, inner, x, (long long *)out);
+    if (op == MMP_R_NANARGMIN)
+      return launch_argreduce<MMP_R_NANARGMIN, T>(outer, len, inner, x, (long long *)out);
     return mmpi::fail(MMP_E_ARG, "unknown arg-reduction op %d", op);
   })
 }

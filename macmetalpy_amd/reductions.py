@@ -96,7 +96,13 @@ def _layout(shape, axes):
 
 
 _CODES = {"sum": _abi.REDUCE_SUM, "prod": _abi.REDUCE_PROD, "max": _abi.REDUCE_MAX,
-          "min": _abi.REDUCE_MIN, "mean": _abi.REDUCE_MEAN}
+          "min": _abi.REDUCE_MIN, "mean": _abi.REDUCE_MEAN,
+          "nansum": _abi.REDUCE_NANSUM, "nanprod": _abi.REDUCE_NANPROD,
+          "nanmax": _abi.REDUCE_NANMAX, "nanmin": _abi.REDUCE_NANMIN,
+          "nanmean": _abi.REDUCE_NANMEAN}
+# NaN-ignoring kinds share the result dtype and empty-slice rules of these
+_BASE_KIND = {"nansum": "sum", "nanprod": "prod", "nanmax": "max", "nanmin": "min",
+              "nanmean": "mean"}
 
 
 def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
@@ -104,10 +110,10 @@ def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
     axes = _axes(axis, a.ndim)
     if dtype is not None:
         a = a.astype(dtype)
-    if kind in ("max", "min"):
+    if kind in ("max", "min", "nanmax", "nanmin"):
         odt = a._dtype
     else:
-        odt = _np_out_dtype(kind, a._dtype)
+        odt = _np_out_dtype(_BASE_KIND.get(kind, kind), a._dtype)
     oshape = _out_shape(a._shape, axes, keepdims)
     red_len = _prod(a._shape) if axes is None else _prod(a._shape[i] for i in axes)
 
@@ -140,6 +146,10 @@ def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
 
 def _empty_reduction(kind, oshape, odt, red_len):
     from . import creation
+    if kind in ("nanmax", "nanmin") and red_len == 0:
+        raise ValueError(f"zero-size array to reduction operation f{kind[3:]} which has no "
+                         "identity")
+    kind = _BASE_KIND.get(kind, kind)
     if red_len == 0:
         if kind == "sum":
             return creation.zeros(oshape, dtype=odt)
@@ -228,20 +238,25 @@ def all(a, axis=None, out=None, keepdims=False, where=np._NoValue):
 
 def _argreduce(a, op, axis, out, keepdims):
     a = _asarray(a)
-    name = "argmax" if op == _abi.REDUCE_ARGMAX else "argmin"
+    name = {_abi.REDUCE_ARGMAX: "argmax", _abi.REDUCE_ARGMIN: "argmin",
+            _abi.REDUCE_NANARGMAX: "nanargmax", _abi.REDUCE_NANARGMIN: "nanargmin"}[op]
     if a.size == 0:
         raise ValueError(f"attempt to get {name} of an empty sequence")
     x = a._ensure_contiguous()
     be = HipBackend()
+    skip_nan = op in (_abi.REDUCE_NANARGMAX, _abi.REDUCE_NANARGMIN)
     if axis is None:
         res = ndarray._empty_device((), np.int64)
         be.argreduce(op, dtype_code(x._dtype), 1, x.size, 1, x._ptr, res._ptr)
+        if skip_nan or not (keepdims or out is not None):
+            idx = int(res.get())  # reference returns a Python int (reductions.py:407)
+            if skip_nan and idx == _abi.ARG_NONE:
+                raise ValueError("All-NaN slice encountered")
         if keepdims:
-            res = res.reshape((1,) * a.ndim)
-            return _finish(res, out)
+            return _finish(res.reshape((1,) * a.ndim), out)
         if out is not None:
             return _finish(res, out)
-        return int(res.get())  # reference returns a Python int (reductions.py:407)
+        return idx
     ax = _normalize_axis(axis, a.ndim)
     outer, length, inner = _prod(x._shape[:ax]), x._shape[ax], _prod(x._shape[ax + 1:])
     if length == 0:
@@ -249,6 +264,8 @@ def _argreduce(a, op, axis, out, keepdims):
     oshape = _out_shape(x._shape, (ax,), keepdims)
     res = ndarray._empty_device(oshape, np.int64)
     be.argreduce(op, dtype_code(x._dtype), outer, length, inner, x._ptr, res._ptr)
+    if skip_nan and res.size and int(max(res)) == _abi.ARG_NONE:
+        raise ValueError("All-NaN slice encountered")
     return _finish(res, out)
 
 

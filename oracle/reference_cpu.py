@@ -78,6 +78,24 @@ def count_nonzero(a, axis=None, keepdims=False):
     return np.count_nonzero(a, axis=axis, keepdims=keepdims)
 
 
+# NaN-aware reductions: the reference's CPU branches call NumPy's nan*
+# functions (nan_ops.py:132-141, 187-196, 229-237, 258-266, 293-302,
+# 346-355, 397-404, 503-510, 571-576, 596-601).
+NAN_REDUCTIONS = {
+    "nansum": np.nansum, "nanprod": np.nanprod, "nanmax": np.nanmax, "nanmin": np.nanmin,
+    "nanmean": np.nanmean, "nanvar": np.nanvar, "nanstd": np.nanstd,
+    "nanargmax": np.nanargmax, "nanargmin": np.nanargmin, "nancumsum": np.nancumsum,
+    "nancumprod": np.nancumprod,
+}
+
+
+def nan_reduce(name, x, **kw):
+    import warnings
+    with warnings.catch_warnings(), np.errstate(all="ignore"):
+        warnings.simplefilter("ignore", RuntimeWarning)
+        return NAN_REDUCTIONS[name](x, **kw)
+
+
 def unary(op_name: str, x: np.ndarray) -> np.ndarray:
     with np.errstate(all="ignore"):
         return UNARY[op_name](x)

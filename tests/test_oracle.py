@@ -278,3 +278,46 @@ def test_where_clip_any_all_count_against_python():
     assert ref.count_nonzero(m) == 3
     assert ref.any_(np.zeros((2, 0)), axis=1).tolist() == [False, False]
     assert ref.all_(np.zeros((2, 0)), axis=1).tolist() == [True, True]
+
+
+# ------------------------------------------------------- NaN reductions
+def test_nan_reductions_against_python_loops():
+    """Each nan* function equals the plain operation over the non-NaN
+    elements of each row (first index for the arg ops); all-NaN rows give
+    0 / 1 / NaN, and the arg ops raise."""
+    rows = [[1.5, np.nan, -2.0, 7.0, 7.0], [np.nan] * 5, [0.0, -0.0, np.nan, -np.inf, 3.0],
+            [2.0, 2.0, 2.0, np.nan, 1.0]]
+    x = np.array(rows, np.float64)
+
+    def clean(r):
+        return [v for v in r if v == v]
+
+    assert ref.nan_reduce("nansum", x, axis=1).tolist() == [sum(clean(r)) for r in rows]
+    np.testing.assert_array_equal(ref.nan_reduce("nanprod", x, axis=1),
+                                  [math.prod(clean(r)) for r in rows])  # 0 * -inf is NaN
+    for name, f in (("nanmax", max), ("nanmin", min)):
+        got = ref.nan_reduce(name, x, axis=1)
+        for g, r in zip(got.tolist(), rows):
+            assert (g != g) if not clean(r) else g == f(clean(r))
+    got = ref.nan_reduce("nanmean", x, axis=1)
+    for g, r in zip(got.tolist(), rows):
+        c = clean(r)
+        assert (g != g) if not c else g == sum(c) / len(c)
+    v1 = ref.nan_reduce("nanvar", x[[0, 3]], axis=1, ddof=1)
+    for g, r in zip(v1.tolist(), (rows[0], rows[3])):
+        c = clean(r)
+        m = sum(c) / len(c)
+        assert math.isclose(g, sum((t - m) ** 2 for t in c) / (len(c) - 1), rel_tol=1e-12)
+    ok = x[[0, 2, 3]]
+    for name, f in (("nanargmax", max), ("nanargmin", min)):
+        got = ref.nan_reduce(name, ok, axis=1).tolist()
+        want = [next(i for i, v in enumerate(r) if v == f(clean(r))) for r in ok.tolist()]
+        assert got == want
+        with pytest.raises(ValueError):
+            ref.nan_reduce(name, x, axis=1)
+    cs = ref.nan_reduce("nancumsum", x[0])
+    acc, want = 0.0, []
+    for v in rows[0]:
+        acc += 0.0 if v != v else v
+        want.append(acc)
+    assert cs.tolist() == want

@@ -309,6 +309,55 @@ def bench_nan(cp, be, reps=10):
     return res
 
 
+# ------------------------------------------------------------- sorting
+def bench_sort(cp, be, reps=5):
+    """Radix sort / argsort of 2^24 and 2^28 float32 keys (N(0,1)) and
+    searchsorted of 2^20 queries into 2^24 sorted keys.  `gkeys_s` is
+    keys per second; `gbs` counts the HBM bytes of the LSD passes as
+    designed (per 8-bit digit pass: keys, and 4-byte indices for argsort,
+    read twice and written once; plus the key-conversion pass)."""
+    rng = np.random.default_rng(12)
+    res = {}
+    for log2n in (24, 28):
+        n = 1 << log2n
+        x = cp.array(rng.standard_normal(n, dtype=np.float32))
+        x._ensure_gpu()
+        cases = {f"sort_f32_2^{log2n}": (lambda: cp.sort(x), 4 * (3 * 4) + 8),
+                 f"argsort_f32_2^{log2n}": (lambda: cp.argsort(x), 4 * (3 * 8) + 12 + 12)}
+        for name, (f, bpe) in cases.items():
+            try:
+                f()
+                cp.synchronize()
+                timer = EventTimer(be)
+                for _ in range(reps):
+                    timer.run(name, f)
+                cp.synchronize()
+                ms, _ = timer.ms(name)
+                timer.close()
+                res[name] = {"kernel_ms": round(ms, 4), "gkeys_s": round(n / ms / 1e6, 2),
+                             "gbs": round(bpe * n / ms / 1e6, 1)}
+            except Exception as e:
+                res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+        if log2n == 24:
+            a = cp.sort(x)
+            q = cp.array(rng.standard_normal(1 << 20, dtype=np.float32))
+            q._ensure_gpu()
+            f = lambda: cp.searchsorted(a, q)  # noqa: E731
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run("searchsorted", f)
+            cp.synchronize()
+            ms, _ = timer.ms("searchsorted")
+            timer.close()
+            res["searchsorted_2^20_in_2^24"] = {"kernel_ms": round(ms, 4),
+                                                "gqueries_s": round((1 << 20) / ms / 1e6, 2)}
+            del a, q
+        del x
+    return res
+
+
 # --------------------------------------------------------------- C5
 def bench_c5(cp, be, reps=10):
     from macmetalpy_amd.workloads import c5_inputs
@@ -494,7 +543,8 @@ def main():
         for name, fn in (("c1_fused_elementwise", bench_c1), ("c3_reduce_scan", bench_c3),
                          ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5),
                          ("logic_where_clip_2p28", bench_logic),
-                         ("nan_reductions_16384sq", bench_nan)):
+                         ("nan_reductions_16384sq", bench_nan),
+                         ("sort_searchsorted", bench_sort)):
             t = time.time()
             try:
                 cfgs[name] = fn(cp, be)

@@ -265,6 +265,33 @@ int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
              int64_t inner, const void *x, void *out);
 
 /* ======================================================================== */
+/* Sorting: replaces sorting._bitonic_sort_1d (sorting.py:59-196, behind    */
+/* sort / argsort :21-56) and searchsorted's GPU path (sorting.py:218-263)   */
+/* ======================================================================== */
+
+/* Sort each of `rows` contiguous rows of `len` elements ascending (NaN
+ * last).  out_values (rows*len of dtype) and / or out_indices (int64,
+ * positions within the row, as np.argsort) may be null, not both.  With
+ * out_indices, rows > 1 or stable != 0 the order is stable (equal to
+ * kind='stable'; -0.0 == +0.0) and values are gathered from x bit for bit;
+ * a 1-D values-only sort keeps every value's bits except the sign of NaNs.
+ * rows*len <= 2^32 - 8192.  x must not alias the outputs. */
+int mmp_sort(int dtype, int64_t rows, int64_t len, const void *x, void *out_values,
+             int64_t *out_indices, int stable);
+
+/* out[i] = insertion index of values[i] into sorted[0..n) (ascending, NaN
+ * last): the first such index (side_right = 0) or the last (1). */
+int mmp_searchsorted(int dtype, int64_t n, const void *sorted, int64_t m,
+                     const void *values, int side_right, int64_t *out);
+
+/* out[i] = src[indices[i]] for elements of `itemsize` (1, 2, 4, 8) bytes;
+ * an index outside [0, nsrc) reads nothing and yields 0 (callers check
+ * ranges).  Replaces the host gathers of take / fancy indexing
+ * (indexing.py) on the sort path. */
+int mmp_take(int itemsize, int64_t nsrc, const void *src, int64_t n,
+             const int64_t *indices, void *out);
+
+/* ======================================================================== */
 /* Matmul: replaces ndarray.__matmul__ + matmul_shader (ndarray.py:1398-1450,*/
 /* _kernels.py:740-759); batched form replaces linalg_top.matmul's CPU path */
 /* (linalg_top.py:105-106)                                                  */

@@ -5,7 +5,7 @@ path (src/macmetalpy/__init__.py:8-236): ndarray, creation, random inputs,
 elementwise ufuncs (arithmetic, transcendental, comparison, bitwise,
 logical, predicates), where / clip, sum/mean/max/min/prod/argmax/argmin,
 any/all/count_nonzero, NaN-aware reductions (nansum, nanmax, nanargmax, ...),
-cumsum/cumprod,
+sort/argsort/searchsorted, cumsum/cumprod,
 matmul / linalg.matmul / dot, RawKernel, set_config and synchronize.
 Unlike the reference (darwin-only, __init__.py:5-6) it imports on any host;
 device work needs libmmp_hip.so and a gfx950 GPU and raises otherwise.
@@ -45,6 +45,7 @@ from .nan_ops import (
     nansum, nanprod, nanmax, nanmin, nanmean, nanvar, nanstd, nanargmax, nanargmin,
     nancumsum, nancumprod,
 )
+from .sorting import sort, argsort, searchsorted
 from .linalg_top import matmul, dot, vdot, inner
 from . import linalg
 from . import random

@@ -91,6 +91,9 @@ _SIGNATURES = {
     "mmp_reduce": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_argreduce": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_scan": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_sort": [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int],
+    "mmp_searchsorted": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp],
+    "mmp_take": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp],
     "mmp_matmul": [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
                    _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64],
     "mmp_rtc_compile": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_c_vp)],
@@ -313,6 +316,19 @@ class HipBackend:
              inner: int, x: int, out: int) -> None:
         _check(self._lib.mmp_scan(op, dcode, out_code, outer, length, inner, x, out),
                "mmp_scan")
+
+    def sort(self, dcode: int, rows: int, length: int, x: int, out_values, out_indices,
+             stable: bool) -> None:
+        _check(self._lib.mmp_sort(dcode, rows, length, x, out_values, out_indices,
+                                  1 if stable else 0), "mmp_sort")
+
+    def searchsorted(self, dcode: int, n: int, sorted_ptr: int, m: int, values: int,
+                     side_right: bool, out: int) -> None:
+        _check(self._lib.mmp_searchsorted(dcode, n, sorted_ptr, m, values,
+                                          1 if side_right else 0, out), "mmp_searchsorted")
+
+    def take(self, itemsize: int, nsrc: int, src: int, n: int, indices: int, out: int) -> None:
+        _check(self._lib.mmp_take(itemsize, nsrc, src, n, indices, out), "mmp_take")
 
     def matmul(self, dcode: int, batch: int, M: int, N: int, K: int,
                A: int, lda: int, sA: int, B: int, ldb: int, sB: int,

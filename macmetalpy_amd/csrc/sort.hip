@@ -1,0 +1,457 @@
+// sort.hip -- sort / argsort along the last axis, searchsorted, take.
+//
+// Replaces the reference's GPU sort, a bitonic network launched from
+// Python one compare-exchange pass at a time (sorting.py:59-196: padding
+// to a power of two, log2(n)^2 / 2 launches, unstable, int32 indices,
+// NaN unordered), and its one-thread binary searchsorted
+// (sorting.py:218-263).
+//
+// Sort: least-significant-digit radix sort with 8-bit digits over
+// order-preserving unsigned keys, stable, three launches per digit:
+//  * k_radix_hist: one 256-bin histogram per 4096-key tile (LDS atomics,
+//    one histogram per wave), written digit-major: counts[d * tiles + b];
+//  * one inclusive scan of the counts (mmp_scan), so that the global
+//    offset of digit d in tile b is incl[d * tiles + b] - counts[...];
+//  * k_radix_scatter: the tile is re-read in 16 rounds of 256 keys; in
+//    each round a wave finds the lanes holding its own digit with eight
+//    64-lane ballots, ranks itself among them, and the 4 waves' counts
+//    are turned into per-digit offsets by one thread per digit; keys are
+//    placed into an LDS staging tile in sorted order and written out from
+//    there, so that consecutive threads write consecutive addresses of one
+//    digit's run (coalesced).  Rounds, waves and lanes follow input order,
+//    which makes every pass stable.
+// Rows (the leading axes of an N-D input) are sorted independently by
+// carrying each key's flat index and adding the row number (index / len)
+// as more significant digits after the key digits.  Keys: float bit
+// patterns with the sign flipped (positive) or all bits inverted
+// (negative); NaN sorts last, as in NumPy.  When an index is carried
+// (argsort, N-D, stable) keys are canonical -- -0.0 equals +0.0 and all
+// NaNs are equal -- and sorted values are gathered from the input by the
+// final index, which reproduces np.sort(kind='stable') bit for bit; a
+// keys-only 1-D sort keeps every value's bits except the sign of NaNs.
+// HBM traffic per digit pass: keys (and 4-byte indices) read twice and
+// written once.
+#include "mmp_ops.h"
+#include "mmp_internal.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kIPT = 16;
+constexpr int kTile = kBlock * kIPT;
+constexpr int kRadix = 256;
+
+template <int B> struct UInt;
+template <> struct UInt<2> { typedef unsigned short type; };
+template <> struct UInt<4> { typedef unsigned int type; };
+template <> struct UInt<8> { typedef unsigned long long type; };
+
+// key type: 16 bits for bool and 16-bit types, else the type's width
+template <typename T> struct KeyOf {
+  typedef typename UInt<(sizeof(T) < 2 ? 2 : sizeof(T))>::type K;
+};
+
+template <typename T, bool CANON>
+__device__ __forceinline__ typename KeyOf<T>::K to_key(T v) {
+  typedef typename KeyOf<T>::K K;
+  if constexpr (mmp_t<T>::is_bool) {
+    return (K)(v ? 1 : 0);
+  } else if constexpr (mmp_t<T>::is_float) {
+    constexpr K sign = (K)1 << (8 * sizeof(K) - 1);
+    K u = __builtin_bit_cast(K, v);
+    const bool nan = (typename mmp_t<T>::C)v != (typename mmp_t<T>::C)v;
+    if (nan) u = CANON ? (K)~(K)0 >> 1 : (K)(u & ~sign);  // positive NaN, above +inf
+    if (CANON && u == sign) u = 0;                          // -0.0 -> +0.0
+    return (u & sign) ? (K)~u : (K)(u | sign);
+  } else if constexpr (mmp_t<T>::is_signed) {
+    constexpr K sign = (K)1 << (8 * sizeof(K) - 1);
+    return (K)((K)v ^ sign);
+  } else {
+    return (K)v;
+  }
+}
+
+template <typename T> __device__ __forceinline__ T from_key(typename KeyOf<T>::K k) {
+  typedef typename KeyOf<T>::K K;
+  if constexpr (mmp_t<T>::is_bool) {
+    return k != 0;
+  } else if constexpr (mmp_t<T>::is_float) {
+    constexpr K sign = (K)1 << (8 * sizeof(K) - 1);
+    return __builtin_bit_cast(T, (K)((k & sign) ? (K)(k ^ sign) : (K)~k));
+  } else if constexpr (mmp_t<T>::is_signed) {
+    constexpr K sign = (K)1 << (8 * sizeof(K) - 1);
+    return (T)(K)(k ^ sign);
+  } else {
+    return (T)k;
+  }
+}
+
+template <typename K, bool ROW>
+__device__ __forceinline__ unsigned digit_of(K key, unsigned id, int shift, unsigned len) {
+  if constexpr (ROW) return ((id / len) >> shift) & 255u;
+  else return (unsigned)(key >> shift) & 255u;
+}
+
+// keys[p] = to_key(x[p]); idx[p] = p
+template <typename T, bool CANON>
+__global__ __launch_bounds__(kBlock) void k_radix_prep(const T *__restrict__ x,
+                                                       typename KeyOf<T>::K *__restrict__ keys,
+                                                       unsigned *__restrict__ idx, unsigned n) {
+  const unsigned p = blockIdx.x * kBlock + threadIdx.x;
+  if (p >= n) return;
+  keys[p] = to_key<T, CANON>(x[p]);
+  if (idx) idx[p] = p;
+}
+
+template <typename K, bool ROW>
+__global__ __launch_bounds__(kBlock) void k_radix_hist(const K *__restrict__ keys,
+                                                       const unsigned *__restrict__ idx,
+                                                       unsigned n, int shift, unsigned len,
+                                                       unsigned *__restrict__ counts,
+                                                       unsigned tiles) {
+  __shared__ unsigned h[kBlock / 64][kRadix];
+  const int t = threadIdx.x, w = t >> 6;
+#pragma unroll
+  for (int k = 0; k < kBlock / 64; ++k) h[k][t] = 0;
+  __syncthreads();
+  const unsigned base = blockIdx.x * (unsigned)kTile;
+#pragma unroll 4
+  for (int r = 0; r < kIPT; ++r) {
+    const unsigned p = base + (unsigned)(r * kBlock + t);
+    if (p < n) {
+      const unsigned d = digit_of<K, ROW>(ROW ? (K)0 : keys[p], ROW ? idx[p] : 0u, shift, len);
+      atomicAdd(&h[w][d], 1u);
+    }
+  }
+  __syncthreads();
+  counts[(size_t)t * tiles + blockIdx.x] = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+}
+
+// exclusive prefix over the 256 threads of a block (value per thread)
+__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned *lds4) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  unsigned incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) lds4[w] = incl;
+  __syncthreads();
+  unsigned before = 0;
+  for (int k = 0; k < w; ++k) before += lds4[k];
+  return before + incl - v;
+}
+
+// FINAL: 0 = intermediate pass (keys and indices to kout / iout);
+// 1 = last pass of a keys-only sort (values to vout);
+// 2 = last pass with indices (row-relative int64 indices to oidx and / or
+//     values gathered from x to vout).
+template <typename T, bool ROW, bool IDX, int FINAL>
+__global__ __launch_bounds__(kBlock) void k_radix_scatter(
+    const typename KeyOf<T>::K *__restrict__ kin, const unsigned *__restrict__ iin,
+    typename KeyOf<T>::K *__restrict__ kout, unsigned *__restrict__ iout, unsigned n, int shift,
+    unsigned len, const unsigned *__restrict__ counts, const unsigned long long *__restrict__ incl,
+    unsigned tiles, const T *__restrict__ x, T *__restrict__ vout, long long *__restrict__ oidx) {
+  typedef typename KeyOf<T>::K K;
+  __shared__ K sk[kTile];
+  __shared__ unsigned si[IDX ? kTile : 1];
+  __shared__ unsigned short wc[2][kBlock / 64][kRadix];
+  __shared__ unsigned run[kRadix];
+  __shared__ unsigned dstart[kRadix];
+  __shared__ unsigned long long goff[kRadix];
+  __shared__ unsigned lds4[kBlock / 64];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const unsigned b = blockIdx.x;
+  const unsigned base = b * (unsigned)kTile;
+  const unsigned ntile = n - base < (unsigned)kTile ? n - base : (unsigned)kTile;
+
+  K key[kIPT];
+  unsigned id[kIPT];
+  unsigned dg[kIPT];
+#pragma unroll
+  for (int r = 0; r < kIPT; ++r) {
+    const unsigned p = base + (unsigned)(r * kBlock + t);
+    const bool valid = p < n;
+    key[r] = valid ? kin[p] : (K)0;
+    id[r] = (IDX && valid) ? iin[p] : 0u;
+    dg[r] = valid ? digit_of<K, ROW>(key[r], id[r], shift, len) : 256u;
+  }
+  {
+    const unsigned c = counts[(size_t)t * tiles + b];
+    const unsigned ex = block_exclusive_scan(c, lds4);
+    dstart[t] = ex;
+    goff[t] = incl[(size_t)t * tiles + b] - c;
+    run[t] = 0;
+#pragma unroll
+    for (int k = 0; k < kBlock / 64; ++k) {
+      wc[0][k][t] = 0;
+      wc[1][k][t] = 0;
+    }
+  }
+  __syncthreads();
+
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int r = 0; r < kIPT; ++r) {
+    const int S = r & 1;
+    const unsigned d = dg[r];
+    const bool valid = d < 256u;
+    unsigned long long m = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool on = (d >> bit) & 1u;
+      const unsigned long long bb = __ballot(valid && on);
+      m &= on ? bb : ~bb;
+    }
+    const unsigned long long lower = m & lt_mask;
+    const unsigned rank = (unsigned)__popcll(lower);
+    if (valid && lower == 0ull) wc[S][w][d] = (unsigned short)__popcll(m);
+    __syncthreads();
+    {
+      // one thread per digit: per-wave offsets of this round; clear the
+      // other set for the next round
+      unsigned acc = run[t];
+#pragma unroll
+      for (int k = 0; k < kBlock / 64; ++k) {
+        const unsigned c = wc[S][k][t];
+        wc[S][k][t] = (unsigned short)acc;
+        acc += c;
+        wc[S ^ 1][k][t] = 0;
+      }
+      run[t] = acc;
+    }
+    __syncthreads();
+    if (valid) {
+      const unsigned pos = dstart[d] + wc[S][w][d] + rank;
+      sk[pos] = key[r];
+      if constexpr (IDX) si[pos] = id[r];
+    }
+  }
+  __syncthreads();
+
+  for (unsigned p = t; p < ntile; p += kBlock) {
+    const K k = sk[p];
+    const unsigned i = IDX ? si[p] : 0u;
+    const unsigned d = digit_of<K, ROW>(k, i, shift, len);
+    const unsigned long long g = goff[d] + (p - dstart[d]);
+    if constexpr (FINAL == 0) {
+      kout[g] = k;
+      if constexpr (IDX) iout[g] = i;
+    } else if constexpr (FINAL == 1) {
+      vout[g] = from_key<T>(k);
+    } else {
+      if (oidx) oidx[g] = (long long)(i % len);
+      if (vout) vout[g] = x[i];
+    }
+  }
+}
+
+template <typename T, bool ROW, bool IDX, int FINAL>
+int launch_scatter(unsigned tiles, const void *kin, const unsigned *iin, void *kout, unsigned *iout,
+                   unsigned n, int shift, unsigned len, const unsigned *counts,
+                   const unsigned long long *incl, const T *x, T *vout, long long *oidx) {
+  typedef typename KeyOf<T>::K K;
+  hipLaunchKernelGGL((k_radix_scatter<T, ROW, IDX, FINAL>), dim3(tiles), dim3(kBlock), 0,
+                     mmpi::stream(), (const K *)kin, iin, (K *)kout, iout, n, shift, len, counts,
+                     incl, tiles, x, vout, oidx);
+  return mmpi::check_launch("mmp_sort(scatter)");
+}
+
+// temporaries from the library's stream-ordered pool, released on scope exit
+struct Temp {
+  void *p = nullptr;
+  ~Temp() {
+    if (p) (void)mmp_free(p);
+  }
+  int get(size_t bytes) { return mmp_alloc(bytes ? bytes : 1, &p); }
+};
+
+template <typename T>
+int sort_impl(long long rows, long long len, const T *x, T *vout, long long *oidx, bool stable) {
+  typedef typename KeyOf<T>::K K;
+  const long long n64 = rows * len;
+  // 32-bit positions: a tile's last position must not wrap
+  if (n64 > 0xffffe000LL) return mmpi::fail(MMP_E_UNSUPPORTED, "mmp_sort: more than 2^32 - 8192 elements");
+  const unsigned n = (unsigned)n64, ulen = (unsigned)len;
+  const bool idx = oidx != nullptr || rows > 1 || stable;
+  const unsigned tiles = (unsigned)mmpi::ceil_div(n, kTile);
+  Temp ka, kb, ia, ib, cnt, inc;
+  if (int st = ka.get((size_t)n * sizeof(K))) return st;
+  if (int st = kb.get((size_t)n * sizeof(K))) return st;
+  if (idx) {
+    if (int st = ia.get((size_t)n * 4)) return st;
+    if (int st = ib.get((size_t)n * 4)) return st;
+  }
+  if (int st = cnt.get((size_t)tiles * kRadix * 4)) return st;
+  if (int st = inc.get((size_t)tiles * kRadix * 8)) return st;
+
+  const unsigned pgrid = (unsigned)mmpi::ceil_div(n, kBlock);
+  if (idx)
+    hipLaunchKernelGGL((k_radix_prep<T, true>), dim3(pgrid), dim3(kBlock), 0, mmpi::stream(), x,
+                       (K *)ka.p, (unsigned *)ia.p, n);
+  else
+    hipLaunchKernelGGL((k_radix_prep<T, false>), dim3(pgrid), dim3(kBlock), 0, mmpi::stream(), x,
+                       (K *)ka.p, (unsigned *)nullptr, n);
+  if (int st = mmpi::check_launch("mmp_sort(prep)")) return st;
+
+  // digit passes: key bytes, then row-number bytes
+  int key_passes = (int)sizeof(K);
+  int row_passes = 0;
+  for (unsigned long long r = (unsigned long long)(rows - 1); r; r >>= 8) ++row_passes;
+  const int passes = key_passes + row_passes;
+  void *kin = ka.p, *kout = kb.p;
+  unsigned *iin = (unsigned *)ia.p, *iout = (unsigned *)ib.p;
+  for (int ps = 0; ps < passes; ++ps) {
+    const bool row = ps >= key_passes;
+    const int shift = 8 * (row ? ps - key_passes : ps);
+    const bool last = ps == passes - 1;
+    if (row)
+      hipLaunchKernelGGL((k_radix_hist<K, true>), dim3(tiles), dim3(kBlock), 0, mmpi::stream(),
+                         (const K *)kin, iin, n, shift, ulen, (unsigned *)cnt.p, tiles);
+    else
+      hipLaunchKernelGGL((k_radix_hist<K, false>), dim3(tiles), dim3(kBlock), 0, mmpi::stream(),
+                         (const K *)kin, iin, n, shift, ulen, (unsigned *)cnt.p, tiles);
+    if (int st = mmpi::check_launch("mmp_sort(hist)")) return st;
+    if (int st = mmp_scan(MMP_S_CUMSUM, MMP_U32, MMP_U64, 1, (int64_t)tiles * kRadix, 1, cnt.p,
+                          inc.p))
+      return st;
+    const unsigned *c = (const unsigned *)cnt.p;
+    const unsigned long long *ic = (const unsigned long long *)inc.p;
+    int st;
+    if (!idx) {
+      st = last ? launch_scatter<T, false, false, 1>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
+                                                    ic, x, vout, oidx)
+                : launch_scatter<T, false, false, 0>(tiles, kin, iin, kout, iout, n, shift, ulen,
+                                                    c, ic, x, vout, oidx);
+    } else if (row) {
+      st = last ? launch_scatter<T, true, true, 2>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
+                                                  ic, x, vout, oidx)
+                : launch_scatter<T, true, true, 0>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
+                                                  ic, x, vout, oidx);
+    } else {
+      st = last ? launch_scatter<T, false, true, 2>(tiles, kin, iin, kout, iout, n, shift, ulen,
+                                                   c, ic, x, vout, oidx)
+                : launch_scatter<T, false, true, 0>(tiles, kin, iin, kout, iout, n, shift, ulen,
+                                                   c, ic, x, vout, oidx);
+    }
+    if (st) return st;
+    void *tk = kin;
+    kin = kout;
+    kout = tk;
+    unsigned *ti = iin;
+    iin = iout;
+    iout = ti;
+  }
+  return MMP_OK;
+}
+
+// -------------------------------------------------------- searchsorted
+// NumPy's order: NaN after everything, -0.0 == +0.0.
+template <typename T> __device__ __forceinline__ bool lt_nan_last(T a_, T b_) {
+  if constexpr (mmp_t<T>::is_float) {
+    typedef typename mmp_t<T>::C C;
+    const C a = (C)a_, b = (C)b_;
+    return a < b || (b != b && a == a);
+  } else {
+    return a_ < b_;
+  }
+}
+
+template <typename T, bool RIGHT>
+__global__ __launch_bounds__(kBlock) void k_searchsorted(const T *__restrict__ a, long long n,
+                                                         const T *__restrict__ v, long long m,
+                                                         long long *__restrict__ out) {
+  const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= m) return;
+  const T q = v[i];
+  long long lo = 0, hi = n;
+  while (lo < hi) {
+    const long long mid = lo + ((hi - lo) >> 1);
+    const bool go_right = RIGHT ? !lt_nan_last(q, a[mid]) : lt_nan_last(a[mid], q);
+    if (go_right) lo = mid + 1;
+    else hi = mid;
+  }
+  out[i] = lo;
+}
+
+// ---------------------------------------------------------------- take
+template <typename U>
+__global__ __launch_bounds__(kBlock) void k_take(const U *__restrict__ src, long long nsrc,
+                                                 const long long *__restrict__ idx, long long n,
+                                                 U *__restrict__ out) {
+  const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const long long j = idx[i];
+  out[i] = (j >= 0 && j < nsrc) ? src[j] : (U)0;  // out-of-range indices read nothing
+}
+
+}  // namespace
+
+extern "C" int mmp_sort(int dtype, int64_t rows, int64_t len, const void *x, void *out_values,
+                        int64_t *out_indices, int stable) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (rows < 0 || len < 0) return mmpi::fail(MMP_E_ARG, "mmp_sort: negative extent");
+  if (rows * len == 0) return MMP_OK;
+  if (!x || (!out_values && !out_indices)) return mmpi::fail(MMP_E_ARG, "mmp_sort: null pointer");
+  MMP_DISPATCH_ALL(dtype, {
+    return sort_impl<T>(rows, len, (const T *)x, (T *)out_values, (long long *)out_indices,
+                        stable != 0);
+  })
+}
+
+extern "C" int mmp_searchsorted(int dtype, int64_t n, const void *sorted, int64_t m,
+                                const void *values, int side_right, int64_t *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (n < 0 || m < 0) return mmpi::fail(MMP_E_ARG, "mmp_searchsorted: negative extent");
+  if (m == 0) return MMP_OK;
+  if (!values || !out || (n > 0 && !sorted))
+    return mmpi::fail(MMP_E_ARG, "mmp_searchsorted: null pointer");
+  const unsigned grid = (unsigned)mmpi::ceil_div(m, kBlock);
+  MMP_DISPATCH_ALL(dtype, {
+    if (side_right)
+      hipLaunchKernelGGL((k_searchsorted<T, true>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
+                         (const T *)sorted, (long long)n, (const T *)values, (long long)m,
+                         (long long *)out);
+    else
+      hipLaunchKernelGGL((k_searchsorted<T, false>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
+                         (const T *)sorted, (long long)n, (const T *)values, (long long)m,
+                         (long long *)out);
+    return mmpi::check_launch("mmp_searchsorted");
+  })
+}
+
+extern "C" int mmp_take(int itemsize, int64_t nsrc, const void *src, int64_t n,
+                        const int64_t *indices, void *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (nsrc < 0 || n < 0) return mmpi::fail(MMP_E_ARG, "mmp_take: negative extent");
+  if (n == 0) return MMP_OK;
+  if (!indices || !out || (nsrc > 0 && !src)) return mmpi::fail(MMP_E_ARG, "mmp_take: null pointer");
+  const unsigned grid = (unsigned)mmpi::ceil_div(n, kBlock);
+  const long long *ix = (const long long *)indices;
+  switch (itemsize) {
+    case 1:
+      hipLaunchKernelGGL((k_take<unsigned char>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
+                         (const unsigned char *)src, (long long)nsrc, ix, (long long)n,
+                         (unsigned char *)out);
+      break;
+    case 2:
+      hipLaunchKernelGGL((k_take<unsigned short>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
+                         (const unsigned short *)src, (long long)nsrc, ix, (long long)n,
+                         (unsigned short *)out);
+      break;
+    case 4:
+      hipLaunchKernelGGL((k_take<unsigned>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
+                         (const unsigned *)src, (long long)nsrc, ix, (long long)n, (unsigned *)out);
+      break;
+    case 8:
+      hipLaunchKernelGGL((k_take<unsigned long long>), dim3(grid), dim3(kBlock), 0,
+                         mmpi::stream(), (const unsigned long long *)src, (long long)nsrc, ix,
+                         (long long)n, (unsigned long long *)out);
+      break;
+    default:
+      return mmpi::fail(MMP_E_ARG, "mmp_take: item size %d", itemsize);
+  }
+  return mmpi::check_launch("mmp_take");
+}

@@ -546,6 +546,19 @@ class ndarray:
         from . import math_ops
         return math_ops.clip(self, min, max, out=out)
 
+    def sort(self, axis=-1, kind=None, order=None):
+        """Sort in place along ``axis`` (NumPy ndarray.sort)."""
+        from . import sorting
+        self._inplace(sorting.sort(self, axis=axis, kind=kind, order=order))
+
+    def argsort(self, axis=-1, kind=None, order=None):
+        from . import sorting
+        return sorting.argsort(self, axis=axis, kind=kind, order=order)
+
+    def searchsorted(self, v, side="left", sorter=None):
+        from . import sorting
+        return sorting.searchsorted(self, v, side=side, sorter=sorter)
+
     def argmax(self, axis=None, out=None, keepdims=False):
         from . import reductions
         return reductions.argmax(self, axis=axis, out=out, keepdims=keepdims)

@@ -96,6 +96,21 @@ def nan_reduce(name, x, **kw):
         return NAN_REDUCTIONS[name](x, **kw)
 
 
+# Sorting: the reference's CPU branches call np.sort / np.argsort /
+# np.searchsorted (sorting.py:30-31, 49-50, 259-262).  argsort is compared
+# with the stable kind (the device sort is stable).
+def sort(x, axis=-1, kind=None):
+    return np.sort(x, axis=axis, kind=kind)
+
+
+def argsort_stable(x, axis=-1):
+    return np.argsort(x, axis=axis, kind="stable")
+
+
+def searchsorted(a, v, side="left", sorter=None):
+    return np.searchsorted(a, v, side=side, sorter=sorter)
+
+
 def unary(op_name: str, x: np.ndarray) -> np.ndarray:
     with np.errstate(all="ignore"):
         return UNARY[op_name](x)

@@ -321,3 +321,35 @@ def test_nan_reductions_against_python_loops():
         acc += 0.0 if v != v else v
         want.append(acc)
     assert cs.tolist() == want
+
+
+# -------------------------------------------------------------- sorting
+def test_sort_argsort_searchsorted_against_python():
+    """np.sort / stable argsort / searchsorted against Python's sorted()
+    with NaN ordered last, stable ties by position, and bisect."""
+    import bisect
+    rng = np.random.default_rng(21)
+    x = rng.integers(-5, 5, 300).astype(np.float64)
+    x[::17] = np.nan
+    x[5] = -0.0
+    xs = x.tolist()
+
+    def key(i):
+        v = xs[i]
+        return (v != v, 0.0 if v != v else v)
+
+    order = sorted(range(len(xs)), key=key)          # stable
+    assert ref.argsort_stable(x).tolist() == order
+    got = ref.sort(x, kind="stable")
+    want = np.array([xs[i] for i in order])
+    assert np.array_equal(got, want, equal_nan=True)
+    assert np.array_equal(np.signbit(got), np.signbit(want))  # -0.0 kept in place
+    a = np.sort(rng.integers(0, 50, 200)).astype(np.int64)
+    al = a.tolist()
+    v = np.arange(-2, 53)
+    assert ref.searchsorted(a, v).tolist() == [bisect.bisect_left(al, t) for t in v.tolist()]
+    assert ref.searchsorted(a, v, side="right").tolist() == [
+        bisect.bisect_right(al, t) for t in v.tolist()]
+    f = np.array([1.0, 2.0, np.nan, np.nan])
+    assert ref.searchsorted(f, [np.nan, np.inf, 2.0], side="left").tolist() == [2, 2, 1]
+    assert ref.searchsorted(f, [np.nan], side="right").tolist() == [4]

@@ -313,17 +313,19 @@ def bench_nan(cp, be, reps=10):
 def bench_sort(cp, be, reps=5):
     """Radix sort / argsort of 2^24 and 2^28 float32 keys (N(0,1)) and
     searchsorted of 2^20 queries into 2^24 sorted keys.  `gkeys_s` is
-    keys per second; `gbs` counts the HBM bytes of the LSD passes as
-    designed (per 8-bit digit pass: keys, and 4-byte indices for argsort,
-    read twice and written once; plus the key-conversion pass)."""
+    keys per second; `gbs` counts the HBM bytes of the four 8-bit LSD
+    passes as designed: per pass the tile histogram reads the keys (4 B)
+    and the scatter reads and writes them (8 B) -- 48 B/key for sort; for
+    argsort the scatter also moves 4-byte indices (the first pass makes
+    them) -- 16 + 3 x 20 = 76 B/key."""
     rng = np.random.default_rng(12)
     res = {}
     for log2n in (24, 28):
         n = 1 << log2n
         x = cp.array(rng.standard_normal(n, dtype=np.float32))
         x._ensure_gpu()
-        cases = {f"sort_f32_2^{log2n}": (lambda: cp.sort(x), 4 * (3 * 4) + 8),
-                 f"argsort_f32_2^{log2n}": (lambda: cp.argsort(x), 4 * (3 * 8) + 12 + 12)}
+        cases = {f"sort_f32_2^{log2n}": (lambda: cp.sort(x), 48),
+                 f"argsort_f32_2^{log2n}": (lambda: cp.argsort(x), 76)}
         for name, (f, bpe) in cases.items():
             try:
                 f()
@@ -448,7 +450,7 @@ def _env(be):
 
 
 ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
-            "cumsum_f32", "matmul_f16")
+            "cumsum_f32", "matmul_f16", "sort_f32")
 
 
 def run_only(cp, be, name, steps):
@@ -465,6 +467,8 @@ def run_only(cp, be, name, steps):
         ci, cf = c3_scan_inputs()
         a = b = cp.array(ci if name == "cumsum_i32" else cf)
         del ci, cf
+    elif name == "sort_f32":
+        a = b = cp.array(np.random.default_rng(12).standard_normal(N28, dtype=np.float32))
     else:  # matmul_f16
         a, b = (cp.array(x) for x in c4_inputs("f16"))
     a._ensure_gpu()
@@ -472,7 +476,8 @@ def run_only(cp, be, name, steps):
     fn = {"add_f32": lambda: a + b, "sin_f32": lambda: cp.sin(a),
           "floor_divide_i32": lambda: cp.floor_divide(a, b), "mod_i32": lambda: cp.mod(a, b),
           "copy_f32": lambda: a.copy(), "cumsum_i32": lambda: cp.cumsum(a),
-          "cumsum_f32": lambda: cp.cumsum(a), "matmul_f16": lambda: a @ b}[name]
+          "cumsum_f32": lambda: cp.cumsum(a), "matmul_f16": lambda: a @ b,
+          "sort_f32": lambda: cp.sort(a)}[name]
     timer = EventTimer(be)
     for _ in range(steps):
         timer.run(name, lambda: _mat(fn()))

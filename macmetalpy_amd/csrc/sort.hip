@@ -12,14 +12,15 @@
 //    one histogram per wave), written digit-major: counts[d * tiles + b];
 //  * one inclusive scan of the counts (mmp_scan), so that the global
 //    offset of digit d in tile b is incl[d * tiles + b] - counts[...];
-//  * k_radix_scatter: the tile is re-read in 16 rounds of 256 keys; in
-//    each round a wave finds the lanes holding its own digit with eight
-//    64-lane ballots, ranks itself among them, and the 4 waves' counts
-//    are turned into per-digit offsets by one thread per digit; keys are
-//    placed into an LDS staging tile in sorted order and written out from
-//    there, so that consecutive threads write consecutive addresses of one
-//    digit's run (coalesced).  Rounds, waves and lanes follow input order,
-//    which makes every pass stable.
+//  * k_radix_scatter: each wave ranks a contiguous quarter of the tile in
+//    rounds of 64 keys: the lanes holding one digit find each other with
+//    eight 64-lane ballots and take consecutive ranks after the digit's
+//    running count in a wave-private LDS counter (no block barrier per
+//    round); the four waves' counts then become per-digit offsets, keys
+//    are placed into an LDS staging tile in sorted order and written out
+//    from there, so that consecutive threads write consecutive addresses
+//    of one digit's run (coalesced).  Waves, rounds and lanes follow input
+//    order, which makes every pass stable.
 // Rows (the leading axes of an N-D input) are sorted independently by
 // carrying each key's flat index and adding the row number (index / len)
 // as more significant digits after the key digits.  Keys: float bit
@@ -34,10 +35,12 @@
 #include "mmp_ops.h"
 #include "mmp_internal.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kIPT = 16;
+constexpr int kIPT = 16;  // 8, 24 and 32 keys per thread measured slower
 constexpr int kTile = kBlock * kIPT;
 constexpr int kRadix = 256;
 
@@ -92,35 +95,53 @@ __device__ __forceinline__ unsigned digit_of(K key, unsigned id, int shift, unsi
   else return (unsigned)(key >> shift) & 255u;
 }
 
-// keys[p] = to_key(x[p]); idx[p] = p
-template <typename T, bool CANON>
-__global__ __launch_bounds__(kBlock) void k_radix_prep(const T *__restrict__ x,
-                                                       typename KeyOf<T>::K *__restrict__ keys,
-                                                       unsigned *__restrict__ idx, unsigned n) {
-  const unsigned p = blockIdx.x * kBlock + threadIdx.x;
-  if (p >= n) return;
-  keys[p] = to_key<T, CANON>(x[p]);
-  if (idx) idx[p] = p;
-}
-
-template <typename K, bool ROW>
-__global__ __launch_bounds__(kBlock) void k_radix_hist(const K *__restrict__ keys,
+// Tile histogram of one digit.  FIRST: the pass reads the input values and
+// converts them to keys on the fly (no separate conversion sweep).  Whole
+// tiles of 16-byte-aligned data are read with 16-byte loads.
+template <typename T, bool ROW, bool FIRST, bool CANON>
+__global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ src,
                                                        const unsigned *__restrict__ idx,
                                                        unsigned n, int shift, unsigned len,
                                                        unsigned *__restrict__ counts,
                                                        unsigned tiles) {
+  typedef typename KeyOf<T>::K K;
+  typedef typename std::conditional<FIRST, T, K>::type E;  // element type read
   __shared__ unsigned h[kBlock / 64][kRadix];
   const int t = threadIdx.x, w = t >> 6;
 #pragma unroll
   for (int k = 0; k < kBlock / 64; ++k) h[k][t] = 0;
   __syncthreads();
   const unsigned base = blockIdx.x * (unsigned)kTile;
+  const E *e = reinterpret_cast<const E *>(src);
+  auto key_at = [&](E v) -> K {
+    if constexpr (FIRST) return to_key<T, CANON>(v);
+    else return v;
+  };
+  constexpr int V = 16 / sizeof(E);
+  if (!ROW && sizeof(E) <= 8 && base + (unsigned)kTile <= n &&
+      ((uintptr_t)(e + base) & 15u) == 0) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *pv = reinterpret_cast<const u32x4 *>(e + base);
 #pragma unroll 4
-  for (int r = 0; r < kIPT; ++r) {
-    const unsigned p = base + (unsigned)(r * kBlock + t);
-    if (p < n) {
-      const unsigned d = digit_of<K, ROW>(ROW ? (K)0 : keys[p], ROW ? idx[p] : 0u, shift, len);
-      atomicAdd(&h[w][d], 1u);
+    for (int j = t; j < kTile / V; j += kBlock) {
+      union {
+        u32x4 v;
+        E x[V];
+      } q;
+      q.v = __builtin_nontemporal_load(pv + j);
+#pragma unroll
+      for (int i = 0; i < V; ++i) atomicAdd(&h[w][(unsigned)(key_at(q.x[i]) >> shift) & 255u], 1u);
+    }
+  } else {
+#pragma unroll 4
+    for (int r = 0; r < kIPT; ++r) {
+      const unsigned p = base + (unsigned)(r * kBlock + t);
+      if (p < n) {
+        unsigned d;
+        if constexpr (ROW) d = ((idx[p] / len) >> shift) & 255u;
+        else d = (unsigned)(key_at(e[p]) >> shift) & 255u;
+        atomicAdd(&h[w][d], 1u);
+      }
     }
   }
   __syncthreads();
@@ -147,57 +168,63 @@ __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned *l
 // 1 = last pass of a keys-only sort (values to vout);
 // 2 = last pass with indices (row-relative int64 indices to oidx and / or
 //     values gathered from x to vout).
-template <typename T, bool ROW, bool IDX, int FINAL>
+template <typename T, bool ROW, bool IDX, int FINAL, bool FIRST>
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(
     const typename KeyOf<T>::K *__restrict__ kin, const unsigned *__restrict__ iin,
     typename KeyOf<T>::K *__restrict__ kout, unsigned *__restrict__ iout, unsigned n, int shift,
     unsigned len, const unsigned *__restrict__ counts, const unsigned long long *__restrict__ incl,
     unsigned tiles, const T *__restrict__ x, T *__restrict__ vout, long long *__restrict__ oidx) {
   typedef typename KeyOf<T>::K K;
+  constexpr int kWaves = kBlock / 64;
+  constexpr int kPerWave = kTile / kWaves;  // contiguous keys ranked by one wave
   __shared__ K sk[kTile];
   __shared__ unsigned si[IDX ? kTile : 1];
-  __shared__ unsigned short wc[2][kBlock / 64][kRadix];
-  __shared__ unsigned run[kRadix];
+  typedef unsigned WC;  // 32-bit: sub-dword LDS stores measured slower
+  __shared__ WC wc[kWaves][kRadix];  // per-wave digit counts, then offsets
   __shared__ unsigned dstart[kRadix];
   __shared__ unsigned long long goff[kRadix];
-  __shared__ unsigned lds4[kBlock / 64];
+  __shared__ unsigned lds4[kWaves];
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const unsigned b = blockIdx.x;
   const unsigned base = b * (unsigned)kTile;
   const unsigned ntile = n - base < (unsigned)kTile ? n - base : (unsigned)kTile;
 
-  K key[kIPT];
-  unsigned id[kIPT];
-  unsigned dg[kIPT];
-#pragma unroll
-  for (int r = 0; r < kIPT; ++r) {
-    const unsigned p = base + (unsigned)(r * kBlock + t);
-    const bool valid = p < n;
-    key[r] = valid ? kin[p] : (K)0;
-    id[r] = (IDX && valid) ? iin[p] : 0u;
-    dg[r] = valid ? digit_of<K, ROW>(key[r], id[r], shift, len) : 256u;
-  }
   {
     const unsigned c = counts[(size_t)t * tiles + b];
-    const unsigned ex = block_exclusive_scan(c, lds4);
-    dstart[t] = ex;
+    dstart[t] = block_exclusive_scan(c, lds4);
     goff[t] = incl[(size_t)t * tiles + b] - c;
-    run[t] = 0;
 #pragma unroll
-    for (int k = 0; k < kBlock / 64; ++k) {
-      wc[0][k][t] = 0;
-      wc[1][k][t] = 0;
-    }
+    for (int k = 0; k < kWaves; ++k) wc[k][t] = 0;
   }
   __syncthreads();
 
+  // Wave w ranks tile positions [w * kPerWave, (w + 1) * kPerWave) in rounds
+  // of 64 consecutive keys; its counters are private to it, so the rounds
+  // need no block barrier.  Within a round the lanes holding one digit find
+  // each other with eight ballots; all of them read the digit's running
+  // count, then the lowest of them adds the group's size.
+  K key[kIPT];
+  unsigned id[kIPT];
+  unsigned short rank[kIPT];
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
 #pragma unroll
+  for (int r = 0; r < kIPT; ++r) {  // all loads first, so that they overlap
+    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
+    const bool valid = p < n;
+    if constexpr (FIRST) {
+      key[r] = valid ? to_key<T, IDX>(x[p]) : (K)0;
+      id[r] = p;
+    } else {
+      key[r] = valid ? kin[p] : (K)0;
+      id[r] = (IDX && valid) ? iin[p] : 0u;
+    }
+  }
+#pragma unroll
   for (int r = 0; r < kIPT; ++r) {
-    const int S = r & 1;
-    const unsigned d = dg[r];
-    const bool valid = d < 256u;
+    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
+    const bool valid = p < n;
+    const unsigned d = valid ? digit_of<K, ROW>(key[r], id[r], shift, len) : 0u;
     unsigned long long m = __ballot(valid);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
@@ -206,25 +233,28 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
       m &= on ? bb : ~bb;
     }
     const unsigned long long lower = m & lt_mask;
-    const unsigned rank = (unsigned)__popcll(lower);
-    if (valid && lower == 0ull) wc[S][w][d] = (unsigned short)__popcll(m);
-    __syncthreads();
-    {
-      // one thread per digit: per-wave offsets of this round; clear the
-      // other set for the next round
-      unsigned acc = run[t];
+    const unsigned c = valid ? wc[w][d] : 0u;
+    rank[r] = (unsigned short)(c + (unsigned)__popcll(lower));
+    if (valid && lower == 0ull) wc[w][d] = (WC)(c + (unsigned)__popcll(m));
+  }
+  __syncthreads();
+  {
+    // wave offsets within each digit of the tile
+    unsigned acc = 0;
 #pragma unroll
-      for (int k = 0; k < kBlock / 64; ++k) {
-        const unsigned c = wc[S][k][t];
-        wc[S][k][t] = (unsigned short)acc;
-        acc += c;
-        wc[S ^ 1][k][t] = 0;
-      }
-      run[t] = acc;
+    for (int k = 0; k < kWaves; ++k) {
+      const unsigned c = wc[k][t];
+      wc[k][t] = (WC)acc;
+      acc += c;
     }
-    __syncthreads();
-    if (valid) {
-      const unsigned pos = dstart[d] + wc[S][w][d] + rank;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kIPT; ++r) {
+    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
+    if (p < n) {
+      const unsigned d = digit_of<K, ROW>(key[r], id[r], shift, len);
+      const unsigned pos = dstart[d] + wc[w][d] + rank[r];
       sk[pos] = key[r];
       if constexpr (IDX) si[pos] = id[r];
     }
@@ -248,12 +278,12 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   }
 }
 
-template <typename T, bool ROW, bool IDX, int FINAL>
+template <typename T, bool ROW, bool IDX, int FINAL, bool FIRST = false>
 int launch_scatter(unsigned tiles, const void *kin, const unsigned *iin, void *kout, unsigned *iout,
                    unsigned n, int shift, unsigned len, const unsigned *counts,
                    const unsigned long long *incl, const T *x, T *vout, long long *oidx) {
   typedef typename KeyOf<T>::K K;
-  hipLaunchKernelGGL((k_radix_scatter<T, ROW, IDX, FINAL>), dim3(tiles), dim3(kBlock), 0,
+  hipLaunchKernelGGL((k_radix_scatter<T, ROW, IDX, FINAL, FIRST>), dim3(tiles), dim3(kBlock), 0,
                      mmpi::stream(), (const K *)kin, iin, (K *)kout, iout, n, shift, len, counts,
                      incl, tiles, x, vout, oidx);
   return mmpi::check_launch("mmp_sort(scatter)");
@@ -287,32 +317,34 @@ int sort_impl(long long rows, long long len, const T *x, T *vout, long long *oid
   if (int st = cnt.get((size_t)tiles * kRadix * 4)) return st;
   if (int st = inc.get((size_t)tiles * kRadix * 8)) return st;
 
-  const unsigned pgrid = (unsigned)mmpi::ceil_div(n, kBlock);
-  if (idx)
-    hipLaunchKernelGGL((k_radix_prep<T, true>), dim3(pgrid), dim3(kBlock), 0, mmpi::stream(), x,
-                       (K *)ka.p, (unsigned *)ia.p, n);
-  else
-    hipLaunchKernelGGL((k_radix_prep<T, false>), dim3(pgrid), dim3(kBlock), 0, mmpi::stream(), x,
-                       (K *)ka.p, (unsigned *)nullptr, n);
-  if (int st = mmpi::check_launch("mmp_sort(prep)")) return st;
-
   // digit passes: key bytes, then row-number bytes
   int key_passes = (int)sizeof(K);
   int row_passes = 0;
   for (unsigned long long r = (unsigned long long)(rows - 1); r; r >>= 8) ++row_passes;
   const int passes = key_passes + row_passes;
-  void *kin = ka.p, *kout = kb.p;
-  unsigned *iin = (unsigned *)ia.p, *iout = (unsigned *)ib.p;
+  void *kin = kb.p, *kout = ka.p;  // the first pass reads x, writes ka
+  unsigned *iin = (unsigned *)ib.p, *iout = (unsigned *)ia.p;
   for (int ps = 0; ps < passes; ++ps) {
     const bool row = ps >= key_passes;
     const int shift = 8 * (row ? ps - key_passes : ps);
     const bool last = ps == passes - 1;
+    const bool first = ps == 0;
     if (row)
-      hipLaunchKernelGGL((k_radix_hist<K, true>), dim3(tiles), dim3(kBlock), 0, mmpi::stream(),
-                         (const K *)kin, iin, n, shift, ulen, (unsigned *)cnt.p, tiles);
+      hipLaunchKernelGGL((k_radix_hist<T, true, false, true>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)kin, iin, n, shift, ulen,
+                         (unsigned *)cnt.p, tiles);
+    else if (first && idx)
+      hipLaunchKernelGGL((k_radix_hist<T, false, true, true>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)x, iin, n, shift, ulen, (unsigned *)cnt.p,
+                         tiles);
+    else if (first)
+      hipLaunchKernelGGL((k_radix_hist<T, false, true, false>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)x, iin, n, shift, ulen, (unsigned *)cnt.p,
+                         tiles);
     else
-      hipLaunchKernelGGL((k_radix_hist<K, false>), dim3(tiles), dim3(kBlock), 0, mmpi::stream(),
-                         (const K *)kin, iin, n, shift, ulen, (unsigned *)cnt.p, tiles);
+      hipLaunchKernelGGL((k_radix_hist<T, false, false, false>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)kin, iin, n, shift, ulen,
+                         (unsigned *)cnt.p, tiles);
     if (int st = mmpi::check_launch("mmp_sort(hist)")) return st;
     if (int st = mmp_scan(MMP_S_CUMSUM, MMP_U32, MMP_U64, 1, (int64_t)tiles * kRadix, 1, cnt.p,
                           inc.p))
@@ -320,7 +352,13 @@ int sort_impl(long long rows, long long len, const T *x, T *vout, long long *oid
     const unsigned *c = (const unsigned *)cnt.p;
     const unsigned long long *ic = (const unsigned long long *)inc.p;
     int st;
-    if (!idx) {
+    if (first) {
+      // the first pass is never the last (keys have at least two bytes)
+      st = idx ? launch_scatter<T, false, true, 0, true>(tiles, kin, iin, kout, iout, n, shift,
+                                                         ulen, c, ic, x, vout, oidx)
+               : launch_scatter<T, false, false, 0, true>(tiles, kin, iin, kout, iout, n, shift,
+                                                          ulen, c, ic, x, vout, oidx);
+    } else if (!idx) {
       st = last ? launch_scatter<T, false, false, 1>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
                                                     ic, x, vout, oidx)
                 : launch_scatter<T, false, false, 0>(tiles, kin, iin, kout, iout, n, shift, ulen,

@@ -230,6 +230,54 @@ __global__ __launch_bounds__(kBlock) void k_copy(const Ti *__restrict__ x,
   }
 }
 
+// Permuted copies (a transpose on two axes p, q, batched over the others):
+// the destination is contiguous along q, the source along p.  A 64 x 64
+// tile goes through LDS (row pitch 65 words, no bank conflicts): read with
+// consecutive threads along p, written with consecutive threads along q, so
+// both sides are coalesced.  The generic kernel reads one of the two with
+// a 64-element stride.
+struct TransDesc {
+  long long np, nq;                // extents of p and q
+  long long sp, sq, dp, dq;        // source / destination strides of p and q
+  int nb;                          // batch dimensions
+  long long bshape[8], bs[8], bd[8];
+  long long tp, tq;                // tiles along p and q
+};
+
+template <typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_copy_transpose(const Ti *__restrict__ x,
+                                                           To *__restrict__ y, TransDesc t) {
+  __shared__ Ti tile[64][65];
+  long long b = blockIdx.x;
+  const long long jq = b % t.tq;
+  b /= t.tq;
+  const long long jp = b % t.tp;
+  b /= t.tp;
+  long long so = 0, dof = 0;
+  for (int k = t.nb - 1; k >= 0; --k) {
+    const long long q = b / t.bshape[k];
+    const long long i = b - q * t.bshape[k];
+    so += i * t.bs[k];
+    dof += i * t.bd[k];
+    b = q;
+  }
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const long long p0 = jp * 64, q0 = jq * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;  // q within the tile
+    const long long pp = p0 + tx, qq = q0 + r;
+    if (pp < t.np && qq < t.nq) tile[r][tx] = x[so + pp * t.sp + qq * t.sq];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;  // p within the tile
+    const long long pp = p0 + r, qq = q0 + tx;
+    if (pp < t.np && qq < t.nq) y[dof + pp * t.dp + qq * t.dq] = mmp_convert<To, Ti>(tile[tx][r]);
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_fill(T *__restrict__ y, long long n, T v) {
   const long long stride = (long long)gridDim.x * kBlock;
@@ -308,9 +356,52 @@ int binary_for_type(int op, long long n, const void *a, const void *b,
   }
 }
 
+// A transpose layout: the destination's innermost dimension q (stride 1)
+// is strided in the source and another dimension p is contiguous there;
+// both extents at least 16.
+bool transpose_desc(const StrideDesc &d, TransDesc *t) {
+  if (d.ndim < 2) return false;
+  const int q = d.ndim - 1;
+  if (d.dstride[q] != 1 || d.sstride[q] == 1 || d.shape[q] < 16) return false;
+  int p = -1;
+  for (int k = 0; k < q; ++k)
+    if (d.sstride[k] == 1) p = k;
+  if (p < 0 || d.shape[p] < 16) return false;
+  t->np = d.shape[p];
+  t->nq = d.shape[q];
+  t->sp = d.sstride[p];
+  t->sq = d.sstride[q];
+  t->dp = d.dstride[p];
+  t->dq = d.dstride[q];
+  t->nb = 0;
+  for (int k = 0; k < q; ++k) {
+    if (k == p) continue;
+    t->bshape[t->nb] = d.shape[k];
+    t->bs[t->nb] = d.sstride[k];
+    t->bd[t->nb] = d.dstride[k];
+    ++t->nb;
+  }
+  t->tp = mmpi::ceil_div(t->np, 64);
+  t->tq = mmpi::ceil_div(t->nq, 64);
+  return true;
+}
+
 template <typename Ti>
 int copy_from(int dst_dtype, long long n, const void *x, void *y,
               const StrideDesc &d, int mode) {
+  TransDesc t;
+  if (mode != 0 && transpose_desc(d, &t)) {
+    long long nbatch = 1;
+    for (int k = 0; k < t.nb; ++k) nbatch *= t.bshape[k];
+    const long long blocks = nbatch * t.tp * t.tq;
+    if (blocks <= 0x7fffffffLL) {
+      MMP_DISPATCH_ALL(dst_dtype, {
+        hipLaunchKernelGGL((k_copy_transpose<Ti, T>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (T *)y, t);
+        return mmpi::check_launch("mmp_copy(transpose)");
+      })
+    }
+  }
   const long long blocks = mmpi::ceil_div(n, kBlock * 4);
   const unsigned grid = (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
   MMP_DISPATCH_ALL(dst_dtype, {

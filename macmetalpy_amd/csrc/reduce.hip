@@ -42,6 +42,7 @@ constexpr long long kMinPerBlock = 16384;
 constexpr long long kTargetBlocks = MMP_REDUCE_TARGET_BLOCKS;
 constexpr long long kMaxSplits = 16384;
 constexpr int kUnroll = MMP_REDUCE_UNROLL;   // 16-byte loads in flight per thread
+constexpr int kColUnroll = 8;                // strided layouts: rows in flight per thread
 constexpr long long kSpinLimit = 1ll << 26;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -589,7 +590,15 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x,
   A v = R::ident();
   if (c < inner) {
     const T *p = x + o * len * inner + c;
-    for (long long l = b0; l < b1; ++l) v = R::comb(v, R::map(p[l * inner]));
+    long long l = b0;
+    for (; l + kColUnroll <= b1; l += kColUnroll) {  // loads first: kColUnroll in flight
+      T q[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) v = R::comb(v, R::map(q[u]));
+    }
+    for (; l < b1; ++l) v = R::comb(v, R::map(p[l * inner]));
   }
   if (S == 1) {
     if (c < inner) out[o * inner + c] = finalize<OP, T, To>(v, len);
@@ -617,23 +626,74 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x,
     __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Strided arg-reduction: grid (ceil(inner / 256), outer, S); thread =
+// column, the reduced axis split over S workgroups combined in index order
+// by the last to arrive (as k_reduce_cols).
 template <int OP, typename T>
 __global__ __launch_bounds__(kBlock) void k_argreduce_cols(const T *__restrict__ x,
                                                           long long *__restrict__ out,
-                                                          long long len, long long inner) {
+                                                          long long len, long long inner, int S,
+                                                          ReduceScratch sc) {
   typedef Arg<OP, T> R;
   typedef typename R::A A;
   typedef typename mmp_t<T>::C C;
+  constexpr int W = words_of<A>();
   const long long o = blockIdx.y;
+  const int s = blockIdx.z;
   const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= inner) return;
-  const T *p = x + o * len * inner + c;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
   A v = R::ident();
-  for (long long l = 0; l < len; ++l) v = R::comb(v, A{(C)p[l * inner], l});
-  out[o * inner + c] = v.i;
+  if (c < inner) {
+    const T *p = x + o * len * inner + c;
+    long long l = b0;
+    for (; l + kColUnroll <= b1; l += kColUnroll) {
+      T q[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) v = R::comb(v, A{(C)q[u], l + u});
+    }
+    for (; l < b1; ++l) v = R::comb(v, A{(C)p[l * inner], l});
+  }
+  if (S == 1) {
+    if (c < inner) out[o * inner + c] = v.i;
+    return;
+  }
+  const long long cb = blockIdx.x, ncb = gridDim.x;
+  unsigned long long *grp = sc.words + (o * ncb + cb) * (long long)S * kBlock * W;
+  put_tagged(grp + ((long long)s * kBlock + threadIdx.x) * W, v, sc.tag);
+  __shared__ int is_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(sc.tickets + o * ncb + cb, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == (unsigned)(S - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  A acc = R::ident();
+  for (int k = 0; k < S; ++k)
+    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.tag,
+                                     sc.timeout));
+  if (c < inner) out[o * inner + c] = acc.i;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------ launch
+// Strided layouts: split the reduced axis so that the launch has about
+// 2 x kTargetBlocks workgroups, each reading at least 64 rows.
+int col_splits(long long col_blocks, long long len) {
+  long long want = (2 * kTargetBlocks + col_blocks - 1) / col_blocks;
+  long long maxs = len / 64 > 0 ? len / 64 : 1;
+  long long s = want < maxs ? want : maxs;
+  if (s < 1) s = 1;
+  if (s > 1024) s = 1024;
+  return (int)s;
+}
+
 int choose_splits(long long rows, long long len) {
   long long want = (kTargetBlocks + rows - 1) / rows;
   long long maxs = (len + kMinPerBlock - 1) / kMinPerBlock;
@@ -675,11 +735,7 @@ int launch_reduce(long long outer, long long len, long long inner, const void *x
   }
   const long long ncb = mmpi::ceil_div(inner, kBlock);
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided reduction: outer extent %lld > 65535", outer);
-  long long want = (kTargetBlocks + outer * ncb - 1) / (outer * ncb);
-  long long maxs = len / 64 > 0 ? len / 64 : 1;
-  int S = (int)(want < maxs ? want : maxs);
-  if (S < 1) S = 1;
-  if (S > 1024) S = 1024;
+  const int S = col_splits(outer * ncb, len);
   if (S > 1) {
     if (int st = reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)) return st;
   }
@@ -704,9 +760,13 @@ int launch_argreduce(long long outer, long long len, long long inner, const void
     return mmpi::check_launch("mmp_argreduce(rows)");
   }
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided argreduce: outer extent %lld > 65535", outer);
-  hipLaunchKernelGGL((k_argreduce_cols<OP, T>),
-                     dim3((unsigned)mmpi::ceil_div(inner, kBlock), (unsigned)outer), dim3(kBlock), 0,
-                     mmpi::stream(), (const T *)x, out, len, inner);
+  const long long ncb = mmpi::ceil_div(inner, kBlock);
+  const int S = col_splits(outer * ncb, len);
+  if (S > 1) {
+    if (int st = reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)) return st;
+  }
+  hipLaunchKernelGGL((k_argreduce_cols<OP, T>), dim3((unsigned)ncb, (unsigned)outer, (unsigned)S),
+                     dim3(kBlock), 0, mmpi::stream(), (const T *)x, out, len, inner, S, sc);
   return mmpi::check_launch("mmp_argreduce(cols)");
 }
 

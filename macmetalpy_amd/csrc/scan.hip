@@ -28,7 +28,8 @@
 // float64 for floats (rounded once per output element).  HBM-bound:
 // sizeof(in) + sizeof(out) bytes per element.
 // Strided scans (inner > 1) run one thread per column, coalesced across
-// columns.
+// columns, with the axis cut into chunks (totals first, then a rescan from
+// each chunk's carry-in) so that narrow arrays still fill the device.
 #include "mmp_ops.h"
 #include "mmp_internal.h"
 
@@ -380,19 +381,68 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
     body(Bool<false>());
 }
 
-// Strided axis: one thread per column, serial along the axis.
-template <int OP, typename Ti, typename To>
-__global__ __launch_bounds__(kBlock) void k_scan_cols(const Ti *__restrict__ x, To *__restrict__ y,
-                                                     long long len, long long inner) {
-  typedef ScanOp<OP, Ti> S;
+// Strided axis: one thread per column; the axis is cut into S chunks so
+// that the launch fills the device.  Phase 1 writes each chunk's column
+// totals; phase 2 starts every chunk from the combined totals of the chunks
+// before it (in order) and scans it.  Traffic: input read twice, output
+// written once.
+constexpr int kColUnroll = 8;  // rows in flight per thread
+
+template <int OP, typename Ti>
+__global__ __launch_bounds__(kBlock) void k_scan_cols_part(const Ti *__restrict__ x,
+                                                          typename ScanOp<OP, Ti>::A *__restrict__ part,
+                                                          long long len, long long inner, int S) {
+  typedef ScanOp<OP, Ti> Sc;
   const long long o = blockIdx.y;
+  const int s = blockIdx.z;
   const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
   if (c >= inner) return;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  const Ti *p = x + o * len * inner + c;
+  typename Sc::A acc = Sc::ident();
+  long long l = b0;
+  for (; l + kColUnroll <= b1; l += kColUnroll) {
+    Ti q[kColUnroll];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) acc = Sc::comb(acc, Sc::map(q[u]));
+  }
+  for (; l < b1; ++l) acc = Sc::comb(acc, Sc::map(p[l * inner]));
+  part[((long long)o * S + s) * inner + c] = acc;
+}
+
+template <int OP, typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_scan_cols(const Ti *__restrict__ x, To *__restrict__ y,
+                                                     const typename ScanOp<OP, Ti>::A *__restrict__ part,
+                                                     long long len, long long inner, int S) {
+  typedef ScanOp<OP, Ti> Sc;
+  const long long o = blockIdx.y;
+  const int s = blockIdx.z;
+  const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= inner) return;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  typename Sc::A acc = Sc::ident();
+  for (int k = 0; k < s; ++k) acc = Sc::comb(acc, part[((long long)o * S + k) * inner + c]);
   const long long off = o * len * inner + c;
-  typename S::A acc = S::ident();
-  for (long long l = 0; l < len; ++l) {
-    acc = S::comb(acc, S::map(x[off + l * inner]));
-    y[off + l * inner] = mmp_convert<To, typename S::A>(acc);
+  long long l = b0;
+  for (; l + kColUnroll <= b1; l += kColUnroll) {
+    Ti q[kColUnroll];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) q[u] = x[off + (l + u) * inner];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      acc = Sc::comb(acc, Sc::map(q[u]));
+      y[off + (l + u) * inner] = mmp_convert<To, typename Sc::A>(acc);
+    }
+  }
+  for (; l < b1; ++l) {
+    acc = Sc::comb(acc, Sc::map(x[off + l * inner]));
+    y[off + l * inner] = mmp_convert<To, typename Sc::A>(acc);
   }
 }
 
@@ -445,10 +495,28 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
       return MMP_OK;
     }
     if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided scan: outer extent %lld > 65535", outer);
-    hipLaunchKernelGGL((k_scan_cols<OP, Ti, To>),
-                       dim3((unsigned)mmpi::ceil_div(inner, kBlock), (unsigned)outer), dim3(kBlock),
-                       0, mmpi::stream(), (const Ti *)x, (To *)y, len, inner);
-    return mmpi::check_launch("mmp_scan(cols)");
+    const long long ncb = mmpi::ceil_div(inner, kBlock);
+    long long want = (2048 + outer * ncb - 1) / (outer * ncb);
+    long long maxs = len / 64 > 0 ? len / 64 : 1;
+    int S = (int)(want < maxs ? want : maxs);
+    if (S < 1) S = 1;
+    if (S > 256) S = 256;
+    const dim3 grid((unsigned)ncb, (unsigned)outer, (unsigned)S);
+    void *part = nullptr;
+    if (S > 1) {
+      if (int st = mmp_alloc((size_t)outer * S * inner * sizeof(A), &part)) return st;
+      hipLaunchKernelGGL((k_scan_cols_part<OP, Ti>), grid, dim3(kBlock), 0, mmpi::stream(),
+                         (const Ti *)x, (A *)part, len, inner, S);
+      if (int st = mmpi::check_launch("mmp_scan(cols, totals)")) {
+        (void)mmp_free(part);
+        return st;
+      }
+    }
+    hipLaunchKernelGGL((k_scan_cols<OP, Ti, To>), grid, dim3(kBlock), 0, mmpi::stream(),
+                       (const Ti *)x, (To *)y, (const A *)part, len, inner, S);
+    const int st = mmpi::check_launch("mmp_scan(cols)");
+    if (part) (void)mmp_free(part);  // stream-ordered: reused only by later work
+    return st;
   }
 }
 

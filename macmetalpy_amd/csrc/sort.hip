@@ -21,12 +21,12 @@
 //    from there, so that consecutive threads write consecutive addresses
 //    of one digit's run (coalesced).  Waves, rounds and lanes follow input
 //    order, which makes every pass stable.
-// Rows (the leading axes of an N-D input) are sorted independently by
-// carrying each key's flat index and adding the row number (index / len)
-// as more significant digits after the key digits.  Keys: float bit
+// Rows (the leading axes of an N-D input) are sorted independently: tiles
+// never cross a row, and the tile counts are scanned in (row, digit, tile)
+// order, so every row's keys land in its own range.  Keys: float bit
 // patterns with the sign flipped (positive) or all bits inverted
 // (negative); NaN sorts last, as in NumPy.  When an index is carried
-// (argsort, N-D, stable) keys are canonical -- -0.0 equals +0.0 and all
+// (argsort, stable) keys are canonical -- -0.0 equals +0.0 and all
 // NaNs are equal -- and sorted values are gathered from the input by the
 // final index, which reproduces np.sort(kind='stable') bit for bit; a
 // keys-only 1-D sort keeps every value's bits except the sign of NaNs.
@@ -89,21 +89,42 @@ template <typename T> __device__ __forceinline__ T from_key(typename KeyOf<T>::K
   }
 }
 
-template <typename K, bool ROW>
-__device__ __forceinline__ unsigned digit_of(K key, unsigned id, int shift, unsigned len) {
-  if constexpr (ROW) return ((id / len) >> shift) & 255u;
-  else return (unsigned)(key >> shift) & 255u;
+template <typename K>
+__device__ __forceinline__ unsigned digit_of(K key, int shift) {
+  return (unsigned)(key >> shift) & 255u;
+}
+
+// Segmented tiling: row r (of `len` elements) owns tiles r * tpr ..
+// r * tpr + tpr - 1; tile j of a row covers row positions
+// [j * kTile, min((j + 1) * kTile, len)).  Tile counts are stored
+// (row, digit, tile)-major, so one inclusive scan over all of them gives
+// every (row, digit, tile) its global output offset: rows stay apart
+// without extra digit passes.
+struct SegTile {
+  unsigned start;  // global position of the tile's first element
+  unsigned count;  // elements in the tile
+  unsigned row, j;
+};
+__device__ __forceinline__ SegTile seg_tile(unsigned b, unsigned len, unsigned tpr) {
+  SegTile t;
+  t.row = b / tpr;
+  t.j = b - t.row * tpr;
+  const unsigned off = t.j * (unsigned)kTile;
+  t.start = t.row * len + off;
+  t.count = len - off < (unsigned)kTile ? len - off : (unsigned)kTile;
+  return t;
+}
+__device__ __forceinline__ size_t count_slot(const SegTile &t, unsigned d, unsigned tpr) {
+  return ((size_t)t.row * kRadix + d) * tpr + t.j;
 }
 
 // Tile histogram of one digit.  FIRST: the pass reads the input values and
 // converts them to keys on the fly (no separate conversion sweep).  Whole
-// tiles of 16-byte-aligned data are read with 16-byte loads.
-template <typename T, bool ROW, bool FIRST, bool CANON>
-__global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ src,
-                                                       const unsigned *__restrict__ idx,
-                                                       unsigned n, int shift, unsigned len,
-                                                       unsigned *__restrict__ counts,
-                                                       unsigned tiles) {
+// 16-byte-aligned tiles are read with 16-byte loads.
+template <typename T, bool FIRST, bool CANON>
+__global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ src, int shift,
+                                                       unsigned len, unsigned tpr,
+                                                       unsigned *__restrict__ counts) {
   typedef typename KeyOf<T>::K K;
   typedef typename std::conditional<FIRST, T, K>::type E;  // element type read
   __shared__ unsigned h[kBlock / 64][kRadix];
@@ -111,17 +132,16 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ 
 #pragma unroll
   for (int k = 0; k < kBlock / 64; ++k) h[k][t] = 0;
   __syncthreads();
-  const unsigned base = blockIdx.x * (unsigned)kTile;
-  const E *e = reinterpret_cast<const E *>(src);
+  const SegTile tl = seg_tile(blockIdx.x, len, tpr);
+  const E *e = reinterpret_cast<const E *>(src) + tl.start;
   auto key_at = [&](E v) -> K {
     if constexpr (FIRST) return to_key<T, CANON>(v);
     else return v;
   };
   constexpr int V = 16 / sizeof(E);
-  if (!ROW && sizeof(E) <= 8 && base + (unsigned)kTile <= n &&
-      ((uintptr_t)(e + base) & 15u) == 0) {
+  if (tl.count == (unsigned)kTile && ((uintptr_t)e & 15u) == 0) {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 *pv = reinterpret_cast<const u32x4 *>(e + base);
+    const u32x4 *pv = reinterpret_cast<const u32x4 *>(e);
 #pragma unroll 4
     for (int j = t; j < kTile / V; j += kBlock) {
       union {
@@ -130,22 +150,14 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ 
       } q;
       q.v = __builtin_nontemporal_load(pv + j);
 #pragma unroll
-      for (int i = 0; i < V; ++i) atomicAdd(&h[w][(unsigned)(key_at(q.x[i]) >> shift) & 255u], 1u);
+      for (int i = 0; i < V; ++i) atomicAdd(&h[w][digit_of<K>(key_at(q.x[i]), shift)], 1u);
     }
   } else {
-#pragma unroll 4
-    for (int r = 0; r < kIPT; ++r) {
-      const unsigned p = base + (unsigned)(r * kBlock + t);
-      if (p < n) {
-        unsigned d;
-        if constexpr (ROW) d = ((idx[p] / len) >> shift) & 255u;
-        else d = (unsigned)(key_at(e[p]) >> shift) & 255u;
-        atomicAdd(&h[w][d], 1u);
-      }
-    }
+    for (unsigned i = t; i < tl.count; i += kBlock)
+      atomicAdd(&h[w][digit_of<K>(key_at(e[i]), shift)], 1u);
   }
   __syncthreads();
-  counts[(size_t)t * tiles + blockIdx.x] = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+  counts[count_slot(tl, t, tpr)] = h[0][t] + h[1][t] + h[2][t] + h[3][t];
 }
 
 // exclusive prefix over the 256 threads of a block (value per thread)
@@ -168,32 +180,32 @@ __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned *l
 // 1 = last pass of a keys-only sort (values to vout);
 // 2 = last pass with indices (row-relative int64 indices to oidx and / or
 //     values gathered from x to vout).
-template <typename T, bool ROW, bool IDX, int FINAL, bool FIRST>
+// FIRST: keys are read from x and converted; indices are the positions.
+template <typename T, bool IDX, int FINAL, bool FIRST>
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(
     const typename KeyOf<T>::K *__restrict__ kin, const unsigned *__restrict__ iin,
-    typename KeyOf<T>::K *__restrict__ kout, unsigned *__restrict__ iout, unsigned n, int shift,
-    unsigned len, const unsigned *__restrict__ counts, const unsigned long long *__restrict__ incl,
-    unsigned tiles, const T *__restrict__ x, T *__restrict__ vout, long long *__restrict__ oidx) {
+    typename KeyOf<T>::K *__restrict__ kout, unsigned *__restrict__ iout, int shift,
+    unsigned len, unsigned tpr, const unsigned *__restrict__ counts,
+    const unsigned long long *__restrict__ incl, const T *__restrict__ x, T *__restrict__ vout,
+    long long *__restrict__ oidx) {
   typedef typename KeyOf<T>::K K;
   constexpr int kWaves = kBlock / 64;
   constexpr int kPerWave = kTile / kWaves;  // contiguous keys ranked by one wave
+  typedef unsigned WC;  // 32-bit: sub-dword LDS stores measured slower
   __shared__ K sk[kTile];
   __shared__ unsigned si[IDX ? kTile : 1];
-  typedef unsigned WC;  // 32-bit: sub-dword LDS stores measured slower
   __shared__ WC wc[kWaves][kRadix];  // per-wave digit counts, then offsets
   __shared__ unsigned dstart[kRadix];
   __shared__ unsigned long long goff[kRadix];
   __shared__ unsigned lds4[kWaves];
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const unsigned b = blockIdx.x;
-  const unsigned base = b * (unsigned)kTile;
-  const unsigned ntile = n - base < (unsigned)kTile ? n - base : (unsigned)kTile;
-
+  const SegTile tl = seg_tile(blockIdx.x, len, tpr);
   {
-    const unsigned c = counts[(size_t)t * tiles + b];
+    const size_t slot = count_slot(tl, t, tpr);
+    const unsigned c = counts[slot];
     dstart[t] = block_exclusive_scan(c, lds4);
-    goff[t] = incl[(size_t)t * tiles + b] - c;
+    goff[t] = incl[slot] - c;
 #pragma unroll
     for (int k = 0; k < kWaves; ++k) wc[k][t] = 0;
   }
@@ -210,8 +222,9 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
 #pragma unroll
   for (int r = 0; r < kIPT; ++r) {  // all loads first, so that they overlap
-    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
-    const bool valid = p < n;
+    const unsigned loc = (unsigned)(w * kPerWave + r * 64 + lane);
+    const bool valid = loc < tl.count;
+    const unsigned p = tl.start + loc;
     if constexpr (FIRST) {
       key[r] = valid ? to_key<T, IDX>(x[p]) : (K)0;
       id[r] = p;
@@ -222,9 +235,9 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   }
 #pragma unroll
   for (int r = 0; r < kIPT; ++r) {
-    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
-    const bool valid = p < n;
-    const unsigned d = valid ? digit_of<K, ROW>(key[r], id[r], shift, len) : 0u;
+    const unsigned loc = (unsigned)(w * kPerWave + r * 64 + lane);
+    const bool valid = loc < tl.count;
+    const unsigned d = valid ? digit_of<K>(key[r], shift) : 0u;
     unsigned long long m = __ballot(valid);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
@@ -251,9 +264,9 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kIPT; ++r) {
-    const unsigned p = base + (unsigned)(w * kPerWave + r * 64 + lane);
-    if (p < n) {
-      const unsigned d = digit_of<K, ROW>(key[r], id[r], shift, len);
+    const unsigned loc = (unsigned)(w * kPerWave + r * 64 + lane);
+    if (loc < tl.count) {
+      const unsigned d = digit_of<K>(key[r], shift);
       const unsigned pos = dstart[d] + wc[w][d] + rank[r];
       sk[pos] = key[r];
       if constexpr (IDX) si[pos] = id[r];
@@ -261,11 +274,11 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   }
   __syncthreads();
 
-  for (unsigned p = t; p < ntile; p += kBlock) {
-    const K k = sk[p];
-    const unsigned i = IDX ? si[p] : 0u;
-    const unsigned d = digit_of<K, ROW>(k, i, shift, len);
-    const unsigned long long g = goff[d] + (p - dstart[d]);
+  for (unsigned q = t; q < tl.count; q += kBlock) {
+    const K k = sk[q];
+    const unsigned i = IDX ? si[q] : 0u;
+    const unsigned d = digit_of<K>(k, shift);
+    const unsigned long long g = goff[d] + (q - dstart[d]);
     if constexpr (FINAL == 0) {
       kout[g] = k;
       if constexpr (IDX) iout[g] = i;
@@ -278,14 +291,14 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   }
 }
 
-template <typename T, bool ROW, bool IDX, int FINAL, bool FIRST = false>
+template <typename T, bool IDX, int FINAL, bool FIRST = false>
 int launch_scatter(unsigned tiles, const void *kin, const unsigned *iin, void *kout, unsigned *iout,
-                   unsigned n, int shift, unsigned len, const unsigned *counts,
+                   int shift, unsigned len, unsigned tpr, const unsigned *counts,
                    const unsigned long long *incl, const T *x, T *vout, long long *oidx) {
   typedef typename KeyOf<T>::K K;
-  hipLaunchKernelGGL((k_radix_scatter<T, ROW, IDX, FINAL, FIRST>), dim3(tiles), dim3(kBlock), 0,
-                     mmpi::stream(), (const K *)kin, iin, (K *)kout, iout, n, shift, len, counts,
-                     incl, tiles, x, vout, oidx);
+  hipLaunchKernelGGL((k_radix_scatter<T, IDX, FINAL, FIRST>), dim3(tiles), dim3(kBlock), 0,
+                     mmpi::stream(), (const K *)kin, iin, (K *)kout, iout, shift, len, tpr,
+                     counts, incl, x, vout, oidx);
   return mmpi::check_launch("mmp_sort(scatter)");
 }
 
@@ -302,11 +315,14 @@ template <typename T>
 int sort_impl(long long rows, long long len, const T *x, T *vout, long long *oidx, bool stable) {
   typedef typename KeyOf<T>::K K;
   const long long n64 = rows * len;
-  // 32-bit positions: a tile's last position must not wrap
+  // 32-bit positions; tile counts addressed with 32-bit tile numbers
   if (n64 > 0xffffe000LL) return mmpi::fail(MMP_E_UNSUPPORTED, "mmp_sort: more than 2^32 - 8192 elements");
-  const unsigned n = (unsigned)n64, ulen = (unsigned)len;
-  const bool idx = oidx != nullptr || rows > 1 || stable;
-  const unsigned tiles = (unsigned)mmpi::ceil_div(n, kTile);
+  const long long tpr64 = mmpi::ceil_div(len, kTile);
+  const long long tiles64 = rows * tpr64;
+  if (tiles64 > 0x7fffffffLL) return mmpi::fail(MMP_E_UNSUPPORTED, "mmp_sort: too many rows");
+  const unsigned n = (unsigned)n64, ulen = (unsigned)len, tpr = (unsigned)tpr64;
+  const unsigned tiles = (unsigned)tiles64;
+  const bool idx = oidx != nullptr || stable;
   Temp ka, kb, ia, ib, cnt, inc;
   if (int st = ka.get((size_t)n * sizeof(K))) return st;
   if (int st = kb.get((size_t)n * sizeof(K))) return st;
@@ -314,65 +330,47 @@ int sort_impl(long long rows, long long len, const T *x, T *vout, long long *oid
     if (int st = ia.get((size_t)n * 4)) return st;
     if (int st = ib.get((size_t)n * 4)) return st;
   }
-  if (int st = cnt.get((size_t)tiles * kRadix * 4)) return st;
-  if (int st = inc.get((size_t)tiles * kRadix * 8)) return st;
+  const size_t nslots = (size_t)tiles * kRadix;
+  if (int st = cnt.get(nslots * 4)) return st;
+  if (int st = inc.get(nslots * 8)) return st;
 
-  // digit passes: key bytes, then row-number bytes
-  int key_passes = (int)sizeof(K);
-  int row_passes = 0;
-  for (unsigned long long r = (unsigned long long)(rows - 1); r; r >>= 8) ++row_passes;
-  const int passes = key_passes + row_passes;
+  const int passes = (int)sizeof(K);
   void *kin = kb.p, *kout = ka.p;  // the first pass reads x, writes ka
   unsigned *iin = (unsigned *)ib.p, *iout = (unsigned *)ia.p;
   for (int ps = 0; ps < passes; ++ps) {
-    const bool row = ps >= key_passes;
-    const int shift = 8 * (row ? ps - key_passes : ps);
-    const bool last = ps == passes - 1;
-    const bool first = ps == 0;
-    if (row)
-      hipLaunchKernelGGL((k_radix_hist<T, true, false, true>), dim3(tiles), dim3(kBlock), 0,
-                         mmpi::stream(), (const void *)kin, iin, n, shift, ulen,
-                         (unsigned *)cnt.p, tiles);
-    else if (first && idx)
-      hipLaunchKernelGGL((k_radix_hist<T, false, true, true>), dim3(tiles), dim3(kBlock), 0,
-                         mmpi::stream(), (const void *)x, iin, n, shift, ulen, (unsigned *)cnt.p,
-                         tiles);
+    const int shift = 8 * ps;
+    const bool first = ps == 0, last = ps == passes - 1;
+    if (first && idx)
+      hipLaunchKernelGGL((k_radix_hist<T, true, true>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)x, shift, ulen, tpr, (unsigned *)cnt.p);
     else if (first)
-      hipLaunchKernelGGL((k_radix_hist<T, false, true, false>), dim3(tiles), dim3(kBlock), 0,
-                         mmpi::stream(), (const void *)x, iin, n, shift, ulen, (unsigned *)cnt.p,
-                         tiles);
+      hipLaunchKernelGGL((k_radix_hist<T, true, false>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)x, shift, ulen, tpr, (unsigned *)cnt.p);
     else
-      hipLaunchKernelGGL((k_radix_hist<T, false, false, false>), dim3(tiles), dim3(kBlock), 0,
-                         mmpi::stream(), (const void *)kin, iin, n, shift, ulen,
-                         (unsigned *)cnt.p, tiles);
+      hipLaunchKernelGGL((k_radix_hist<T, false, false>), dim3(tiles), dim3(kBlock), 0,
+                         mmpi::stream(), (const void *)kin, shift, ulen, tpr, (unsigned *)cnt.p);
     if (int st = mmpi::check_launch("mmp_sort(hist)")) return st;
-    if (int st = mmp_scan(MMP_S_CUMSUM, MMP_U32, MMP_U64, 1, (int64_t)tiles * kRadix, 1, cnt.p,
-                          inc.p))
+    if (int st = mmp_scan(MMP_S_CUMSUM, MMP_U32, MMP_U64, 1, (int64_t)nslots, 1, cnt.p, inc.p))
       return st;
     const unsigned *c = (const unsigned *)cnt.p;
     const unsigned long long *ic = (const unsigned long long *)inc.p;
     int st;
     if (first) {
       // the first pass is never the last (keys have at least two bytes)
-      st = idx ? launch_scatter<T, false, true, 0, true>(tiles, kin, iin, kout, iout, n, shift,
-                                                         ulen, c, ic, x, vout, oidx)
-               : launch_scatter<T, false, false, 0, true>(tiles, kin, iin, kout, iout, n, shift,
-                                                          ulen, c, ic, x, vout, oidx);
-    } else if (!idx) {
-      st = last ? launch_scatter<T, false, false, 1>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
-                                                    ic, x, vout, oidx)
-                : launch_scatter<T, false, false, 0>(tiles, kin, iin, kout, iout, n, shift, ulen,
-                                                    c, ic, x, vout, oidx);
-    } else if (row) {
-      st = last ? launch_scatter<T, true, true, 2>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
-                                                  ic, x, vout, oidx)
-                : launch_scatter<T, true, true, 0>(tiles, kin, iin, kout, iout, n, shift, ulen, c,
-                                                  ic, x, vout, oidx);
-    } else {
-      st = last ? launch_scatter<T, false, true, 2>(tiles, kin, iin, kout, iout, n, shift, ulen,
+      st = idx ? launch_scatter<T, true, 0, true>(tiles, kin, iin, kout, iout, shift, ulen, tpr,
                                                    c, ic, x, vout, oidx)
-                : launch_scatter<T, false, true, 0>(tiles, kin, iin, kout, iout, n, shift, ulen,
-                                                   c, ic, x, vout, oidx);
+               : launch_scatter<T, false, 0, true>(tiles, kin, iin, kout, iout, shift, ulen, tpr,
+                                                    c, ic, x, vout, oidx);
+    } else if (!idx) {
+      st = last ? launch_scatter<T, false, 1>(tiles, kin, iin, kout, iout, shift, ulen, tpr, c, ic,
+                                              x, vout, oidx)
+                : launch_scatter<T, false, 0>(tiles, kin, iin, kout, iout, shift, ulen, tpr, c, ic,
+                                              x, vout, oidx);
+    } else {
+      st = last ? launch_scatter<T, true, 2>(tiles, kin, iin, kout, iout, shift, ulen, tpr, c, ic,
+                                             x, vout, oidx)
+                : launch_scatter<T, true, 0>(tiles, kin, iin, kout, iout, shift, ulen, tpr, c, ic,
+                                             x, vout, oidx);
     }
     if (st) return st;
     void *tk = kin;

@@ -1,0 +1,148 @@
+"""Host-side logic on the CPU (no device): dtype resolution against NumPy
+for every op and dtype pair, weak-scalar rules, broadcasting, reduction
+layouts and result dtypes, op-table consistency.  These are the decisions
+the Python layer makes before any kernel runs (reference:
+ndarray._binary_op / _unary_op, ndarray.py:960-1243; _dtypes.py:77-146;
+_broadcasting.py:8-76; reductions.py:74-163)."""
+import itertools
+import warnings
+
+import numpy as np
+import pytest
+
+from macmetalpy_amd import _abi, _dtypes, reductions
+from macmetalpy_amd._broadcasting import broadcast_shapes, broadcast_strides
+from macmetalpy_amd._config import set_config
+
+DTYPES = [np.dtype(d) for d in (np.bool_, np.int16, np.uint16, np.int32, np.uint32, np.int64,
+                                np.uint64, np.float16, np.float32, np.float64)]
+
+
+_NARROW = {np.dtype(np.int8): np.dtype(np.int16), np.dtype(np.uint8): np.dtype(np.uint16)}
+
+
+def _numpy_dtype(ufunc, *ops):
+    """NumPy's result dtype, with int8 / uint8 mapped as the device maps them."""
+    d = _raw_numpy_dtype(ufunc, *ops)
+    return _NARROW.get(d, d)
+
+
+def _raw_numpy_dtype(ufunc, *ops):
+    args = [np.empty(0, dtype=o) if isinstance(o, np.dtype) else o for o in ops]
+    with np.errstate(all="ignore"), warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        return ufunc(*args).dtype
+
+
+@pytest.mark.parametrize("name", sorted(set(_abi.UNARY_OPS) | set(_abi.EXPR_UNARY_OPS)))
+def test_unary_result_dtypes_match_numpy(name):
+    ufunc = (_abi.UNARY_OPS.get(name) or (None, None))[1] or _abi.EXPR_UNARY_OPS[name][0]
+    for dt in DTYPES:
+        try:
+            want = _numpy_dtype(ufunc, dt)
+        except TypeError:
+            with pytest.raises(TypeError):
+                _dtypes.ufunc_result_dtype(ufunc, dt)
+            continue
+        assert _dtypes.ufunc_result_dtype(ufunc, dt) == want, (name, dt)
+
+
+@pytest.mark.parametrize("name", sorted(set(_abi.BINARY_OPS) | set(_abi.EXPR_BINARY_OPS)))
+def test_binary_result_dtypes_match_numpy(name):
+    ufunc = (_abi.BINARY_OPS.get(name) or (None, None))[1] or _abi.EXPR_BINARY_OPS[name][0]
+    for a, b in itertools.product(DTYPES, DTYPES):
+        try:
+            want = _numpy_dtype(ufunc, a, b)
+        except TypeError:
+            with pytest.raises(TypeError):
+                _dtypes.ufunc_result_dtype(ufunc, a, b)
+            continue
+        assert _dtypes.ufunc_result_dtype(ufunc, a, b) == want, (name, a, b)
+
+
+@pytest.mark.parametrize("scalar", [2, -3, 2.5, True])
+def test_weak_python_scalars(scalar):
+    """NEP 50: a Python scalar takes the array's dtype where it fits."""
+    for dt in DTYPES:
+        for ufunc in (np.add, np.multiply, np.maximum, np.less):
+            try:
+                want = _numpy_dtype(ufunc, dt, scalar)
+            except (TypeError, OverflowError):
+                continue
+            assert _dtypes.ufunc_result_dtype(ufunc, dt, scalar) == want, (ufunc, dt, scalar)
+            # cached second lookup agrees
+            assert _dtypes.ufunc_result_dtype(ufunc, dt, scalar) == want
+
+
+def test_integer_scalar_out_of_range_raises():
+    with pytest.raises(OverflowError):
+        _dtypes.ufunc_result_dtype(np.add, np.dtype(np.int16), 1 << 40)
+
+
+def test_float64_policy_and_narrow_ints():
+    assert _dtypes.resolve_dtype(np.int8) == np.int16
+    assert _dtypes.resolve_dtype(np.uint8) == np.uint16
+    assert _dtypes.resolve_dtype(None) == np.float32
+    assert _dtypes.resolve_dtype(np.float64) == np.float64
+    with pytest.raises(TypeError):
+        _dtypes.resolve_dtype(np.complex128)
+    set_config(float64_behavior="downcast", warn_on_downcast=True)
+    with pytest.warns(UserWarning):
+        assert _dtypes.resolve_dtype(np.float64) == np.float32
+    set_config(warn_on_downcast=False)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert _dtypes.resolve_dtype(np.float64) == np.float32
+
+
+@pytest.mark.parametrize("shapes", [((3, 1, 5), (4, 1)), ((), (7,)), ((2, 3), (1, 3), (2, 1)),
+                                    ((0, 3), (1, 3)), ((1,), (5, 0))])
+def test_broadcast_shapes_match_numpy(shapes):
+    assert broadcast_shapes(*shapes) == np.broadcast_shapes(*shapes)
+
+
+def test_broadcast_shapes_mismatch_and_strides():
+    with pytest.raises(ValueError):
+        broadcast_shapes((3,), (4,))
+    # a (1, 5) row viewed as (4, 5): rows have stride 0
+    assert tuple(broadcast_strides((1, 5), (4, 5), (5, 1))) == (0, 1)
+    assert tuple(broadcast_strides((5,), (2, 3, 5), (1,))) == (0, 0, 1)
+
+
+@pytest.mark.parametrize("kind", ["sum", "prod", "mean", "cumsum", "cumprod", "var"])
+def test_reduction_result_dtypes_match_numpy(kind):
+    fn = {"sum": np.sum, "prod": np.prod, "mean": np.mean, "cumsum": np.cumsum,
+          "cumprod": np.cumprod, "var": np.var}[kind]
+    for dt in DTYPES:
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            want = fn(np.zeros(1, dtype=dt)).dtype
+        assert reductions._np_out_dtype(kind, dt) == want, (kind, dt)
+
+
+def test_reduction_layouts_and_shapes():
+    assert reductions._axes(None, 3) is None
+    assert reductions._axes(-1, 3) == (2,)
+    assert reductions._axes((2, 0), 3) == (0, 2)
+    assert reductions._out_shape((4, 5, 6), (1,), False) == (4, 6)
+    assert reductions._out_shape((4, 5, 6), (1,), True) == (4, 1, 6)
+    assert reductions._out_shape((4, 5, 6), None, True) == (1, 1, 1)
+    # (outer, len, inner) views of a contiguous array; None = not one run
+    assert reductions._layout((4, 5, 6), None) == (1, 120, 1)
+    assert reductions._layout((4, 5, 6), (1,)) == (4, 5, 6)
+    assert reductions._layout((4, 5, 6), (1, 2)) == (4, 30, 1)
+    assert reductions._layout((4, 5, 6), (0, 2)) is None
+
+
+def test_op_tables_are_consistent():
+    """Every op the dispatcher may emit has a device function, and codes of
+    precompiled ops are unique."""
+    for name, (code, ufunc, fn) in _abi.UNARY_OPS.items():
+        assert _abi.UNARY_FN[name] == fn and isinstance(ufunc, np.ufunc)
+    for name, (code, ufunc, fn) in _abi.BINARY_OPS.items():
+        assert _abi.BINARY_FN[name] == fn and isinstance(ufunc, np.ufunc)
+    codes = [c for n, (c, _, _) in _abi.BINARY_OPS.items()]
+    assert len(set(codes)) == len(codes)
+    assert set(_abi.EXPR_UNARY_OPS).isdisjoint(_abi.UNARY_OPS)
+    assert set(_abi.EXPR_BINARY_OPS).isdisjoint(_abi.BINARY_OPS)
+    assert _abi.BOOL_RESULT_OPS <= set(_abi.EXPR_UNARY_OPS) | set(_abi.EXPR_BINARY_OPS)

@@ -230,6 +230,57 @@ __global__ __launch_bounds__(kBlock) void k_copy(const Ti *__restrict__ x,
   }
 }
 
+// Contiguous cast / copy with vector accesses: per step a thread converts
+// E = 16 / sizeof(To) consecutive elements and writes them with one 16-byte
+// store, so the lanes of a store instruction cover one contiguous span;
+// the matching input (E * sizeof(Ti) bytes: 2 .. 64) is read with the
+// widest loads that fit.  4 steps per thread per tile; the last partial
+// tile element by element.
+template <int B> struct VecBytes;
+template <> struct VecBytes<2> { typedef unsigned short type; };
+template <> struct VecBytes<4> { typedef unsigned int type; };
+template <> struct VecBytes<8> { typedef unsigned int type __attribute__((ext_vector_type(2))); };
+template <> struct VecBytes<16> { typedef unsigned int type __attribute__((ext_vector_type(4))); };
+
+template <typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_copy_vec(const Ti *__restrict__ x, To *__restrict__ y,
+                                                     long long n) {
+  constexpr int E = 16 / (int)sizeof(To);        // elements per thread per step
+  constexpr int IB = E * (int)sizeof(Ti);        // input bytes per thread per step
+  constexpr int LB = IB < 16 ? IB : 16;          // bytes per load
+  constexpr int NL = IB / LB;                    // loads per step
+  typedef typename VecBytes<LB>::type LV;
+  typedef typename VecBytes<16>::type SV;
+  constexpr int U = 4;
+  constexpr long long TILE = (long long)kBlock * E * U;
+  const long long t0 = (long long)blockIdx.x * TILE;
+  if (t0 + TILE <= n) {
+    union In {
+      LV v[NL];
+      Ti e[E];
+    } in[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const LV *src = reinterpret_cast<const LV *>(x + t0 + ((long long)u * kBlock + threadIdx.x) * E);
+#pragma unroll
+      for (int c = 0; c < NL; ++c) in[u].v[c] = __builtin_nontemporal_load(src + c);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      union Out {
+        SV v;
+        To e[E];
+      } o;
+#pragma unroll
+      for (int k = 0; k < E; ++k) o.e[k] = mmp_convert<To, Ti>(in[u].e[k]);
+      __builtin_nontemporal_store(o.v, reinterpret_cast<SV *>(y + t0 + ((long long)u * kBlock + threadIdx.x) * E));
+    }
+    return;
+  }
+  for (long long i = t0 + threadIdx.x; i < n && i < t0 + TILE; i += kBlock)
+    y[i] = mmp_convert<To, Ti>(x[i]);
+}
+
 // Permuted copies (a transpose on two axes p, q, batched over the others):
 // the destination is contiguous along q, the source along p.  A 64 x 64
 // tile goes through LDS (row pitch 65 words, no bank conflicts): read with
@@ -389,6 +440,18 @@ bool transpose_desc(const StrideDesc &d, TransDesc *t) {
 template <typename Ti>
 int copy_from(int dst_dtype, long long n, const void *x, void *y,
               const StrideDesc &d, int mode) {
+  if (mode == 0 && aligned16(x) && aligned16(y)) {
+    MMP_DISPATCH_ALL(dst_dtype, {
+      constexpr long long tile = (long long)kBlock * (16 / (long long)sizeof(T)) * 4;
+      const long long blocks = mmpi::ceil_div(n, tile);
+      if (blocks <= 0x7fffffffLL) {
+        hipLaunchKernelGGL((k_copy_vec<Ti, T>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (T *)y, n);
+        return mmpi::check_launch("mmp_copy(contiguous)");
+      }
+      break;  // leave the dtype switch: generic path below
+    })
+  }
   TransDesc t;
   if (mode != 0 && transpose_desc(d, &t)) {
     long long nbatch = 1;

@@ -110,3 +110,24 @@ def test_device_creation_large():
     assert small._np_data is not None  # small arrays stay on the host until used
     r = cp.zeros((1 << 17,)) + cp.arange(1 << 17, dtype=np.float32)
     assert np.array_equal(r.get(), np.arange(1 << 17, dtype=np.float32))
+
+
+@pytest.mark.parametrize("src,dst", [(np.float32, np.float16), (np.float16, np.float32),
+                                     (np.float32, np.float64), (np.int32, np.int64),
+                                     (np.float64, np.int32), (np.bool_, np.float32),
+                                     (np.int16, np.uint16), (np.float32, np.float32)])
+@pytest.mark.parametrize("n", [1, 1000, 65536 + 7, (1 << 20) + 3])
+def test_contiguous_casts(src, dst, n):
+    """Vector (16-byte) contiguous cast path and its element-wise tail; an
+    offset view takes the unaligned path."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 50).astype(src)
+    cx = cp.array(x)
+    cx._ensure_gpu()  # device-resident: the cast runs on the device
+    with np.errstate(all="ignore"):
+        want = x.astype(dst)
+    got = cx.astype(dst).get()
+    assert got.dtype == want.dtype and np.array_equal(got, want, equal_nan=True)
+    if n > 3:
+        got2 = cx[3:].astype(dst).get()
+        assert np.array_equal(got2, want[3:], equal_nan=True)

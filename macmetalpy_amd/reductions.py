@@ -164,11 +164,27 @@ def _empty_reduction(kind, oshape, odt, red_len):
     return creation.empty(oshape, dtype=odt)
 
 
+def _masked(a, where, fill):
+    """``a`` with the elements outside the ``where`` mask replaced by
+    ``fill`` (lazy: fuses into the reduction that consumes it).  NumPy's
+    reductions with ``where=`` skip those elements; for sum / prod / max /
+    min that equals reducing the masked array (the reference's CPU branches
+    hand ``where`` to NumPy, e.g. reductions.py:89-103)."""
+    from ._broadcasting import broadcast_shapes
+    from ._elementwise import where as _where
+    a = _asarray(a)
+    m = where if isinstance(where, ndarray) else _asarray(np.asarray(where, dtype=bool))
+    if broadcast_shapes(m._shape, a._shape) != a._shape:
+        raise ValueError(f"where mask of shape {m._shape} does not broadcast to {a._shape}")
+    return _where(m, a, fill)
+
+
 def sum(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
         where=np._NoValue):
-    """Sum of elements (reference reductions.py:74-113)."""
+    """Sum of elements (reference reductions.py:74-113); ``where`` masks
+    elements out (they count as 0)."""
     if where is not np._NoValue:
-        raise NotImplementedError("sum(where=...) is not supported on the device")
+        a = _masked(a, where, 0)
     r = _reduce(a, "sum", axis, dtype, None, keepdims)
     if initial is not np._NoValue:
         r = r + initial
@@ -177,36 +193,51 @@ def sum(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
 
 def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
     """Arithmetic mean (reference reductions.py:116-163): the float64 sum
-    divided by the count in float64, rounded once to the result dtype."""
-    if where is not np._NoValue:
-        raise NotImplementedError("mean(where=...) is not supported on the device")
-    return _reduce(a, "mean", axis, dtype, out, keepdims)
+    divided by the count in float64, rounded once to the result dtype.  With
+    ``where``: the masked sum over the number of selected elements (NaN
+    where none is selected, as NumPy)."""
+    if where is None or where is np._NoValue:
+        return _reduce(a, "mean", axis, dtype, out, keepdims)
+    a = _asarray(a)
+    odt = _np_out_dtype("mean", a._dtype if dtype is None else resolve_dtype(dtype))
+    tot = _reduce(_masked(a, where, 0).astype(np.float64), "sum", axis, None, None, keepdims)
+    everywhere = (a == a) | (a != a)          # True with a's shape (NaN included)
+    cnt = _reduce(_masked(everywhere, where, False), "sum", axis, None, None, keepdims)
+    return _finish((tot / cnt).astype(odt), out)
 
 
 def prod(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
          where=np._NoValue):
+    if where is not np._NoValue:
+        a = _masked(a, where, 1)
     r = _reduce(a, "prod", axis, dtype, None, keepdims)
     if initial is not np._NoValue:
         r = r * initial
     return _finish(r, out)
 
 
-def max(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._NoValue):
-    """Maximum; NaN propagates (NumPy)."""
-    r = _reduce(a, "max", axis, None, None, keepdims)
+def _extreme(a, kind, axis, out, keepdims, initial, where):
+    from .ufunc_ops import maximum, minimum
+    if where is not np._NoValue:
+        if initial is np._NoValue:
+            raise ValueError(f"reduction operation '{'maximum' if kind == 'max' else 'minimum'}'"
+                             " does not have an identity, so to use a where mask one has to "
+                             "specify 'initial'")
+        a = _masked(a, where, initial)
+    r = _reduce(a, kind, axis, None, None, keepdims)
     if initial is not np._NoValue:
-        from .ufunc_ops import maximum
-        r = maximum(r, initial)
+        r = (maximum if kind == "max" else minimum)(r, initial)
     return _finish(r, out)
+
+
+def max(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._NoValue):
+    """Maximum; NaN propagates (NumPy).  ``where`` needs ``initial``."""
+    return _extreme(a, "max", axis, out, keepdims, initial, where)
 
 
 def min(a, axis=None, out=None, keepdims=False, initial=np._NoValue, where=np._NoValue):
-    """Minimum; NaN propagates (NumPy)."""
-    r = _reduce(a, "min", axis, None, None, keepdims)
-    if initial is not np._NoValue:
-        from .ufunc_ops import minimum
-        r = minimum(r, initial)
-    return _finish(r, out)
+    """Minimum; NaN propagates (NumPy).  ``where`` needs ``initial``."""
+    return _extreme(a, "min", axis, out, keepdims, initial, where)
 
 
 amax = max
@@ -216,23 +247,25 @@ amin = min
 def any(a, axis=None, out=None, keepdims=False, where=np._NoValue):
     """True where any element along ``axis`` is nonzero (reference
     reductions.py:248-278).  One fused pass counts ``a != 0`` (NaN counts as
-    true); an empty reduction is False.  Returns a bool ndarray (0-d for
-    axis=None), as the reference does."""
-    if where is not np._NoValue:
-        raise NotImplementedError("any(where=...) is not supported on the device")
+    true; masked-out elements count as false); an empty reduction is False.
+    Returns a bool ndarray (0-d for axis=None), as the reference does."""
     a = _asarray(a)
-    r = _reduce(a != 0, "sum", axis, None, None, keepdims) > 0
+    t = a != 0
+    if where is not np._NoValue:
+        t = _masked(t, where, False)
+    r = _reduce(t, "sum", axis, None, None, keepdims) > 0
     return _finish(r, out)
 
 
 def all(a, axis=None, out=None, keepdims=False, where=np._NoValue):
     """True where every element along ``axis`` is nonzero (reference
-    reductions.py:281-311); counts ``a == 0`` in one fused pass; an empty
-    reduction is True."""
-    if where is not np._NoValue:
-        raise NotImplementedError("all(where=...) is not supported on the device")
+    reductions.py:281-311); counts ``a == 0`` (masked-out elements do not
+    count) in one fused pass; an empty reduction is True."""
     a = _asarray(a)
-    r = _reduce(a == 0, "sum", axis, None, None, keepdims) == 0
+    t = a == 0
+    if where is not np._NoValue:
+        t = _masked(t, where, False)
+    r = _reduce(t, "sum", axis, None, None, keepdims) == 0
     return _finish(r, out)
 
 

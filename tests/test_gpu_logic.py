@@ -257,3 +257,40 @@ def test_any_all_empty_and_lazy():
         _same(cp.any(cp.sqrt(cx) > 1.5).get(), np.asarray(np.any(np.sqrt(x) > 1.5)))
         _same(cp.all(cp.isfinite(cx * 0.0)).get(), np.asarray(np.all(np.isfinite(x * 0.0))))
     assert cp.count_nonzero(cp.isnan(cx)) == int(np.count_nonzero(np.isnan(x)))
+
+
+# ------------------------------------------------------- where= masks
+def test_reductions_with_where_masks():
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((37, 515)).astype(np.float32)
+    x[3, 7] = np.nan
+    m_row = rng.random(515) < 0.6               # broadcast along rows
+    m_full = rng.random((37, 515)) < 0.5
+    m_full[3, 7] = False                        # the NaN is masked out
+    cx = cp.array(x)
+    x64 = x.astype(np.float64)
+    for m in (m_row, m_full, cp.array(m_full)):
+        mn = m.get() if hasattr(m, "get") else m
+        for axis in (None, 1, 0):
+            got = cp.sum(cx, axis=axis, where=m).get()
+            want = np.sum(x64, axis=axis, where=mn)
+            assert np.allclose(got, want, rtol=1e-5, atol=1e-5, equal_nan=True)
+            with np.errstate(all="ignore"):
+                gm = cp.mean(cx, axis=axis, where=m).get()
+                wm = np.mean(x64, axis=axis, where=mn)
+            assert gm.dtype == np.float32
+            assert np.allclose(gm, wm, rtol=1e-5, atol=1e-6, equal_nan=True)
+            _same(cp.max(cx, axis=axis, where=m, initial=-5.0).get(),
+                  np.max(x, axis=axis, where=mn, initial=-5.0))
+            _same(cp.min(cx, axis=axis, where=m, initial=5.0).get(),
+                  np.min(x, axis=axis, where=mn, initial=5.0))
+            _same(cp.any(cx > 1, axis=axis, where=m).get(), np.asarray(np.any(x > 1, axis=axis, where=mn)))
+            _same(cp.all(cx > -3, axis=axis, where=m).get(), np.asarray(np.all(x > -3, axis=axis, where=mn)))
+    p = (1 + 0.01 * rng.standard_normal((8, 100))).astype(np.float32)
+    mp = rng.random((8, 100)) < 0.5
+    assert np.allclose(cp.prod(cp.array(p), axis=1, where=mp).get(),
+                       np.prod(p.astype(np.float64), axis=1, where=mp), rtol=1e-5)
+    with pytest.raises(ValueError):
+        cp.max(cx, where=m_row)                 # needs initial, as NumPy
+    with pytest.raises(ValueError):
+        cp.sum(cx, where=np.ones((2, 2), bool))

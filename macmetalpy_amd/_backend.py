@@ -169,6 +169,9 @@ class DeviceBuffer:
         return f"DeviceBuffer(0x{self.ptr:x}, {self.nbytes} bytes)"
 
 
+_U32x3 = ctypes.c_uint32 * 3
+
+
 class HipBackend:
     """Process-wide device context (one GPU, one stream)."""
 
@@ -349,11 +352,12 @@ class HipBackend:
         """Launch a compiled kernel on the library stream; ``grid`` counts
         workgroups, ``args`` are ctypes scalars/structs in kernel-parameter
         order."""
-        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
-        b = (ctypes.c_uint32 * 3)(*(list(block) + [1] * (3 - len(block))))
-        ptrs = (_c_vp * max(1, len(args)))(
-            *[ctypes.cast(ctypes.byref(a), _c_vp) for a in args])
-        _check(self._lib.mmp_rtc_launch(kernel, g, b, shared, ptrs), "mmp_rtc_launch")
+        g = _U32x3(*grid) if len(grid) == 3 else _U32x3(*(tuple(grid) + (1, 1, 1))[:3])
+        b = _U32x3(*block) if len(block) == 3 else _U32x3(*(tuple(block) + (1, 1, 1))[:3])
+        ptrs = (_c_vp * max(1, len(args)))(*[ctypes.addressof(a) for a in args])
+        st = self._lib.mmp_rtc_launch(kernel, g, b, shared, ptrs)
+        if st:
+            _check(st, "mmp_rtc_launch")
 
 
 def rtc_build(source: str, options: str = "", arch: str = "gfx950") -> bytes:

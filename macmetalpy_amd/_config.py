@@ -37,7 +37,8 @@ class MacMetalConfig:
 
 
 def get_config() -> MacMetalConfig:
-    return MacMetalConfig()
+    inst = MacMetalConfig._instance
+    return inst if inst is not None else MacMetalConfig()
 
 
 def set_config(

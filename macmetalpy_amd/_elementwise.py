@@ -62,24 +62,29 @@ def _asarray(x):
 
 
 # ----------------------------------------------------- lazy dependents
+_PRUNE_AT = 64
+
+
 def track_lazy(arr) -> None:
     """Register lazy ``arr`` with every device buffer its DAG reads, so an
-    in-place write to one of those buffers first evaluates ``arr``.  Entries
-    are weak and removed when ``arr`` dies or is evaluated (``untrack``)."""
-    key = id(arr)
+    in-place write to one of those buffers first evaluates ``arr``.  The
+    entries are plain weak references: ``flush_lazy`` skips dead and
+    already evaluated arrays, and a buffer's list is pruned of them when it
+    grows past ``_PRUNE_AT`` entries."""
+    ref = weakref.ref(arr)
     for buf in arr._fusion_node._buffers:
         deps = buf.lazy_dependents
         if deps is None:
-            deps = buf.lazy_dependents = {}
-        deps[key] = weakref.ref(arr, lambda _r, d=deps, k=key: d.pop(k, None))
+            buf.lazy_dependents = [ref]
+            continue
+        deps.append(ref)
+        if len(deps) > _PRUNE_AT:
+            deps[:] = [r for r in deps if _pending(r) is not None]
 
 
-def untrack_lazy(arr, node) -> None:
-    key = id(arr)
-    for buf in node._buffers:
-        deps = buf.lazy_dependents
-        if deps:
-            deps.pop(key, None)
+def _pending(ref):
+    arr = ref()
+    return arr if arr is not None and arr._fusion_node is not None else None
 
 
 def flush_lazy(buffer) -> None:
@@ -90,11 +95,11 @@ def flush_lazy(buffer) -> None:
     deps = buffer.lazy_dependents
     if not deps:
         return
-    for ref in list(deps.values()):
-        arr = ref()
-        if arr is not None and arr._fusion_node is not None:
+    buffer.lazy_dependents = None
+    for ref in deps:
+        arr = _pending(ref)
+        if arr is not None:
             materialize(arr)
-    deps.clear()
 
 
 # ----------------------------------------------------------- node helpers
@@ -139,13 +144,26 @@ def _materialise_operand(x, shape, dtype):
 
 
 # ------------------------------------------------------------------ ops
+_UNARY_DTYPES: dict = {}
+
+
+def _unary_dtypes(op_name, dt):
+    """(result dtype, dtype the operand is read as) of a unary op."""
+    key = (op_name, dt)
+    hit = _UNARY_DTYPES.get(key)
+    if hit is None:
+        ent = _abi.UNARY_OPS.get(op_name)
+        ufunc = ent[1] if ent is not None else _abi.EXPR_UNARY_OPS[op_name][0]
+        rdt = ufunc_result_dtype(ufunc, dt)
+        # predicates read the operand as it is; other ops compute in the result dtype
+        hit = _UNARY_DTYPES[key] = (rdt, dt if op_name in _abi.BOOL_RESULT_OPS else rdt)
+    return hit
+
+
 def unary(op_name: str, x):
-    x = _asarray(x)
-    ent = _abi.UNARY_OPS.get(op_name)
-    ufunc = ent[1] if ent is not None else _abi.EXPR_UNARY_OPS[op_name][0]
-    rdt = ufunc_result_dtype(ufunc, x._dtype)
-    # predicates read the operand as it is; other ops compute in the result dtype
-    idt = x._dtype if op_name in _abi.BOOL_RESULT_OPS else rdt
+    if type(x) is not _ndarray():
+        x = _asarray(x)
+    rdt, idt = _unary_dtypes(op_name, x._dtype)
     if x.size == 0:
         return _empty(x._shape, rdt)
     if not get_config().fusion:
@@ -168,6 +186,24 @@ def _scalar_operand(v):
     return v
 
 
+_BINARY_DTYPES: dict = {}
+
+
+def _binary_dtypes(op_name, ka, kb):
+    """(result dtype, dtype both operands are read as) of a binary op on
+    operand dtypes / Python scalars ``ka``, ``kb``."""
+    if op_name in _abi.COMPARE_OPS or op_name in _abi.BOOL_RESULT_OPS:
+        # NumPy compares (and tests truth) in the operands' common dtype and
+        # returns bool
+        ufunc = (_abi.COMPARE_OPS.get(op_name) or _abi.EXPR_BINARY_OPS[op_name])[0]
+        ufunc_result_dtype(ufunc, ka, kb)  # raises for invalid operands
+        return np.dtype(np.bool_), resolve_dtype(np.result_type(ka, kb))
+    ent = _abi.BINARY_OPS.get(op_name)
+    ufunc = ent[1] if ent is not None else _abi.EXPR_BINARY_OPS[op_name][0]
+    rdt = ufunc_result_dtype(ufunc, ka, kb)
+    return rdt, rdt
+
+
 def binary(op_name: str, a, b):
     nd = _ndarray()
     a_arr = isinstance(a, nd)
@@ -183,18 +219,14 @@ def binary(op_name: str, a, b):
         a_arr = True
     ka = a._dtype if a_arr else _scalar_operand(a)
     kb = b._dtype if b_arr else _scalar_operand(b)
-    if op_name in _abi.COMPARE_OPS or op_name in _abi.BOOL_RESULT_OPS:
-        # NumPy compares (and tests truth) in the operands' common dtype and
-        # returns bool
-        ufunc = (_abi.COMPARE_OPS.get(op_name) or _abi.EXPR_BINARY_OPS[op_name])[0]
-        ufunc_result_dtype(ufunc, ka, kb)  # raises for invalid operands
-        odt = resolve_dtype(np.result_type(ka, kb))
-        rdt = np.dtype(np.bool_)
+    if a_arr and b_arr:
+        key = (op_name, ka, kb)
+        hit = _BINARY_DTYPES.get(key)
+        if hit is None:
+            hit = _BINARY_DTYPES[key] = _binary_dtypes(op_name, ka, kb)
+        rdt, odt = hit
     else:
-        ent = _abi.BINARY_OPS.get(op_name)
-        ufunc = ent[1] if ent is not None else _abi.EXPR_BINARY_OPS[op_name][0]
-        rdt = ufunc_result_dtype(ufunc, ka, kb)
-        odt = rdt
+        rdt, odt = _binary_dtypes(op_name, ka, kb)
     sa = a._shape if a_arr else ()
     sb = b._shape if b_arr else ()
     shape = broadcast_shapes(sa, sb)

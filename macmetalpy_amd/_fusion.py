@@ -195,9 +195,11 @@ class _Program:
 
     def _visit(self, node):
         nid = id(node)
-        if nid in self._memo:
-            return self._memo[nid]
-        if isinstance(node, InputNode):
+        idx = self._memo.get(nid)
+        if idx is not None:
+            return idx
+        cls = type(node)
+        if cls is InputNode:
             key = (id(node._buffer), node._offset, node._strides, node._shape, node._dtype)
             k = self._leaf_index.get(key)
             if k is None:
@@ -205,20 +207,20 @@ class _Program:
                 self._leaf_index[key] = k
                 self.arrays.append(node)
             step = ("load", k)
-        elif isinstance(node, ScalarNode):
+        elif cls is UnaryOpNode:
+            step = ("unary", node._op_name, self._visit(node._input))
+        elif cls is BinaryOpNode:
+            step = ("binary", node._op_name, self._visit(node._lhs), self._visit(node._rhs))
+        elif cls is ScalarNode:
             step = ("scalar", len(self.scalars))
             self.scalars.append(node)
-        elif isinstance(node, CastNode):
+        elif cls is CastNode:
             step = ("cast", self._visit(node._input))
-        elif isinstance(node, UnaryOpNode):
-            step = ("unary", node._op_name, self._visit(node._input))
-        elif isinstance(node, BinaryOpNode):
-            step = ("binary", node._op_name, self._visit(node._lhs), self._visit(node._rhs))
-        elif isinstance(node, WhereNode):
+        elif cls is WhereNode:
             step = ("where", self._visit(node._cond), self._visit(node._x),
                     self._visit(node._y))
         else:
-            raise TypeError(f"unknown fusion node {type(node).__name__}")
+            raise TypeError(f"unknown fusion node {cls.__name__}")
         self.steps.append(step)
         self.dtypes.append(node._dtype)
         idx = len(self.steps) - 1
@@ -705,8 +707,6 @@ def materialize(arr) -> None:
     be = HipBackend()
     buf = be.create_buffer(arr.size, arr._dtype)
     materialize_node(node, buf.ptr)
-    from ._elementwise import untrack_lazy
-    untrack_lazy(arr, node)
     arr._buffer = buf
     arr._fusion_node = None
     arr._np_data = None

@@ -210,15 +210,16 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm16(const T *__restrict__ A,
 //  * Two stages as separate LDS arrays, k loop unrolled by two, so the
 //    compiler can tell that the MFMA reads of one stage never alias the
 //    loads in flight into the other; slab kt + 1 is loaded while slab kt
-//    runs, and the barrier at the end of each slab waits for this wave's
-//    loads (vmcnt) before publishing the stage.
+//    runs, and the barrier in the middle of each slab waits for this
+//    wave's loads (vmcnt) before publishing the stage.  LDS reads run one
+//    half-slab ahead of the MFMAs, across the barrier.
 //  * The MFMA is issued as C^T = B^T A^T (operands swapped), so a lane's
 //    four accumulators are four consecutive columns of one C row: the
 //    epilogue writes 8 B per lane per 16 x 16 tile.
 //  * Workgroup ids are remapped so that the tiles one XCD runs together
 //    (ids are dealt round-robin over the eight XCDs) form 4-row groups:
 //    concurrent workgroups on an XCD share A and B panels in its L2.
-// Measured at 8192^3 float16 on MI355X: 1.17-1.18 PF/s (0.93-0.94 ms);
+// Measured at 8192^3 float16 on MI355X: 1.21-1.24 PF/s (0.89-0.91 ms);
 // torch.matmul (hipBLASLt) on the same device 1.22 PF/s.  Register-staged loading
 // (global -> VGPR -> ds_write, B transposed with v_perm) reached 0.88 PF/s;
 // a four-stage 32-deep variant of this kernel 1.10 PF/s (twice the
@@ -258,28 +259,39 @@ __global__ __launch_bounds__(512, 1) void k_gemm16_dma(
   auto fb = [](int k) { return 2 * ((k & 3) | (((k >> 3) & 3) << 2)); };
 
   // Loads: waves 0-3 fill B (each wave 8 instructions x 2 rows of 512 B),
-  // waves 4-7 fill A (each wave 8 instructions x 8 rows of 128 B).  Per
-  // lane, the global offset (halves) of instruction p for slab k0 = 0.
-  const bool b_role = wave < 4;
-  const int w4 = wave & 3;
-  long long goff[8];
+  // waves 4-7 fill A (each wave 8 instructions x 8 rows of 128 B).  The
+  // XOR swizzle of instruction p depends on p only through (p & 1) for A
+  // and (p & 1, p >> 2) for B, so a lane keeps 4 per-lane offsets (32-bit:
+  // the host keeps lda and ldb below 2^28) and the rest is wave-uniform.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int w4 = wv & 3;
+  const bool b_role = wv < 4;
+  unsigned loff[4];
+  if (b_role) {
+    const int h = lane >> 5, slot = lane & 31;  // row 16 w4 + 2p + h
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int inst = w4 * 8 + p;              // 0..31 within the stage
-    if (b_role) {
-      const int row = inst * 2 + (lane >> 5), slot = lane & 31;
-      goff[p] = (long long)row * ldb + (slot ^ fb(row)) * 8;
-    } else {
-      const int row = inst * 8 + (lane >> 3), slot = lane & 7;
-      goff[p] = (long long)row * lda + (slot ^ swz(row)) * 8;
+    for (int v = 0; v < 4; ++v) {
+      const int f = 2 * ((2 * (v & 1) + h) | (((2 * w4 + (v >> 1)) & 3) << 2));  // fb(row)
+      loff[v] = (unsigned)h * (unsigned)ldb + (unsigned)((slot ^ f) * 8);
+    }
+  } else {
+    const int l3 = lane >> 3, slot = lane & 7;  // row 64 w4 + 8p + l3
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int sw = (4 * (v & 1) + (lane >> 4)) & 7;  // swz(row); entries 2, 3 repeat 0, 1
+      loff[v] = (unsigned)l3 * (unsigned)lda + (unsigned)((slot ^ sw) * 8);
     }
   }
   auto issue = [&](unsigned short *As_, unsigned short *Bs_, int k0) {
     const unsigned short *g = b_role ? Bg + (long long)k0 * ldb : Ag + k0;
     unsigned short *dst = b_role ? Bs_ : As_;
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
-      __builtin_amdgcn_global_load_lds(g + goff[p], dst + (w4 * 8 + p) * 512, 16, 0, 0);
+    for (int p = 0; p < 8; ++p) {
+      const long long sp = b_role ? (long long)(16 * w4 + 2 * p) * ldb
+                                  : (long long)(64 * w4 + 8 * p) * lda;
+      const unsigned lo = loff[(p & 1) | ((p >> 2) << 1)];
+      __builtin_amdgcn_global_load_lds(g + sp + lo, dst + (w4 * 8 + p) * 512, 16, 0, 0);
+    }
   };
 
   f4 acc[I][J];
@@ -290,65 +302,90 @@ __global__ __launch_bounds__(512, 1) void k_gemm16_dma(
 
   const int fr = lane & 15, grp = lane >> 4;
   const int fch[2] = {((grp + 0) ^ swz(fr)) * 8, ((grp + 4) ^ swz(fr)) * 8};
-  auto mfmas = [&](const unsigned short *As_, const unsigned short *Bs_) {
+  // The fragments of one 32-deep half-slab: I A and J B fragments.
+  auto read_half = [&](const unsigned short *As_, const unsigned short *Bs_, int s, V (&af)[I],
+                       V (&bf)[J]) {
 #pragma unroll
-    for (int s = 0; s < BK / 32; ++s) {
-      V af[I], bf[J];
+    for (int j = 0; j < J; ++j) {
+      // lane (group grp, index q) addresses k row 32s + 8grp + q/4 (+4),
+      // columns 4 (q % 4) .. +3 of the 16-column tile
+      const int q = fr;
+      const int col = wn * TN + j * 16 + 4 * (q & 3);
+      const int k1 = s * 32 + grp * 8 + (q >> 2), k2 = k1 + 4;
+      const int c8 = col >> 3, w = col & 7;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4 *)(Bs_ + k1 * TB + ((c8 ^ fb(k1)) << 3) + w));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4 *)(Bs_ + k2 * TB + ((c8 ^ fb(k2)) << 3) + w));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      bf[j] = __builtin_bit_cast(V, v8);
+    }
 #pragma unroll
-      for (int i = 0; i < I; ++i)
-        af[i] = *reinterpret_cast<const V *>(&As_[(wm * TM + i * 16 + fr) * BK + fch[s]]);
+    for (int i = 0; i < I; ++i)
+      af[i] = *reinterpret_cast<const V *>(&As_[(wm * TM + i * 16 + fr) * BK + fch[s]]);
+  };
+  auto mfma_half = [&](const V (&af)[I], const V (&bf)[J]) {
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        // lane (group grp, index q) addresses k row 32s + 8grp + q/4 (+4),
-        // columns 4 (q % 4) .. +3 of the 16-column tile
-        const int q = fr;
-        const int col = wn * TN + j * 16 + 4 * (q & 3);
-        const int k1 = s * 32 + grp * 8 + (q >> 2), k2 = k1 + 4;
-        const int c8 = col >> 3, w = col & 7;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4 *)(Bs_ + k1 * TB + ((c8 ^ fb(k1)) << 3) + w));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4 *)(Bs_ + k2 * TB + ((c8 ^ fb(k2)) << 3) + w));
-        typedef short s16x8 __attribute__((ext_vector_type(8)));
-        const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        bf[j] = __builtin_bit_cast(V, v8);
-      }
+    for (int i = 0; i < I; ++i)
 #pragma unroll
-      for (int i = 0; i < I; ++i)
+      for (int j = 0; j < J; ++j) acc[i][j] = Half16<T>::mfma(bf[j], af[i], acc[i][j]);
+  };
+  // A half-slab's 32 MFMAs with the 16 LDS reads of the next half-slab
+  // placed one after each of the first 16 (the reads are done well before
+  // the barrier or the MFMAs that need them).  The empty asm after each
+  // half keeps those reads in the half (the compiler would otherwise sink
+  // the reads of the next slab below the loop test, into a burst).
+  auto sched_half = [&]() {
 #pragma unroll
-        for (int j = 0; j < J; ++j) acc[i][j] = Half16<T>::mfma(bf[j], af[i], acc[i][j]);
+    for (int m = 0; m < 32; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (m < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
   };
 
+  // Pipeline: each 64-deep slab is two halves with one barrier between
+  // them.  Before the barrier: MFMAs of the first half, reads of the second
+  // half.  The barrier (which waits for this wave's copies) publishes the
+  // other stage, so after it: the copy of the slab two ahead into the stage
+  // just consumed, then MFMAs of the second half with the reads of the next
+  // slab's first half.  Copies past the last slab reload the last slab into
+  // a stage that is no longer read; reads past it read a stale stage and
+  // are never used.  (1.17-1.18 -> 1.21-1.24 PF/s at 8192^3 over a single
+  // read burst after each barrier.)
   const int nk = K / BK;
-  // Instruction order within a slab: the 16 LDS reads of the first 32-deep
-  // half, then its MFMAs with the second half's 16 reads placed one after
-  // every other MFMA, then the second half's MFMAs.  Left to itself the
-  // compiler reads two A fragments at a time and waits for them right
-  // before their MFMAs; this order keeps a half-slab of reads in flight
-  // (1.07 -> 1.17 PF/s at 8192^3).
-  auto sched = [&]() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
-#pragma unroll
-    for (int m = 0; m < 64; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if (m < 32 && (m & 1)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  };
+  V f0a[I], f0b[J], f1a[I], f1b[J];
   issue(As0, Bs0, 0);
   __syncthreads();
+  issue(As1, Bs1, min(1, nk - 1) * BK);
+  read_half(As0, Bs0, 0, f0a, f0b);
   for (int kt = 0; kt < nk; kt += 2) {
-    if (kt + 1 < nk) issue(As1, Bs1, (kt + 1) * BK);
-    mfmas(As0, Bs0);
-    sched();
+    // slab kt in stage 0
+    mfma_half(f0a, f0b);
+    read_half(As0, Bs0, 1, f1a, f1b);
+    sched_half();
+    asm volatile("" ::: "memory");
     __syncthreads();
+    issue(As0, Bs0, min(kt + 2, nk - 1) * BK);
+    mfma_half(f1a, f1b);
+    read_half(As1, Bs1, 0, f0a, f0b);
+    sched_half();
+    asm volatile("" ::: "memory");
     if (kt + 1 < nk) {
-      if (kt + 2 < nk) issue(As0, Bs0, (kt + 2) * BK);
-      mfmas(As1, Bs1);
-      sched();
+      // slab kt + 1 in stage 1
+      mfma_half(f0a, f0b);
+      read_half(As1, Bs1, 1, f1a, f1b);
+      sched_half();
+      asm volatile("" ::: "memory");
       __syncthreads();
+      issue(As1, Bs1, min(kt + 3, nk - 1) * BK);
+      mfma_half(f1a, f1b);
+      read_half(As0, Bs0, 0, f0a, f0b);
+      sched_half();
+      asm volatile("" ::: "memory");
     }
   }
+  __syncthreads();  // no copy into LDS may be in flight when the workgroup ends
 
   T *Cb = C + bz * sC;
   const int cr = lane & 15, cc = (lane >> 4) * 4;
@@ -545,6 +582,7 @@ template <typename T>
 int launch16(long long batch, int M, int N, int K, const void *A, long long lda, long long sA,
              const void *B, long long ldb, long long sB, void *C, long long ldc, long long sC) {
   if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+      lda < (1ll << 28) && ldb < (1ll << 28) &&
       ldc % 4 == 0 && sA % 8 == 0 && sB % 8 == 0 && sC % 4 == 0 && al(A, 16) && al(B, 16) &&
       al(C, 8) && (long long)(M / 256) * (N / 256) * batch >= MMP_GEMM16_BIG_MIN_TILES) {
     const int tm = M / 256, tn = N / 256;

@@ -52,11 +52,13 @@ def test_matmul_mfma_layout_known_answer():
     assert np.array_equal((cp.array(e) @ cp.array(m)).get(), m)
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(1, 2048, 4096, 320), (2, 2048, 2048, 192)])
+@pytest.mark.parametrize("batch,m,n,k", [(1, 2048, 4096, 320), (2, 2048, 2048, 192),
+                                         (1, 4096, 2048, 256), (1, 4096, 2048, 64)])
 def test_matmul_f16_large_tile_exact(batch, m, n, k):
     """Products with at least 128 tiles of 256 x 256 take the large-tile
     float16 kernel (split A/B loading, swizzled LDS, swapped-operand
-    epilogue, XCD tile remap; an odd number of 64-deep slabs for k = 320).
+    epilogue, XCD tile remap; odd and even numbers of 64-deep slabs, and a
+    single slab, through the two-stage pipeline).
     Operands in {-1, 0, 1} make every sum an integer of magnitude <= k, exact
     in fp32 and in the float16 output, so the whole result must equal
     NumPy's."""

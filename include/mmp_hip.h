@@ -291,6 +291,32 @@ int mmp_searchsorted(int dtype, int64_t n, const void *sorted, int64_t m,
 int mmp_take(int itemsize, int64_t nsrc, const void *src, int64_t n,
              const int64_t *indices, void *out);
 
+/* ---------------------------------------------------------- indexing
+ * Advanced indexing and the indexing routines on the device.  Replace the
+ * reference's host paths: ndarray.__getitem__ / __setitem__ with integer
+ * or boolean arrays (ndarray.py:874-891, 943-957, NumPy on the host) and
+ * indexing.py (take, put, putmask, place, compress, extract, nonzero,
+ * flatnonzero, argwhere: NumPy on the host, indexing.py:24-391). */
+
+/* Gather rows: out row i (row_words words of `word` = 1, 2, 4, 8 or 16
+ * bytes) = the row_words words starting at word offsets[i] * unit of src.
+ * Words outside [0, src_bytes / word) read as 0 (callers check indices).
+ * src and out must be aligned to `word`. */
+int mmp_gather(int word, const void *src, int64_t src_bytes, const int64_t *offsets,
+               int64_t unit, int64_t n, int64_t row_words, void *out);
+
+/* Scatter rows: the row_words words at word offsets[i] * unit of dst =
+ * row i of src (src_rows = n), or its only row (src_rows = 1).  Targets
+ * outside dst are skipped; when two offsets are equal, which row lands is
+ * unspecified (as for NumPy's advanced assignment). */
+int mmp_scatter(int word, void *dst, int64_t dst_bytes, const int64_t *offsets, int64_t unit,
+                int64_t n, int64_t row_words, const void *src, int64_t src_rows);
+
+/* Positions of the selected elements: incl is the inclusive int64 count
+ * (cumsum) of a mask of n elements, count = incl[n - 1]; out[k] = the
+ * position of the k-th selected element, k < count. */
+int mmp_nonzero(int64_t n, const int64_t *incl, int64_t count, int64_t *out);
+
 /* ======================================================================== */
 /* Matmul: replaces ndarray.__matmul__ + matmul_shader (ndarray.py:1398-1450,*/
 /* _kernels.py:740-759); batched form replaces linalg_top.matmul's CPU path */

@@ -37,6 +37,8 @@ from .ufunc_ops import (
     logical_xor, logical_not, isnan, isinf, isfinite, signbit,
 )
 from .math_ops import where, clip, count_nonzero
+from .indexing import (take, put, take_along_axis, put_along_axis, putmask, place, compress,
+                       extract, nonzero, flatnonzero, argwhere)
 from .reductions import (
     sum, mean, prod, max, min, amax, amin, argmax, argmin, any, all, cumsum, cumprod, var,
     std, cumulative_sum, cumulative_prod,

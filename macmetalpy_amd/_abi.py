@@ -172,7 +172,7 @@ EXPORTS = (
     "mmp_unary", "mmp_binary", "mmp_binary_scalar", "mmp_copy",
     "mmp_copy_strided", "mmp_fill",
     "mmp_reduce", "mmp_argreduce", "mmp_scan", "mmp_matmul",
-    "mmp_sort", "mmp_searchsorted", "mmp_take",
+    "mmp_sort", "mmp_searchsorted", "mmp_take", "mmp_gather", "mmp_scatter", "mmp_nonzero",
     "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch",
     "mmp_wait_status",
     "mmp_debug_fail_next",

@@ -94,6 +94,9 @@ _SIGNATURES = {
     "mmp_sort": [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int],
     "mmp_searchsorted": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp],
     "mmp_take": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp],
+    "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp],
+    "mmp_scatter": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64],
+    "mmp_nonzero": [_c_i64, _c_vp, _c_i64, _c_vp],
     "mmp_matmul": [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
                    _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64],
     "mmp_rtc_compile": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_c_vp)],
@@ -332,6 +335,19 @@ class HipBackend:
 
     def take(self, itemsize: int, nsrc: int, src: int, n: int, indices: int, out: int) -> None:
         _check(self._lib.mmp_take(itemsize, nsrc, src, n, indices, out), "mmp_take")
+
+    def gather(self, word: int, src: int, src_bytes: int, offsets: int, unit: int, n: int,
+               row_words: int, out: int) -> None:
+        _check(self._lib.mmp_gather(word, src, src_bytes, offsets, unit, n, row_words, out),
+               "mmp_gather")
+
+    def scatter(self, word: int, dst: int, dst_bytes: int, offsets: int, unit: int, n: int,
+                row_words: int, src: int, src_rows: int) -> None:
+        _check(self._lib.mmp_scatter(word, dst, dst_bytes, offsets, unit, n, row_words, src,
+                                     src_rows), "mmp_scatter")
+
+    def nonzero(self, n: int, incl: int, count: int, out: int) -> None:
+        _check(self._lib.mmp_nonzero(n, incl, count, out), "mmp_nonzero")
 
     def matmul(self, dcode: int, batch: int, M: int, N: int, K: int,
                A: int, lda: int, sA: int, B: int, ldb: int, sB: int,

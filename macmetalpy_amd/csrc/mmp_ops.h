@@ -659,6 +659,16 @@ template <typename To, typename From> MMP_DI To mmp_convert(From v) {
     }
   } else if constexpr (mmp_t<From>::is_bool) {
     return (To)(v ? 1 : 0);
+  } else if constexpr (mmp_t<From>::is_float && !mmp_t<To>::is_float && !mmp_t<To>::is_signed) {
+    // float -> unsigned: truncate to int64 first, then wrap, as NumPy's C
+    // cast does on x86-64 (-1.0 -> 0xffff for uint16); values of 2^63 and
+    // more only fit uint64 directly
+    typedef typename mmp_t<From>::C F;
+    const F f = (F)v;
+    if constexpr (sizeof(To) == 8) {
+      if (f >= (F)9223372036854775808.0) return (To)f;
+    }
+    return (To)(long long)f;
   } else if constexpr (sizeof(From) == 2 && mmp_t<From>::is_float) {
     return (To)(float)v;  // half -> widen first
   } else {

@@ -21,10 +21,10 @@ __all__ = ["where", "clip", "count_nonzero"]
 def where(condition, x=None, y=None):
     """Elements of ``x`` where ``condition`` is true, else of ``y``
     (reference math_ops.py:106-155; NumPy's result dtype and broadcasting).
-    The one-argument form (``nonzero``) is not provided."""
+    The one-argument form is ``nonzero(condition)``."""
     if x is None and y is None:
-        raise NotImplementedError("where(condition) (nonzero) is not supported; "
-                                  "pass x and y")
+        from .indexing import nonzero
+        return nonzero(condition)
     if x is None or y is None:
         raise ValueError("either both or neither of x and y should be given")
     return _ew.where(condition, x, y)

@@ -296,8 +296,8 @@ class ndarray:
             raise ValueError(f"cannot reshape array of size {self.size} into shape {new_shape}")
         if self._fusion_node is not None and self._shape == new_shape:
             return self
-        if self._np_data is not None:
-            return ndarray._from_np_direct(self._np_data.reshape(new_shape))
+        # views of host-resident data live on the device, so that writes
+        # through either alias reach the other
         src = self._ensure_contiguous()
         base = src._base if src._base is not None else src
         return ndarray(src._buffer, new_shape, self._dtype, offset=src._offset, base=base)
@@ -317,8 +317,6 @@ class ndarray:
         axes = tuple(_normalize_axis(a, self.ndim) for a in axes)
         if sorted(axes) != list(range(self.ndim)):
             raise ValueError("axes don't match array")
-        if self._np_data is not None:
-            return ndarray._from_np_direct(np.ascontiguousarray(np.transpose(self._np_data, axes)))
         self._materialize_if_lazy()
         return self._view(tuple(self._shape[a] for a in axes),
                           tuple(self._strides[a] for a in axes), self._offset)
@@ -345,8 +343,6 @@ class ndarray:
                 if self._shape[a] != 1:
                     raise ValueError("cannot select an axis to squeeze out which has size not equal to one")
             keep = [i for i in range(self.ndim) if i not in axes]
-        if self._np_data is not None:
-            return ndarray._from_np_direct(self._np_data.reshape([self._shape[i] for i in keep]))
         self._materialize_if_lazy()
         return self._view(tuple(self._shape[i] for i in keep),
                           tuple(self._strides[i] for i in keep), self._offset)
@@ -400,34 +396,32 @@ class ndarray:
         return tuple(shape), tuple(strides), offset
 
     def __getitem__(self, key):
-        if isinstance(key, ndarray):
-            key = key.get()
-        elif isinstance(key, tuple):
-            key = tuple(k.get() if isinstance(k, ndarray) else k for k in key)
-        if self._np_data is not None:
-            return ndarray._from_np_direct(np.asarray(self._np_data[key]))
-        basic = self._basic_index(key)
-        if basic is not None:
-            self._materialize_if_lazy()
-            return self._view(*basic)
-        # advanced (integer / boolean array) indexing: gather on the host
-        return ndarray._from_np_direct(np.asarray(self.get()[key]))
+        if not _advanced_key(key):
+            if self._np_data is not None:
+                if _scalar_key(key, self.ndim):  # one element: read it where it is
+                    return ndarray._from_np_direct(np.asarray(self._np_data[key]))
+                self._ensure_gpu()  # a view: both aliases on the device
+            basic = self._basic_index(key)
+            if basic is not None:
+                self._materialize_if_lazy()
+                return self._view(*basic)
+        # integer / boolean array indices: gathered on the device
+        from . import indexing
+        return indexing.getitem(self, key)
 
     def __setitem__(self, key, value):
-        if isinstance(key, ndarray):
-            key = key.get()
-        elif isinstance(key, tuple):
-            key = tuple(k.get() if isinstance(k, ndarray) else k for k in key)
+        if _advanced_key(key):
+            from . import indexing
+            indexing.setitem(self, key, value)
+            return
         if self._np_data is not None and not isinstance(value, ndarray):
             self._np_data[key] = value
             return
         self._ensure_gpu()
         basic = self._basic_index(key)
         if basic is None:
-            host = self.get()
-            host[key] = value.get() if isinstance(value, ndarray) else value
-            self.set(host)
-            return
+            raise IndexError("only integers, slices (`:`), ellipsis (`...`), numpy.newaxis "
+                             "(`None`) and integer or boolean arrays are valid indices")
         shape, strides, offset = basic
         if _prod(shape) == 0:
             return
@@ -555,6 +549,22 @@ class ndarray:
         from . import sorting
         return sorting.argsort(self, axis=axis, kind=kind, order=order)
 
+    def nonzero(self):
+        from .indexing import nonzero
+        return nonzero(self)
+
+    def take(self, indices, axis=None, out=None, mode="raise"):
+        from .indexing import take
+        return take(self, indices, axis=axis, out=out, mode=mode)
+
+    def put(self, indices, values, mode="raise"):
+        from .indexing import put
+        return put(self, indices, values, mode=mode)
+
+    def compress(self, condition, axis=None, out=None):
+        from .indexing import compress
+        return compress(condition, self, axis=axis, out=out)
+
     def searchsorted(self, v, side="left", sorter=None):
         from . import sorting
         return sorting.searchsorted(self, v, side=side, sorter=sorter)
@@ -595,7 +605,7 @@ class ndarray:
         if dtype == self._dtype and not copy:
             return self
         if self._np_data is not None:
-            return ndarray._from_np_direct(self._np_data.astype(dtype))
+            self._ensure_gpu()
         if self._fusion_node is not None:
             from ._fusion import CastNode
             out = ndarray._lazy(CastNode(self._fusion_node, dtype))
@@ -705,6 +715,25 @@ class ndarray:
     def __array_namespace__(self, *, api_version=None):
         import macmetalpy_amd
         return macmetalpy_amd
+
+
+def _scalar_key(key, ndim) -> bool:
+    """Whether ``key`` is one integer per dimension (selects one element)."""
+    items = key if isinstance(key, tuple) else (key,)
+    return len(items) == ndim and all(
+        isinstance(k, (int, np.integer)) and not isinstance(k, (bool, np.bool_)) for k in items)
+
+
+def _advanced_key(key) -> bool:
+    """Whether ``key`` holds an integer or boolean array (or a sequence or a
+    boolean scalar), i.e. needs NumPy's advanced indexing."""
+    items = key if isinstance(key, tuple) else (key,)
+    for k in items:
+        if isinstance(k, (ndarray, np.ndarray, list, bool, np.bool_)):
+            return True
+        if isinstance(k, tuple):
+            return True
+    return False
 
 
 def _reconstruct(np_array):

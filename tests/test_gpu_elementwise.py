@@ -285,6 +285,24 @@ def test_astype_and_copies():
     _bits_equal(X.T.get(), x.T)
 
 
+@pytest.mark.parametrize("src", [np.float16, np.float32, np.float64])
+def test_float_to_unsigned_casts_wrap(src):
+    """Negative floats cast to unsigned integers wrap through int64, as
+    NumPy's C casts on x86-64 (-1.0 -> 65535 for uint16), in the copy
+    kernels and in fused casts; float64 values of 2^63 and more go to
+    uint64 directly."""
+    x = np.array([-1.0, -2.5, -300.75, 0.0, 1.9, 250.5, -65535.0, 40000.0], src)
+    if src == np.float64:
+        x = np.concatenate([x, [2.0 ** 63, 1.5 * 2.0 ** 63, -2.0 ** 40]])
+    for dt in (np.uint16, np.uint32, np.uint64):
+        with np.errstate(invalid="ignore"):
+            want = x.astype(dt)
+        ok = np.isfinite(x) & ((np.abs(x.astype(np.float64)) < np.iinfo(dt).max) if dt != np.uint64
+                               else True)
+        assert np.array_equal(cp.array(x).astype(dt).get()[ok], want[ok]), dt
+        assert np.array_equal((cp.array(x) + 0).astype(dt).get()[ok], want[ok]), dt
+
+
 def test_empty_and_tiny():
     e = cp.array(np.zeros((0, 3), np.float32))
     assert (cp.sin(e) + 1).shape == (0, 3)

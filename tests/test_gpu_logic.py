@@ -184,8 +184,10 @@ def test_where_scalars_truthy_conditions_and_lazy_inputs():
         want = np.where(x > 0, np.sqrt(x), x * np.float32(2.0))
     _same(got.get(), want)
     _same(cp.where(cp.array(np.zeros((0, 3), bool)), 1.0, 2.0).get(), np.where(np.zeros((0, 3), bool), 1.0, 2.0))
-    with pytest.raises(NotImplementedError):
-        cp.where(cp.array(c))
+    got1 = cp.where(cp.array(c))
+    assert len(got1) == c.ndim
+    for g, w in zip(got1, np.where(c)):
+        _same(g.get(), w)
 
 
 @pytest.mark.parametrize("dtype", FLOAT_DTYPES + [np.int32, np.uint16, np.int64])

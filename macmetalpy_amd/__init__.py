@@ -35,6 +35,8 @@ from .ufunc_ops import (
     invert, bitwise_not, bitwise_invert, bitwise_and, bitwise_or, bitwise_xor, left_shift,
     right_shift, bitwise_left_shift, bitwise_right_shift, logical_and, logical_or,
     logical_xor, logical_not, isnan, isinf, isfinite, signbit,
+    spacing, bitwise_count, conjugate, conj, ldexp, gcd, lcm, frexp, modf, vecdot, matvec,
+    vecmat,
 )
 from .math_ops import where, clip, count_nonzero
 from .indexing import (take, put, take_along_axis, put_along_axis, putmask, place, compress,

@@ -132,6 +132,13 @@ EXPR_UNARY_OPS: dict[str, tuple[np.ufunc, str]] = {
     "isinf_op": (np.isinf, "op_isinf"),
     "isfinite_op": (np.isfinite, "op_isfinite"),
     "signbit_op": (np.signbit, "op_signbit"),
+    "spacing_op": (np.spacing, "op_spacing"),
+    "bitwise_count_op": (np.bitwise_count, "op_bitwise_count"),
+    # frexp / modf have two outputs; each output is its own op, typed like
+    # np.sin (integers -> float64, float16 stays float16), as NumPy types them
+    "frexp_mant_op": (np.sin, "op_frexp_mant"),
+    "frexp_exp_op": (np.sin, "op_frexp_exp"),
+    "modf_frac_op": (np.sin, "op_modf_frac"),
 }
 EXPR_BINARY_OPS: dict[str, tuple[np.ufunc, str]] = {
     "bit_and_op": (np.bitwise_and, "op_bitwise_and"),
@@ -142,12 +149,19 @@ EXPR_BINARY_OPS: dict[str, tuple[np.ufunc, str]] = {
     "logical_and_op": (np.logical_and, "op_logical_and"),
     "logical_or_op": (np.logical_or, "op_logical_or"),
     "logical_xor_op": (np.logical_xor, "op_logical_xor"),
+    "ldexp_op": (np.ldexp, "op_ldexp"),
+    "gcd_op": (np.gcd, "op_gcd"),
+    "lcm_op": (np.lcm, "op_lcm"),
 }
 # Ops with a bool result that read their operands in the operands' own
 # (common) dtype, like the comparisons.
 BOOL_RESULT_OPS = frozenset({"logical_not_op", "isnan_op", "isinf_op", "isfinite_op",
                              "signbit_op", "logical_and_op", "logical_or_op",
                              "logical_xor_op"})
+
+# Unary ops that read their operand in its own dtype (the result has
+# another one).
+OWN_INPUT_OPS = frozenset({"bitwise_count_op"})
 
 # op_name -> mmp_ops.h function, for every unary / binary op
 UNARY_FN = {k: v[2] for k, v in UNARY_OPS.items()}

@@ -156,7 +156,8 @@ def _unary_dtypes(op_name, dt):
         ufunc = ent[1] if ent is not None else _abi.EXPR_UNARY_OPS[op_name][0]
         rdt = ufunc_result_dtype(ufunc, dt)
         # predicates read the operand as it is; other ops compute in the result dtype
-        hit = _UNARY_DTYPES[key] = (rdt, dt if op_name in _abi.BOOL_RESULT_OPS else rdt)
+        own = op_name in _abi.BOOL_RESULT_OPS or op_name in _abi.OWN_INPUT_OPS
+        hit = _UNARY_DTYPES[key] = (rdt, dt if own else rdt)
     return hit
 
 

@@ -647,6 +647,118 @@ template <typename T> MMP_DI bool op_signbit(T a) {
   else return false;
 }
 
+// Unsigned integer with the size of T (bit patterns of floats).
+template <int N> struct mmp_bits_of;
+template <> struct mmp_bits_of<2> { typedef mmp_u16 type; };
+template <> struct mmp_bits_of<4> { typedef mmp_u32 type; };
+template <> struct mmp_bits_of<8> { typedef mmp_u64 type; };
+
+// np.spacing, NumPy's two definitions: float32 / float64 take the step to
+// the next value away from zero, signed like x (npy_spacing: +-0 -> the
+// smallest subnormal, +-largest finite -> +-inf); float16 takes the step to
+// the next value toward +inf, always positive (npy_half_spacing: 65504 ->
+// inf, -0 -> the smallest subnormal).  inf and NaN give NaN.  Neighbouring
+// values differ by an exactly representable step.
+template <typename T> MMP_DI T op_spacing(T a) {
+  if constexpr (!mmp_t<T>::is_float) {
+    return a;
+  } else {
+    typedef typename mmp_bits_of<sizeof(T)>::type B;
+    typedef typename mmp_t<T>::C C;
+    const C x = (C)a;
+    if (__builtin_isnan(x) || __builtin_isinf(x)) return (T)(C)__builtin_nan("");
+    const B sign = (B)((B)1 << (8 * sizeof(T) - 1));
+    const B b = __builtin_bit_cast(B, a);
+    if ((B)(b & (B)~sign) == 0) return __builtin_bit_cast(T, (B)1);
+    if constexpr (sizeof(T) == 2) {
+      const B up = (b & sign) ? (B)(b - 1) : (B)(b + 1);  // toward +inf
+      return (T)((C)__builtin_bit_cast(T, up) - x);
+    } else {
+      return (T)((C)__builtin_bit_cast(T, (B)(b + 1)) - x);  // away from zero
+    }
+  }
+}
+// np.bitwise_count: set bits of |x|
+template <typename T> MMP_DI int op_bitwise_count(T a) {
+  if constexpr (mmp_t<T>::is_bool) {
+    return a ? 1 : 0;
+  } else {
+    typedef typename mmp_t<T>::U U;
+    const U m = (mmp_t<T>::is_signed && a < (T)0) ? (U)((U)0 - (U)a) : (U)a;
+    return __builtin_popcountll((unsigned long long)m);
+  }
+}
+// np.frexp, as two ops: the mantissa in [0.5, 1) and the exponent (as a
+// value of T, converted to int32 by the caller); 0, inf and NaN keep their
+// value with exponent 0.
+template <typename T> MMP_DI T op_frexp_mant(T a) {
+  typedef typename mmp_t<T>::C C;
+  const C x = (C)a;
+  if (!__builtin_isfinite(x) || x == (C)0) return a;
+  int e;
+  return (T)__builtin_frexp(x, &e);
+}
+template <> MMP_DI float op_frexp_mant(float a) {
+  if (!__builtin_isfinite(a) || a == 0.f) return a;
+  int e;
+  return __builtin_frexpf(a, &e);
+}
+template <typename T> MMP_DI T op_frexp_exp(T a) {
+  typedef typename mmp_t<T>::C C;
+  const C x = (C)a;
+  if (!__builtin_isfinite(x) || x == (C)0) return (T)0;
+  int e;
+  if constexpr (sizeof(C) == 4) (void)__builtin_frexpf((float)x, &e);
+  else (void)__builtin_frexp((double)x, &e);
+  return (T)(C)e;
+}
+// np.modf fractional part (the integral part is trunc)
+template <typename T> MMP_DI T op_modf_frac(T a) {
+  typedef typename mmp_t<T>::C C;
+  const C x = (C)a;
+  if (__builtin_isinf(x)) return (T)__builtin_copysignf(0.f, (float)x);
+  return (T)__builtin_copysignf((float)(x - __builtin_truncf(x)), (float)x);
+}
+template <> MMP_DI float op_modf_frac(float a) {
+  if (__builtin_isinf(a)) return __builtin_copysignf(0.f, a);
+  const float t = __builtin_truncf(a);
+  return __builtin_copysignf(a - t, a);
+}
+template <> MMP_DI double op_modf_frac(double a) {
+  if (__builtin_isinf(a)) return __builtin_copysign(0.0, a);
+  const double t = __builtin_trunc(a);
+  return __builtin_copysign(a - t, a);
+}
+// np.ldexp(x, n); n arrives converted to T and is clamped far outside the
+// exponent range (the result saturates anyway)
+template <typename T> MMP_DI T op_ldexp(T a, T b) {
+  typedef typename mmp_t<T>::C C;
+  C n = (C)b;
+  n = n > (C)100000 ? (C)100000 : (n < (C)-100000 ? (C)-100000 : n);
+  if constexpr (sizeof(C) == 4) return (T)__builtin_ldexpf((float)a, (int)n);
+  else return (T)__builtin_ldexp((double)a, (int)n);
+}
+// np.gcd / np.lcm on magnitudes (Euclid), results wrapped to T
+template <typename T> MMP_DI T op_gcd(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  U x = (mmp_t<T>::is_signed && a < (T)0) ? (U)((U)0 - (U)a) : (U)a;
+  U y = (mmp_t<T>::is_signed && b < (T)0) ? (U)((U)0 - (U)b) : (U)b;
+  while (y) {
+    const U t = (U)(x % y);
+    x = y;
+    y = t;
+  }
+  return (T)x;
+}
+template <typename T> MMP_DI T op_lcm(T a, T b) {
+  typedef typename mmp_t<T>::U U;
+  const U x = (mmp_t<T>::is_signed && a < (T)0) ? (U)((U)0 - (U)a) : (U)a;
+  const U y = (mmp_t<T>::is_signed && b < (T)0) ? (U)((U)0 - (U)b) : (U)b;
+  if (!x || !y) return (T)0;
+  const U g = (U)op_gcd<T>((T)x, (T)y);
+  return (T)(U)(x / g * y);
+}
+
 // =====================================================================
 // Conversions (astype).  bool targets test != 0 (NaN -> true).
 // =====================================================================

@@ -699,18 +699,14 @@ class ndarray:
 
     # ------------------------------------------------- numpy protocols
     def __array_ufunc__(self, ufunc, method, *inputs, **kwargs):
-        """Route NumPy ufunc calls on device arrays to the device op
-        (reference ndarray.py:2681-2720)."""
+        """Route NumPy ufunc calls on device arrays to the device ops
+        (reference ndarray.py:2681-2720, which falls back to NumPy on the
+        host): ``__call__`` with ``out=`` / ``dtype=`` / ``where=`` (with
+        ``out``), ``reduce`` and ``accumulate`` of the ufuncs that have a
+        reduction or scan.  Anything else returns NotImplemented, so NumPy
+        raises TypeError rather than computing on the host."""
         from . import _ufunc_table
-        if method == "__call__" and not kwargs:
-            fn = _ufunc_table.lookup(ufunc)
-            if fn is not None:
-                return fn(*inputs)
-        np_inputs = tuple(x.get() if isinstance(x, ndarray) else x for x in inputs)
-        res = getattr(ufunc, method)(*np_inputs, **kwargs)
-        if isinstance(res, np.ndarray):
-            return ndarray._from_np_direct(res)
-        return res
+        return _ufunc_table.dispatch(ufunc, method, inputs, kwargs)
 
     def __array_namespace__(self, *, api_version=None):
         import macmetalpy_amd

@@ -161,3 +161,61 @@ def divmod(x1, x2, /):
 
 
 __all__ += ["float_power", "divmod"]
+
+
+for _name, _op, _doc in [
+    ("spacing", "spacing_op", "Distance to the next representable magnitude, signed like x."),
+    ("bitwise_count", "bitwise_count_op", "Number of 1-bits in |x|."),
+    ("conjugate", "positive_op", "Complex conjugate (the identity for real dtypes)."),
+    ("conj", "positive_op", "Complex conjugate (the identity for real dtypes)."),
+]:
+    _unary(_name, _op, _doc)
+
+for _name, _op, _doc in [
+    ("ldexp", "ldexp_op", "x1 * 2**x2."),
+    ("gcd", "gcd_op", "Greatest common divisor of |x1| and |x2|."),
+    ("lcm", "lcm_op", "Lowest common multiple of |x1| and |x2|."),
+]:
+    _binary(_name, _op, _doc)
+
+
+def frexp(x, /):
+    """(mantissa, int32 exponent) with x = mantissa * 2**exponent."""
+    import numpy as np
+    return ew.unary("frexp_mant_op", x), ew.unary("frexp_exp_op", x).astype(np.int32)
+
+
+def modf(x, /):
+    """(fractional part, integral part), both with the sign of x."""
+    from . import creation
+    from ._dtypes import ufunc_result_dtype
+    import numpy as np
+    xa = creation.asarray(x)
+    fdt = ufunc_result_dtype(np.sin, xa.dtype)
+    return ew.unary("modf_frac_op", xa), ew.unary("trunc_op", xa.astype(fdt))
+
+
+def vecdot(x1, x2, /, *, axis=-1):
+    """Dot products of vectors along ``axis`` (real dtypes)."""
+    from .reductions import sum as _sum
+    return _sum(ew.binary("mul_op", x1, x2), axis=axis)
+
+
+def matvec(x1, x2, /):
+    """Matrix-vector products over the last two / last dimension."""
+    from .linalg_top import matmul
+    from . import creation
+    v = creation.asarray(x2)
+    return matmul(x1, v.reshape(tuple(v.shape) + (1,))).squeeze(-1)
+
+
+def vecmat(x1, x2, /):
+    """Vector-matrix products over the last dimension / last two."""
+    from .linalg_top import matmul
+    from . import creation
+    v = creation.asarray(x1)
+    r = matmul(v.reshape(tuple(v.shape[:-1]) + (1, v.shape[-1])), x2)
+    return r.squeeze(-2)
+
+
+__all__ += ["frexp", "modf", "vecdot", "matvec", "vecmat"]

@@ -39,6 +39,15 @@ from .ufunc_ops import (
     vecmat,
 )
 from .math_ops import where, clip, count_nonzero
+from .manipulation import (
+    concatenate, concat, stack, vstack, hstack, dstack, column_stack, split, array_split,
+    hsplit, vsplit, dsplit, unstack, tile, repeat, flip, fliplr, flipud, rot90, roll,
+    broadcast_to, broadcast_arrays, moveaxis, rollaxis, swapaxes, squeeze, expand_dims,
+    atleast_1d, atleast_2d, atleast_3d, diagonal, diag, trace, tril, triu, copy, copyto,
+    append, ptp, diff, outer, meshgrid, cross, kron, tensordot, average, unique,
+    permute_dims, matrix_transpose,
+)
+from .statistics import median, quantile, percentile, nanmedian, nanquantile, nanpercentile
 from .indexing import (take, put, take_along_axis, put_along_axis, putmask, place, compress,
                        extract, nonzero, flatnonzero, argwhere)
 from .reductions import (
@@ -78,10 +87,6 @@ def materialize(*arrays) -> None:
     (_fusion.materialize, ndarray.py:478-481)."""
     for a in arrays:
         a._materialize_if_lazy()
-
-
-def expand_dims(a, axis):
-    return asarray(a).expand_dims(axis)
 
 
 def reshape(a, shape):

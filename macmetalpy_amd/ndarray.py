@@ -348,10 +348,8 @@ class ndarray:
                           tuple(self._strides[i] for i in keep), self._offset)
 
     def expand_dims(self, axis) -> "ndarray":
-        ax = _normalize_axis(axis, self.ndim + 1)
-        shape = list(self._shape)
-        shape.insert(ax, 1)
-        return self.reshape(tuple(shape))
+        from .manipulation import expand_dims
+        return expand_dims(self, axis)
 
     # ------------------------------------------------------- indexing
     def _basic_index(self, key):

@@ -360,6 +360,70 @@ def bench_sort(cp, be, reps=5):
     return res
 
 
+# ------------------------------------------------- indexing / manipulation
+def _time(cp, be, name, f, reps):
+    f()
+    cp.synchronize()
+    timer = EventTimer(be)
+    for _ in range(reps):
+        timer.run(name, f)
+    cp.synchronize()
+    ms, _ = timer.ms(name)
+    timer.close()
+    return ms
+
+
+def bench_indexing(cp, be, reps=5):
+    """Advanced indexing, manipulation and order statistics on 2^26-element
+    float32 inputs.  `gbs` counts the bytes each operation must move:
+    a[idx] (2^26 random int64 indices): 8 B index + 4 B read + 4 B write per
+    element; a[a > 0] (about half selected): the mask pass (4 B read + 1 B
+    written), its scan (1 B read + 8 B written), the positions (8 B read +
+    8 B per selected element written) and the gather (8 + 4 + 4 B per
+    selected element); concatenate of two 2^25 arrays: 8 B per element;
+    tile 2^13 x 2^13 -> 2x: 4 B read once, 8 B written per source element.
+    median / quantile of (8192, 8192) along axis 1 are timed per call (the
+    radix sort of the rows dominates: 48 B per element as designed)."""
+    rng = np.random.default_rng(13)
+    n = 1 << 26
+    x = cp.array(rng.standard_normal(n, dtype=np.float32))
+    x._ensure_gpu()
+    idx = cp.array(rng.integers(0, n, n))
+    idx._ensure_gpu()
+    res = {}
+    cases = {
+        "gather_a[idx]_2^26": (lambda: x[idx], 16 * n),
+        "mask_a[a>0]_2^26": (lambda: x[x > 0], (5 + 9 + 8) * n + (8 + 8 + 8) * (n // 2)),
+        "concatenate_2x2^25": (lambda: cp.concatenate([x[: n // 2], x[n // 2:]]), 8 * n),
+        "tile_8192sq_2x2": (lambda: cp.tile(x.reshape(8192, 8192), (2, 2)), 4 * n + 16 * n),
+        "take_along_axis_8192sq": (None, 0),
+    }
+    m = x.reshape(8192, 8192)
+    order = cp.argsort(m[:, :64], axis=1)
+    order._ensure_gpu()
+    cases["take_along_axis_8192sq"] = (lambda: cp.take_along_axis(m[:, :64], order, axis=1),
+                                       (8 + 4 + 4) * 8192 * 64)
+    for name, (f, nbytes) in cases.items():
+        try:
+            ms = _time(cp, be, name, f, reps)
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1)}
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    for name, f in (("median_axis1_8192sq", lambda: cp.median(m, axis=1)),
+                    ("quantile_0.9_axis1_8192sq", lambda: cp.quantile(m, 0.9, axis=1)),
+                    ("nanmedian_axis1_8192sq", lambda: cp.nanmedian(m, axis=1)),
+                    ("unique_int32_2^24", lambda: cp.unique(ui))):
+        try:
+            if name.startswith("unique"):
+                ui = cp.array(rng.integers(0, 1 << 20, 1 << 24).astype(np.int32))
+                ui._ensure_gpu()
+            ms = _time(cp, be, name, f, reps)
+            res[name] = {"kernel_ms": round(ms, 4)}
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
 # --------------------------------------------------------------- C5
 def bench_c5(cp, be, reps=10):
     from macmetalpy_amd.workloads import c5_inputs
@@ -549,7 +613,8 @@ def main():
                          ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5),
                          ("logic_where_clip_2p28", bench_logic),
                          ("nan_reductions_16384sq", bench_nan),
-                         ("sort_searchsorted", bench_sort)):
+                         ("sort_searchsorted", bench_sort),
+                         ("indexing_manipulation", bench_indexing)):
             t = time.time()
             try:
                 cfgs[name] = fn(cp, be)

@@ -300,10 +300,14 @@ int mmp_take(int itemsize, int64_t nsrc, const void *src, int64_t n,
 
 /* Gather rows: out row i (row_words words of `word` = 1, 2, 4, 8 or 16
  * bytes) = the row_words words starting at word offsets[i] * unit of src.
- * Words outside [0, src_bytes / word) read as 0 (callers check indices).
+ * Words outside [0, src_bytes / word) read as 0.  wrap > 0 makes offsets
+ * row indices of an axis of length wrap: negatives count from the end and
+ * an index outside [-wrap, wrap) reads 0 and sets *flag (flag may be
+ * NULL) -- NumPy's IndexError, checked by the caller after the call.
  * src and out must be aligned to `word`. */
 int mmp_gather(int word, const void *src, int64_t src_bytes, const int64_t *offsets,
-               int64_t unit, int64_t n, int64_t row_words, void *out);
+               int64_t unit, int64_t wrap, uint32_t *flag, int64_t n, int64_t row_words,
+               void *out);
 
 /* Scatter rows: the row_words words at word offsets[i] * unit of dst =
  * row i of src (src_rows = n), or its only row (src_rows = 1).  Targets

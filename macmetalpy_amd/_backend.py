@@ -94,7 +94,7 @@ _SIGNATURES = {
     "mmp_sort": [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int],
     "mmp_searchsorted": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp],
     "mmp_take": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp],
-    "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp],
+    "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp],
     "mmp_scatter": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64],
     "mmp_nonzero": [_c_i64, _c_vp, _c_i64, _c_vp],
     "mmp_matmul": [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
@@ -337,9 +337,9 @@ class HipBackend:
         _check(self._lib.mmp_take(itemsize, nsrc, src, n, indices, out), "mmp_take")
 
     def gather(self, word: int, src: int, src_bytes: int, offsets: int, unit: int, n: int,
-               row_words: int, out: int) -> None:
-        _check(self._lib.mmp_gather(word, src, src_bytes, offsets, unit, n, row_words, out),
-               "mmp_gather")
+               row_words: int, out: int, wrap: int = 0, flag: int = 0) -> None:
+        _check(self._lib.mmp_gather(word, src, src_bytes, offsets, unit, wrap, flag or None, n,
+                                    row_words, out), "mmp_gather")
 
     def scatter(self, word: int, dst: int, dst_bytes: int, offsets: int, unit: int, n: int,
                 row_words: int, src: int, src_rows: int) -> None:

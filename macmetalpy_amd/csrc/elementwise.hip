@@ -230,6 +230,40 @@ __global__ __launch_bounds__(kBlock) void k_copy(const Ti *__restrict__ x,
   }
 }
 
+// Strided copy by rows: each workgroup takes one row (all dimensions but
+// the last) and a tile of kRowTile columns, resolves the row's source and
+// destination offsets once, then copies along the row -- coalesced when
+// the last dimension's strides are 0 or 1 (broadcasts, tiles, slices).
+// The generic kernel above pays a 64-bit division per dimension for every
+// element.
+constexpr int kRowTile = kBlock * 4;
+
+template <typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_copy_rows(const Ti *__restrict__ x,
+                                                      To *__restrict__ y, StrideDesc d,
+                                                      long long ctiles) {
+  const int last = d.ndim - 1;
+  const long long len = d.shape[last];
+  const long long b = blockIdx.x;
+  const long long row = b / ctiles;
+  const long long c0 = (b - row * ctiles) * kRowTile;
+  long long rem = row, so = 0, dof = 0;
+  for (int k = last - 1; k >= 0; --k) {
+    const long long s = d.shape[k];
+    const long long q = rem / s;
+    const long long idx = rem - q * s;
+    so += idx * d.sstride[k];
+    dof += idx * d.dstride[k];
+    rem = q;
+  }
+  const long long ss = d.sstride[last], ds = d.dstride[last];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const long long c = c0 + u * kBlock + threadIdx.x;
+    if (c < len) y[dof + c * ds] = mmp_convert<To, Ti>(x[so + c * ss]);
+  }
+}
+
 // Contiguous cast / copy with vector accesses: per step a thread converts
 // E = 16 / sizeof(To) consecutive elements and writes them with one 16-byte
 // store, so the lanes of a store instruction cover one contiguous span;
@@ -462,6 +496,26 @@ int copy_from(int dst_dtype, long long n, const void *x, void *y,
         hipLaunchKernelGGL((k_copy_transpose<Ti, T>), dim3((unsigned)blocks), dim3(kBlock), 0,
                            mmpi::stream(), (const Ti *)x, (T *)y, t);
         return mmpi::check_launch("mmp_copy(transpose)");
+      })
+    }
+  }
+  if (mode != 0 && d.ndim >= 2 && d.shape[d.ndim - 1] >= 256) {
+    const long long len = d.shape[d.ndim - 1];
+    const long long ctiles = mmpi::ceil_div(len, kRowTile);
+    const long long blocks = (n / len) * ctiles;
+    if (blocks <= 0x7fffffffLL) {
+      StrideDesc e = d;
+      if (mode == 1) {  // contiguous destination: C strides of the shape
+        long long acc = 1;
+        for (int k = e.ndim - 1; k >= 0; --k) {
+          e.dstride[k] = acc;
+          acc *= e.shape[k];
+        }
+      }
+      MMP_DISPATCH_ALL(dst_dtype, {
+        hipLaunchKernelGGL((k_copy_rows<Ti, T>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                           mmpi::stream(), (const Ti *)x, (T *)y, e, ctiles);
+        return mmpi::check_launch("mmp_copy(rows)");
       })
     }
   }

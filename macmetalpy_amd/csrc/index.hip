@@ -44,16 +44,28 @@ __device__ __forceinline__ void split(long long w, long long wpr, long long &i, 
   }
 }
 
+// wrap > 0: the offsets are row indices in [-wrap, wrap) (negatives count
+// from the end); any other index reads nothing and sets *flag.
 template <typename W, bool SMALL>
 __global__ __launch_bounds__(kBlock) void k_gather(const W *__restrict__ src, long long src_words,
                                                    const long long *__restrict__ off, long long unit,
+                                                   long long wrap, unsigned *__restrict__ flag,
                                                    long long n, long long wpr, W *__restrict__ out) {
   const long long total = n * wpr;
   for (long long w = (long long)blockIdx.x * kBlock + threadIdx.x; w < total;
        w += (long long)gridDim.x * kBlock) {
     long long i, c;
     split<SMALL>(w, wpr, i, c);
-    const long long s = off[i] * unit + c;
+    long long o = off[i];
+    if (wrap > 0) {
+      if (o < 0) o += wrap;
+      if (o < 0 || o >= wrap) {
+        if (flag) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        out[w] = W{};
+        continue;
+      }
+    }
+    const long long s = o * unit + c;
     out[w] = (s >= 0 && s < src_words) ? src[s] : W{};
   }
 }
@@ -86,16 +98,17 @@ __global__ __launch_bounds__(kBlock) void k_nonzero(const long long *__restrict_
 
 template <typename W>
 int gather_w(const void *src, long long src_bytes, const long long *off, long long unit,
-             long long n, long long wpr, void *out) {
+             long long wrap, unsigned *flag, long long n, long long wpr, void *out) {
   const long long total = n * wpr;
   const bool small = total < (1ll << 31) && wpr < (1ll << 31);
   const unsigned grid = grid_for(total);
+  const long long words = src_bytes / (long long)sizeof(W);
   if (small)
     hipLaunchKernelGGL((k_gather<W, true>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
-                       (const W *)src, src_bytes / (long long)sizeof(W), off, unit, n, wpr, (W *)out);
+                       (const W *)src, words, off, unit, wrap, flag, n, wpr, (W *)out);
   else
     hipLaunchKernelGGL((k_gather<W, false>), dim3(grid), dim3(kBlock), 0, mmpi::stream(),
-                       (const W *)src, src_bytes / (long long)sizeof(W), off, unit, n, wpr, (W *)out);
+                       (const W *)src, words, off, unit, wrap, flag, n, wpr, (W *)out);
   return mmpi::check_launch("mmp_gather");
 }
 
@@ -123,20 +136,21 @@ bool word_ok(int word, const void *a, const void *b) {
 }  // namespace
 
 extern "C" int mmp_gather(int word, const void *src, int64_t src_bytes, const int64_t *offsets,
-                          int64_t unit, int64_t n, int64_t row_words, void *out) {
+                          int64_t unit, int64_t wrap, uint32_t *flag, int64_t n,
+                          int64_t row_words, void *out) {
   if (int st = mmpi::ensure_init()) return st;
-  if (src_bytes < 0 || n < 0 || row_words < 0 || unit < 0)
+  if (src_bytes < 0 || n < 0 || row_words < 0 || unit < 0 || wrap < 0)
     return mmpi::fail(MMP_E_ARG, "mmp_gather: negative extent");
   if (n == 0 || row_words == 0) return MMP_OK;
   if (!offsets || !out || !src) return mmpi::fail(MMP_E_ARG, "mmp_gather: null pointer");
   if (!word_ok(word, src, out)) return mmpi::fail(MMP_E_ARG, "mmp_gather: word size %d / alignment", word);
   const long long *o = (const long long *)offsets;
   switch (word) {
-    case 1: return gather_w<unsigned char>(src, src_bytes, o, unit, n, row_words, out);
-    case 2: return gather_w<unsigned short>(src, src_bytes, o, unit, n, row_words, out);
-    case 4: return gather_w<unsigned>(src, src_bytes, o, unit, n, row_words, out);
-    case 8: return gather_w<unsigned long long>(src, src_bytes, o, unit, n, row_words, out);
-    default: return gather_w<u32x4>(src, src_bytes, o, unit, n, row_words, out);
+    case 1: return gather_w<unsigned char>(src, src_bytes, o, unit, wrap, flag, n, row_words, out);
+    case 2: return gather_w<unsigned short>(src, src_bytes, o, unit, wrap, flag, n, row_words, out);
+    case 4: return gather_w<unsigned>(src, src_bytes, o, unit, wrap, flag, n, row_words, out);
+    case 8: return gather_w<unsigned long long>(src, src_bytes, o, unit, wrap, flag, n, row_words, out);
+    default: return gather_w<u32x4>(src, src_bytes, o, unit, wrap, flag, n, row_words, out);
   }
 }
 

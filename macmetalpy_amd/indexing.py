@@ -31,6 +31,7 @@ import math
 import numpy as np
 
 from ._backend import HipBackend
+from ._dtypes import dtype_code
 from . import _elementwise as ew
 from .ndarray import ndarray, _prod, _normalize_axis
 
@@ -300,11 +301,63 @@ class _Plan:
         self.n = _prod(self.rshape)
 
 
+def _row_index(a: ndarray, key):
+    """The index array when ``key`` is one integer array on axis 0 followed
+    only by whole slices and ``a`` has contiguous rows, else None."""
+    items = key if isinstance(key, tuple) else (key,)
+    if not items or a.ndim == 0 or a._strides[0] < 0:
+        return None
+    k0 = items[0]
+    if not isinstance(k0, (ndarray, np.ndarray, list)):
+        return None
+    if any(not (isinstance(k, slice) and k == slice(None)) for k in items[1:]):
+        return None
+    if len(items) > a.ndim:
+        return None
+    from ._fusion import _c_contig_strides
+    if tuple(a._strides[1:]) != _c_contig_strides(a.shape[1:]):
+        return None
+    idx = _asarray(k0)
+    return idx if idx._dtype.kind in "iu" else None
+
+
+def _gather_rows(a: ndarray, idx: ndarray) -> ndarray:
+    """a[idx] along axis 0 with the raw indices: the kernel wraps negative
+    indices and flags out-of-range ones, so no offset array and no bounds
+    reductions are needed (the message is worked out only on error)."""
+    be = HipBackend()
+    isz = a._dtype.itemsize
+    rows = a.shape[1:]
+    rowbytes = _prod(rows) * isz
+    off_b, st_b = a._offset * isz, a._strides[0] * isz
+    word = 16
+    while word > 1 and (rowbytes % word or st_b % word or off_b % word):
+        word //= 2
+    ix = idx.astype(_I64) if idx._dtype != _I64 else idx
+    ix = ix._ensure_contiguous()
+    out = ndarray._empty_device(tuple(idx.shape) + tuple(rows), a._dtype)
+    if out.size == 0:
+        if ix.size and a.shape[0] == 0:
+            raise IndexError(f"index {int(ix.ravel()[0])} is out of bounds for axis 0 with size 0")
+        return out
+    flag = ndarray._empty_device((1,), np.uint32)
+    be.fill(dtype_code(flag._dtype), 1, np.zeros(1, np.uint32), flag._ptr)
+    be.gather(word, a._buffer.ptr + off_b, a._buffer.nbytes - off_b, ix._ptr, st_b // word,
+              ix.size, rowbytes // word, out._ptr, wrap=a.shape[0], flag=flag._ptr)
+    if int(flag.get()[0]):
+        _norm_index(ix, a.shape[0], 0)  # raises NumPy's IndexError
+    return out
+
+
 def getitem(a: ndarray, key, mode: str = "raise") -> ndarray:
     """``a[key]`` for keys with integer or boolean arrays (a new array);
     ``mode`` treats out-of-range indices as np.take does."""
     a._materialize_if_lazy()
     a._ensure_gpu()
+    if mode == "raise":
+        idx = _row_index(a, key)
+        if idx is not None:
+            return _gather_rows(a, idx)
     plan = _Plan(a, key, mode)
     out = ndarray._empty_device(plan.rshape + plan.row_shape, a._dtype)
     if out.size:

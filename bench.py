@@ -551,6 +551,14 @@ def run_only(cp, be, name, steps):
     print(json.dumps({"only": name, "steps": steps, "kernel_ms": round(ms, 4)}), flush=True)
 
 
+CONFIG_SECTIONS = {
+    "c1_fused_elementwise": bench_c1, "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
+    "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
+    "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,
+    "indexing_manipulation": bench_indexing,
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -561,6 +569,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=ONLY_OPS, default=None,
                     help="run one headline op `--steps` times and exit (profiling)")
+    ap.add_argument("--config", choices=sorted(CONFIG_SECTIONS), default=None,
+                    help="run one configuration section, print its JSON and exit (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -572,6 +582,9 @@ def main():
     be = HipBackend()
     if args.only:
         run_only(cp, be, args.only, args.steps)
+        return
+    if args.config:
+        print(json.dumps({args.config: CONFIG_SECTIONS[args.config](cp, be)}), flush=True)
         return
 
     c2 = bench_c2(cp, be, args.steps, args.warmup)
@@ -609,12 +622,7 @@ def main():
     }
     if args.suite == "all":
         cfgs = {}
-        for name, fn in (("c1_fused_elementwise", bench_c1), ("c3_reduce_scan", bench_c3),
-                         ("c4_matmul", bench_c4), ("c5_fusion_chain", bench_c5),
-                         ("logic_where_clip_2p28", bench_logic),
-                         ("nan_reductions_16384sq", bench_nan),
-                         ("sort_searchsorted", bench_sort),
-                         ("indexing_manipulation", bench_indexing)):
+        for name, fn in CONFIG_SECTIONS.items():
             t = time.time()
             try:
                 cfgs[name] = fn(cp, be)

@@ -231,12 +231,16 @@ __global__ __launch_bounds__(kBlock) void k_copy(const Ti *__restrict__ x,
 }
 
 // Strided copy by rows: each workgroup takes one row (all dimensions but
-// the last) and a tile of kRowTile columns, resolves the row's source and
+// the last) and a tile of kRowTile (4096) columns, resolves the row's source and
 // destination offsets once, then copies along the row -- coalesced when
 // the last dimension's strides are 0 or 1 (broadcasts, tiles, slices).
 // The generic kernel above pays a 64-bit division per dimension for every
 // element.
-constexpr int kRowTile = kBlock * 4;
+#ifndef MMP_ROW_ITEMS
+#define MMP_ROW_ITEMS 16
+#endif
+constexpr int kRowItems = MMP_ROW_ITEMS;
+constexpr int kRowTile = kBlock * kRowItems;
 
 template <typename Ti, typename To>
 __global__ __launch_bounds__(kBlock) void k_copy_rows(const Ti *__restrict__ x,
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kBlock) void k_copy_rows(const Ti *__restrict__ x,
   }
   const long long ss = d.sstride[last], ds = d.dstride[last];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < kRowItems; ++u) {
     const long long c = c0 + u * kBlock + threadIdx.x;
     if (c < len) y[dof + c * ds] = mmp_convert<To, Ti>(x[so + c * ss]);
   }

@@ -52,13 +52,24 @@ from .indexing import (take, put, take_along_axis, put_along_axis, putmask, plac
                        extract, nonzero, flatnonzero, argwhere)
 from .reductions import (
     sum, mean, prod, max, min, amax, amin, argmax, argmin, any, all, cumsum, cumprod, var,
-    std, cumulative_sum, cumulative_prod,
+    std,
 )
 from .nan_ops import (
     nansum, nanprod, nanmax, nanmin, nanmean, nanvar, nanstd, nanargmax, nanargmin,
     nancumsum, nancumprod,
 )
 from .sorting import sort, argsort, searchsorted
+from .extras import (
+    isclose, allclose, array_equal, array_equiv, isin, in1d, intersect1d, union1d, setdiff1d,
+    setxor1d, round, around, fix, nan_to_num, real, imag, angle, isreal, iscomplex,
+    real_if_close, sinc, interp, bincount, digitize, histogram, lexsort, partition,
+    argpartition, cov, corrcoef, select, piecewise, choose, gradient, trapezoid, convolve,
+    correlate, identity, tri, logspace, geomspace, vander, indices, ix_, fill_diagonal,
+    diag_indices, diag_indices_from, tril_indices, triu_indices, tril_indices_from,
+    triu_indices_from, ravel_multi_index, unravel_index, finfo, iinfo, result_type, can_cast,
+    promote_types, isscalar, ndim, shape, size, asnumpy, get_array_module, cumulative_sum,
+    cumulative_prod,
+)
 from .linalg_top import matmul, dot, vdot, inner
 from . import linalg
 from . import random

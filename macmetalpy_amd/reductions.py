@@ -27,7 +27,7 @@ from ._dtypes import dtype_code, resolve_dtype
 from .ndarray import ndarray, _normalize_axis, _prod
 
 __all__ = ["sum", "mean", "prod", "max", "min", "amax", "amin", "argmax", "argmin", "any", "all",
-           "cumsum", "cumprod", "var", "std", "cumulative_sum", "cumulative_prod"]
+           "cumsum", "cumprod", "var", "std"]
 
 _OUT_DTYPE_CACHE: dict = {}
 
@@ -341,21 +341,6 @@ def cumsum(a, axis=None, dtype=None, out=None):
 
 def cumprod(a, axis=None, dtype=None, out=None):
     return _scan(a, _abi.SCAN_CUMPROD, "cumprod", axis, dtype, out)
-
-
-def cumulative_sum(x, /, *, axis=None, dtype=None, out=None, include_initial=False):
-    r = cumsum(x, axis=axis if axis is not None else (0 if _asarray(x).ndim == 1 else None),
-               dtype=dtype, out=out)
-    if include_initial:
-        raise NotImplementedError("include_initial=True is not supported")
-    return r
-
-
-def cumulative_prod(x, /, *, axis=None, dtype=None, out=None, include_initial=False):
-    if include_initial:
-        raise NotImplementedError("include_initial=True is not supported")
-    return cumprod(x, axis=axis if axis is not None else (0 if _asarray(x).ndim == 1 else None),
-                   dtype=dtype, out=out)
 
 
 def var(a, axis=None, dtype=None, out=None, ddof=0, keepdims=False):

@@ -70,7 +70,36 @@ from .extras import (
     promote_types, isscalar, ndim, shape, size, asnumpy, get_array_module, cumulative_sum,
     cumulative_prod,
 )
+from .extras import histogram_bin_edges
+from .routines import (
+    einsum, einsum_path, pad, insert, delete, diagflat, ediff1d, histogramdd, histogram2d,
+    packbits, unpackbits, poly, polyval, polyadd, polysub, polymul, polydiv, polyder, polyint,
+    polyfit, roots, poly1d, bartlett, blackman, hamming, hanning, kaiser, i0, unwrap,
+    unique_all, unique_counts, unique_inverse, unique_values, mgrid, ogrid, r_, c_, s_,
+    index_exp, block, apply_along_axis, apply_over_axes, resize, trim_zeros, isposinf,
+    isneginf, mask_indices, asanyarray, asarray_chkfinite, asfortranarray, require, astype,
+    broadcast_shapes, fastCopyAndTranspose, row_stack, trapz, isnat,
+)
+from .host_api import (
+    False_, True_, ScalarType, byte, ubyte, short, ushort, intc, uintc, uint, longlong,
+    ulonglong, int_, intp, uintp, int8, uint8, single, double, half, longdouble, float_,
+    longfloat, csingle, cdouble, clongdouble, complex64, complex128, complex_, cfloat,
+    singlecomplex, longcomplex, clongfloat, bytes_, str_, object_, void, datetime64,
+    timedelta64, generic, number, integer, signedinteger, unsignedinteger, inexact, floating,
+    complexfloating, character, flexible, dtype, sctypeDict, typecodes, little_endian,
+    euler_gamma, issubdtype, isdtype, mintypecode, typename, iterable, broadcast, flatiter,
+    ndindex, common_type, min_scalar_type, iscomplexobj, isrealobj, isfortran,
+    may_share_memory, shares_memory, array2string, array_repr, array_str, set_printoptions,
+    get_printoptions, printoptions, format_float_positional, format_float_scientific,
+    base_repr, binary_repr, info, errstate, seterr, geterr, seterrcall, geterrcall, getbufsize,
+    setbufsize, get_include, show_config, show_runtime, save, savez, savez_compressed, load,
+    loadtxt, savetxt, genfromtxt, fromfile, fromregex, frombuffer, fromstring, fromiter,
+    from_dlpack, fromfunction, memmap, busday_count, busday_offset, busdaycalendar, is_busday,
+    datetime_as_string, datetime_data, matrix, asmatrix, bmat, recarray, record, vectorize,
+    frompyfunc, nditer, sort_complex, geterrobj, seterrobj, set_numeric_ops,
+)
 from .linalg_top import matmul, dot, vdot, inner
+from ._backend import HipBackend as MetalBackend  # the reference's backend class name
 from . import linalg
 from . import random
 

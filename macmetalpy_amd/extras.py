@@ -21,7 +21,7 @@ from .ndarray import ndarray, _normalize_axis, _prod
 __all__ = ["isclose", "allclose", "array_equal", "array_equiv", "isin", "in1d", "intersect1d",
            "union1d", "setdiff1d", "setxor1d", "round", "around", "fix", "nan_to_num", "real",
            "imag", "angle", "isreal", "iscomplex", "real_if_close", "sinc", "interp", "bincount",
-           "digitize", "histogram", "lexsort", "partition", "argpartition", "cov", "corrcoef",
+           "digitize", "histogram", "histogram_bin_edges", "lexsort", "partition", "argpartition", "cov", "corrcoef",
            "select", "piecewise", "choose", "gradient", "trapezoid", "convolve", "correlate",
            "identity", "tri", "logspace", "geomspace", "vander", "indices", "ix_",
            "fill_diagonal", "diag_indices", "diag_indices_from", "tril_indices",
@@ -337,6 +337,54 @@ def bincount(x, weights=None, minlength=0):
     return c[1:] - c[:-1]
 
 
+def _outer_edges(x, range):
+    """First and last edge as NumPy takes them: the range's values, or the
+    data's own min / max scalars (so float32 data gets float32 edges),
+    widened by 0.5 when equal."""
+    from . import reductions
+    if range is not None:
+        lo, hi = range
+        if lo > hi:
+            raise ValueError("max must be larger than min in range parameter.")
+        if not (np.isfinite(lo) and np.isfinite(hi)):
+            raise ValueError(f"supplied range of [{lo}, {hi}] is not finite")
+    elif x.size == 0:
+        lo, hi = 0, 1
+    else:
+        lo, hi = reductions.min(x).get()[()], reductions.max(x).get()[()]
+        if not (np.isfinite(lo) and np.isfinite(hi)):
+            raise ValueError(f"autodetected range of [{lo}, {hi}] is not finite")
+    if lo == hi:
+        lo, hi = lo - 0.5, hi + 0.5
+    return lo, hi
+
+
+def _hist_edges(x, bins, range):
+    """Host bin edges of a 1-D histogram (a few values, computed as NumPy's
+    _get_bin_edges does for integer and array bins)."""
+    if isinstance(bins, str):
+        raise NotImplementedError("histogram bin estimators (bins=str) are not supported")
+    if np.ndim(bins) == 0:
+        n = int(bins)
+        if n < 1:
+            raise ValueError("`bins` must be positive, when an integer")
+        lo, hi = _outer_edges(x, range)
+        bin_type = np.result_type(lo, hi, x.dtype)
+        if np.issubdtype(bin_type, np.integer):
+            bin_type = np.result_type(bin_type, float)
+        return np.linspace(lo, hi, n + 1, endpoint=True, dtype=bin_type)
+    edges = np.asarray(bins.get() if isinstance(bins, ndarray) else bins)
+    if edges.ndim != 1:
+        raise ValueError("`bins` must be 1d, when an array")
+    if np.any(edges[:-1] > edges[1:]):
+        raise ValueError("`bins` must increase monotonically, when an array")
+    return edges
+
+
+def histogram_bin_edges(a, bins=10, range=None, weights=None):
+    return _asarray(_hist_edges(_asarray(a).ravel(), bins, range))
+
+
 def histogram(a, bins=10, range=None, density=None, weights=None):
     """Counts per bin (right-open bins, the last one closed) from the sorted
     values and binary searches of the edges; edges as NumPy computes them."""
@@ -344,30 +392,7 @@ def histogram(a, bins=10, range=None, density=None, weights=None):
     from .indexing import take
     from . import reductions
     x = _asarray(a).ravel()
-    if isinstance(bins, (int, np.integer)):
-        if range is None:
-            if x.size:
-                # the data's own scalars, as NumPy takes them: for float32
-                # data the edges are then computed in float32
-                lo, hi = reductions.min(x).get()[()], reductions.max(x).get()[()]
-            else:
-                lo, hi = 0, 1
-        else:
-            lo, hi = range
-        if lo > hi:
-            raise ValueError("max must be larger than min in range parameter.")
-        if not (np.isfinite(lo) and np.isfinite(hi)):
-            raise ValueError(f"autodetected range of [{lo}, {hi}] is not finite")
-        if lo == hi:
-            lo, hi = lo - 0.5, hi + 0.5
-        bin_type = np.result_type(lo, hi, x.dtype)
-        if np.issubdtype(bin_type, np.integer):
-            bin_type = np.result_type(bin_type, float)
-        edges = np.linspace(lo, hi, int(bins) + 1, endpoint=True, dtype=bin_type)
-    else:
-        edges = np.asarray(bins.get() if isinstance(bins, ndarray) else bins)
-        if np.any(edges[:-1] > edges[1:]):
-            raise ValueError("`bins` must increase monotonically, when an array")
+    edges = _hist_edges(x, bins, range)
     nb = edges.size - 1
     ge = _asarray(edges)
     if weights is None:

@@ -322,6 +322,52 @@ int mmp_scatter(int word, void *dst, int64_t dst_bytes, const int64_t *offsets, 
 int mmp_nonzero(int64_t n, const int64_t *incl, int64_t count, int64_t *out);
 
 /* ======================================================================== */
+/* Dense factorizations: replace the reference's NumPy / LAPACK calls in    */
+/* linalg.py (solve, inv, det, slogdet :37-61, 149-159; cholesky :83-88;    */
+/* qr :97-105; eigh, eigvalsh :63-69, 122-127; svd, svdvals, pinv,          */
+/* matrix_rank, cond, lstsq :71-81, 129-183, 269-274).  Batches of          */
+/* contiguous row-major matrices, dtype MMP_F32 or MMP_F64, one workgroup   */
+/* per matrix, batch <= 2^31 - 1.                                           */
+/* ======================================================================== */
+
+/* In-place LU with partial pivoting of `batch` n x n matrices (n <= 32768):
+ * unit-lower L below the diagonal, U on and above it; piv[b*n + k] = the
+ * row swapped with row k at step k (0-based); info[b] = 1-based index of
+ * the first exactly-zero pivot, 0 if none. */
+int mmp_lu(int dtype, void *a, int64_t batch, int64_t n, int32_t *piv, int32_t *info);
+
+/* Solves A X = B in place of b (n x nrhs per matrix) from mmp_lu's output. */
+int mmp_lu_solve(int dtype, const void *lu, const int32_t *piv, void *b, int64_t batch, int64_t n,
+                 int64_t nrhs);
+
+/* In-place lower Cholesky factor (upper triangle zeroed) of symmetric
+ * positive-definite matrices read from their lower triangle; info[b] =
+ * 1-based index of the first non-positive pivot, 0 if none. */
+int mmp_cholesky(int dtype, void *a, int64_t batch, int64_t n, int32_t *info);
+
+/* Householder QR of m x n matrices in place: R on and above the diagonal,
+ * reflector vectors (implicit leading 1) below it, tau[b*min(m,n) + k]
+ * (LAPACK geqrf's convention). */
+int mmp_qr(int dtype, void *a, void *tau, int64_t batch, int64_t m, int64_t n);
+
+/* The first qcols (min(m,n) <= qcols <= m) columns of Q = H_0 ... H_{k-1}
+ * from mmp_qr's output, into q (m x qcols per matrix). */
+int mmp_qr_q(int dtype, const void *a, const void *tau, int64_t batch, int64_t m, int64_t n,
+             int64_t qcols, void *q);
+
+/* Cyclic Jacobi eigen-decomposition of symmetric n x n matrices (n <= 2048):
+ * a is overwritten with a nearly diagonal matrix holding the eigenvalues
+ * (unsorted) on its diagonal, v (n x n) receives the eigenvectors as
+ * columns; sweeps[b] = Jacobi sweeps used (at most 60). */
+int mmp_eigh(int dtype, void *a, void *v, int64_t batch, int64_t n, int32_t *sweeps);
+
+/* One-sided Jacobi: rotates the rows of w (rows x len, rows <= len,
+ * rows <= 8192) until they are mutually orthogonal, applying the same
+ * rotations to vt (rows x rows, set to I first); the row norms of w are
+ * then the singular values.  sweeps[b] = sweeps used (at most 60). */
+int mmp_svd(int dtype, void *w, void *vt, int64_t batch, int64_t rows, int64_t len, int32_t *sweeps);
+
+/* ======================================================================== */
 /* Matmul: replaces ndarray.__matmul__ + matmul_shader (ndarray.py:1398-1450,*/
 /* _kernels.py:740-759); batched form replaces linalg_top.matmul's CPU path */
 /* (linalg_top.py:105-106)                                                  */

@@ -97,6 +97,13 @@ _SIGNATURES = {
     "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp],
     "mmp_scatter": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64],
     "mmp_nonzero": [_c_i64, _c_vp, _c_i64, _c_vp],
+    "mmp_lu": [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_lu_solve": [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64],
+    "mmp_cholesky": [_c_int, _c_vp, _c_i64, _c_i64, _c_vp],
+    "mmp_qr": [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64],
+    "mmp_qr_q": [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp],
+    "mmp_eigh": [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp],
+    "mmp_svd": [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp],
     "mmp_matmul": [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
                    _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64],
     "mmp_rtc_compile": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_c_vp)],
@@ -348,6 +355,27 @@ class HipBackend:
 
     def nonzero(self, n: int, incl: int, count: int, out: int) -> None:
         _check(self._lib.mmp_nonzero(n, incl, count, out), "mmp_nonzero")
+
+    def lu(self, dcode, a, batch, n, piv, info) -> None:
+        _check(self._lib.mmp_lu(dcode, a, batch, n, piv, info), "mmp_lu")
+
+    def lu_solve(self, dcode, lu, piv, b, batch, n, nrhs) -> None:
+        _check(self._lib.mmp_lu_solve(dcode, lu, piv, b, batch, n, nrhs), "mmp_lu_solve")
+
+    def cholesky(self, dcode, a, batch, n, info) -> None:
+        _check(self._lib.mmp_cholesky(dcode, a, batch, n, info), "mmp_cholesky")
+
+    def qr(self, dcode, a, tau, batch, m, n) -> None:
+        _check(self._lib.mmp_qr(dcode, a, tau, batch, m, n), "mmp_qr")
+
+    def qr_q(self, dcode, a, tau, batch, m, n, qcols, q) -> None:
+        _check(self._lib.mmp_qr_q(dcode, a, tau, batch, m, n, qcols, q), "mmp_qr_q")
+
+    def eigh(self, dcode, a, v, batch, n, sweeps) -> None:
+        _check(self._lib.mmp_eigh(dcode, a, v, batch, n, sweeps), "mmp_eigh")
+
+    def svd(self, dcode, w, vt, batch, rows, length, sweeps) -> None:
+        _check(self._lib.mmp_svd(dcode, w, vt, batch, rows, length, sweeps), "mmp_svd")
 
     def matmul(self, dcode: int, batch: int, M: int, N: int, K: int,
                A: int, lda: int, sA: int, B: int, ldb: int, sB: int,

@@ -1,0 +1,531 @@
+// linalg.hip -- batched dense factorizations for cp.linalg, one workgroup
+// per matrix of a contiguous row-major batch, float32 and float64.
+//
+// Replaces the reference's NumPy/LAPACK host calls in linalg.py
+// (solve / inv / det / slogdet :37-61, 149-159; cholesky :83-88; qr
+// :97-105; eigh / eigvalsh :63-69, 122-127; svd / svdvals / pinv /
+// matrix_rank / cond / lstsq :71-81, 129-183, 269-274).
+//
+//  * mmp_lu: right-looking LU with partial pivoting (the first row of
+//    largest |a| in the column, as LAPACK's getrf picks), unit-lower L and
+//    U packed in place, pivots as LAPACK's 0-based row swaps, info = first
+//    exactly-zero pivot (1-based) or 0.
+//  * mmp_lu_solve: row swaps, forward then backward substitution for nrhs
+//    right-hand sides (threads over rows x rhs per elimination step).
+//  * mmp_cholesky: right-looking lower Cholesky; info = first non-positive
+//    pivot (1-based); the strict upper triangle is zeroed.
+//  * mmp_qr / mmp_qr_q: Householder QR with LAPACK's reflector convention
+//    (beta = -sign(alpha) * ||x||, tau = (beta - alpha) / beta, v(0) = 1),
+//    R in the upper triangle, reflectors below it, then Q accumulated
+//    backwards into the first qcols columns of I (one wavefront per column).
+//  * mmp_eigh: cyclic two-sided Jacobi for symmetric matrices, disjoint
+//    rotation pairs per round (round-robin ordering), rows then columns
+//    updated per round, eigenvectors accumulated in V.
+//  * mmp_svd: one-sided (Hestenes) Jacobi orthogonalising the rows of W
+//    (rows <= len), one wavefront per row pair, row rotations mirrored in
+//    VT; the row norms are the singular values.
+// Every loop is bounded (the Jacobi sweeps by kMaxSweeps), so each
+// workgroup exits.
+#include <limits>
+
+#include "mmp_ops.h"
+#include "mmp_internal.h"
+
+namespace {
+
+constexpr int kT = 256;           // LU / Cholesky / QR workgroup
+constexpr int kJ = 1024;          // Jacobi workgroup (16 wavefronts)
+constexpr int kMaxSweeps = 60;
+constexpr int kMaxEighN = 2048;   // rotation table in LDS: kMaxEighN / 2 pairs
+constexpr int kMaxSvdRows = 8192;
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over the workgroup, the same value in every thread (fixed order).
+template <int NT, typename T>
+__device__ T block_sum(T v, T *lds) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  T r = T(0);
+  for (int i = 0; i < NT / 64; ++i) r += lds[i];
+  return r;
+}
+
+// Round-robin pairing of N (even) indices: N - 1 rounds, N / 2 disjoint
+// pairs per round, every pair met once per sweep.
+__device__ __forceinline__ void pair_of(int r, int pi, int N, int &p, int &q) {
+  if (pi == 0) {
+    p = N - 1;
+    q = r;
+  } else {
+    p = (r + pi) % (N - 1);
+    q = (r - pi + (N - 1)) % (N - 1);
+  }
+}
+
+// ------------------------------------------------------------------- LU
+template <typename T>
+__global__ __launch_bounds__(kT) void k_getrf(T *__restrict__ a, int n, int *__restrict__ piv,
+                                              int *__restrict__ info) {
+  T *A = a + (long long)blockIdx.x * n * n;
+  int *P = piv + (long long)blockIdx.x * n;
+  __shared__ T sval[kT / 64];
+  __shared__ int sidx[kT / 64];
+  const int tid = threadIdx.x;
+  int first_zero = 0;
+  for (int k = 0; k < n; ++k) {
+    T best = T(-1);
+    int bi = n;
+    for (int i = k + tid; i < n; i += kT) {
+      const T v = fabs(A[(long long)i * n + k]);
+      if (v > best) {
+        best = v;
+        bi = i;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const T ov = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+    __syncthreads();
+    if ((tid & 63) == 0) {
+      sval[tid >> 6] = best;
+      sidx[tid >> 6] = bi;
+    }
+    __syncthreads();
+    best = sval[0];
+    bi = sidx[0];
+    for (int w = 1; w < kT / 64; ++w)
+      if (sval[w] > best || (sval[w] == best && sidx[w] < bi)) {
+        best = sval[w];
+        bi = sidx[w];
+      }
+    const int p = bi < n ? bi : k;  // an all-NaN column keeps its row
+    if (tid == 0) P[k] = p;
+    if (p != k)
+      for (int j = tid; j < n; j += kT) {
+        const T t = A[(long long)k * n + j];
+        A[(long long)k * n + j] = A[(long long)p * n + j];
+        A[(long long)p * n + j] = t;
+      }
+    __syncthreads();
+    const T d = A[(long long)k * n + k];
+    if (d == T(0)) {  // the whole column is zero: nothing to eliminate
+      if (!first_zero) first_zero = k + 1;
+      continue;
+    }
+    for (int i = k + 1 + tid; i < n; i += kT) A[(long long)i * n + k] /= d;
+    __syncthreads();
+    const int m = n - k - 1;
+    const long long mm = (long long)m * m;
+    for (long long t = tid; t < mm; t += kT) {
+      const int i = k + 1 + (int)(t / m), j = k + 1 + (int)(t % m);
+      A[(long long)i * n + j] -= A[(long long)i * n + k] * A[(long long)k * n + j];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) info[blockIdx.x] = first_zero;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_getrs(const T *__restrict__ lu, const int *__restrict__ piv,
+                                              T *__restrict__ b, int n, int nrhs) {
+  const T *A = lu + (long long)blockIdx.x * n * n;
+  const int *P = piv + (long long)blockIdx.x * n;
+  T *B = b + (long long)blockIdx.x * n * nrhs;
+  const int tid = threadIdx.x;
+  for (int c = tid; c < nrhs; c += kT)
+    for (int k = 0; k < n; ++k) {
+      const int p = P[k];
+      if (p != k) {
+        const T t = B[(long long)k * nrhs + c];
+        B[(long long)k * nrhs + c] = B[(long long)p * nrhs + c];
+        B[(long long)p * nrhs + c] = t;
+      }
+    }
+  __syncthreads();
+  for (int k = 0; k < n - 1; ++k) {
+    const long long tot = (long long)(n - k - 1) * nrhs;
+    for (long long t = tid; t < tot; t += kT) {
+      const int i = k + 1 + (int)(t / nrhs), c = (int)(t % nrhs);
+      B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
+    }
+    __syncthreads();
+  }
+  for (int k = n - 1; k >= 0; --k) {
+    for (int c = tid; c < nrhs; c += kT) B[(long long)k * nrhs + c] /= A[(long long)k * n + k];
+    __syncthreads();
+    const long long tot = (long long)k * nrhs;
+    for (long long t = tid; t < tot; t += kT) {
+      const int i = (int)(t / nrhs), c = (int)(t % nrhs);
+      B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
+    }
+    __syncthreads();
+  }
+}
+
+// -------------------------------------------------------------- Cholesky
+template <typename T>
+__global__ __launch_bounds__(kT) void k_potrf(T *__restrict__ a, int n, int *__restrict__ info) {
+  T *A = a + (long long)blockIdx.x * n * n;
+  const int tid = threadIdx.x;
+  int bad = 0;
+  for (int k = 0; k < n; ++k) {
+    const T d = A[(long long)k * n + k];
+    if (!(d > T(0))) {  // same value in every thread: a uniform exit
+      bad = k + 1;
+      break;
+    }
+    const T l = sqrt(d);
+    __syncthreads();
+    if (tid == 0) A[(long long)k * n + k] = l;
+    for (int i = k + 1 + tid; i < n; i += kT) A[(long long)i * n + k] /= l;
+    __syncthreads();
+    const int m = n - k - 1;
+    const long long mm = (long long)m * m;
+    for (long long t = tid; t < mm; t += kT) {
+      const int i = k + 1 + (int)(t / m), j = k + 1 + (int)(t % m);
+      if (j <= i) A[(long long)i * n + j] -= A[(long long)i * n + k] * A[(long long)j * n + k];
+    }
+    __syncthreads();
+  }
+  const long long nn = (long long)n * n;
+  for (long long t = tid; t < nn; t += kT)
+    if ((int)(t % n) > (int)(t / n)) A[t] = T(0);
+  if (tid == 0) info[blockIdx.x] = bad;
+}
+
+// -------------------------------------------------------------------- QR
+template <typename T>
+__global__ __launch_bounds__(kT) void k_geqrf(T *__restrict__ a, int m, int n, T *__restrict__ tau) {
+  const int kmin = m < n ? m : n;
+  T *A = a + (long long)blockIdx.x * m * n;
+  T *TAU = tau + (long long)blockIdx.x * kmin;
+  __shared__ T red[kT / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int k = 0; k < kmin; ++k) {
+    T part = T(0);
+    for (int i = k + 1 + tid; i < m; i += kT) {
+      const T v = A[(long long)i * n + k];
+      part += v * v;
+    }
+    const T xn2 = block_sum<kT>(part, red);
+    const T alpha = A[(long long)k * n + k];
+    T t = T(0);
+    if (xn2 != T(0)) {
+      const T beta = -copysign(sqrt(alpha * alpha + xn2), alpha);
+      t = (beta - alpha) / beta;
+      const T sc = T(1) / (alpha - beta);
+      __syncthreads();  // alpha read everywhere before A[k][k] changes
+      for (int i = k + 1 + tid; i < m; i += kT) A[(long long)i * n + k] *= sc;
+      if (tid == 0) A[(long long)k * n + k] = beta;
+    }
+    if (tid == 0) TAU[k] = t;
+    __syncthreads();
+    if (t != T(0)) {
+      for (int j = k + 1 + wave; j < n; j += kT / 64) {
+        const T akj = A[(long long)k * n + j];
+        T w = T(0);
+        for (int i = k + 1 + lane; i < m; i += 64) w += A[(long long)i * n + k] * A[(long long)i * n + j];
+        w = wave_sum(w) + akj;
+        if (lane == 0) A[(long long)k * n + j] = akj - t * w;
+        for (int i = k + 1 + lane; i < m; i += 64) A[(long long)i * n + j] -= t * A[(long long)i * n + k] * w;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_orgqr(const T *__restrict__ a, const T *__restrict__ tau, int m,
+                                              int n, int qc, T *__restrict__ q) {
+  const int kmin = m < n ? m : n;
+  const T *A = a + (long long)blockIdx.x * m * n;
+  const T *TAU = tau + (long long)blockIdx.x * kmin;
+  T *Q = q + (long long)blockIdx.x * m * qc;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long long tot = (long long)m * qc;
+  for (long long t = tid; t < tot; t += kT) Q[t] = (t / qc == t % qc) ? T(1) : T(0);
+  __syncthreads();
+  for (int k = kmin - 1; k >= 0; --k) {
+    const T t = TAU[k];
+    if (t == T(0)) continue;
+    for (int j = k + wave; j < qc; j += kT / 64) {
+      const T qkj = Q[(long long)k * qc + j];
+      T w = T(0);
+      for (int i = k + 1 + lane; i < m; i += 64) w += A[(long long)i * n + k] * Q[(long long)i * qc + j];
+      w = wave_sum(w) + qkj;
+      if (lane == 0) Q[(long long)k * qc + j] = qkj - t * w;
+      for (int i = k + 1 + lane; i < m; i += 64) Q[(long long)i * qc + j] -= t * A[(long long)i * n + k] * w;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------ symmetric Jacobi
+template <typename T>
+__global__ __launch_bounds__(kJ) void k_syevj(T *__restrict__ a, T *__restrict__ v, int n,
+                                              int *__restrict__ sweeps_out) {
+  T *A = a + (long long)blockIdx.x * n * n;
+  T *V = v + (long long)blockIdx.x * n * n;
+  __shared__ T cs[kMaxEighN];  // (c, s) of each pair of the round
+  __shared__ int s_rot;
+  const int tid = threadIdx.x;
+  const int N = n + (n & 1);
+  const int npair = N / 2;
+  const T eps = std::numeric_limits<T>::epsilon();
+  const long long nn = (long long)n * n;
+  for (long long t = tid; t < nn; t += kJ) V[t] = (t / n == t % n) ? T(1) : T(0);
+  int sweep = 0;
+  for (; sweep < kMaxSweeps; ++sweep) {
+    if (tid == 0) s_rot = 0;
+    __syncthreads();
+    for (int r = 0; r < N - 1; ++r) {
+      for (int pi = tid; pi < npair; pi += kJ) {
+        int p, q;
+        pair_of(r, pi, N, p, q);
+        T c = T(1), s = T(0);
+        if (p < n && q < n) {
+          const T app = A[(long long)p * n + p], aqq = A[(long long)q * n + q];
+          const T apq = A[(long long)p * n + q];
+          if (apq != T(0) && fabs(apq) > eps * sqrt(fabs(app * aqq))) {
+            const T th = (aqq - app) / (T(2) * apq);
+            const T tt = (th >= T(0) ? T(1) : T(-1)) / (fabs(th) + sqrt(T(1) + th * th));
+            c = T(1) / sqrt(T(1) + tt * tt);
+            s = tt * c;
+            if (s != T(0)) s_rot = 1;
+          }
+        }
+        cs[2 * pi] = c;
+        cs[2 * pi + 1] = s;
+      }
+      __syncthreads();
+      const long long work = (long long)npair * n;
+      for (long long t = tid; t < work; t += kJ) {
+        const int pi = (int)(t / n), j = (int)(t % n);
+        const T s = cs[2 * pi + 1];
+        if (s == T(0)) continue;
+        int p, q;
+        pair_of(r, pi, N, p, q);
+        const T c = cs[2 * pi];
+        const T x = A[(long long)p * n + j], y = A[(long long)q * n + j];
+        A[(long long)p * n + j] = c * x - s * y;
+        A[(long long)q * n + j] = s * x + c * y;
+      }
+      __syncthreads();
+      for (long long t = tid; t < work; t += kJ) {
+        const int pi = (int)(t / n), i = (int)(t % n);
+        const T s = cs[2 * pi + 1];
+        if (s == T(0)) continue;
+        int p, q;
+        pair_of(r, pi, N, p, q);
+        const T c = cs[2 * pi];
+        const T x = A[(long long)i * n + p], y = A[(long long)i * n + q];
+        A[(long long)i * n + p] = c * x - s * y;
+        A[(long long)i * n + q] = s * x + c * y;
+        const T vx = V[(long long)i * n + p], vy = V[(long long)i * n + q];
+        V[(long long)i * n + p] = c * vx - s * vy;
+        V[(long long)i * n + q] = s * vx + c * vy;
+      }
+      __syncthreads();
+    }
+    const int rotated = s_rot;
+    __syncthreads();
+    if (!rotated) break;
+  }
+  if (tid == 0) sweeps_out[blockIdx.x] = sweep;
+}
+
+// ------------------------------------------------------ one-sided Jacobi
+template <typename T>
+__global__ __launch_bounds__(kJ) void k_gesvj(T *__restrict__ w, T *__restrict__ vt, int r, int L,
+                                              int *__restrict__ sweeps_out) {
+  T *W = w + (long long)blockIdx.x * r * L;
+  T *VT = vt + (long long)blockIdx.x * r * r;
+  __shared__ int s_rot;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = r + (r & 1);
+  const int npair = N / 2;
+  const T eps = std::numeric_limits<T>::epsilon();
+  const long long rr = (long long)r * r;
+  for (long long t = tid; t < rr; t += kJ) VT[t] = (t / r == t % r) ? T(1) : T(0);
+  int sweep = 0;
+  for (; sweep < kMaxSweeps; ++sweep) {
+    if (tid == 0) s_rot = 0;
+    __syncthreads();
+    for (int rd = 0; rd < N - 1; ++rd) {
+      for (int pi = wave; pi < npair; pi += kJ / 64) {
+        int p, q;
+        pair_of(rd, pi, N, p, q);
+        if (p >= r || q >= r) continue;
+        T al = T(0), be = T(0), ga = T(0);
+        for (int j = lane; j < L; j += 64) {
+          const T x = W[(long long)p * L + j], y = W[(long long)q * L + j];
+          al += x * x;
+          be += y * y;
+          ga += x * y;
+        }
+        al = wave_sum(al);
+        be = wave_sum(be);
+        ga = wave_sum(ga);
+        if (ga != T(0) && fabs(ga) > eps * sqrt(al * be)) {
+          const T ze = (be - al) / (T(2) * ga);
+          const T tt = (ze >= T(0) ? T(1) : T(-1)) / (fabs(ze) + sqrt(T(1) + ze * ze));
+          const T c = T(1) / sqrt(T(1) + tt * tt), s = c * tt;
+          if (s != T(0)) {
+            for (int j = lane; j < L; j += 64) {
+              const T x = W[(long long)p * L + j], y = W[(long long)q * L + j];
+              W[(long long)p * L + j] = c * x - s * y;
+              W[(long long)q * L + j] = s * x + c * y;
+            }
+            for (int j = lane; j < r; j += 64) {
+              const T x = VT[(long long)p * r + j], y = VT[(long long)q * r + j];
+              VT[(long long)p * r + j] = c * x - s * y;
+              VT[(long long)q * r + j] = s * x + c * y;
+            }
+            if (lane == 0) s_rot = 1;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    const int rotated = s_rot;
+    __syncthreads();
+    if (!rotated) break;
+  }
+  if (tid == 0) sweeps_out[blockIdx.x] = sweep;
+}
+
+int check_common(const char *what, int dtype, long long batch) {
+  if (dtype != MMP_F32 && dtype != MMP_F64)
+    return mmpi::fail(MMP_E_UNSUPPORTED, "%s: dtype %d (float32 / float64 only)", what, dtype);
+  if (batch < 0 || batch > 0x7fffffffll) return mmpi::fail(MMP_E_ARG, "%s: batch %lld", what, batch);
+  return MMP_OK;
+}
+
+}  // namespace
+
+extern "C" int mmp_lu(int dtype, void *a, int64_t batch, int64_t n, int32_t *piv, int32_t *info) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_lu", dtype, batch)) return st;
+  if (n < 0 || n > 32768) return mmpi::fail(MMP_E_ARG, "mmp_lu: n %lld", (long long)n);
+  if (batch == 0 || n == 0) return MMP_OK;
+  if (!a || !piv || !info) return mmpi::fail(MMP_E_ARG, "mmp_lu: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_getrf<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (float *)a,
+                       (int)n, (int *)piv, (int *)info);
+  else
+    hipLaunchKernelGGL(k_getrf<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (double *)a,
+                       (int)n, (int *)piv, (int *)info);
+  return mmpi::check_launch("mmp_lu");
+}
+
+extern "C" int mmp_lu_solve(int dtype, const void *lu, const int32_t *piv, void *b, int64_t batch,
+                            int64_t n, int64_t nrhs) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_lu_solve", dtype, batch)) return st;
+  if (n < 0 || n > 32768 || nrhs < 0 || nrhs > 0x7fffffffll)
+    return mmpi::fail(MMP_E_ARG, "mmp_lu_solve: n %lld nrhs %lld", (long long)n, (long long)nrhs);
+  if (batch == 0 || n == 0 || nrhs == 0) return MMP_OK;
+  if (!lu || !piv || !b) return mmpi::fail(MMP_E_ARG, "mmp_lu_solve: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_getrs<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+                       (const float *)lu, (const int *)piv, (float *)b, (int)n, (int)nrhs);
+  else
+    hipLaunchKernelGGL(k_getrs<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+                       (const double *)lu, (const int *)piv, (double *)b, (int)n, (int)nrhs);
+  return mmpi::check_launch("mmp_lu_solve");
+}
+
+extern "C" int mmp_cholesky(int dtype, void *a, int64_t batch, int64_t n, int32_t *info) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_cholesky", dtype, batch)) return st;
+  if (n < 0 || n > 32768) return mmpi::fail(MMP_E_ARG, "mmp_cholesky: n %lld", (long long)n);
+  if (batch == 0 || n == 0) return MMP_OK;
+  if (!a || !info) return mmpi::fail(MMP_E_ARG, "mmp_cholesky: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_potrf<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (float *)a,
+                       (int)n, (int *)info);
+  else
+    hipLaunchKernelGGL(k_potrf<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (double *)a,
+                       (int)n, (int *)info);
+  return mmpi::check_launch("mmp_cholesky");
+}
+
+extern "C" int mmp_qr(int dtype, void *a, void *tau, int64_t batch, int64_t m, int64_t n) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_qr", dtype, batch)) return st;
+  if (m < 0 || n < 0 || m > 0x7fffffffll || n > 0x7fffffffll)
+    return mmpi::fail(MMP_E_ARG, "mmp_qr: shape %lld x %lld", (long long)m, (long long)n);
+  if (batch == 0 || m == 0 || n == 0) return MMP_OK;
+  if (!a || !tau) return mmpi::fail(MMP_E_ARG, "mmp_qr: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_geqrf<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (float *)a,
+                       (int)m, (int)n, (float *)tau);
+  else
+    hipLaunchKernelGGL(k_geqrf<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (double *)a,
+                       (int)m, (int)n, (double *)tau);
+  return mmpi::check_launch("mmp_qr");
+}
+
+extern "C" int mmp_qr_q(int dtype, const void *a, const void *tau, int64_t batch, int64_t m, int64_t n,
+                        int64_t qcols, void *q) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_qr_q", dtype, batch)) return st;
+  const long long kmin = m < n ? m : n;
+  if (m < 0 || n < 0 || m > 0x7fffffffll || n > 0x7fffffffll || qcols < kmin || qcols > m)
+    return mmpi::fail(MMP_E_ARG, "mmp_qr_q: shape %lld x %lld, qcols %lld", (long long)m,
+                      (long long)n, (long long)qcols);
+  if (batch == 0 || m == 0 || qcols == 0) return MMP_OK;
+  if (!a || !tau || !q) return mmpi::fail(MMP_E_ARG, "mmp_qr_q: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_orgqr<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+                       (const float *)a, (const float *)tau, (int)m, (int)n, (int)qcols, (float *)q);
+  else
+    hipLaunchKernelGGL(k_orgqr<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+                       (const double *)a, (const double *)tau, (int)m, (int)n, (int)qcols, (double *)q);
+  return mmpi::check_launch("mmp_qr_q");
+}
+
+extern "C" int mmp_eigh(int dtype, void *a, void *v, int64_t batch, int64_t n, int32_t *sweeps) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_eigh", dtype, batch)) return st;
+  if (n < 0 || n > kMaxEighN) return mmpi::fail(MMP_E_ARG, "mmp_eigh: n %lld (at most %d)", (long long)n, kMaxEighN);
+  if (batch == 0 || n == 0) return MMP_OK;
+  if (!a || !v || !sweeps) return mmpi::fail(MMP_E_ARG, "mmp_eigh: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_syevj<float>, dim3((unsigned)batch), dim3(kJ), 0, mmpi::stream(), (float *)a,
+                       (float *)v, (int)n, (int *)sweeps);
+  else
+    hipLaunchKernelGGL(k_syevj<double>, dim3((unsigned)batch), dim3(kJ), 0, mmpi::stream(), (double *)a,
+                       (double *)v, (int)n, (int *)sweeps);
+  return mmpi::check_launch("mmp_eigh");
+}
+
+extern "C" int mmp_svd(int dtype, void *w, void *vt, int64_t batch, int64_t rows, int64_t len,
+                       int32_t *sweeps) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (int st = check_common("mmp_svd", dtype, batch)) return st;
+  if (rows < 0 || rows > kMaxSvdRows || len < rows || len > 0x7fffffffll)
+    return mmpi::fail(MMP_E_ARG, "mmp_svd: rows %lld len %lld (rows <= len, rows <= %d)", (long long)rows,
+                      (long long)len, kMaxSvdRows);
+  if (batch == 0 || rows == 0) return MMP_OK;
+  if (!w || !vt || !sweeps) return mmpi::fail(MMP_E_ARG, "mmp_svd: null pointer");
+  if (dtype == MMP_F32)
+    hipLaunchKernelGGL(k_gesvj<float>, dim3((unsigned)batch), dim3(kJ), 0, mmpi::stream(), (float *)w,
+                       (float *)vt, (int)rows, (int)len, (int *)sweeps);
+  else
+    hipLaunchKernelGGL(k_gesvj<double>, dim3((unsigned)batch), dim3(kJ), 0, mmpi::stream(), (double *)w,
+                       (double *)vt, (int)rows, (int)len, (int *)sweeps);
+  return mmpi::check_launch("mmp_svd");
+}

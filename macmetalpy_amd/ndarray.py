@@ -710,6 +710,218 @@ class ndarray:
         import macmetalpy_amd
         return macmetalpy_amd
 
+    def __array_function__(self, func, types, args, kwargs):
+        """NumPy functions called with device arrays run this library's
+        function of the same name (``numpy.linalg`` ones the ``linalg``
+        namespace's), as the reference dispatches (ndarray.py:2722-2729);
+        a function without a device counterpart returns NotImplemented, so
+        NumPy raises TypeError instead of computing on the host."""
+        import macmetalpy_amd as mod
+        name = getattr(func, "__name__", "")
+        where = getattr(func, "__module__", "") or ""
+        if where.startswith("numpy.linalg"):
+            target = getattr(mod.linalg, name, None)
+        elif where.startswith("numpy.fft"):
+            target = None
+        else:
+            target = getattr(mod, name, None)
+        if target is None or target is func or not callable(target):
+            return NotImplemented
+        return target(*args, **kwargs)
+
+    @classmethod
+    def __class_getitem__(cls, item):
+        return cls
+
+    def __contains__(self, value):
+        return bool((self == value).any())
+
+    def __copy__(self):
+        return self.copy()
+
+    def __deepcopy__(self, memo):
+        return self.copy()
+
+    def __delitem__(self, key):
+        raise ValueError("cannot delete array elements")
+
+    def __imatmul__(self, o):
+        from .linalg_top import matmul
+        r = matmul(self, o)
+        if tuple(r.shape) != self._shape:
+            raise ValueError("matmul: in-place result would change the array's shape")
+        return self._inplace(r)
+
+    def __rdivmod__(self, o):
+        return o // self, o % self
+
+    def __dlpack__(self, *, stream=None, max_version=None, dl_device=None, copy=None):
+        """A host copy's DLPack capsule (as the reference exports)."""
+        return self.get().__dlpack__()
+
+    def __dlpack_device__(self):
+        return (1, 0)
+
+    # ---------------------------------------------- more NumPy methods
+    def view(self, dtype=None, type=None):
+        """Same device bytes read as another dtype; a different item size
+        needs a contiguous last axis whose byte length it divides."""
+        import builtins
+        self._materialize_if_lazy()
+        if self._np_data is not None:
+            self._ensure_gpu()
+        if dtype is None or (isinstance(dtype, builtins.type) and issubclass(dtype, ndarray)):
+            return ndarray(self._buffer, self._shape, self._dtype, self._strides, self._offset,
+                           self._base if self._base is not None else self)
+        new = np.dtype(dtype)
+        from ._dtypes import dtype_code
+        dtype_code(new)
+        old = self._dtype.itemsize
+        base = self._base if self._base is not None else self
+        if new.itemsize == old:
+            return ndarray(self._buffer, self._shape, new, self._strides, self._offset, base)
+        if not self._shape or self._strides[-1] != 1:
+            raise ValueError("To change to a dtype of a different size, the last axis must be "
+                             "contiguous")
+        nbytes_last = self._shape[-1] * old
+        if nbytes_last % new.itemsize:
+            raise ValueError("When changing to a smaller dtype, its size must be a divisor of the "
+                             "size of original dtype" if new.itemsize < old else
+                             "When changing to a larger dtype, its size must be a divisor of the "
+                             "total size in bytes of the last axis of the array.")
+        if (self._offset * old) % new.itemsize or any((st * old) % new.itemsize
+                                                      for st in self._strides[:-1]):
+            raise ValueError("the array's offset or strides are not a multiple of the new "
+                             "dtype's size")
+        shape = self._shape[:-1] + (nbytes_last // new.itemsize,)
+        strides = tuple(st * old // new.itemsize for st in self._strides[:-1]) + (1,)
+        return ndarray(self._buffer, shape, new, strides, self._offset * old // new.itemsize, base)
+
+    def byteswap(self, inplace=False):
+        """Byte order reversed per element with shifts on the unsigned view."""
+        size = self._dtype.itemsize
+        if size == 1 or self._dtype == np.bool_:
+            r = self.copy()
+        else:
+            ut = {2: np.uint16, 4: np.uint32, 8: np.uint64}[size]
+            u = self._ensure_contiguous().view(ut)
+            acc = None
+            for k in range(size):
+                byte = (u >> ut(8 * k)) & ut(0xFF)
+                part = byte << ut(8 * (size - 1 - k))
+                acc = part if acc is None else (acc | part)
+            r = acc.astype(ut).view(self._dtype)
+        if inplace:
+            self[...] = r
+            return self
+        return r
+
+    def partition(self, kth, axis=-1, kind="introselect", order=None):
+        """In place; a full sort satisfies every kth."""
+        from .extras import partition
+        self[...] = partition(self, kth, axis=axis)
+
+    def argpartition(self, kth, axis=-1, kind="introselect", order=None):
+        from .extras import argpartition
+        return argpartition(self, kth, axis=axis)
+
+    def choose(self, choices, out=None, mode="raise"):
+        from .extras import choose
+        return choose(self, choices, out=out, mode=mode)
+
+    def conj(self):
+        return self.copy()
+
+    conjugate = conj
+
+    def diagonal(self, offset=0, axis1=0, axis2=1):
+        from .manipulation import diagonal
+        return diagonal(self, offset, axis1, axis2)
+
+    def trace(self, offset=0, axis1=0, axis2=1, dtype=None, out=None):
+        from .manipulation import trace
+        return trace(self, offset, axis1, axis2, dtype, out)
+
+    def ptp(self, axis=None, out=None, keepdims=False):
+        from .manipulation import ptp
+        return ptp(self, axis=axis, out=out, keepdims=keepdims)
+
+    def repeat(self, repeats, axis=None):
+        from .manipulation import repeat
+        return repeat(self, repeats, axis=axis)
+
+    def round(self, decimals=0, out=None):
+        from .extras import round as _round
+        return _round(self, decimals, out=out)
+
+    def resize(self, *new_shape, refcheck=True):
+        """In place, as NumPy's method: the flat data kept, zeros appended."""
+        if len(new_shape) == 1 and not isinstance(new_shape[0], (int, np.integer)):
+            new_shape = tuple(new_shape[0])
+        shp = tuple(int(x) for x in new_shape)
+        from .creation import zeros
+        n = _prod(shp)
+        out = zeros((n,), dtype=self._dtype)
+        k = min(n, self.size)
+        if k:
+            out[:k] = self.ravel()[:k]
+        out = out.reshape(shp)._ensure_contiguous()
+        self._buffer, self._np_data = out._buffer, None
+        self._shape, self._strides, self._offset, self._base = out._shape, out._strides, 0, None
+        self._fusion_node = None
+
+    def itemset(self, *args):
+        if not args:
+            raise ValueError("itemset must have at least one argument")
+        *idx, value = args
+        if not idx:
+            self.reshape(-1)[0:1] = value
+        elif len(idx) == 1 and isinstance(idx[0], (int, np.integer)):
+            flat = self.ravel()
+            flat[idx[0]] = value
+            if flat._buffer is not self._buffer:
+                self[...] = flat.reshape(self._shape)
+        else:
+            self[tuple(idx[0]) if len(idx) == 1 else tuple(idx)] = value
+
+    def setflags(self, write=None, align=None, uic=None):
+        """Device arrays stay writeable and aligned; the flags are accepted."""
+        return None
+
+    def to_device(self, device, /, *, stream=None):
+        return self
+
+    @property
+    def data(self):
+        """Device address of the first element (an integer), for callers
+        handing the buffer to their own kernels."""
+        self._ensure_gpu()
+        return self._ptr
+
+    def getfield(self, dtype, offset=0):
+        if offset != 0 or np.dtype(dtype).itemsize != self._dtype.itemsize:
+            raise NotImplementedError("getfield needs offset 0 and an equal item size")
+        return self.view(dtype).copy()
+
+    def setfield(self, val, dtype, offset=0):
+        if offset != 0 or np.dtype(dtype).itemsize != self._dtype.itemsize:
+            raise NotImplementedError("setfield needs offset 0 and an equal item size")
+        self.view(dtype)[...] = val
+
+    def tobytes(self, order="C"):
+        return self.get().tobytes(order)
+
+    tostring = tobytes
+
+    def tofile(self, fid, sep="", format="%s"):
+        self.get().tofile(fid, sep=sep, format=format)
+
+    def dump(self, file):
+        self.get().dump(file)
+
+    def dumps(self):
+        return self.get().dumps()
+
 
 def _scalar_key(key, ndim) -> bool:
     """Whether ``key`` is one integer per dimension (selects one element)."""

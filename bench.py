@@ -551,11 +551,99 @@ def run_only(cp, be, name, steps):
     print(json.dumps({"only": name, "steps": steps, "kernel_ms": round(ms, 4)}), flush=True)
 
 
+def bench_linalg(cp, be, reps=3):
+    """Dense factorizations (one workgroup per matrix): GFLOP/s counts the
+    textbook flops -- LU 2/3 n^3 plus 2 n^2 per right-hand side for solve,
+    Cholesky 1/3 n^3, Householder QR 2 m n^2 - 2/3 n^3; the Jacobi methods
+    (eigh, SVD) are timed per call.  Batched shapes fill the chip; a single
+    large matrix runs on one CU (a blocked multi-workgroup factorization is
+    the next step for it)."""
+    rng = np.random.default_rng(21)
+    LA = cp.linalg
+
+    def mat(shape, dt, spd=False):
+        a = rng.standard_normal(shape)
+        a = a + np.eye(shape[-1]) * shape[-1] * 0.5
+        if spd:
+            a = a @ np.swapaxes(a, -1, -2)
+        d = cp.array(a.astype(dt))
+        d._ensure_gpu()
+        return d
+
+    res = {}
+    a1k, b1k = mat((1024, 1024), np.float64), cp.array(rng.standard_normal((1024, 1)))
+    ab, bb = mat((4096, 64, 64), np.float32), cp.array(rng.standard_normal((4096, 64, 1)).astype(np.float32))
+    s1k, sb = mat((1024, 1024), np.float64, spd=True), mat((4096, 32, 32), np.float32, spd=True)
+    q = cp.array(rng.standard_normal((1024, 256)))
+    e = mat((256, 256), np.float64)
+    e = (e + e.T) * 0.5
+    eb = cp.array(np.swapaxes(rng.standard_normal((1024, 32, 32)), 1, 2).astype(np.float32))
+    eb = (eb + eb.swapaxes(1, 2)) * 0.5
+    sv = cp.array(rng.standard_normal((512, 256)))
+    cases = {
+        "solve_f64_1024": (lambda: LA.solve(a1k, b1k), 2 / 3 * 1024 ** 3 + 2 * 1024 ** 2),
+        "solve_f32_4096x64": (lambda: LA.solve(ab, bb), 4096 * (2 / 3 * 64 ** 3 + 2 * 64 ** 2)),
+        "inv_f64_1024": (lambda: LA.inv(a1k), 2 / 3 * 1024 ** 3 + 2 * 1024 ** 3),
+        "cholesky_f64_1024": (lambda: LA.cholesky(s1k), 1024 ** 3 / 3),
+        "cholesky_f32_4096x32": (lambda: LA.cholesky(sb), 4096 * 32 ** 3 / 3),
+        "qr_f64_1024x256": (lambda: LA.qr(q), 2 * 1024 * 256 ** 2 - 2 / 3 * 256 ** 3),
+        "eigh_f64_256": (lambda: LA.eigh(e), None),
+        "eigh_f32_1024x32": (lambda: LA.eigvalsh(eb), None),
+        "svd_f64_512x256": (lambda: LA.svd(sv, full_matrices=False), None),
+    }
+    for name, (f, flops) in cases.items():
+        try:
+            ms = _time(cp, be, name, f, reps)
+            res[name] = {"ms": round(ms, 3)}
+            if flops:
+                res[name]["gflops"] = round(flops / ms / 1e6, 1)
+        except Exception as ex:
+            res[name] = {"error": f"{type(ex).__name__}: {ex}"[:300]}
+    return res
+
+
+def bench_routines(cp, be, reps=5):
+    """Routines composed of device ops at 2^24-2^26 elements; `gbs` counts
+    the bytes of the inputs read and the result written once."""
+    rng = np.random.default_rng(22)
+    n = 1 << 24
+    x = cp.array(rng.standard_normal(n).astype(np.float32))
+    x._ensure_gpu()
+    t = cp.array(rng.standard_normal(1 << 20).astype(np.float32))
+    ints = cp.array(rng.integers(0, 1000, n).astype(np.int32))
+    m = x.reshape(4096, 4096)
+    xp = cp.array(np.sort(rng.standard_normal(4096)))
+    fp = cp.array(rng.standard_normal(4096))
+    x64 = x.astype(np.float64)
+    cases = {
+        "isclose_f32_2^24": (lambda: cp.isclose(x, x * 1.0000001), 9 * n),
+        "isin_2^24_in_2^20": (lambda: cp.isin(x, t), 5 * n),
+        "histogram_100_2^24": (lambda: cp.histogram(x, bins=100), 4 * n),
+        "bincount_int32_2^24": (lambda: cp.bincount(ints), 4 * n),
+        "interp_f64_2^24": (lambda: cp.interp(x64, xp, fp), 16 * n),
+        "pad_reflect_4096sq_+64": (lambda: cp.pad(m, 64, mode="reflect"), 4 * n + 4 * 4224 ** 2),
+        "einsum_bij,bjk_256x128": (lambda: cp.einsum("bij,bjk->bik", m.reshape(256, 128, 512),
+                                                      m.reshape(256, 512, 128)), None),
+        "cov_64x2^18": (lambda: cp.cov(x.reshape(64, 1 << 18)), None),
+    }
+    res = {}
+    for name, (f, nbytes) in cases.items():
+        try:
+            ms = _time(cp, be, name, f, reps)
+            res[name] = {"kernel_ms": round(ms, 4)}
+            if nbytes:
+                res[name]["gbs"] = round(nbytes / ms / 1e6, 1)
+        except Exception as ex:
+            res[name] = {"error": f"{type(ex).__name__}: {ex}"[:300]}
+    return res
+
+
 CONFIG_SECTIONS = {
     "c1_fused_elementwise": bench_c1, "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
     "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
     "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,
-    "indexing_manipulation": bench_indexing,
+    "indexing_manipulation": bench_indexing, "linalg": bench_linalg,
+    "routines": bench_routines,
 }
 
 

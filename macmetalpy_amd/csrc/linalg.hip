@@ -38,6 +38,10 @@ constexpr int kJ = 1024;          // Jacobi workgroup (16 wavefronts)
 constexpr int kMaxSweeps = 60;
 constexpr int kMaxEighN = 2048;   // rotation table in LDS: kMaxEighN / 2 pairs
 constexpr int kMaxSvdRows = 8192;
+constexpr int kNb = 64;             // panel width of the blocked LU
+constexpr int kBlockedMinN = 256;   // from this order a few matrices use the blocked LU
+constexpr int kBlockedMaxBatch = 64;
+constexpr int kRhsChunk = 32;       // right-hand sides per workgroup in the substitution
 
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
@@ -137,14 +141,17 @@ __global__ __launch_bounds__(kT) void k_getrf(T *__restrict__ a, int n, int *__r
   if (tid == 0) info[blockIdx.x] = first_zero;
 }
 
+// Workgroup (b, y) handles right-hand sides [y * kRhsChunk, ...) of matrix b.
 template <typename T>
 __global__ __launch_bounds__(kT) void k_getrs(const T *__restrict__ lu, const int *__restrict__ piv,
                                               T *__restrict__ b, int n, int nrhs) {
   const T *A = lu + (long long)blockIdx.x * n * n;
   const int *P = piv + (long long)blockIdx.x * n;
-  T *B = b + (long long)blockIdx.x * n * nrhs;
+  const int c0 = blockIdx.y * kRhsChunk;
+  const int cw = nrhs - c0 < kRhsChunk ? nrhs - c0 : kRhsChunk;
+  T *B = b + (long long)blockIdx.x * n * nrhs + c0;
   const int tid = threadIdx.x;
-  for (int c = tid; c < nrhs; c += kT)
+  for (int c = tid; c < cw; c += kT)
     for (int k = 0; k < n; ++k) {
       const int p = P[k];
       if (p != k) {
@@ -155,23 +162,178 @@ __global__ __launch_bounds__(kT) void k_getrs(const T *__restrict__ lu, const in
     }
   __syncthreads();
   for (int k = 0; k < n - 1; ++k) {
-    const long long tot = (long long)(n - k - 1) * nrhs;
+    const long long tot = (long long)(n - k - 1) * cw;
     for (long long t = tid; t < tot; t += kT) {
-      const int i = k + 1 + (int)(t / nrhs), c = (int)(t % nrhs);
+      const int i = k + 1 + (int)(t / cw), c = (int)(t % cw);
       B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
     }
     __syncthreads();
   }
   for (int k = n - 1; k >= 0; --k) {
-    for (int c = tid; c < nrhs; c += kT) B[(long long)k * nrhs + c] /= A[(long long)k * n + k];
+    for (int c = tid; c < cw; c += kT) B[(long long)k * nrhs + c] /= A[(long long)k * n + k];
     __syncthreads();
-    const long long tot = (long long)k * nrhs;
+    const long long tot = (long long)k * cw;
     for (long long t = tid; t < tot; t += kT) {
-      const int i = (int)(t / nrhs), c = (int)(t % nrhs);
+      const int i = (int)(t / cw), c = (int)(t % cw);
       B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
     }
     __syncthreads();
   }
+}
+
+// ------------------------------------------------------------ blocked LU
+// One n x n matrix (leading dimension n), panels of kNb columns:
+// k_getf2_panel factors rows j0.., columns j0..j0+jb with partial pivoting
+// (one workgroup), k_laswp applies its row swaps to the other columns,
+// k_trsm_ll forms U12 = L11^-1 A12 (one thread per column), and the
+// trailing update A22 -= L21 U12 is a device matmul into scratch followed
+// by k_sub_block.
+template <typename T>
+__global__ __launch_bounds__(kT) void k_getf2_panel(T *__restrict__ a, int n, int j0, int jb,
+                                                    int *__restrict__ piv, int *__restrict__ info) {
+  T *P = a + (long long)j0 * n + j0;
+  const int m = n - j0;
+  __shared__ T sval[kT / 64];
+  __shared__ int sidx[kT / 64];
+  const int tid = threadIdx.x;
+  int first_zero = 0;
+  for (int k = 0; k < jb; ++k) {
+    T best = T(-1);
+    int bi = m;
+    for (int i = k + tid; i < m; i += kT) {
+      const T v = fabs(P[(long long)i * n + k]);
+      if (v > best) {
+        best = v;
+        bi = i;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const T ov = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+    __syncthreads();
+    if ((tid & 63) == 0) {
+      sval[tid >> 6] = best;
+      sidx[tid >> 6] = bi;
+    }
+    __syncthreads();
+    best = sval[0];
+    bi = sidx[0];
+    for (int w = 1; w < kT / 64; ++w)
+      if (sval[w] > best || (sval[w] == best && sidx[w] < bi)) {
+        best = sval[w];
+        bi = sidx[w];
+      }
+    const int p = bi < m ? bi : k;
+    if (tid == 0) piv[j0 + k] = j0 + p;
+    if (p != k)
+      for (int j = tid; j < jb; j += kT) {
+        const T t = P[(long long)k * n + j];
+        P[(long long)k * n + j] = P[(long long)p * n + j];
+        P[(long long)p * n + j] = t;
+      }
+    __syncthreads();
+    const T d = P[(long long)k * n + k];
+    if (d == T(0)) {
+      if (!first_zero) first_zero = j0 + k + 1;
+      continue;
+    }
+    for (int i = k + 1 + tid; i < m; i += kT) P[(long long)i * n + k] /= d;
+    __syncthreads();
+    const int rows = m - k - 1, cols = jb - k - 1;
+    const long long tot = (long long)rows * cols;
+    for (long long t = tid; t < tot; t += kT) {
+      const int i = k + 1 + (int)(t / cols), j = k + 1 + (int)(t % cols);
+      P[(long long)i * n + j] -= P[(long long)i * n + k] * P[(long long)k * n + j];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    if (j0 == 0) info[0] = first_zero;
+    else if (info[0] == 0) info[0] = first_zero;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_laswp(T *__restrict__ a, int n, const int *__restrict__ piv,
+                                              int k0, int k1) {
+  const int c = blockIdx.x * kT + threadIdx.x;
+  if (c >= n || (c >= k0 && c < k1)) return;  // the panel's own columns are swapped already
+  for (int k = k0; k < k1; ++k) {
+    const int p = piv[k];
+    if (p != k) {
+      const T t = a[(long long)k * n + c];
+      a[(long long)k * n + c] = a[(long long)p * n + c];
+      a[(long long)p * n + c] = t;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_trsm_ll(T *__restrict__ a, int n, int j0, int jb) {
+  const int c = j0 + jb + blockIdx.x * kT + threadIdx.x;
+  if (c >= n) return;
+  const T *L = a + (long long)j0 * n + j0;
+  T *B = a + (long long)j0 * n;
+  for (int i = 1; i < jb; ++i) {
+    T s = B[(long long)i * n + c];
+    for (int k = 0; k < i; ++k) s -= L[(long long)i * n + k] * B[(long long)k * n + c];
+    B[(long long)i * n + c] = s;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_sub_block(T *__restrict__ a, int n, int r0, int mr, int nc,
+                                                  const T *__restrict__ c) {
+  const long long tot = (long long)mr * nc;
+  for (long long t = (long long)blockIdx.x * kT + threadIdx.x; t < tot; t += (long long)gridDim.x * kT) {
+    const int i = (int)(t / nc), j = (int)(t % nc);
+    a[(long long)(r0 + i) * n + r0 + j] -= c[t];
+  }
+}
+
+template <typename T>
+int lu_blocked(int dtype, T *a, long long batch, int n, int *piv, int *info) {
+  const long long m2max = (long long)(n - kNb);
+  void *tmp = nullptr;
+  if (m2max > 0)
+    if (int st = mmp_alloc((size_t)(m2max * m2max) * sizeof(T), &tmp)) return st;
+  int st = MMP_OK;
+  const unsigned cgrid = (unsigned)mmpi::ceil_div(n, kT);
+  for (long long b = 0; b < batch && st == MMP_OK; ++b) {
+    T *A = a + b * (long long)n * n;
+    int *P = piv + b * n;
+    int *I = info + b;
+    for (int j0 = 0; j0 < n && st == MMP_OK; j0 += kNb) {
+      const int jb = n - j0 < kNb ? n - j0 : kNb;
+      hipLaunchKernelGGL(k_getf2_panel<T>, dim3(1), dim3(kT), 0, mmpi::stream(), A, n, j0, jb, P, I);
+      hipLaunchKernelGGL(k_laswp<T>, dim3(cgrid), dim3(kT), 0, mmpi::stream(), A, n, (const int *)P, j0,
+                         j0 + jb);
+      const int n2 = n - j0 - jb;
+      if (n2 > 0) {
+        hipLaunchKernelGGL(k_trsm_ll<T>, dim3((unsigned)mmpi::ceil_div(n2, kT)), dim3(kT), 0,
+                           mmpi::stream(), A, n, j0, jb);
+        st = mmp_matmul(dtype, 1, n2, n2, jb, A + (long long)(j0 + jb) * n + j0, n, 0,
+                        A + (long long)j0 * n + j0 + jb, n, 0, tmp, n2, 0);
+        if (st == MMP_OK) {
+          const long long tot = (long long)n2 * n2;
+          const long long g = mmpi::ceil_div(tot, kT);
+          hipLaunchKernelGGL(k_sub_block<T>, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(kT), 0,
+                             mmpi::stream(), A, n, j0 + jb, n2, n2, (const T *)tmp);
+        }
+      }
+      if (st == MMP_OK) st = mmpi::check_launch("mmp_lu (blocked)");
+    }
+  }
+  if (tmp) {
+    const int fs = mmp_free(tmp);
+    if (st == MMP_OK) st = fs;
+  }
+  return st;
 }
 
 // -------------------------------------------------------------- Cholesky
@@ -203,6 +365,124 @@ __global__ __launch_bounds__(kT) void k_potrf(T *__restrict__ a, int n, int *__r
   for (long long t = tid; t < nn; t += kT)
     if ((int)(t % n) > (int)(t / n)) A[t] = T(0);
   if (tid == 0) info[blockIdx.x] = bad;
+}
+
+// ------------------------------------------------------ blocked Cholesky
+// One n x n matrix, panels of kNb columns: the diagonal block is factored
+// by one workgroup (k_potrf_diag), L21 = A21 L11^-T row by row
+// (k_trsm_rlt, one thread per row), A22 -= L21 L21^T through the device
+// matmul (L21^T staged by k_transpose_block) and k_sub_block; the strict
+// upper triangle is zeroed at the end.
+template <typename T>
+__global__ __launch_bounds__(kT) void k_potrf_diag(T *__restrict__ a, int n, int j0, int jb,
+                                                   int *__restrict__ info) {
+  T *A = a + (long long)j0 * n + j0;
+  const int tid = threadIdx.x;
+  int bad = 0;
+  if (info[0] != 0) return;  // an earlier panel failed: leave the rest
+  for (int k = 0; k < jb; ++k) {
+    const T d = A[(long long)k * n + k];
+    if (!(d > T(0))) {
+      bad = j0 + k + 1;
+      break;
+    }
+    const T l = sqrt(d);
+    __syncthreads();
+    if (tid == 0) A[(long long)k * n + k] = l;
+    for (int i = k + 1 + tid; i < jb; i += kT) A[(long long)i * n + k] /= l;
+    __syncthreads();
+    const int m = jb - k - 1;
+    for (int t = tid; t < m * m; t += kT) {
+      const int i = k + 1 + t / m, j = k + 1 + t % m;
+      if (j <= i) A[(long long)i * n + j] -= A[(long long)i * n + k] * A[(long long)j * n + k];
+    }
+    __syncthreads();
+  }
+  if (tid == 0 && bad) info[0] = bad;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_trsm_rlt(T *__restrict__ a, int n, int j0, int jb) {
+  const int r = j0 + jb + blockIdx.x * kT + threadIdx.x;
+  if (r >= n) return;
+  const T *L = a + (long long)j0 * n + j0;
+  T *X = a + (long long)r * n + j0;
+  for (int k = 0; k < jb; ++k) {
+    T s = X[k];
+    for (int l = 0; l < k; ++l) s -= X[l] * L[(long long)k * n + l];
+    X[k] = s / L[(long long)k * n + k];
+  }
+}
+
+// out (jb x m2, contiguous) = transpose of A[r0 .. r0+m2)[j0 .. j0+jb)
+template <typename T>
+__global__ __launch_bounds__(kT) void k_transpose_block(const T *__restrict__ a, int n, int r0, int j0,
+                                                        int m2, int jb, T *__restrict__ out) {
+  const long long tot = (long long)m2 * jb;
+  for (long long t = (long long)blockIdx.x * kT + threadIdx.x; t < tot; t += (long long)gridDim.x * kT) {
+    const int k = (int)(t / m2), i = (int)(t % m2);
+    out[t] = a[(long long)(r0 + i) * n + j0 + k];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_zero_upper(T *__restrict__ a, int n) {
+  const long long tot = (long long)n * n;
+  for (long long t = (long long)blockIdx.x * kT + threadIdx.x; t < tot; t += (long long)gridDim.x * kT)
+    if ((int)(t % n) > (int)(t / n)) a[t] = T(0);
+}
+
+template <typename T>
+__global__ void k_set_zero(int *__restrict__ p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+template <typename T>
+int cholesky_blocked(int dtype, T *a, long long batch, int n, int *info) {
+  const long long m2max = (long long)(n - kNb);
+  void *tmp = nullptr, *tr = nullptr;
+  if (m2max > 0) {
+    if (int st = mmp_alloc((size_t)(m2max * m2max) * sizeof(T), &tmp)) return st;
+    if (int st = mmp_alloc((size_t)(m2max * kNb) * sizeof(T), &tr)) {
+      mmp_free(tmp);
+      return st;
+    }
+  }
+  hipLaunchKernelGGL(k_set_zero<T>, dim3(1), dim3(kT), 0, mmpi::stream(), info, (int)batch);
+  int st = mmpi::check_launch("mmp_cholesky (blocked)");
+  for (long long b = 0; b < batch && st == MMP_OK; ++b) {
+    T *A = a + b * (long long)n * n;
+    int *I = info + b;
+    for (int j0 = 0; j0 < n && st == MMP_OK; j0 += kNb) {
+      const int jb = n - j0 < kNb ? n - j0 : kNb;
+      hipLaunchKernelGGL(k_potrf_diag<T>, dim3(1), dim3(kT), 0, mmpi::stream(), A, n, j0, jb, I);
+      const int m2 = n - j0 - jb;
+      if (m2 > 0) {
+        hipLaunchKernelGGL(k_trsm_rlt<T>, dim3((unsigned)mmpi::ceil_div(m2, kT)), dim3(kT), 0,
+                           mmpi::stream(), A, n, j0, jb);
+        const long long g1 = mmpi::ceil_div((long long)m2 * jb, kT);
+        hipLaunchKernelGGL(k_transpose_block<T>, dim3((unsigned)(g1 < 4096 ? g1 : 4096)), dim3(kT), 0,
+                           mmpi::stream(), (const T *)A, n, j0 + jb, j0, m2, jb, (T *)tr);
+        st = mmp_matmul(dtype, 1, m2, m2, jb, A + (long long)(j0 + jb) * n + j0, n, 0, tr, m2, 0, tmp,
+                        m2, 0);
+        if (st == MMP_OK) {
+          const long long g = mmpi::ceil_div((long long)m2 * m2, kT);
+          hipLaunchKernelGGL(k_sub_block<T>, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(kT), 0,
+                             mmpi::stream(), A, n, j0 + jb, m2, m2, (const T *)tmp);
+        }
+      }
+      if (st == MMP_OK) st = mmpi::check_launch("mmp_cholesky (blocked)");
+    }
+    if (st == MMP_OK) {
+      const long long g = mmpi::ceil_div((long long)n * n, kT);
+      hipLaunchKernelGGL(k_zero_upper<T>, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(kT), 0,
+                         mmpi::stream(), A, n);
+      st = mmpi::check_launch("mmp_cholesky (blocked)");
+    }
+  }
+  if (tmp) mmp_free(tmp);
+  if (tr) mmp_free(tr);
+  return st;
 }
 
 // -------------------------------------------------------------------- QR
@@ -310,9 +590,9 @@ __global__ __launch_bounds__(kJ) void k_syevj(T *__restrict__ a, T *__restrict__
         cs[2 * pi + 1] = s;
       }
       __syncthreads();
-      const long long work = (long long)npair * n;
-      for (long long t = tid; t < work; t += kJ) {
-        const int pi = (int)(t / n), j = (int)(t % n);
+      const int work = npair * n;  // <= 2^21
+      for (int t = tid; t < work; t += kJ) {
+        const int pi = t / n, j = t - pi * n;  // lanes along a row: coalesced
         const T s = cs[2 * pi + 1];
         if (s == T(0)) continue;
         int p, q;
@@ -323,8 +603,10 @@ __global__ __launch_bounds__(kJ) void k_syevj(T *__restrict__ a, T *__restrict__
         A[(long long)q * n + j] = s * x + c * y;
       }
       __syncthreads();
-      for (long long t = tid; t < work; t += kJ) {
-        const int pi = (int)(t / n), i = (int)(t % n);
+      for (int t = tid; t < work; t += kJ) {
+        // lanes over consecutive pairs of one row: the round-robin pairs
+        // are runs of consecutive columns, so the accesses coalesce
+        const int i = t / npair, pi = t - i * npair;
         const T s = cs[2 * pi + 1];
         if (s == T(0)) continue;
         int p, q;
@@ -421,6 +703,9 @@ extern "C" int mmp_lu(int dtype, void *a, int64_t batch, int64_t n, int32_t *piv
   if (n < 0 || n > 32768) return mmpi::fail(MMP_E_ARG, "mmp_lu: n %lld", (long long)n);
   if (batch == 0 || n == 0) return MMP_OK;
   if (!a || !piv || !info) return mmpi::fail(MMP_E_ARG, "mmp_lu: null pointer");
+  if (n >= kBlockedMinN && batch <= kBlockedMaxBatch)
+    return dtype == MMP_F32 ? lu_blocked<float>(dtype, (float *)a, batch, (int)n, (int *)piv, (int *)info)
+                            : lu_blocked<double>(dtype, (double *)a, batch, (int)n, (int *)piv, (int *)info);
   if (dtype == MMP_F32)
     hipLaunchKernelGGL(k_getrf<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (float *)a,
                        (int)n, (int *)piv, (int *)info);
@@ -438,11 +723,13 @@ extern "C" int mmp_lu_solve(int dtype, const void *lu, const int32_t *piv, void 
     return mmpi::fail(MMP_E_ARG, "mmp_lu_solve: n %lld nrhs %lld", (long long)n, (long long)nrhs);
   if (batch == 0 || n == 0 || nrhs == 0) return MMP_OK;
   if (!lu || !piv || !b) return mmpi::fail(MMP_E_ARG, "mmp_lu_solve: null pointer");
+  const dim3 grid((unsigned)batch, (unsigned)mmpi::ceil_div(nrhs, kRhsChunk));
+  if (grid.y > 65535) return mmpi::fail(MMP_E_ARG, "mmp_lu_solve: nrhs %lld too large", (long long)nrhs);
   if (dtype == MMP_F32)
-    hipLaunchKernelGGL(k_getrs<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+    hipLaunchKernelGGL(k_getrs<float>, grid, dim3(kT), 0, mmpi::stream(),
                        (const float *)lu, (const int *)piv, (float *)b, (int)n, (int)nrhs);
   else
-    hipLaunchKernelGGL(k_getrs<double>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(),
+    hipLaunchKernelGGL(k_getrs<double>, grid, dim3(kT), 0, mmpi::stream(),
                        (const double *)lu, (const int *)piv, (double *)b, (int)n, (int)nrhs);
   return mmpi::check_launch("mmp_lu_solve");
 }
@@ -453,6 +740,9 @@ extern "C" int mmp_cholesky(int dtype, void *a, int64_t batch, int64_t n, int32_
   if (n < 0 || n > 32768) return mmpi::fail(MMP_E_ARG, "mmp_cholesky: n %lld", (long long)n);
   if (batch == 0 || n == 0) return MMP_OK;
   if (!a || !info) return mmpi::fail(MMP_E_ARG, "mmp_cholesky: null pointer");
+  if (n >= kBlockedMinN && batch <= kBlockedMaxBatch)
+    return dtype == MMP_F32 ? cholesky_blocked<float>(dtype, (float *)a, batch, (int)n, (int *)info)
+                            : cholesky_blocked<double>(dtype, (double *)a, batch, (int)n, (int *)info);
   if (dtype == MMP_F32)
     hipLaunchKernelGGL(k_potrf<float>, dim3((unsigned)batch), dim3(kT), 0, mmpi::stream(), (float *)a,
                        (int)n, (int *)info);

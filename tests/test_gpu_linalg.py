@@ -247,3 +247,44 @@ def test_larger_batched():
     _close(LA.eigvalsh(cp.array(s)), np.linalg.eigvalsh(s), 1e-9, 1e-10)
     r = _m((160, 90), np.float64, 123, well=False)
     _close(LA.svdvals(cp.array(r)), np.linalg.svd(r, compute_uv=False), 1e-9, 1e-10)
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_blocked_lu_sizes(dt):
+    # orders >= 256 take the blocked LU (64-column panels, matmul updates)
+    rt, at = TOL[dt]
+    for n in (256, 300, 517):
+        a = _m((n, n), dt, 200 + n)
+        b = _m((n, 3), dt, 201 + n, well=False)
+        _close(LA.solve(cp.array(a), cp.array(b)), np.linalg.solve(a, b), rt * 10, at * 10)
+        sg, ld = LA.slogdet(cp.array(a))
+        ws, wl = np.linalg.slogdet(a)
+        _close(sg, ws, 0, 0)
+        _close(ld, wl, rt * 10, at * 10)
+    a = _m((260, 260), dt, 210)
+    _close(LA.inv(cp.array(a)), np.linalg.inv(a), rt * 10, at * 10)
+    p = np.eye(300, dtype=dt)[np.random.default_rng(3).permutation(300)] * 2
+    _close(LA.det(cp.array(p)), np.linalg.det(p).astype(dt), rt * 10, 0)
+    A = _m((3, 280, 280), dt, 211)
+    B = _m((3, 280, 2), dt, 212, well=False)
+    _close(LA.solve(cp.array(A), cp.array(B)), np.linalg.solve(A, B), rt * 10, at * 10)
+    s = _m((320, 320), dt, 213)
+    s[:, 100] = 0
+    with pytest.raises(LA.LinAlgError):
+        LA.solve(cp.array(s), cp.array(np.ones(320, dt)))
+    _close(LA.det(cp.array(s)), np.zeros((), dt), 0, 0)
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_blocked_cholesky_sizes(dt):
+    # orders >= 256 take the blocked Cholesky (only the lower triangle is read)
+    rt, at = TOL[dt]
+    for n in (256, 333):
+        a = _m((n, n), np.float64, 300 + n, spd=True)
+        lo = np.tril(a) + np.triu(np.full((n, n), 7.0), 1)   # garbage above the diagonal
+        want = np.linalg.cholesky(a.astype(dt))
+        _close(LA.cholesky(cp.array(lo.astype(dt))), want, rt * 10, at * n)
+    bad = _m((300, 300), np.float64, 310, spd=True)
+    bad[200, 200] = -1.0
+    with pytest.raises(LA.LinAlgError):
+        LA.cholesky(cp.array(bad.astype(dt)))

@@ -161,21 +161,22 @@ __global__ __launch_bounds__(kT) void k_getrs(const T *__restrict__ lu, const in
       }
     }
   __syncthreads();
+  // thread -> (row group r0, column c) once, no division per element; the
+  // r0 < rstep threads cover every (row group, column) pair exactly once
+  const int c = tid % cw, r0 = tid / cw, rstep = kT / cw;
   for (int k = 0; k < n - 1; ++k) {
-    const long long tot = (long long)(n - k - 1) * cw;
-    for (long long t = tid; t < tot; t += kT) {
-      const int i = k + 1 + (int)(t / cw), c = (int)(t % cw);
-      B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
+    if (r0 < rstep) {
+      const T bk = B[(long long)k * nrhs + c];
+      for (int i = k + 1 + r0; i < n; i += rstep) B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * bk;
     }
     __syncthreads();
   }
   for (int k = n - 1; k >= 0; --k) {
-    for (int c = tid; c < cw; c += kT) B[(long long)k * nrhs + c] /= A[(long long)k * n + k];
+    if (tid < cw) B[(long long)k * nrhs + tid] /= A[(long long)k * n + k];
     __syncthreads();
-    const long long tot = (long long)k * cw;
-    for (long long t = tid; t < tot; t += kT) {
-      const int i = (int)(t / cw), c = (int)(t % cw);
-      B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * B[(long long)k * nrhs + c];
+    if (r0 < rstep) {
+      const T bk = B[(long long)k * nrhs + c];
+      for (int i = r0; i < k; i += rstep) B[(long long)i * nrhs + c] -= A[(long long)i * n + k] * bk;
     }
     __syncthreads();
   }
@@ -244,11 +245,12 @@ __global__ __launch_bounds__(kT) void k_getf2_panel(T *__restrict__ a, int n, in
     }
     for (int i = k + 1 + tid; i < m; i += kT) P[(long long)i * n + k] /= d;
     __syncthreads();
-    const int rows = m - k - 1, cols = jb - k - 1;
-    const long long tot = (long long)rows * cols;
-    for (long long t = tid; t < tot; t += kT) {
-      const int i = k + 1 + (int)(t / cols), j = k + 1 + (int)(t % cols);
-      P[(long long)i * n + j] -= P[(long long)i * n + k] * P[(long long)k * n + j];
+    // rank-1 update: lane = column (jb <= 64), wavefronts take rows in turn
+    const int lane = tid & 63, wave = tid >> 6;
+    if (lane < jb - k - 1) {
+      const int j = k + 1 + lane;
+      const T ukj = P[(long long)k * n + j];
+      for (int i = k + 1 + wave; i < m; i += kT / 64) P[(long long)i * n + j] -= P[(long long)i * n + k] * ukj;
     }
     __syncthreads();
   }
@@ -492,6 +494,7 @@ __global__ __launch_bounds__(kT) void k_geqrf(T *__restrict__ a, int m, int n, T
   T *A = a + (long long)blockIdx.x * m * n;
   T *TAU = tau + (long long)blockIdx.x * kmin;
   __shared__ T red[kT / 64];
+  __shared__ T part_lds[kT / 64][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int k = 0; k < kmin; ++k) {
     T part = T(0);
@@ -513,15 +516,26 @@ __global__ __launch_bounds__(kT) void k_geqrf(T *__restrict__ a, int m, int n, T
     if (tid == 0) TAU[k] = t;
     __syncthreads();
     if (t != T(0)) {
-      for (int j = k + 1 + wave; j < n; j += kT / 64) {
-        const T akj = A[(long long)k * n + j];
-        T w = T(0);
-        for (int i = k + 1 + lane; i < m; i += 64) w += A[(long long)i * n + k] * A[(long long)i * n + j];
-        w = wave_sum(w) + akj;
-        if (lane == 0) A[(long long)k * n + j] = akj - t * w;
-        for (int i = k + 1 + lane; i < m; i += 64) A[(long long)i * n + j] -= t * A[(long long)i * n + k] * w;
+      // lane = column of a 64-column chunk, wavefronts split the rows; the
+      // four partial dot products meet in LDS
+      for (int jc = k + 1; jc < n; jc += 64) {
+        const int j = jc + lane;
+        T part = T(0);
+        if (j < n)
+          for (int i = k + 1 + wave; i < m; i += kT / 64) part += A[(long long)i * n + k] * A[(long long)i * n + j];
+        // A[k][j] is read by every wavefront before the barrier and
+        // written by wavefront 0 after it
+        const T akj = j < n ? A[(long long)k * n + j] : T(0);
+        part_lds[wave][lane] = part;
+        __syncthreads();
+        if (j < n) {
+          T w = akj;
+          for (int q = 0; q < kT / 64; ++q) w += part_lds[q][lane];
+          for (int i = k + 1 + wave; i < m; i += kT / 64) A[(long long)i * n + j] -= t * A[(long long)i * n + k] * w;
+          if (wave == 0) A[(long long)k * n + j] = akj - t * w;
+        }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
 }
@@ -533,6 +547,7 @@ __global__ __launch_bounds__(kT) void k_orgqr(const T *__restrict__ a, const T *
   const T *A = a + (long long)blockIdx.x * m * n;
   const T *TAU = tau + (long long)blockIdx.x * kmin;
   T *Q = q + (long long)blockIdx.x * m * qc;
+  __shared__ T part_lds[kT / 64][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long long tot = (long long)m * qc;
   for (long long t = tid; t < tot; t += kT) Q[t] = (t / qc == t % qc) ? T(1) : T(0);
@@ -540,15 +555,22 @@ __global__ __launch_bounds__(kT) void k_orgqr(const T *__restrict__ a, const T *
   for (int k = kmin - 1; k >= 0; --k) {
     const T t = TAU[k];
     if (t == T(0)) continue;
-    for (int j = k + wave; j < qc; j += kT / 64) {
-      const T qkj = Q[(long long)k * qc + j];
-      T w = T(0);
-      for (int i = k + 1 + lane; i < m; i += 64) w += A[(long long)i * n + k] * Q[(long long)i * qc + j];
-      w = wave_sum(w) + qkj;
-      if (lane == 0) Q[(long long)k * qc + j] = qkj - t * w;
-      for (int i = k + 1 + lane; i < m; i += 64) Q[(long long)i * qc + j] -= t * A[(long long)i * n + k] * w;
+    for (int jc = k; jc < qc; jc += 64) {
+      const int j = jc + lane;
+      T part = T(0);
+      if (j < qc)
+        for (int i = k + 1 + wave; i < m; i += kT / 64) part += A[(long long)i * n + k] * Q[(long long)i * qc + j];
+      const T qkj = j < qc ? Q[(long long)k * qc + j] : T(0);
+      part_lds[wave][lane] = part;
+      __syncthreads();
+      if (j < qc) {
+        T w = qkj;
+        for (int q = 0; q < kT / 64; ++q) w += part_lds[q][lane];
+        for (int i = k + 1 + wave; i < m; i += kT / 64) Q[(long long)i * qc + j] -= t * A[(long long)i * n + k] * w;
+        if (wave == 0) Q[(long long)k * qc + j] = qkj - t * w;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 

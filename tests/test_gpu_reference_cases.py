@@ -4,7 +4,7 @@ Each test restates one case (or one parametrised group) of the reference's
 test suite -- same inputs, same operations, same tolerances -- against the
 device implementation; the citation names the reference test it follows.
 The reference compares against NumPy at run time, so NumPy is the expected
-value here too.  Where this build deliberately differs from the reference
+value here too.  Where the device library deliberately differs from the reference
 (float64 kept on the device, NumPy integer semantics), the NumPy result is
 the one checked.
 """

@@ -102,6 +102,7 @@ from .linalg_top import matmul, dot, vdot, inner
 from ._backend import HipBackend as MetalBackend  # the reference's backend class name
 from . import linalg
 from . import random
+from . import fft
 
 # NumPy 2 aliases (reference __init__.py:262-272)
 acos = arccos

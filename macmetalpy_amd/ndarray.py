@@ -722,7 +722,7 @@ class ndarray:
         if where.startswith("numpy.linalg"):
             target = getattr(mod.linalg, name, None)
         elif where.startswith("numpy.fft"):
-            target = None
+            target = getattr(mod.fft, name, None)
         else:
             target = getattr(mod, name, None)
         if target is None or target is func or not callable(target):

@@ -42,8 +42,9 @@ def test_array_function_dispatch():
     _same(np.tile(d, (2, 1)), np.tile(x, (2, 1)))
     np.testing.assert_allclose(_h(np.linalg.norm(d)), np.linalg.norm(x), rtol=1e-6)
     assert isinstance(np.linalg.inv(cp.array(np.eye(3))), cp.ndarray)
-    with pytest.raises(TypeError):
+    with pytest.raises(NotImplementedError):
         np.fft.fft(d)
+    _same(np.fft.fftshift(d), np.fft.fftshift(x))
 
 
 def test_view_byteswap():
@@ -116,3 +117,15 @@ def test_methods():
     _same(pickle.loads(pickle.dumps(d)), x)
     assert d.to_device("gpu") is d
     _same(d.conj(), x)
+
+
+def test_fft_namespace():
+    for n, d in ((8, 1.0), (9, 0.1), (1, 2.0)):
+        np.testing.assert_array_equal(_h(cp.fft.fftfreq(n, d)), np.fft.fftfreq(n, d))
+        np.testing.assert_array_equal(_h(cp.fft.rfftfreq(n, d)), np.fft.rfftfreq(n, d))
+    x = np.arange(30, dtype=np.float32).reshape(5, 6)
+    for axes in (None, 0, 1, (0, 1)):
+        _same(cp.fft.fftshift(cp.array(x), axes=axes), np.fft.fftshift(x, axes=axes))
+        _same(cp.fft.ifftshift(cp.array(x), axes=axes), np.fft.ifftshift(x, axes=axes))
+    with pytest.raises(NotImplementedError):
+        cp.fft.fft(cp.array(x))

@@ -36,6 +36,30 @@ def _batch_operand(x, batch_shape, mat_shape):
     return x._broadcast_copy(tuple(batch_shape) + tuple(mat_shape), x._dtype), _prod(mat_shape)
 
 
+_SPLITK_MAX_OUT = 128 * 128   # outputs too few to fill the device with tiles
+_SPLITK_MIN_K = 16384
+_SPLITK_CHUNK = 2048
+
+
+def _matmul_split_k(rdt, M, N, K, A, B, res):
+    """A small output with a long sum (e.g. X @ X.T of a wide X): the K
+    range is cut into chunks that run as one batched matmul, so that every
+    chunk gets its own workgroups, and the partial products are summed
+    (float64 accumulation) into the result."""
+    from .reductions import sum as _sum
+    kc = _SPLITK_CHUNK
+    nb = K // kc
+    rem = K - nb * kc
+    isz = rdt.itemsize
+    part = ndarray._empty_device((nb + (1 if rem else 0), M, N), rdt)
+    be = HipBackend()
+    be.matmul(dtype_code(rdt), nb, M, N, kc, A._ptr, K, kc, B._ptr, N, kc * N, part._ptr, N, M * N)
+    if rem:
+        be.matmul(dtype_code(rdt), 1, M, N, rem, A._ptr + nb * kc * isz, K, 0,
+                  B._ptr + nb * kc * N * isz, N, 0, part._ptr + nb * M * N * isz, N, M * N)
+    res[...] = _sum(part, axis=0)
+
+
 def matmul(x1, x2, out=None, **kwargs):
     a, b = _asarray(x1), _asarray(x2)
     if a.ndim == 0 or b.ndim == 0:
@@ -66,6 +90,9 @@ def matmul(x1, x2, out=None, **kwargs):
     if res.size:
         if K == 0:
             res.fill(0)
+        elif (batch == 1 and M * N <= _SPLITK_MAX_OUT and K >= _SPLITK_MIN_K
+              and rdt in (np.float32, np.float64)):
+            _matmul_split_k(rdt, M, N, K, A, B, res)
         else:
             HipBackend().matmul(dtype_code(rdt), batch, M, N, K, A._ptr, K, sA, B._ptr, N, sB,
                                 res._ptr, N, M * N)

@@ -288,3 +288,18 @@ def test_blocked_cholesky_sizes(dt):
     bad[200, 200] = -1.0
     with pytest.raises(LA.LinAlgError):
         LA.cholesky(cp.array(bad.astype(dt)))
+
+
+def test_split_k_matmul():
+    # small outputs with long sums run as a batched matmul over K chunks
+    rng = np.random.default_rng(400)
+    for dt, rt in ((np.float64, 1e-12), (np.float32, 2e-5)):
+        for (m, k, n) in ((64, 40000, 32), (1, 16384, 1), (100, 20001, 100), (3, 70000, 5)):
+            a = rng.standard_normal((m, k)).astype(dt)
+            b = rng.standard_normal((k, n)).astype(dt)
+            want = a.astype(np.float64) @ b.astype(np.float64)
+            got = _h(cp.matmul(cp.array(a), cp.array(b)))
+            assert got.dtype == dt and got.shape == (m, n)
+            np.testing.assert_allclose(got, want, rtol=rt, atol=rt * np.sqrt(k) * 5)
+    x = rng.standard_normal((64, 1 << 18))
+    np.testing.assert_allclose(_h(cp.cov(cp.array(x))), np.cov(x), rtol=1e-10, atol=1e-12)

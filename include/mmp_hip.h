@@ -321,6 +321,18 @@ int mmp_scatter(int word, void *dst, int64_t dst_bytes, const int64_t *offsets, 
  * position of the k-th selected element, k < count. */
 int mmp_nonzero(int64_t n, const int64_t *incl, int64_t count, int64_t *out);
 
+/* Integer counts (replace the NumPy host calls behind bincount / histogram,
+ * math_ext.py).  counts (int64) are zeroed first, then:
+ * mmp_bincount: counts[v] = number of integer elements equal to v, for v in
+ * [0, nbins) (dtype MMP_BOOL .. MMP_U64; other values are not counted).
+ * mmp_histogram: counts[b] = number of elements with edges[b] <= x <
+ * edges[b+1] (the last bin also takes x == edges[nedges-1]), compared in
+ * double; NaN and out-of-range values are not counted (dtype MMP_I16,
+ * MMP_U16, MMP_I32, MMP_U32, MMP_F16, MMP_F32, MMP_F64; nedges >= 2). */
+int mmp_bincount(int dtype, int64_t n, const void *x, int64_t nbins, int64_t *counts);
+int mmp_histogram(int dtype, int64_t n, const void *x, int64_t nedges, const double *edges,
+                  int64_t *counts);
+
 /* ======================================================================== */
 /* Dense factorizations: replace the reference's NumPy / LAPACK calls in    */
 /* linalg.py (solve, inv, det, slogdet :37-61, 149-159; cholesky :83-88;    */

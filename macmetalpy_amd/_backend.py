@@ -97,6 +97,8 @@ _SIGNATURES = {
     "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp],
     "mmp_scatter": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64],
     "mmp_nonzero": [_c_i64, _c_vp, _c_i64, _c_vp],
+    "mmp_bincount": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp],
+    "mmp_histogram": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp],
     "mmp_lu": [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_lu_solve": [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64],
     "mmp_cholesky": [_c_int, _c_vp, _c_i64, _c_i64, _c_vp],
@@ -355,6 +357,12 @@ class HipBackend:
 
     def nonzero(self, n: int, incl: int, count: int, out: int) -> None:
         _check(self._lib.mmp_nonzero(n, incl, count, out), "mmp_nonzero")
+
+    def bincount(self, dcode, n, x, nbins, counts) -> None:
+        _check(self._lib.mmp_bincount(dcode, n, x, nbins, counts), "mmp_bincount")
+
+    def histogram(self, dcode, n, x, nedges, edges, counts) -> None:
+        _check(self._lib.mmp_histogram(dcode, n, x, nedges, edges, counts), "mmp_histogram")
 
     def lu(self, dcode, a, batch, n, piv, info) -> None:
         _check(self._lib.mmp_lu(dcode, a, batch, n, piv, info), "mmp_lu")

@@ -300,8 +300,9 @@ def digitize(x, bins, right=False):
 
 
 def bincount(x, weights=None, minlength=0):
-    """Counts (or weight sums) of non-negative integers: sort, then the
-    run boundaries by binary search."""
+    """Counts of non-negative integers with the device counting kernel;
+    weight sums (float64) from the values sorted by key and the run
+    boundaries found by binary search (a fixed summation order)."""
     from .sorting import sort, argsort, searchsorted
     from .indexing import take
     from . import reductions
@@ -310,22 +311,25 @@ def bincount(x, weights=None, minlength=0):
     if a.ndim != 1:
         raise ValueError("object too deep for desired array")
     if a.dtype.kind not in "iub":
-        raise TypeError("Cannot cast array data from dtype('float64') to dtype('int64') "
+        raise TypeError(f"Cannot cast array data from dtype('{a.dtype}') to dtype('int64') "
                         "according to the rule 'safe'")
     if minlength < 0:
         raise ValueError("'minlength' must not be negative")
     if a.size == 0:
         return zeros((minlength,), dtype=np.float64 if weights is not None else np.int64)
-    ai = a.astype(np.int64)
-    lo = int(reductions.min(ai))
-    if lo < 0:
+    lo, hi = int(reductions.min(a)), int(reductions.max(a))
+    if lo < 0 or hi > np.iinfo(np.int64).max:   # uint64 beyond 2^63 reads as negative
         raise ValueError("'list' argument must have no negative elements")
-    nb = builtins.max(int(reductions.max(ai)) + 1, minlength)
-    edges = arange(nb + 1, dtype=np.int64)
+    nb = builtins.max(hi + 1, minlength)
     if weights is None:
-        s = sort(ai)
-        pos = searchsorted(s, edges, side="left")
-        return pos[1:] - pos[:-1]
+        from ._backend import HipBackend
+        from ._dtypes import dtype_code
+        src = a._ensure_contiguous()
+        out = ndarray._empty_device((nb,), np.int64)
+        HipBackend().bincount(dtype_code(src.dtype), src.size, src._ptr, nb, out._ptr)
+        return out
+    ai = a.astype(np.int64)
+    edges = arange(nb + 1, dtype=np.int64)
     w = _asarray(weights).astype(np.float64)
     order = argsort(ai)
     s = take(ai, order)
@@ -395,7 +399,17 @@ def histogram(a, bins=10, range=None, density=None, weights=None):
     edges = _hist_edges(x, bins, range)
     nb = edges.size - 1
     ge = _asarray(edges)
-    if weights is None:
+    exact = x.dtype.kind == "f" or x.dtype.itemsize <= 4
+    if weights is None and exact and x.dtype != np.bool_ and nb >= 1:
+        # counts by the device kernel; comparisons in double are exact for
+        # these dtypes and for the edges (float16 / float32 / float64 / int)
+        from ._backend import HipBackend
+        from ._dtypes import dtype_code
+        src = x._ensure_contiguous()
+        e64 = _asarray(np.asarray(edges, dtype=np.float64))._ensure_gpu()
+        hist = ndarray._empty_device((nb,), np.int64)
+        HipBackend().histogram(dtype_code(src.dtype), src.size, src._ptr, nb + 1, e64._ptr, hist._ptr)
+    elif weights is None:
         s = sort(x)
         left = searchsorted(s, ge, side="left")
         last = searchsorted(s, ge[nb:], side="right")

@@ -134,6 +134,15 @@ def test_bincount_digitize_histogram():
            rtol=0, atol=1e-13 * np.abs(w).sum())
     with pytest.raises(ValueError):
         cp.bincount(cp.array(np.array([1, -1], np.int32)))
+    for dt in (np.int16, np.uint16, np.uint32, np.int64, np.bool_):
+        xs = (x % 2).astype(dt) if dt == np.bool_ else x.astype(dt)
+        _same(cp.bincount(cp.array(xs)), np.bincount(xs))
+    big = np.random.default_rng(5).integers(0, 20000, 50000).astype(np.int32)   # global-atomic path
+    _same(cp.bincount(cp.array(big)), np.bincount(big))
+    _same(cp.bincount(cp.array(big), minlength=30000), np.bincount(big, minlength=30000))
+    _same(cp.bincount(cp.array(np.array([1, 2, 2], np.uint64))), np.bincount(np.array([1, 2, 2], np.uint64)))
+    with pytest.raises(ValueError):
+        cp.bincount(cp.array(np.array([2 ** 63 + 5], np.uint64)))
     v = rng.standard_normal(3000).astype(np.float32) * 3
     bins = np.array([-2.0, -1.0, 0.0, 0.5, 1.0, 3.0], dtype=np.float32)
     for right in (False, True):
@@ -162,6 +171,15 @@ def test_bincount_digitize_histogram():
     _same(cp.histogram(cp.array(vv), bins=8, weights=cp.array(iw))[0],
           np.histogram(vv, bins=8, weights=iw)[0])
     _same(cp.histogram(cp.array(x), bins=10)[0], np.histogram(x, bins=10)[0])
+    for dt in (np.float16, np.float64, np.int16, np.uint32):
+        vd = (vv * 10).astype(dt)
+        for kb in (5, 64, np.array([-20.0, -3.5, 0.0, 0.0, 2.0, 7.0, 20.0])):
+            _same(cp.histogram(cp.array(vd), bins=kb)[0], np.histogram(vd, bins=kb)[0])
+    many = np.linspace(-3, 3, 6001)                                   # global-atomic path
+    _same(cp.histogram(cp.array(vv), bins=cp.array(many))[0], np.histogram(vv, bins=many)[0])
+    _same(cp.histogram(cp.array(vv), bins=5000)[0], np.histogram(vv, bins=5000)[0])
+    _same(cp.histogram(cp.array(np.array([], np.float32)), bins=4)[0],
+          np.histogram(np.array([], np.float32), bins=4)[0])
     _same(cp.histogram(cp.array(x), bins=10)[1], np.histogram(x, bins=10)[1])
 
 

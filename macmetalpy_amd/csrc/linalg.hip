@@ -43,6 +43,28 @@ constexpr int kBlockedMinN = 256;   // from this order a few matrices use the bl
 constexpr int kBlockedMaxBatch = 64;
 constexpr int kRhsChunk = 32;       // right-hand sides per workgroup in the substitution
 
+// dst[r] -= src[r] * f for rows r = r0, r0 + S, ... < m of two columns of
+// row-major matrices (leading dimensions ldd, lds): eight rows are loaded
+// before any is stored (the stores never touch the loaded source column),
+// so the loads overlap instead of waiting one by one.
+template <typename T, int S>
+__device__ __forceinline__ void axpy_rows(T *__restrict__ dst, long long ldd, const T *__restrict__ src,
+                                          long long lds, int r0, int m, T f) {
+  constexpr int U = 8;
+  int r = r0;
+  for (; r + (U - 1) * S < m; r += U * S) {
+    T x[U], y[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      x[u] = src[(long long)(r + u * S) * lds];
+      y[u] = dst[(long long)(r + u * S) * ldd];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) dst[(long long)(r + u * S) * ldd] = y[u] - x[u] * f;
+  }
+  for (; r < m; r += S) dst[(long long)r * ldd] -= src[(long long)r * lds] * f;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -250,7 +272,7 @@ __global__ __launch_bounds__(kT) void k_getf2_panel(T *__restrict__ a, int n, in
     if (lane < jb - k - 1) {
       const int j = k + 1 + lane;
       const T ukj = P[(long long)k * n + j];
-      for (int i = k + 1 + wave; i < m; i += kT / 64) P[(long long)i * n + j] -= P[(long long)i * n + k] * ukj;
+      axpy_rows<T, kT / 64>(P + j, n, P + k, n, k + 1 + wave, m, ukj);
     }
     __syncthreads();
   }
@@ -521,8 +543,10 @@ __global__ __launch_bounds__(kT) void k_geqrf(T *__restrict__ a, int m, int n, T
       for (int jc = k + 1; jc < n; jc += 64) {
         const int j = jc + lane;
         T part = T(0);
-        if (j < n)
+        if (j < n) {
+#pragma unroll 8
           for (int i = k + 1 + wave; i < m; i += kT / 64) part += A[(long long)i * n + k] * A[(long long)i * n + j];
+        }
         // A[k][j] is read by every wavefront before the barrier and
         // written by wavefront 0 after it
         const T akj = j < n ? A[(long long)k * n + j] : T(0);
@@ -531,7 +555,7 @@ __global__ __launch_bounds__(kT) void k_geqrf(T *__restrict__ a, int m, int n, T
         if (j < n) {
           T w = akj;
           for (int q = 0; q < kT / 64; ++q) w += part_lds[q][lane];
-          for (int i = k + 1 + wave; i < m; i += kT / 64) A[(long long)i * n + j] -= t * A[(long long)i * n + k] * w;
+          axpy_rows<T, kT / 64>(A + j, n, A + k, n, k + 1 + wave, m, t * w);
           if (wave == 0) A[(long long)k * n + j] = akj - t * w;
         }
         __syncthreads();
@@ -558,15 +582,17 @@ __global__ __launch_bounds__(kT) void k_orgqr(const T *__restrict__ a, const T *
     for (int jc = k; jc < qc; jc += 64) {
       const int j = jc + lane;
       T part = T(0);
-      if (j < qc)
+      if (j < qc) {
+#pragma unroll 8
         for (int i = k + 1 + wave; i < m; i += kT / 64) part += A[(long long)i * n + k] * Q[(long long)i * qc + j];
+      }
       const T qkj = j < qc ? Q[(long long)k * qc + j] : T(0);
       part_lds[wave][lane] = part;
       __syncthreads();
       if (j < qc) {
         T w = qkj;
         for (int q = 0; q < kT / 64; ++q) w += part_lds[q][lane];
-        for (int i = k + 1 + wave; i < m; i += kT / 64) Q[(long long)i * qc + j] -= t * A[(long long)i * n + k] * w;
+        axpy_rows<T, kT / 64>(Q + j, qc, A + k, n, k + 1 + wave, m, t * w);
         if (wave == 0) Q[(long long)k * qc + j] = qkj - t * w;
       }
       __syncthreads();

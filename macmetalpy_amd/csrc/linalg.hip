@@ -65,6 +65,33 @@ __device__ __forceinline__ void axpy_rows(T *__restrict__ dst, long long ldd, co
   for (; r < m; r += S) dst[(long long)r * ldd] -= src[(long long)r * lds] * f;
 }
 
+// Rows x, y (length len) := (c x - s y, s x + c y), lanes striding by 64,
+// eight elements per lane loaded before any is stored.
+template <typename T>
+__device__ __forceinline__ void rotate_rows(T *__restrict__ x, T *__restrict__ y, int len, int lane, T c,
+                                            T s) {
+  constexpr int U = 8;
+  int j = lane;
+  for (; j + (U - 1) * 64 < len; j += U * 64) {
+    T a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      a[u] = x[j + u * 64];
+      b[u] = y[j + u * 64];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      x[j + u * 64] = c * a[u] - s * b[u];
+      y[j + u * 64] = s * a[u] + c * b[u];
+    }
+  }
+  for (; j < len; j += 64) {
+    const T a = x[j], b = y[j];
+    x[j] = c * a - s * b;
+    y[j] = s * a + c * b;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -699,6 +726,7 @@ __global__ __launch_bounds__(kJ) void k_gesvj(T *__restrict__ w, T *__restrict__
         pair_of(rd, pi, N, p, q);
         if (p >= r || q >= r) continue;
         T al = T(0), be = T(0), ga = T(0);
+#pragma unroll 8
         for (int j = lane; j < L; j += 64) {
           const T x = W[(long long)p * L + j], y = W[(long long)q * L + j];
           al += x * x;
@@ -713,16 +741,8 @@ __global__ __launch_bounds__(kJ) void k_gesvj(T *__restrict__ w, T *__restrict__
           const T tt = (ze >= T(0) ? T(1) : T(-1)) / (fabs(ze) + sqrt(T(1) + ze * ze));
           const T c = T(1) / sqrt(T(1) + tt * tt), s = c * tt;
           if (s != T(0)) {
-            for (int j = lane; j < L; j += 64) {
-              const T x = W[(long long)p * L + j], y = W[(long long)q * L + j];
-              W[(long long)p * L + j] = c * x - s * y;
-              W[(long long)q * L + j] = s * x + c * y;
-            }
-            for (int j = lane; j < r; j += 64) {
-              const T x = VT[(long long)p * r + j], y = VT[(long long)q * r + j];
-              VT[(long long)p * r + j] = c * x - s * y;
-              VT[(long long)q * r + j] = s * x + c * y;
-            }
+            rotate_rows(W + (long long)p * L, W + (long long)q * L, L, lane, c, s);
+            rotate_rows(VT + (long long)p * r, VT + (long long)q * r, r, lane, c, s);
             if (lane == 0) s_rot = 1;
           }
         }

@@ -13,8 +13,9 @@ Results agree with NumPy's to rounding (LAPACK blocks its algorithms and
 orders its sums differently); singular vectors and eigenvectors are unique
 only up to sign, so they agree through reconstruction, not entry by entry.
 float32 stays float32, integers and bool compute in float64, float16 is
-refused (as NumPy's linalg refuses it).  ``eig`` / ``eigvals`` (complex
-results) are not provided.
+refused (as NumPy's linalg refuses it).  ``eig`` / ``eigvals`` serve
+exactly symmetric matrices (real eigenpairs); general matrices, whose
+eigenpairs can be complex, raise NotImplementedError.
 """
 from __future__ import annotations
 
@@ -40,6 +41,7 @@ SlogdetResult = namedtuple("SlogdetResult", ["sign", "logabsdet"])
 QRResult = namedtuple("QRResult", ["Q", "R"])
 EighResult = namedtuple("EighResult", ["eigenvalues", "eigenvectors"])
 SVDResult = namedtuple("SVDResult", ["U", "S", "Vh"])
+EigResult = namedtuple("EigResult", ["eigenvalues", "eigenvectors"])
 
 
 def _asarray(a):
@@ -279,14 +281,32 @@ def eigvalsh(a, UPLO="L"):
     return _eigh(a, UPLO, False)[0]
 
 
+def _exactly_symmetric(A):
+    from .reductions import all as _all
+    return bool(_all(A == A.swapaxes(-1, -2)))
+
+
 def eig(a):
-    raise NotImplementedError("eig (complex eigenpairs of a general matrix) is not supported "
-                              "on the device; use eigh for symmetric matrices")
+    """Exactly symmetric matrices: their eigenpairs are real, which NumPy
+    returns as real arrays too (ascending here, LAPACK's geev order there;
+    vectors unit length, sign arbitrary).  A general matrix can have
+    complex eigenpairs, which device arrays cannot hold."""
+    A = _asarray(a)
+    _square(A)
+    if not _exactly_symmetric(A):
+        raise NotImplementedError("eig of a non-symmetric matrix (complex eigenpairs) is not "
+                                  "supported on the device")
+    w, v = _eigh(A, "L", True)
+    return EigResult(w, v)
 
 
 def eigvals(a):
-    raise NotImplementedError("eigvals (complex eigenvalues of a general matrix) is not "
-                              "supported on the device; use eigvalsh for symmetric matrices")
+    A = _asarray(a)
+    _square(A)
+    if not _exactly_symmetric(A):
+        raise NotImplementedError("eigvals of a non-symmetric matrix (complex eigenvalues) is "
+                                  "not supported on the device")
+    return _eigh(A, "L", False)[0]
 
 
 # -------------------------------------------------------------------- SVD

@@ -303,3 +303,18 @@ def test_split_k_matmul():
             np.testing.assert_allclose(got, want, rtol=rt, atol=rt * np.sqrt(k) * 5)
     x = rng.standard_normal((64, 1 << 18))
     np.testing.assert_allclose(_h(cp.cov(cp.array(x))), np.cov(x), rtol=1e-10, atol=1e-12)
+
+
+def test_eig_symmetric():
+    g = _m((6, 6), np.float64, 500, well=False)
+    s = (g + g.T) / 2
+    w, v = LA.eig(cp.array(s))
+    ww = np.linalg.eig(s)[0]
+    assert _h(w).dtype == ww.dtype == np.float64
+    np.testing.assert_allclose(np.sort(_h(w)), np.sort(ww), rtol=1e-10, atol=1e-12)
+    vh = _h(v)
+    np.testing.assert_allclose(s @ vh, vh * _h(w)[None, :], rtol=0, atol=1e-10)
+    np.testing.assert_allclose(np.sort(_h(LA.eigvals(cp.array(s)))), np.sort(np.linalg.eigvals(s)),
+                               rtol=1e-10, atol=1e-12)
+    with pytest.raises(NotImplementedError):
+        LA.eig(cp.array(g))

@@ -113,6 +113,7 @@ def test_views_and_axes():
     _same(gz, z)
 
 
+@pytest.mark.filterwarnings("ignore:Arrays of 2-dimensional vectors are deprecated")
 def test_small_arithmetic():
     a = _x((6, 5))
     g = cp.array(a)

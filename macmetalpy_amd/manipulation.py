@@ -671,6 +671,10 @@ def average(a, axis=None, weights=None, returned=False, *, keepdims=False):
 
 
 # ------------------------------------------------------------ set / stats
+_UNIQUE_COUNT_MIN = 1 << 16      # from this size, integer unique may count instead of sort
+_UNIQUE_COUNT_RANGE = 1 << 22    # value range counted (32 MiB of int64 counts at most)
+
+
 def unique(ar, return_index=False, return_inverse=False, return_counts=False, axis=None,
            *, equal_nan=True):
     """Sorted unique elements of the flattened array (device sort, then the
@@ -693,6 +697,17 @@ def unique(ar, return_index=False, return_inverse=False, return_counts=False, ax
         if return_counts:
             res.append(ndarray._empty_device((0,), np.int64))
         return res[0] if len(res) == 1 else tuple(res)
+    if (not return_index and not return_inverse and x.dtype.kind in "iu"
+            and n >= _UNIQUE_COUNT_MIN):
+        lo, hi = int(reductions.min(x)), int(reductions.max(x))
+        if hi - lo < _UNIQUE_COUNT_RANGE:
+            # small value range: counts per value (the counting kernel) give
+            # the sorted distinct values and their counts exactly
+            from .extras import bincount
+            counts = bincount(x - lo if lo else x)
+            nz = _flat_nonzero(counts != 0)
+            vals = (nz + lo).astype(x.dtype) if lo else nz.astype(x.dtype)
+            return (vals, take(counts, nz)) if return_counts else vals
     perm = argsort(x, kind="stable")
     s = take(x, perm)
     first = ndarray._empty_device((n,), np.bool_)

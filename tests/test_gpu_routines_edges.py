@@ -69,3 +69,18 @@ def test_scalars_and_size_one():
     _same(cp.gradient(cp.array(np.array([1.0, 4.0]))), np.gradient(np.array([1.0, 4.0])))
     _same(cp.cumulative_sum(cp.array(np.array([], np.int32)), include_initial=True),
           np.cumulative_sum(np.array([], np.int32), include_initial=True))
+
+
+def test_unique_counting_path():
+    # integer inputs of >= 2^16 elements with a value range < 2^22 are counted
+    rng = np.random.default_rng(77)
+    for dt, lo, hi in ((np.int32, -500, 500), (np.int64, 10 ** 12, 10 ** 12 + 3000), (np.uint16, 0, 60000),
+                       (np.int16, -3, 3), (np.uint32, 7, 8)):
+        x = rng.integers(lo, hi, 1 << 17).astype(dt)
+        _same(cp.unique(cp.array(x)), np.unique(x))
+        g, c = cp.unique(cp.array(x), return_counts=True)
+        wv, wc = np.unique(x, return_counts=True)
+        _same(g, wv)
+        _same(c, wc)
+    wide = rng.integers(-2 ** 40, 2 ** 40, 1 << 17)               # range too wide: sorted path
+    _same(cp.unique(cp.array(wide)), np.unique(wide))

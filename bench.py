@@ -514,15 +514,16 @@ def _env(be):
 
 
 ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
-            "cumsum_f32", "matmul_f16", "sort_f32")
+            "cumsum_f32", "matmul_f16", "sort_f32", "c5_fused", "sum_all", "sum_axis1",
+            "argmax_all", "argmax_axis1", "c1_2p20")
 
 
 def run_only(cp, be, name, steps):
     """One op of a benchmark workload, `steps` launches (for counter
     profiling); copy_f32 is a plain strided-copy kernel of 2^28 floats
     (1 GiB read + 1 GiB written) used to calibrate the byte counters."""
-    from macmetalpy_amd.workloads import (c2_float_inputs, c2_int_inputs, c3_scan_inputs,
-                                          c4_inputs)
+    from macmetalpy_amd.workloads import (c1_inputs, c2_float_inputs, c2_int_inputs, c3_matrix,
+                                          c3_scan_inputs, c4_inputs, c5_inputs)
     if name in ("add_f32", "sin_f32", "copy_f32"):
         a, b = (cp.array(x) for x in c2_float_inputs(N28))
     elif name in ("floor_divide_i32", "mod_i32"):
@@ -533,6 +534,12 @@ def run_only(cp, be, name, steps):
         del ci, cf
     elif name == "sort_f32":
         a = b = cp.array(np.random.default_rng(12).standard_normal(N28, dtype=np.float32))
+    elif name == "c5_fused":
+        a, b = (cp.array(x) for x in c5_inputs())
+    elif name in ("sum_all", "sum_axis1", "argmax_all", "argmax_axis1"):
+        a = b = cp.array(c3_matrix())
+    elif name == "c1_2p20":
+        a = b = cp.array(c1_inputs(1 << 20))
     else:  # matmul_f16
         a, b = (cp.array(x) for x in c4_inputs("f16"))
     a._ensure_gpu()
@@ -541,7 +548,13 @@ def run_only(cp, be, name, steps):
           "floor_divide_i32": lambda: cp.floor_divide(a, b), "mod_i32": lambda: cp.mod(a, b),
           "copy_f32": lambda: a.copy(), "cumsum_i32": lambda: cp.cumsum(a),
           "cumsum_f32": lambda: cp.cumsum(a), "matmul_f16": lambda: a @ b,
-          "sort_f32": lambda: cp.sort(a)}[name]
+          "sort_f32": lambda: cp.sort(a),
+          "c5_fused": lambda: cp.sum(cp.tanh(a * b + 1.0) * cp.exp(-cp.abs(a))
+                                     - cp.log1p(a * a), axis=1),
+          "sum_all": lambda: cp.sum(a), "sum_axis1": lambda: cp.sum(a, axis=1),
+          "argmax_all": lambda: cp.argmax(a, axis=None, keepdims=True),
+          "argmax_axis1": lambda: cp.argmax(a, axis=1),
+          "c1_2p20": lambda: cp.sqrt(cp.abs(a)) + cp.exp(-a ** 2)}[name]
     timer = EventTimer(be)
     for _ in range(steps):
         timer.run(name, lambda: _mat(fn()))

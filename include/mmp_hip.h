@@ -41,6 +41,9 @@ extern "C" {
 #define MMP_E_UNSUPPORTED 5 /* op / dtype combination not implemented     */
 #define MMP_E_RTC 6        /* hiprtc compile failed (log in last_error)   */
 #define MMP_E_INJECTED 7   /* failure forced by mmp_debug_fail_next       */
+#define MMP_E_WAIT 8       /* a device-side bounded wait ran out (a scan or
+                              reduction result since the last sync may be
+                              wrong); reported by mmp_sync / mmp_d2h      */
 
 /* ---- dtype codes (numpy dtype -> code, see macmetalpy_amd/_abi.py) ---- */
 #define MMP_BOOL 0
@@ -175,13 +178,17 @@ int mmp_memory_stats(size_t *in_use, size_t *cached);
 /* Host<->device copies.  The reference reads unified memory through
  * getBufferPointer (_metal_backend.py:233-236, ndarray.py:576-618); HBM is
  * discrete, so get()/set() become explicit copies.  h2d/d2h are synchronous
- * with respect to the host buffer; d2d is stream-ordered. */
+ * with respect to the host buffer; d2d is stream-ordered.  mmp_d2h returns
+ * MMP_E_WAIT (after completing the copy) when a device-side bounded wait
+ * ran out since the last check -- see mmp_wait_status. */
 int mmp_h2d(void *dst, const void *src, size_t bytes);
 int mmp_d2h(void *dst, const void *src, size_t bytes);
 int mmp_d2d(void *dst, const void *src, size_t bytes);
 
 /* Wait for all enqueued work.  Replaces MetalBackend.synchronize
- * (_metal_backend.py:359-372: dispatch of `_sync` with wait=True). */
+ * (_metal_backend.py:359-372: dispatch of `_sync` with wait=True).  Returns
+ * MMP_E_WAIT when a device-side bounded wait ran out since the last check
+ * (the flags live in pinned host memory, so the check costs no copy). */
 int mmp_sync(void);
 
 /* Stream-ordered timing events on the library stream (benchmarks). */
@@ -419,17 +426,23 @@ int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
 
 /* ---- device-side wait status ------------------------------------------ */
 /* Split reductions and scans combine results across workgroups with
- * bounded waits; a wait that runs out records a flag and lets the kernel
- * finish instead of hanging.  Waits for the library stream, stores the
- * flags raised since the last call in *flags (bit 0: scan look-back,
- * bit 1: reduction combine) and clears them.  Non-zero means a result
- * produced since the last call may be wrong.  No counterpart in the
- * reference (its Metal scan and reductions use separate passes). */
+ * bounded waits; a wait that runs out records a flag (pinned host memory,
+ * written by the kernel) and lets the kernel finish instead of hanging.
+ * Waits for the library stream, stores the flags raised since the last
+ * check in *flags (bit 0: scan look-back, bit 1: reduction combine) and
+ * clears them.  Non-zero means a result produced since the last check may
+ * be wrong; mmp_sync and mmp_d2h report the same flags as MMP_E_WAIT.  No
+ * counterpart in the reference (its Metal scan and reductions use
+ * separate passes). */
 int mmp_wait_status(uint32_t *flags);
 
 /* ---- test hooks -------------------------------------------------------- */
 /* Make the next `count`-th call of kind (1 = mmp_alloc, 2 = mmp_rtc_compile,
- * 3 = kernel launch) fail with MMP_E_INJECTED.  count 0 disables. */
+ * 3 = kernel launch) fail with MMP_E_INJECTED.  Kind 4: the `count`-th next
+ * split reduction or scan waits for a tag that its writers never write,
+ * with a spin limit of 64, so its bounded wait runs out at once (the
+ * kernel still finishes) and the next mmp_sync / mmp_d2h returns
+ * MMP_E_WAIT.  count 0 disables. */
 int mmp_debug_fail_next(int kind, int count);
 
 #ifdef __cplusplus

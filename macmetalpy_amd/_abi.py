@@ -19,6 +19,7 @@ MMP_E_ARG = 4
 MMP_E_UNSUPPORTED = 5
 MMP_E_RTC = 6
 MMP_E_INJECTED = 7
+MMP_E_WAIT = 8
 
 # ---- dtype codes ----------------------------------------------------------
 DTYPE_CODES: dict[np.dtype, int] = {

@@ -27,7 +27,8 @@ import numpy as np
 
 from . import _abi
 
-__all__ = ["HipBackend", "DeviceBuffer", "HipError", "lib_path", "load_library"]
+__all__ = ["HipBackend", "DeviceBuffer", "HipError", "HipWaitTimeoutError", "lib_path",
+           "load_library"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
@@ -52,7 +53,13 @@ class HipOutOfMemoryError(HipError, MemoryError):
     """Device allocation failed."""
 
 
+class HipWaitTimeoutError(HipError):
+    """A device-side bounded wait of a split reduction or scan ran out, so a
+    result computed since the last synchronisation may be wrong."""
+
+
 _ERR_CLASSES = {
+    _abi.MMP_E_WAIT: HipWaitTimeoutError,
     _abi.MMP_E_UNSUPPORTED: HipUnsupportedError,
     _abi.MMP_E_ARG: HipArgumentError,
     _abi.MMP_E_OOM: HipOutOfMemoryError,
@@ -263,6 +270,14 @@ class HipBackend:
         f = ctypes.c_uint32()
         _check(self._lib.mmp_wait_status(ctypes.byref(f)), "mmp_wait_status")
         return f.value
+
+    def debug_fail_next(self, kind: int, count: int = 1) -> None:
+        """Test hook: make the ``count``-th next call of ``kind`` fail (1
+        allocation, 2 runtime compile, 3 kernel launch) or, for kind 4, make
+        the ``count``-th next split reduction or scan give up its bounded
+        wait at once (reported as HipWaitTimeoutError by the next
+        synchronize / get)."""
+        _check(self._lib.mmp_debug_fail_next(int(kind), int(count)), "mmp_debug_fail_next")
 
     def memory_stats(self) -> tuple[int, int]:
         a, b = _c_sz(), _c_sz()

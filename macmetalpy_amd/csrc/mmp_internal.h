@@ -36,6 +36,27 @@ enum { SCRATCH_REDUCE_PARTIALS = 0, SCRATCH_REDUCE_TICKETS = 1,
 // the flag array never needs clearing between calls.
 uint32_t next_generation();
 
+// Flags of device-side bounded waits that ran out, in pinned host memory
+// that kernels write with system-scope stores: word 0 scan look-back,
+// word 1 reduction combine.  Read (and cleared) by the host after a stream
+// synchronisation, so checking them costs no device round trip.
+unsigned *wait_flags();
+// Flags raised since the last call (bit 0 scan, bit 1 reduction), cleared.
+// Only meaningful after the stream has been synchronised.
+uint32_t take_wait_flags();
+
+// Parameters of the next bounded cross-workgroup wait.  Normally the spin
+// limit is large and readers expect the call's own tag (tag_offset 0).
+// mmp_debug_fail_next(4, n) makes the n-th next split reduction or scan
+// wait for a tag its writers never write, with a spin limit of 64, so the
+// wait runs out at once and the kernel still finishes (a test of the
+// timeout reporting that needs no hung or faulting kernel).
+struct WaitParams {
+  long long spin_limit;
+  unsigned tag_offset;
+};
+WaitParams wait_params();
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace mmpi

@@ -43,7 +43,6 @@ constexpr long long kTargetBlocks = MMP_REDUCE_TARGET_BLOCKS;
 constexpr long long kMaxSplits = 16384;
 constexpr int kUnroll = MMP_REDUCE_UNROLL;   // 16-byte loads in flight per thread
 constexpr int kColUnroll = 8;                // strided layouts: rows in flight per thread
-constexpr long long kSpinLimit = 1ll << 26;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 template <typename T> union Pack {
@@ -429,7 +428,7 @@ __device__ __forceinline__ void put_tagged(unsigned long long *slot, const A &v,
 // Spins (bounded) until every word of the slot carries `tag`.
 template <typename A>
 __device__ __forceinline__ A get_tagged(const unsigned long long *slot, unsigned tag,
-                                        unsigned *timeout) {
+                                        unsigned *timeout, long long spin_limit) {
   constexpr int W = words_of<A>();
   unsigned buf[W];
 #pragma unroll
@@ -438,8 +437,8 @@ __device__ __forceinline__ A get_tagged(const unsigned long long *slot, unsigned
     long long spins = 0;
     while (((w = __hip_atomic_load(slot + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
            tag) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins > spin_limit) {
+        __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -454,8 +453,10 @@ __device__ __forceinline__ A get_tagged(const unsigned long long *slot, unsigned
 struct ReduceScratch {
   unsigned long long *words;  // tagged partial words
   unsigned *tickets;          // arrival counters (left at 0)
-  unsigned *timeout;          // set to 1 if a wait ran out
-  unsigned tag;               // this call's generation
+  unsigned *timeout;          // pinned host word, set to 1 if a wait ran out
+  unsigned tag;               // this call's generation (written)
+  unsigned read_tag;          // tag the combine waits for (== tag unless forced)
+  long long spin_limit;       // bound of every wait
 };
 
 // Last-arrival combine of the S partials of one row.  Returns true in the
@@ -496,7 +497,7 @@ __device__ bool last_block_combine(typename R::A v, unsigned long long *words, u
       if (k >= S) break;
       bool ok = true;
 #pragma unroll
-      for (int j = 0; j < W; ++j) ok = ok && (unsigned)(w[b][j] >> 32) == sc.tag;
+      for (int j = 0; j < W; ++j) ok = ok && (unsigned)(w[b][j] >> 32) == sc.read_tag;
       A part;
       if (ok) {
         unsigned buf[W];
@@ -504,7 +505,7 @@ __device__ bool last_block_combine(typename R::A v, unsigned long long *words, u
         for (int j = 0; j < W; ++j) buf[j] = (unsigned)w[b][j];
         __builtin_memcpy(&part, buf, sizeof(A));
       } else {
-        part = get_tagged<A>(words + (long long)k * W, sc.tag, sc.timeout);
+        part = get_tagged<A>(words + (long long)k * W, sc.read_tag, sc.timeout, sc.spin_limit);
       }
       acc = R::comb(acc, part);
     }
@@ -619,8 +620,8 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x,
   if (!is_last) return;
   A acc = R::ident();
   for (int k = 0; k < S; ++k)
-    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.tag,
-                                     sc.timeout));
+    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.read_tag,
+                                     sc.timeout, sc.spin_limit));
   if (c < inner) out[o * inner + c] = finalize<OP, T, To>(acc, len);
   if (threadIdx.x == 0)
     __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -675,8 +676,8 @@ __global__ __launch_bounds__(kBlock) void k_argreduce_cols(const T *__restrict__
   if (!is_last) return;
   A acc = R::ident();
   for (int k = 0; k < S; ++k)
-    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.tag,
-                                     sc.timeout));
+    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.read_tag,
+                                     sc.timeout, sc.spin_limit));
   if (c < inner) out[o * inner + c] = acc.i;
   if (threadIdx.x == 0)
     __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -712,9 +713,11 @@ int reduce_scratch(long long count, long long nticket, ReduceScratch *sc) {
   if (st) return st;
   sc->tickets = (unsigned *)mmpi::scratch(mmpi::SCRATCH_REDUCE_TICKETS, 4ull * nticket, &st);
   if (st) return st;
-  sc->timeout = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st) + 2;
-  if (st) return st;
+  sc->timeout = mmpi::wait_flags() + 1;
   sc->tag = mmpi::next_generation();
+  const mmpi::WaitParams wp = mmpi::wait_params();
+  sc->read_tag = (sc->tag + wp.tag_offset) & 0x3fffffffu;
+  sc->spin_limit = wp.spin_limit;
   return MMP_OK;
 }
 

@@ -62,6 +62,7 @@ size_t round_size(size_t b) {
 void *g_scratch[mmpi::SCRATCH_NSLOTS] = {};
 size_t g_scratch_size[mmpi::SCRATCH_NSLOTS] = {};
 uint32_t g_generation = 0;
+unsigned *g_wait_flags = nullptr;  // pinned host words written by kernels
 
 // ---- fault injection (mmp_debug_fail_next) -------------------------------
 int g_fail_kind = 0, g_fail_count = 0;
@@ -93,6 +94,12 @@ int init_locked(int device) {
   if (int st = mmpi::check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking),
                                "hipStreamCreateWithFlags"))
     return st;
+  void *flags = nullptr;
+  if (int st = mmpi::check_hip(hipHostMalloc(&flags, 256, hipHostMallocMapped | hipHostMallocCoherent),
+                               "hipHostMalloc(wait flags)"))
+    return st;
+  std::memset(flags, 0, 256);
+  g_wait_flags = static_cast<unsigned *>(flags);
   g_dev.stream = s;
   g_dev.id = device;
   g_dev.cus = prop.multiProcessorCount;
@@ -188,6 +195,24 @@ void *scratch(int slot, size_t bytes, int *status) {
   return p;
 }
 
+unsigned *wait_flags() { return g_wait_flags; }
+
+uint32_t take_wait_flags() {
+  if (!g_wait_flags) return 0;
+  volatile unsigned *w = g_wait_flags;
+  const uint32_t f = (w[0] ? 1u : 0u) | (w[1] ? 2u : 0u);
+  if (f) {
+    w[0] = 0;
+    w[1] = 0;
+  }
+  return f;
+}
+
+WaitParams wait_params() {
+  if (inject(4)) return WaitParams{64, 1u};
+  return WaitParams{1ll << 26, 0u};
+}
+
 uint32_t next_generation() {
   // 30 usable bits (flags keep 2 state bits); 0 is never used so that
   // zero-filled scratch never matches a live generation.
@@ -197,6 +222,19 @@ uint32_t next_generation() {
 }
 
 }  // namespace mmpi
+
+namespace {
+// After a stream synchronisation: report device-side waits that ran out.
+int check_waits() {
+  const uint32_t f = mmpi::take_wait_flags();
+  if (!f) return MMP_OK;
+  return mmpi::fail(MMP_E_WAIT,
+                    "a device-side bounded wait ran out (%s%s): a %s result computed since the "
+                    "last synchronisation may be wrong",
+                    (f & 1u) ? "scan look-back" : "", f == 3u ? ", reduction combine" : (f == 2u ? "reduction combine" : ""),
+                    f == 1u ? "cumsum / cumprod" : (f == 2u ? "reduction" : "scan or reduction"));
+}
+}  // namespace
 
 // ========================================================================
 // C ABI
@@ -315,7 +353,9 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_dev.stream),
                                "hipMemcpyAsync(D2H)"))
     return st;
-  return mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize");
+  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+    return st;
+  return check_waits();
 }
 
 int mmp_d2d(void *dst, const void *src, size_t bytes) {
@@ -328,7 +368,9 @@ int mmp_d2d(void *dst, const void *src, size_t bytes) {
 
 int mmp_sync(void) {
   if (!g_dev.ready) return MMP_OK;
-  return mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize");
+  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+    return st;
+  return check_waits();
 }
 
 int mmp_event_create(void **ev) {
@@ -480,24 +522,14 @@ int mmp_wait_status(uint32_t *flags) {
   if (!flags) return mmpi::fail(MMP_E_ARG, "null pointer");
   *flags = 0;
   if (int st = mmpi::ensure_init()) return st;
-  // words: [0] scan ticket, [1] scan look-back timeout, [2] reduction timeout
-  unsigned *w = static_cast<unsigned *>(g_scratch[mmpi::SCRATCH_SCAN_COUNTER]);
-  if (!w) return MMP_OK;
   if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
     return st;
-  unsigned h[3] = {0, 0, 0};
-  if (int st = mmpi::check_hip(hipMemcpy(h, w, sizeof h, hipMemcpyDeviceToHost), "hipMemcpy"))
-    return st;
-  *flags = (h[1] ? 1u : 0u) | (h[2] ? 2u : 0u);
-  if (*flags) {
-    if (int st = mmpi::check_hip(hipMemset(w + 1, 0, 2 * sizeof(unsigned)), "hipMemset"))
-      return st;
-  }
+  *flags = mmpi::take_wait_flags();
   return MMP_OK;
 }
 
 int mmp_debug_fail_next(int kind, int count) {
-  if (kind < 0 || kind > 3 || count < 0) return mmpi::fail(MMP_E_ARG, "bad injection request");
+  if (kind < 0 || kind > 4 || count < 0) return mmpi::fail(MMP_E_ARG, "bad injection request");
   g_fail_kind = count > 0 ? kind : 0;
   g_fail_count = count;
   return MMP_OK;

@@ -39,7 +39,6 @@ constexpr int kBlock = 256;
 constexpr int kItems = 16;                // consecutive elements per thread per sub-tile
 constexpr int kSubTile = kBlock * kItems; // 4096 elements staged through LDS at a time
 constexpr int kPad = kSubTile / kItems;   // one pad word per thread row in LDS
-constexpr long long kSpinLimit = 1ll << 26;
 // A tile (one ticket, one look-back) is kSub sub-tiles: 16384 elements for
 // 1-, 2- and 4-byte inputs, 8192 for 8-byte inputs (register budget).  A
 // same-address atomic ticket costs ~11 ns per workgroup on MI355X and the
@@ -104,7 +103,9 @@ __device__ __forceinline__ void publish(unsigned long long *d, A v, unsigned tag
 struct ScanScratch {
   unsigned *counter;          // tile ticket (left at 0 by the last tile)
   unsigned long long *desc;   // 2 words per tile
-  unsigned *timeout;          // set to 1 if a look-back wait ran out
+  unsigned *timeout;          // pinned host word, set to 1 if a look-back wait ran out
+  unsigned read_gen;          // generation look-back readers expect (== gen unless forced)
+  long long spin_limit;       // bound of every look-back wait
 };
 
 template <bool B> struct Bool { static constexpr bool value = B; };
@@ -164,7 +165,7 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
         const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
-        state = (t0 == t1 && (t0 >> 2) == gen) ? (t0 & 3u) : 0u;
+        state = (t0 == t1 && (t0 >> 2) == sc.read_gen) ? (t0 & 3u) : 0u;
         val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
       }
       const unsigned long long incl = __ballot(state == 2u) & in_window;
@@ -172,8 +173,8 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
       const int p = incl ? __ffsll((long long)incl) - 1 : kLook;  // nearest inclusive lane
       const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
       if (bad & nearer) {
-        if (++spins > kSpinLimit) {
-          if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++spins > sc.spin_limit) {
+          if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -198,8 +199,8 @@ __device__ typename S::A tail_prefix(const ScanScratch &sc, long long pred, unsi
   const unsigned long long w0 = __hip_atomic_load(sc.desc + 2 * pred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned long long w1 = __hip_atomic_load(sc.desc + 2 * pred + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
-  if (!(t0 == t1 && t0 == ((gen << 2) | 2u)))
-    __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!(t0 == t1 && t0 == ((sc.read_gen << 2) | 2u)))
+    __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   return __builtin_bit_cast(typename S::A, (w0 & 0xffffffffull) | (w1 << 32));
 }
 
@@ -472,11 +473,14 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
       ScanScratch sc;
       sc.counter = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st);
       if (st) return st;
-      sc.timeout = sc.counter + 1;
+      sc.timeout = mmpi::wait_flags();
       sc.desc = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES,
                                                       16ull * (ntiles > 0 ? ntiles : 1), &st);
       if (st) return st;
       const unsigned gen = mmpi::next_generation();
+      const mmpi::WaitParams wp = mmpi::wait_params();
+      sc.read_gen = (gen + wp.tag_offset) & 0x3fffffffu;
+      sc.spin_limit = wp.spin_limit;
       if (!vec) {
         hipLaunchKernelGGL((k_scan_rows<OP, Ti, To, 1>), dim3((unsigned)ntiles), dim3(kBlock), 0,
                            mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);

@@ -263,6 +263,7 @@ def _eigh(a, UPLO, want_vectors):
     sweeps = _ints((b,))
     if b and n:
         HipBackend().eigh(dtype_code(dt), a3._ptr, v._ptr, b, n, sweeps._ptr)
+        _check_converged(sweeps, "Eigenvalues did not converge")
     w = diagonal(a3, 0, 1, 2).copy()
     order = argsort(w, axis=-1)
     w = take_along_axis(w, order, axis=-1)
@@ -281,6 +282,23 @@ def eigvalsh(a, UPLO="L"):
     return _eigh(a, UPLO, False)[0]
 
 
+# Sweep cap of the device Jacobi kernels (csrc/linalg.hip, kMaxSweeps): a
+# matrix whose rotations have not died out by then reports that count.
+_MAX_SWEEPS = 60
+
+
+def _check_converged(sweeps, msg):
+    """Raise LinAlgError (NumPy's message) when a Jacobi solve of the batch
+    used every allowed sweep without converging."""
+    if int(sweeps.max()) >= _MAX_SWEEPS:
+        raise LinAlgError(msg)
+
+
+def _all_finite(A):
+    from .reductions import all as _all
+    return bool(_all(ew.unary("isfinite_op", A)))
+
+
 def _exactly_symmetric(A):
     from .reductions import all as _all
     return bool(_all(A == A.swapaxes(-1, -2)))
@@ -293,6 +311,8 @@ def eig(a):
     complex eigenpairs, which device arrays cannot hold."""
     A = _asarray(a)
     _square(A)
+    if A.size and not _all_finite(A):
+        raise LinAlgError("Array must not contain infs or NaNs")
     if not _exactly_symmetric(A):
         raise NotImplementedError("eig of a non-symmetric matrix (complex eigenpairs) is not "
                                   "supported on the device")
@@ -303,6 +323,8 @@ def eig(a):
 def eigvals(a):
     A = _asarray(a)
     _square(A)
+    if A.size and not _all_finite(A):
+        raise LinAlgError("Array must not contain infs or NaNs")
     if not _exactly_symmetric(A):
         raise NotImplementedError("eigvals of a non-symmetric matrix (complex eigenvalues) is "
                                   "not supported on the device")
@@ -324,7 +346,10 @@ def _svd(A, dt, compute_uv):
     vt = ndarray._empty_device((b, r, r), dt)
     sweeps = _ints((b,))
     if b and r:
+        if not _all_finite(W):  # LAPACK's gesdd does not converge on NaN / inf
+            raise LinAlgError("SVD did not converge")
         HipBackend().svd(dtype_code(dt), W._ptr, vt._ptr, b, r, L, sweeps._ptr)
+        _check_converged(sweeps, "SVD did not converge")
     s = ew.unary("sqrt_op", _sum(W * W, axis=-1))
     order = argsort(-s, axis=-1)
     s = take_along_axis(s, order, axis=-1)

@@ -704,9 +704,19 @@ def unique(ar, return_index=False, return_inverse=False, return_counts=False, ax
             # small value range: counts per value (the counting kernel) give
             # the sorted distinct values and their counts exactly
             from .extras import bincount
-            counts = bincount(x - lo if lo else x)
+            # offsets from the minimum: narrow signed inputs are widened
+            # first (hi - lo may exceed their range, e.g. full-range int16)
+            if x.dtype.kind == "i" and x.dtype.itemsize < 8:
+                off = x.astype(np.int64) - lo
+            else:
+                off = x - lo if lo else x
+            counts = bincount(off)
             nz = _flat_nonzero(counts != 0)
-            vals = (nz + lo).astype(x.dtype) if lo else nz.astype(x.dtype)
+            # back in x's dtype: nz + lo fits it, so its wrapping add is exact
+            # (and a uint64 minimum above the int64 range stays representable)
+            vals = nz.astype(x.dtype)
+            if lo:
+                vals = vals + x.dtype.type(lo)
             return (vals, take(counts, nz)) if return_counts else vals
     perm = argsort(x, kind="stable")
     s = take(x, perm)

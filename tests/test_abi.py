@@ -95,3 +95,21 @@ def test_rtc_build_without_device():
     assert code[:4] == b"\x7fELF"
     with pytest.raises(HipError, match="hiprtc compile failed"):
         rtc_build('extern "C" __global__ void k(float* x) { not valid c++ }', "-O3")
+
+
+def test_error_classes_and_hook_validation():
+    """Status codes map to the Python error classes callers catch; the
+    test hook rejects unknown kinds without touching a device."""
+    from macmetalpy_amd import _abi
+    from macmetalpy_amd import _backend as B
+    assert B._ERR_CLASSES[_abi.MMP_E_WAIT] is B.HipWaitTimeoutError
+    assert issubclass(B.HipWaitTimeoutError, B.HipError)
+    assert issubclass(B.HipOutOfMemoryError, MemoryError)
+    lib = B.load_library()
+    assert lib.mmp_debug_fail_next(5, 1) == _abi.MMP_E_ARG
+    assert lib.mmp_debug_fail_next(-1, 1) == _abi.MMP_E_ARG
+    assert lib.mmp_debug_fail_next(4, 0) == 0
+    import re
+    hdr = open(os.path.join(ROOT, "include", "mmp_hip.h")).read()
+    codes = dict(re.findall(r"#define (MMP_E_\w+) (\d+)", hdr))
+    assert int(codes["MMP_E_WAIT"]) == _abi.MMP_E_WAIT == 8

@@ -1,0 +1,120 @@
+"""Failure paths of the device library, forced from the host.
+
+Every case makes a call fail without a faulting or hung kernel: allocation,
+runtime-compile and launch failures are injected by the library's test hook
+(``mmp_debug_fail_next``), and a bounded cross-workgroup wait of a split
+reduction or scan is made to give up at once by having its readers expect
+a tag that no writer produces (the kernel still finishes).  The reference
+has no error channel below Python (its metalgpu calls return void,
+_metal_backend.py:221-263); its Python-level errors (``ndarray.py:355-359``,
+``_dtypes.py:133-134``) are covered by the host-logic tests.
+"""
+import gc
+
+import numpy as np
+import pytest
+
+import macmetalpy_amd as cp
+from macmetalpy_amd._backend import HipBackend, HipError, HipWaitTimeoutError
+
+pytestmark = pytest.mark.gpu
+
+
+def _in_use():
+    gc.collect()
+    cp.synchronize()
+    return HipBackend().memory_stats()[0]
+
+
+@pytest.fixture
+def be():
+    b = HipBackend()
+    yield b
+    b.debug_fail_next(0, 0)  # disarm whatever a failed test left armed
+
+
+def test_forced_reduction_wait_timeout_raises_on_synchronize(be):
+    x_np = np.random.default_rng(40).standard_normal(1 << 22).astype(np.float32)
+    x = cp.array(x_np)
+    good = float(cp.sum(x).get())
+    be.debug_fail_next(4, 1)
+    s = cp.sum(x)
+    with pytest.raises(HipWaitTimeoutError, match="reduction"):
+        cp.synchronize()
+    del s
+    # the flags were cleared by the report; the next sum is right again
+    assert be.wait_status() == 0
+    assert float(cp.sum(x).get()) == good
+    assert abs(good - float(np.sum(x_np, dtype=np.float64))) <= 1e-5 * abs(good) + 1e-3
+
+
+def test_forced_reduction_wait_timeout_raises_on_get(be):
+    x = cp.array(np.random.default_rng(41).standard_normal((4, 1 << 20)).astype(np.float32))
+    be.debug_fail_next(4, 1)
+    m = cp.max(x, axis=1)
+    with pytest.raises(HipWaitTimeoutError):
+        m.get()
+    assert be.wait_status() == 0
+
+
+def test_forced_scan_wait_timeout_raises(be):
+    x_np = np.random.default_rng(42).integers(-100, 100, 1 << 22, dtype=np.int32)
+    x = cp.array(x_np)
+    be.debug_fail_next(4, 1)
+    c = cp.cumsum(x)
+    with pytest.raises(HipWaitTimeoutError, match="scan"):
+        c.get()
+    assert be.wait_status() == 0
+    assert np.array_equal(cp.cumsum(x).get(), np.cumsum(x_np))
+
+
+def test_injected_allocation_failure_leaks_nothing(be):
+    a = cp.array(np.ones(1 << 20, np.float32))
+    b = cp.array(np.full(1 << 20, 2.0, np.float32))
+    (a + b).get()  # warm caches
+    before = _in_use()
+    be.debug_fail_next(1, 1)
+    with pytest.raises(HipError, match="injected"):
+        (a + b)._materialize_if_lazy()
+    assert _in_use() == before
+    assert np.array_equal((a + b).get(), np.full(1 << 20, 3.0, np.float32))
+
+
+def test_injected_launch_failure_leaks_nothing(be):
+    a = cp.array(np.arange(1 << 20, dtype=np.float32))
+    (a * 2.0).get()
+    before = _in_use()
+    be.debug_fail_next(3, 1)
+    with pytest.raises(HipError, match="injected"):
+        (a * 2.0)._materialize_if_lazy()
+    assert _in_use() == before
+    assert np.array_equal((a * 2.0).get(), np.arange(1 << 20, dtype=np.float32) * 2)
+
+
+def test_injected_compile_failure_is_not_cached(be):
+    g = np.random.default_rng(43)
+    a_np = g.uniform(0.5, 2.0, 4097).astype(np.float32)
+    b_np = g.uniform(0.5, 2.0, 4097).astype(np.float32)
+    a, b = cp.array(a_np), cp.array(b_np)
+    a._ensure_gpu()
+    b._ensure_gpu()
+    before = _in_use()
+
+    def expr():  # a structure no other test builds: compiled on first use
+        return cp.hypot(cp.arctan(a), cp.cbrt(b) * 0.375) - cp.expm1(a) * 0.625
+
+    be.debug_fail_next(2, 1)
+    with pytest.raises(HipError, match="injected"):
+        expr()._materialize_if_lazy()
+    assert _in_use() == before
+    with np.errstate(all="ignore"):
+        want = (np.hypot(np.arctan(a_np), np.cbrt(b_np) * np.float32(0.375))
+                - np.expm1(a_np) * np.float32(0.625))
+    got = expr().get()
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_rawkernel_compile_error_carries_the_log(be):
+    k = cp.RawKernel('extern "C" __global__ void bad(float* x) { x[0] = undefined_name; }', "bad")
+    with pytest.raises(HipError, match="undefined_name"):
+        k((64,), (cp.zeros(64, dtype=np.float32),))

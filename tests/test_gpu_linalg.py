@@ -318,3 +318,21 @@ def test_eig_symmetric():
                                rtol=1e-10, atol=1e-12)
     with pytest.raises(NotImplementedError):
         LA.eig(cp.array(g))
+
+
+def test_nan_input_and_convergence_errors():
+    """NumPy's behaviour on non-finite input: svd (and what is built on it)
+    raises LinAlgError('SVD did not converge'), eig / eigvals refuse NaN /
+    inf, eigh returns without raising."""
+    a = np.array([[np.nan, 0.0], [0.0, 1.0]])
+    A = cp.array(a)
+    for f in (cp.linalg.svd, cp.linalg.pinv, cp.linalg.matrix_rank, cp.linalg.cond):
+        with pytest.raises(cp.linalg.LinAlgError, match="SVD did not converge"):
+            f(A)
+        with pytest.raises(np.linalg.LinAlgError):
+            getattr(np.linalg, f.__name__)(a)
+    for f in (cp.linalg.eig, cp.linalg.eigvals):
+        with pytest.raises(cp.linalg.LinAlgError, match="infs or NaNs"):
+            f(A)
+    w, v = cp.linalg.eigh(A)  # no error, as NumPy
+    assert w.shape == (2,)

@@ -82,5 +82,15 @@ def test_unique_counting_path():
         wv, wc = np.unique(x, return_counts=True)
         _same(g, wv)
         _same(c, wc)
+    # full-range int16 (hi - lo > 32767 wraps in int16) and uint64 values
+    # above the int64 range in a small window
+    full16 = rng.integers(-32768, 32767, 1 << 17, endpoint=True).astype(np.int16)
+    big_u64 = (np.uint64(2 ** 64 - 5000) + rng.integers(0, 4000, 1 << 17).astype(np.uint64))
+    for x in (full16, big_u64):
+        g, c = cp.unique(cp.array(x), return_counts=True)
+        wv, wc = np.unique(x, return_counts=True)
+        _same(g, wv)
+        _same(c, wc)
+        _same(cp.unique(cp.array(x)), wv)
     wide = rng.integers(-2 ** 40, 2 ** 40, 1 << 17)               # range too wide: sorted path
     _same(cp.unique(cp.array(wide)), np.unique(wide))

@@ -5,6 +5,7 @@ the Python layer makes before any kernel runs (reference:
 ndarray._binary_op / _unary_op, ndarray.py:960-1243; _dtypes.py:77-146;
 _broadcasting.py:8-76; reductions.py:74-163)."""
 import itertools
+import os
 import warnings
 
 import numpy as np
@@ -146,3 +147,14 @@ def test_op_tables_are_consistent():
     assert set(_abi.EXPR_UNARY_OPS).isdisjoint(_abi.UNARY_OPS)
     assert set(_abi.EXPR_BINARY_OPS).isdisjoint(_abi.BINARY_OPS)
     assert _abi.BOOL_RESULT_OPS <= set(_abi.EXPR_UNARY_OPS) | set(_abi.EXPR_BINARY_OPS)
+
+
+def test_jacobi_convergence_check():
+    """A batch member that used every allowed Jacobi sweep raises NumPy's
+    LinAlgError message; fewer sweeps pass."""
+    from macmetalpy_amd import linalg as LA
+    LA._check_converged(np.array([3, 59, 12]), "SVD did not converge")
+    with pytest.raises(np.linalg.LinAlgError, match="SVD did not converge"):
+        LA._check_converged(np.array([3, LA._MAX_SWEEPS, 12]), "SVD did not converge")
+    src = open(os.path.join(os.path.dirname(LA.__file__), "csrc", "linalg.hip")).read()
+    assert f"constexpr int kMaxSweeps = {LA._MAX_SWEEPS};" in src

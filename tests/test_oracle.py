@@ -353,3 +353,195 @@ def test_sort_argsort_searchsorted_against_python():
     f = np.array([1.0, 2.0, np.nan, np.nan])
     assert ref.searchsorted(f, [np.nan, np.inf, 2.0], side="left").tolist() == [2, 2, 1]
     assert ref.searchsorted(f, [np.nan], side="right").tolist() == [4]
+
+
+# ------------------------------------------- pins added for every remaining def
+def test_mean_f64_closed_forms():
+    """mean of arange(n) is (n-1)/2; along each axis of a known matrix the
+    means are the row / column midpoints; mean == sum / count."""
+    for n in (1, 2, 7, 100001):
+        assert ref.mean_f64(np.arange(n, dtype=np.float32)) == (n - 1) / 2
+    m = np.arange(12, dtype=np.float32).reshape(3, 4)   # m[i, j] = 4 i + j
+    assert ref.mean_f64(m, axis=1).tolist() == [1.5, 5.5, 9.5]
+    assert ref.mean_f64(m, axis=0).tolist() == [4.0, 5.0, 6.0, 7.0]
+    assert ref.mean_f64(m) == 5.5
+    x = np.random.default_rng(31).standard_normal((17, 33)).astype(np.float32)
+    for ax, cnt in ((None, x.size), (0, 17), (1, 33)):
+        assert np.allclose(ref.mean_f64(x, axis=ax), ref.sum_f64(x, axis=ax) / cnt,
+                           rtol=1e-15, atol=0)
+    # float64 accumulation: a float32 accumulator would lose the small term
+    big = np.array([2.0 ** 25, 1.0, -(2.0 ** 25), 1.0], np.float32)
+    assert ref.mean_f64(big) == 0.5
+    assert ref.mean_f64(big).dtype == np.float64
+
+
+def test_normwise_rel_error_known_answers():
+    """||c - ref|| / ||ref||: c=[3,5], ref=[3,4] -> 1/5; invariant under a
+    common scale; a transposed result is an error, not zero."""
+    assert math.isclose(ref.normwise_rel_error([3.0, 5.0], [3.0, 4.0]), 0.2, rel_tol=1e-15)
+    for s in (1e-3, 7.0, 1e6):
+        assert math.isclose(ref.normwise_rel_error([3.0 * s, 5.0 * s], [3.0 * s, 4.0 * s]),
+                            0.2, rel_tol=1e-12)
+    a = np.array([[1.0, 2.0], [3.0, 4.0]])
+    # ||a.T - a||_F = sqrt(2) * 1, ||a||_F = sqrt(30)
+    assert math.isclose(ref.normwise_rel_error(a.T, a), math.sqrt(2.0 / 30.0), rel_tol=1e-14)
+    assert ref.normwise_rel_error(-a, a) == 2.0
+
+
+def test_fusion_chain_float32_path_against_python_loop():
+    """fusion_chain (the reference's float32 np.sum) and fusion_chain_terms
+    against per-element math-module loops; the float32 sum stays within
+    float32 accumulation error of the exact row sum."""
+    g = np.random.default_rng(8)
+    x = g.standard_normal((4, 257)).astype(np.float32)
+    r = g.uniform(0.5, 2.0, (1, 257)).astype(np.float32)
+    terms = ref.fusion_chain_terms(x, r)
+    assert terms.dtype == np.float32 and terms.shape == (4, 257)
+    pos = np.array([[math.tanh(float(np.float32(x[i, j] * r[0, j]) + np.float32(1.0)))
+                     * math.exp(-abs(float(x[i, j]))) for j in range(257)] for i in range(4)])
+    neg = np.array([[math.log1p(float(np.float32(x[i, j] * x[i, j]))) for j in range(257)]
+                    for i in range(4)])
+    loop_t = pos - neg
+    # each float32 term is within a few roundings of its two parts' size
+    eps = float(np.finfo(np.float32).eps)
+    assert np.all(np.abs(terms - loop_t) <= 4 * eps * (np.abs(pos) + np.abs(neg)))
+    z = ref.fusion_chain(x, r)
+    assert z.dtype == np.float32 and z.shape == (4,)
+    exact = loop_t.sum(axis=1)
+    bound = 257 * eps * (np.abs(pos) + np.abs(neg)).sum(axis=1)
+    assert np.all(np.abs(z - exact) <= bound)
+    # a dropped term (no log1p) or a wrong sign would be far outside the bound
+    wrong = np.sum(np.tanh(x * r + np.float32(1.0)) * np.exp(-np.abs(x)), axis=1)
+    assert np.all(np.abs(wrong - exact) > bound)
+
+
+# Known answers for every entry of the oracle's unary table: exact values a
+# plausible mistake (floor vs trunc, rint vs round-half-away, degrees vs
+# radians, log2 vs log10, reciprocal vs negation ...) would violate.
+_PI32 = np.float32(math.pi)
+UNARY_KNOWN = {
+    "neg_op": ([2.5, -0.0, 3.0], [-2.5, 0.0, -3.0]),
+    "negative_op": ([2.5, -1.0], [-2.5, 1.0]),
+    "positive_op": ([2.5, -1.0], [2.5, -1.0]),
+    "abs_op": ([-2.5, 3.0, -0.0], [2.5, 3.0, 0.0]),
+    "sign_op": ([-3.0, 0.0, 7.5], [-1.0, 0.0, 1.0]),
+    "square_op": ([-3.0, 1.5], [9.0, 2.25]),
+    "reciprocal_op": ([4.0, -0.5], [0.25, -2.0]),
+    "sqrt_op": ([16.0, 2.25, 0.0], [4.0, 1.5, 0.0]),
+    "cbrt_op": ([-27.0, 8.0, 0.125], [-3.0, 2.0, 0.5]),
+    "exp_op": ([0.0], [1.0]),
+    "exp2_op": ([3.0, -1.0, 10.0], [8.0, 0.5, 1024.0]),
+    "expm1_op": ([0.0], [0.0]),
+    "log_op": ([1.0], [0.0]),
+    "log2_op": ([1024.0, 0.25, 1.0], [10.0, -2.0, 0.0]),
+    "log10_op": ([1000.0, 0.01, 1.0], [3.0, -2.0, 0.0]),
+    "log1p_op": ([0.0], [0.0]),
+    "sin_op": ([0.0], [0.0]),
+    "cos_op": ([0.0], [1.0]),
+    "tan_op": ([0.0], [0.0]),
+    "asin_op": ([0.0, 1.0], [0.0, np.float32(math.pi / 2)]),
+    "acos_op": ([1.0, -1.0], [0.0, _PI32]),
+    "atan_op": ([0.0, 1.0], [0.0, np.float32(math.pi / 4)]),
+    "sinh_op": ([0.0], [0.0]),
+    "cosh_op": ([0.0], [1.0]),
+    "tanh_op": ([0.0, 20.0, -20.0], [0.0, 1.0, -1.0]),
+    "asinh_op": ([0.0], [0.0]),
+    "acosh_op": ([1.0], [0.0]),
+    "atanh_op": ([0.0], [0.0]),
+    # halves and negatives separate floor / ceil / rint / trunc / round
+    "floor_op": ([-2.5, -1.5, -0.5, 0.5, 1.5, 2.5], [-3.0, -2.0, -1.0, 0.0, 1.0, 2.0]),
+    "ceil_op": ([-2.5, -1.5, -0.5, 0.5, 1.5, 2.5], [-2.0, -1.0, -0.0, 1.0, 2.0, 3.0]),
+    "rint_op": ([-2.5, -1.5, -0.5, 0.5, 1.5, 2.5], [-2.0, -2.0, -0.0, 0.0, 2.0, 2.0]),
+    "trunc_op": ([-2.5, -1.5, -0.5, 0.5, 1.5, 2.5], [-2.0, -1.0, -0.0, 0.0, 1.0, 2.0]),
+    "degrees_op": ([_PI32, 0.0], [np.float32(180.0), 0.0]),
+    "radians_op": ([180.0, 90.0], [_PI32, np.float32(math.pi / 2)]),
+    "invert_op": ([0, -1, 5], [-1, 0, -6]),
+    "logical_not_op": ([0.0, 2.0, -0.0], [True, False, True]),
+    "isnan_op": ([np.nan, 1.0, np.inf], [True, False, False]),
+    "isinf_op": ([np.nan, -np.inf, np.inf, 1.0], [False, True, True, False]),
+    "isfinite_op": ([np.nan, np.inf, 1.0], [False, False, True]),
+    "signbit_op": ([-0.0, 0.0, -1.0, 2.0], [True, False, True, False]),
+}
+
+
+# float32 library functions (not correctly rounded in NumPy): ULP-bounded
+_UNARY_LIBM = frozenset({"cbrt_op", "exp2_op", "log2_op", "log10_op", "asin_op", "acos_op",
+                         "atan_op", "degrees_op", "radians_op"})
+
+
+def test_unary_table_known_answers_cover_every_entry():
+    assert set(UNARY_KNOWN) == set(ref.UNARY), set(ref.UNARY) ^ set(UNARY_KNOWN)
+    for op, (xs, want) in UNARY_KNOWN.items():
+        dt = np.int32 if op == "invert_op" else np.float32
+        got = ref.unary(op, np.array(xs, dtype=dt))
+        w = np.array(want, dtype=got.dtype)
+        assert got.dtype in (np.dtype(dt), np.dtype(np.bool_)), (op, got.dtype)
+        if op in _UNARY_LIBM:  # NumPy's float32 libm: within 2 ULP
+            assert int(ref.ulp_distance(got, w).max()) <= 2, (op, got, w)
+            continue
+        assert np.array_equal(got, w), (op, got, w)
+        if got.dtype.kind == "f":  # signed zeros are part of the answer
+            assert np.array_equal(np.signbit(got), np.signbit(w)), (op, got, w)
+
+
+BINARY_KNOWN = {
+    "add_op": ([1.5, -2.0], [2.25, 2.0], [3.75, 0.0]),
+    "sub_op": ([1.5, -2.0], [2.25, 2.0], [-0.75, -4.0]),
+    "mul_op": ([1.5, -2.0], [2.0, 3.0], [3.0, -6.0]),
+    "div_op": ([1.0, -3.0], [4.0, 2.0], [0.25, -1.5]),
+    "pow_op": ([2.0, 9.0, 4.0], [10.0, 0.5, -1.0], [1024.0, 3.0, 0.25]),
+    "mod_op": ([-7.0, 7.0], [3.0, -3.0], [2.0, -2.0]),
+    "fmod_op": ([-7.0, 7.0], [3.0, -3.0], [-1.0, 1.0]),
+    "floor_divide_op": ([-7.0, 7.0], [2.0, -2.0], [-4.0, -4.0]),
+    "min_op": ([1.0, np.nan], [2.0, 0.0], [1.0, np.nan]),
+    "max_op": ([1.0, np.nan], [2.0, 0.0], [2.0, np.nan]),
+    "fmin_op": ([1.0, np.nan], [2.0, 0.0], [1.0, 0.0]),
+    "fmax_op": ([1.0, np.nan], [2.0, 0.0], [2.0, 0.0]),
+    "atan2_op": ([1.0, 0.0], [1.0, -1.0], [np.float32(math.pi / 4), _PI32]),
+    "hypot_op": ([3.0, 5.0], [4.0, 12.0], [5.0, 13.0]),
+    "copysign_op": ([2.0, -3.0], [-1.0, 0.0], [-2.0, 3.0]),
+    "logaddexp_op": ([0.0], [0.0], [np.float32(math.log(2.0))]),
+    "logaddexp2_op": ([1.0, 3.0], [1.0, 3.0], [2.0, 4.0]),
+    "heaviside_op": ([-1.0, 0.0, 2.0], [0.5, 0.5, 0.5], [0.0, 0.5, 1.0]),
+    "nextafter_op": ([1.0], [2.0], [np.nextafter(np.float32(1.0), np.float32(2.0))]),
+    "bit_and_op": ([12, -1], [10, 7], [8, 7]),
+    "bit_or_op": ([12, -8], [10, 1], [14, -7]),
+    "bit_xor_op": ([12, -1], [10, 0], [6, -1]),
+    "lshift_op": ([1, 3], [4, 1], [16, 6]),
+    "rshift_op": ([16, -16], [2, 2], [4, -4]),
+    "logical_and_op": ([1.0, 0.0, 2.0], [1.0, 1.0, 0.0], [True, False, False]),
+    "logical_or_op": ([1.0, 0.0, 0.0], [0.0, 0.0, 3.0], [True, False, True]),
+    "logical_xor_op": ([1.0, 0.0, 1.0], [1.0, 0.0, 0.0], [False, False, True]),
+}
+
+
+def test_binary_table_known_answers_cover_every_entry():
+    assert set(BINARY_KNOWN) == set(ref.BINARY), set(ref.BINARY) ^ set(BINARY_KNOWN)
+    for op, (xa, xb, want) in BINARY_KNOWN.items():
+        dt = np.int32 if op in ("bit_and_op", "bit_or_op", "bit_xor_op", "lshift_op",
+                                "rshift_op") else np.float32
+        got = ref.binary(op, np.array(xa, dtype=dt), np.array(xb, dtype=dt))
+        w = np.array(want, dtype=got.dtype)
+        if op in ("atan2_op", "logaddexp_op"):  # float32 libm: within 2 ULP
+            assert int(ref.ulp_distance(got, w).max()) <= 2, (op, got, w)
+            continue
+        assert np.array_equal(got, w, equal_nan=got.dtype.kind == "f"), (op, got, w)
+
+
+def test_correctly_rounded_helper():
+    # float64 evaluation rounded once: sqrt(2) and e to the nearest float32
+    assert ref.correctly_rounded(np.sqrt, np.float32(2.0)) == np.float32(1.4142135)
+    assert ref.correctly_rounded(np.exp, np.float32(1.0)) == np.float32(2.7182817)
+    got = ref.correctly_rounded(np.sin, np.array([0.5], np.float32))
+    assert got.dtype == np.float32 and got[0] == np.float32(math.sin(0.5))
+
+
+def test_every_oracle_function_is_exercised_here():
+    """Each public function of the NumPy restatement is called by a test in
+    this file (so none is left without a check)."""
+    import inspect
+    src = open(__file__).read()
+    names = [n for n, f in inspect.getmembers(ref, inspect.isfunction)
+             if f.__module__ == ref.__name__ and not n.startswith("_")]
+    missing = [n for n in names if f"ref.{n}(" not in src]
+    assert not missing, missing

@@ -253,6 +253,24 @@ int mmp_fill(int dtype, int64_t n, const void *value, void *out);
 int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
                int64_t inner, const void *x, void *out);
 
+/* mmp_reduce for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, kernels
+ * and results as mmp_reduce, but the cross-workgroup partials and tickets
+ * live in a static device array of 4 MiB (16 KiB of tickets + 4 MiB -
+ * 16 KiB of partial words) set up by mmp_init, one copy per device held
+ * until the process ends; the call itself allocates nothing and never
+ * initialises the library (returns MMP_E_ARG before mmp_init).  Reductions
+ * along the last axis split exactly as mmp_reduce does (at most 2047
+ * partials: they always fit); strided reductions lower their split count
+ * until the partials fit, so a floating sum may round differently from
+ * mmp_reduce there.  A layout whose partials still do not fit is rejected
+ * with MMP_E_ARG.  Every call on a device shares its array: calls must not
+ * overlap on one device (they are ordered when issued from one thread on
+ * the library stream). */
+int mmp_reduce_noalloc(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+                       int64_t inner, const void *x, void *out);
+
 /* Same view; out (outer, inner) int64 indices of the first max/min
  * (MMP_R_ARGMAX / MMP_R_ARGMIN); a NaN counts as the extreme (first NaN
  * wins), as np.argmax does.  MMP_R_NANARGMAX / MMP_R_NANARGMIN skip NaNs

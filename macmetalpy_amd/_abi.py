@@ -186,7 +186,7 @@ EXPORTS = (
     "mmp_event_destroy",
     "mmp_unary", "mmp_binary", "mmp_binary_scalar", "mmp_copy",
     "mmp_copy_strided", "mmp_fill",
-    "mmp_reduce", "mmp_argreduce", "mmp_scan", "mmp_matmul",
+    "mmp_reduce", "mmp_reduce_noalloc", "mmp_argreduce", "mmp_scan", "mmp_matmul",
     "mmp_sort", "mmp_searchsorted", "mmp_take", "mmp_gather", "mmp_scatter", "mmp_nonzero",
     "mmp_bincount", "mmp_histogram",
     "mmp_lu", "mmp_lu_solve", "mmp_cholesky", "mmp_qr", "mmp_qr_q", "mmp_eigh", "mmp_svd",

@@ -96,6 +96,7 @@ _SIGNATURES = {
     "mmp_copy_strided": [_c_int, _c_int, _c_int, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p],
     "mmp_fill": [_c_int, _c_i64, _c_vp, _c_vp],
     "mmp_reduce": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    "mmp_reduce_noalloc": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_argreduce": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_scan": [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     "mmp_sort": [_c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int],

@@ -14,6 +14,12 @@ hipStream_t stream();
 int ensure_init();
 // Number of compute units of the current device.
 int cu_count();
+// Whether mmp_init has run, and the library's device.
+bool initialized();
+int device_id();
+// Resolve and clear the device's copy of mmp_reduce_noalloc's static
+// scratch (reduce.hip); called once per device by mmp_init.
+int noalloc_setup(int device);
 
 // Record an error message for mmp_last_error and return `code`.
 int fail(int code, const char *fmt, ...);

@@ -721,14 +721,35 @@ int reduce_scratch(long long count, long long nticket, ReduceScratch *sc) {
   return MMP_OK;
 }
 
+// Scratch of the allocation-free entry point (mmp_reduce_noalloc): the
+// static array `scratch` below, tickets first, then tagged partial words.
+constexpr size_t kNoAllocBytes = 4u << 20;
+constexpr size_t kNoAllocTicketBytes = 16u << 10;
+
+// Splits of a strided reduction for mmp_reduce_noalloc: the library's
+// choice, lowered until the partials fit the static scratch (S = 1 needs
+// none).
+template <typename A> int noalloc_col_splits(int S, long long groups) {
+  const long long per_split = groups * (long long)kBlock * words_of<A>() * 8;
+  const long long fit = (long long)(kNoAllocBytes - kNoAllocTicketBytes) / per_split;
+  if (S > fit) S = fit > 1 ? (int)fit : 1;
+  return S;
+}
+
+template <typename A>
+int noalloc_scratch(long long count, long long nticket, ReduceScratch *sc);
+
 template <int OP, typename T, typename To>
-int launch_reduce(long long outer, long long len, long long inner, const void *x, void *out) {
+int launch_reduce(long long outer, long long len, long long inner, const void *x, void *out,
+                  bool noalloc) {
   typedef typename Red<OP, T>::A A;
   ReduceScratch sc{};
   if (inner == 1) {
     const int S = choose_splits(outer, len);
     if (S > 1) {
-      if (int st = reduce_scratch<A>(outer * S, outer, &sc)) return st;
+      if (int st = noalloc ? noalloc_scratch<A>(outer * S, outer, &sc)
+                           : reduce_scratch<A>(outer * S, outer, &sc))
+        return st;
     }
     const long long grid = outer * S;
     if (grid > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "reduction grid too large");
@@ -738,9 +759,12 @@ int launch_reduce(long long outer, long long len, long long inner, const void *x
   }
   const long long ncb = mmpi::ceil_div(inner, kBlock);
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided reduction: outer extent %lld > 65535", outer);
-  const int S = col_splits(outer * ncb, len);
+  int S = col_splits(outer * ncb, len);
+  if (noalloc) S = noalloc_col_splits<A>(S, outer * ncb);
   if (S > 1) {
-    if (int st = reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)) return st;
+    if (int st = noalloc ? noalloc_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)
+                         : reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc))
+      return st;
   }
   hipLaunchKernelGGL((k_reduce_cols<OP, T, To>), dim3((unsigned)ncb, (unsigned)outer, (unsigned)S),
                      dim3(kBlock), 0, mmpi::stream(), (const T *)x, (To *)out, len, inner, S, sc);
@@ -788,30 +812,59 @@ template <int OP, typename T, typename To> constexpr bool out_ok() {
 }
 
 template <int OP, typename T, typename To>
-int reduce_to(long long outer, long long len, long long inner, const void *x, void *out) {
+int reduce_to(long long outer, long long len, long long inner, const void *x, void *out,
+              bool noalloc) {
   if constexpr (!out_ok<OP, T, To>()) {
     return mmpi::fail(MMP_E_UNSUPPORTED, "reduction op %d: unsupported output dtype", OP);
   } else {
-    return launch_reduce<OP, T, To>(outer, len, inner, x, out);
+    return launch_reduce<OP, T, To>(outer, len, inner, x, out, noalloc);
   }
 }
 
 template <int OP, typename T>
 int reduce_out(int out_dtype, long long outer, long long len, long long inner, const void *x,
-               void *out) {
+               void *out, bool noalloc) {
   switch (out_dtype) {
-    case MMP_F32: return reduce_to<OP, T, float>(outer, len, inner, x, out);
-    case MMP_F64: return reduce_to<OP, T, double>(outer, len, inner, x, out);
-    case MMP_F16: return reduce_to<OP, T, mmp_half>(outer, len, inner, x, out);
-    case MMP_I64: return reduce_to<OP, T, mmp_i64>(outer, len, inner, x, out);
-    case MMP_U64: return reduce_to<OP, T, mmp_u64>(outer, len, inner, x, out);
-    case MMP_I32: return reduce_to<OP, T, mmp_i32>(outer, len, inner, x, out);
-    case MMP_U32: return reduce_to<OP, T, mmp_u32>(outer, len, inner, x, out);
-    case MMP_I16: return reduce_to<OP, T, mmp_i16>(outer, len, inner, x, out);
-    case MMP_U16: return reduce_to<OP, T, mmp_u16>(outer, len, inner, x, out);
-    case MMP_BOOL: return reduce_to<OP, T, bool>(outer, len, inner, x, out);
+    case MMP_F32: return reduce_to<OP, T, float>(outer, len, inner, x, out, noalloc);
+    case MMP_F64: return reduce_to<OP, T, double>(outer, len, inner, x, out, noalloc);
+    case MMP_F16: return reduce_to<OP, T, mmp_half>(outer, len, inner, x, out, noalloc);
+    case MMP_I64: return reduce_to<OP, T, mmp_i64>(outer, len, inner, x, out, noalloc);
+    case MMP_U64: return reduce_to<OP, T, mmp_u64>(outer, len, inner, x, out, noalloc);
+    case MMP_I32: return reduce_to<OP, T, mmp_i32>(outer, len, inner, x, out, noalloc);
+    case MMP_U32: return reduce_to<OP, T, mmp_u32>(outer, len, inner, x, out, noalloc);
+    case MMP_I16: return reduce_to<OP, T, mmp_i16>(outer, len, inner, x, out, noalloc);
+    case MMP_U16: return reduce_to<OP, T, mmp_u16>(outer, len, inner, x, out, noalloc);
+    case MMP_BOOL: return reduce_to<OP, T, bool>(outer, len, inner, x, out, noalloc);
     default: return mmpi::fail(MMP_E_UNSUPPORTED, "reduction output dtype %d", out_dtype);
   }
+}
+
+template <typename T>
+int reduce_op(int op, int out_dtype, int64_t outer, int64_t len, int64_t inner, const void *x,
+              void *out, bool noalloc) {
+  switch (op) {
+    case MMP_R_SUM: return reduce_out<MMP_R_SUM, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_PROD: return reduce_out<MMP_R_PROD, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_MAX: return reduce_out<MMP_R_MAX, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_MIN: return reduce_out<MMP_R_MIN, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_MEAN: return reduce_out<MMP_R_MEAN, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_NANSUM:
+      return reduce_out<MMP_R_NANSUM, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_NANPROD:
+      return reduce_out<MMP_R_NANPROD, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_NANMAX:
+      return reduce_out<MMP_R_NANMAX, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_NANMIN:
+      return reduce_out<MMP_R_NANMIN, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    case MMP_R_NANMEAN:
+      return reduce_out<MMP_R_NANMEAN, T>(out_dtype, outer, len, inner, x, out, noalloc);
+    default: return mmpi::fail(MMP_E_ARG, "unknown reduction op %d", op);
+  }
+}
+
+int reduce_dispatch(int op, int dtype, int out_dtype, int64_t outer, int64_t len, int64_t inner,
+                    const void *x, void *out, bool noalloc) {
+  MMP_DISPATCH_ALL(dtype, { return reduce_op<T>(op, out_dtype, outer, len, inner, x, out, noalloc); })
 }
 
 int check_view(long long outer, long long len, long long inner, const void *x, const void *out) {
@@ -821,28 +874,81 @@ int check_view(long long outer, long long len, long long inner, const void *x, c
   return MMP_OK;
 }
 
+__global__ void k_zero_words(unsigned long long *p, long long n) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    p[i] = 0ull;
+}
+
 }  // namespace
+
+// The allocation-free entry point's scratch: one copy per device (each GPU
+// the library runs on holds it until the process ends).  In host code the
+// name is only a stand-in for the symbol; kernels get the device address
+// that hipGetSymbolAddress returned for the current device.
+static __device__ __align__(256) unsigned long long scratch[kNoAllocBytes / 8];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void *g_noalloc_ptr[kMaxDevices] = {};
+
+template <typename A>
+int noalloc_scratch(long long count, long long nticket, ReduceScratch *sc) {
+  const int dev = mmpi::device_id();
+  void *base = (dev >= 0 && dev < kMaxDevices) ? g_noalloc_ptr[dev] : nullptr;
+  if (!base) return mmpi::fail(MMP_E_ARG, "mmp_reduce_noalloc: scratch not set up on device %d", dev);
+  const unsigned long long words_bytes = 8ull * words_of<A>() * (unsigned long long)count;
+  if ((unsigned long long)nticket * 4ull > kNoAllocTicketBytes ||
+      words_bytes > kNoAllocBytes - kNoAllocTicketBytes)
+    return mmpi::fail(MMP_E_ARG,
+                      "mmp_reduce_noalloc: this reduction needs %llu bytes of partials and %lld "
+                      "tickets; the static scratch holds %zu bytes and %zu tickets",
+                      words_bytes, nticket, kNoAllocBytes - kNoAllocTicketBytes,
+                      kNoAllocTicketBytes / 4);
+  sc->tickets = static_cast<unsigned *>(base);
+  sc->words = reinterpret_cast<unsigned long long *>(static_cast<char *>(base) + kNoAllocTicketBytes);
+  sc->timeout = mmpi::wait_flags() + 1;
+  sc->tag = mmpi::next_generation();
+  const mmpi::WaitParams wp = mmpi::wait_params();
+  sc->read_tag = (sc->tag + wp.tag_offset) & 0x3fffffffu;
+  sc->spin_limit = wp.spin_limit;
+  return MMP_OK;
+}
+}  // namespace
+
+namespace mmpi {
+// Called by mmp_init with `device` current and the library stream created:
+// resolve this device's copy of `scratch` and clear it (tickets must start
+// at zero; every kernel leaves the tickets it used at zero).
+int noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(MMP_E_ARG, "device %d out of range", device);
+  void *p = nullptr;
+  if (int st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)), "hipGetSymbolAddress(scratch)"))
+    return st;
+  hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, stream(),
+                     static_cast<unsigned long long *>(p), (long long)(kNoAllocBytes / 8));
+  if (int st = check_hip(hipGetLastError(), "noalloc scratch clear")) return st;
+  g_noalloc_ptr[device] = p;
+  return MMP_OK;
+}
+}  // namespace mmpi
 
 extern "C" int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
                           int64_t inner, const void *x, void *out) {
   if (int st = mmpi::ensure_init()) return st;
   if (int st = check_view(outer, len, inner, x, out)) return st;
   if (outer * inner == 0) return MMP_OK;
-  MMP_DISPATCH_ALL(dtype, {
-    switch (op) {
-      case MMP_R_SUM: return reduce_out<MMP_R_SUM, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_PROD: return reduce_out<MMP_R_PROD, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_MAX: return reduce_out<MMP_R_MAX, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_MIN: return reduce_out<MMP_R_MIN, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_MEAN: return reduce_out<MMP_R_MEAN, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_NANSUM: return reduce_out<MMP_R_NANSUM, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_NANPROD: return reduce_out<MMP_R_NANPROD, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_NANMAX: return reduce_out<MMP_R_NANMAX, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_NANMIN: return reduce_out<MMP_R_NANMIN, T>(out_dtype, outer, len, inner, x, out);
-      case MMP_R_NANMEAN: return reduce_out<MMP_R_NANMEAN, T>(out_dtype, outer, len, inner, x, out);
-      default: return mmpi::fail(MMP_E_ARG, "unknown reduction op %d", op);
-    }
-  })
+  return reduce_dispatch(op, dtype, out_dtype, outer, len, inner, x, out, false);
+}
+
+extern "C" int mmp_reduce_noalloc(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
+                                  int64_t inner, const void *x, void *out) {
+  // Never initialises the library itself: initialisation allocates.
+  if (!mmpi::initialized())
+    return mmpi::fail(MMP_E_ARG, "mmp_reduce_noalloc: call mmp_init first");
+  if (int st = check_view(outer, len, inner, x, out)) return st;
+  if (outer * inner == 0) return MMP_OK;
+  return reduce_dispatch(op, dtype, out_dtype, outer, len, inner, x, out, true);
 }
 
 extern "C" int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len, int64_t inner,

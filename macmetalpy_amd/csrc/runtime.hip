@@ -107,6 +107,7 @@ int init_locked(int device) {
   g_dev.max_threads = prop.maxThreadsPerBlock;
   g_dev.total_mem = (int64_t)prop.totalGlobalMem;
   g_dev.arch = prop.gcnArchName;
+  if (int st = mmpi::noalloc_setup(device)) return st;
   g_dev.ready = true;
   return MMP_OK;
 }
@@ -167,6 +168,8 @@ int ensure_init() {
 }
 
 int cu_count() { return g_dev.cus; }
+bool initialized() { return g_dev.ready; }
+int device_id() { return g_dev.ready ? g_dev.id : -1; }
 
 void *scratch(int slot, size_t bytes, int *status) {
   *status = MMP_OK;

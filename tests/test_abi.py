@@ -113,3 +113,20 @@ def test_error_classes_and_hook_validation():
     hdr = open(os.path.join(ROOT, "include", "mmp_hip.h")).read()
     codes = dict(re.findall(r"#define (MMP_E_\w+) (\d+)", hdr))
     assert int(codes["MMP_E_WAIT"]) == _abi.MMP_E_WAIT == 8
+
+
+def test_reduce_noalloc_refuses_before_init():
+    """The allocation-free reduction never initialises the library (that
+    allocates): before mmp_init it returns MMP_E_ARG without a device."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from macmetalpy_amd._backend import load_library\n"
+            "lib = load_library()\n"
+            "st = lib.mmp_reduce_noalloc(0, 8, 8, 1, 16, 1, 4096, 8192)\n"
+            "print(st, lib.mmp_last_error().decode())\n") % ROOT
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    st, msg = out.stdout.split(" ", 1)
+    assert int(st) == _abi.MMP_E_ARG and "mmp_init" in msg

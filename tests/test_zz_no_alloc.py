@@ -1,0 +1,107 @@
+"""mmp_reduce_noalloc against mmp_reduce, through the C ABI.
+
+The allocation-free variant keeps its cross-workgroup partials in a static
+device array; it must give mmp_reduce's results (bit for bit where it
+splits the same way, within the float32 reduction tolerance of 1e-5
+relative where it lowers a strided split to fit) on two calls in a row,
+the second smaller, and must leave the allocator untouched.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from macmetalpy_amd import _abi
+from macmetalpy_amd._backend import HipBackend, load_library
+
+pytestmark = pytest.mark.gpu
+
+F32, F64, I32, I64 = (_abi.DTYPE_CODES[np.dtype(t)] for t in
+                      (np.float32, np.float64, np.int32, np.int64))
+
+
+def _dev(be, arr):
+    return be.array_to_buffer(np.ascontiguousarray(arr))
+
+
+def _both(be, lib, op, x, out_dt, outer, length, inner):
+    """Run both entry points on the same device input; return host results
+    and the allocator's (in_use, cached) around the no-alloc call."""
+    buf = _dev(be, x)
+    dc = _abi.DTYPE_CODES[x.dtype]
+    oc = _abi.DTYPE_CODES[np.dtype(out_dt)]
+    n_out = outer * inner
+    o1 = be.create_buffer(n_out, out_dt)
+    o2 = be.create_buffer(n_out, out_dt)
+    assert lib.mmp_reduce(op, dc, oc, outer, length, inner, buf.ptr, o1.ptr) == 0
+    be.synchronize()
+    stats0 = be.memory_stats()
+    st = lib.mmp_reduce_noalloc(op, dc, oc, outer, length, inner, buf.ptr, o2.ptr)
+    assert st == 0, lib.mmp_last_error().decode()
+    be.synchronize()
+    stats1 = be.memory_stats()
+    r1 = be.read_buffer(o1, 0, np.empty(n_out, out_dt))
+    r2 = be.read_buffer(o2, 0, np.empty(n_out, out_dt))
+    return r1, r2, stats0, stats1
+
+
+CASES = [
+    # (op, dtype, out dtype, (outer, len, inner) first, then smaller)
+    (_abi.REDUCE_SUM, np.float32, np.float32, (3, 1 << 20, 1), (2, 1 << 18, 1)),
+    (_abi.REDUCE_MEAN, np.float32, np.float32, (1, 1 << 22, 1), (1, 100003, 1)),
+    (_abi.REDUCE_MAX, np.float32, np.float32, (5, 1 << 19, 1), (1, 1 << 17, 1)),
+    (_abi.REDUCE_SUM, np.int32, np.int64, (2, 1 << 21, 1), (1, 70001, 1)),
+    (_abi.REDUCE_NANMEAN, np.float64, np.float64, (1, 1 << 20, 1), (3, 1 << 16, 1)),
+    (_abi.REDUCE_SUM, np.float32, np.float32, (1, 4096, 300), (2, 1024, 100)),
+    (_abi.REDUCE_SUM, np.int32, np.int64, (1, 8192, 257), (1, 1000, 33)),
+]
+
+
+@pytest.mark.parametrize("op,dt,odt,first,second", CASES)
+def test_noalloc_matches_reduce_twice(op, dt, odt, first, second):
+    be = HipBackend()
+    lib = load_library()
+    rng = np.random.default_rng(90 + op)
+    for shape in (first, second):
+        outer, length, inner = shape
+        if np.dtype(dt).kind == "f":
+            x = rng.standard_normal(outer * length * inner).astype(dt)
+            if op == _abi.REDUCE_NANMEAN:
+                x[::97] = np.nan
+        else:
+            x = rng.integers(-1000, 1000, outer * length * inner).astype(dt)
+        r1, r2, s0, s1 = _both(be, lib, op, x, odt, outer, length, inner)
+        assert s0 == s1, (s0, s1)  # nothing allocated or freed
+        assert r1.tobytes() == r2.tobytes(), (shape, r1[:4], r2[:4])
+
+
+def test_noalloc_lowered_strided_split_within_tolerance():
+    """(65536, 2048) along axis 0: mmp_reduce splits the column sums into
+    more partials than the static scratch holds, so the no-alloc variant
+    uses fewer (float64 partials either way): float32 results within 1e-5
+    relative of the float64 sums, integer sums bit-exact; then a smaller
+    input."""
+    be = HipBackend()
+    lib = load_library()
+    rng = np.random.default_rng(95)
+    for rows, cols in ((65536, 2048), (8192, 512)):
+        xf = rng.standard_normal((rows, cols)).astype(np.float32)
+        r1, r2, s0, s1 = _both(be, lib, _abi.REDUCE_SUM, xf, np.float32, 1, rows, cols)
+        assert s0 == s1
+        want = xf.astype(np.float64).sum(axis=0)
+        scale = np.abs(xf).astype(np.float64).sum(axis=0)
+        assert np.all(np.abs(r2 - want) <= 1e-5 * scale)
+        assert np.all(np.abs(r1 - want) <= 1e-5 * scale)
+        xi = rng.integers(-50, 50, (rows, cols)).astype(np.int32)
+        q1, q2, _, _ = _both(be, lib, _abi.REDUCE_SUM, xi, np.int64, 1, rows, cols)
+        assert np.array_equal(q1, q2) and np.array_equal(q2, xi.sum(axis=0, dtype=np.int64))
+
+
+def test_noalloc_rejects_bad_arguments():
+    be = HipBackend()
+    lib = load_library()
+    x = be.create_buffer(16, np.float32)
+    o = be.create_buffer(1, np.float32)
+    assert lib.mmp_reduce_noalloc(_abi.REDUCE_SUM, F32, F32, 1, 0, 1, x.ptr, o.ptr) == _abi.MMP_E_ARG
+    assert lib.mmp_reduce_noalloc(99, F32, F32, 1, 16, 1, x.ptr, o.ptr) == _abi.MMP_E_ARG
+    assert lib.mmp_reduce_noalloc(_abi.REDUCE_SUM, F32, F32, 1, 16, 1, None, o.ptr) == _abi.MMP_E_ARG

@@ -164,6 +164,13 @@ BOOL_RESULT_OPS = frozenset({"logical_not_op", "isnan_op", "isinf_op", "isfinite
 # another one).
 OWN_INPUT_OPS = frozenset({"bitwise_count_op"})
 
+# Ops with a fast_math form in mmp_ops.h (``<fn>_fast``: hardware
+# transcendentals for float32 / float16; other dtypes take the accurate op).
+FAST_MATH_OPS = frozenset({
+    "exp_op", "exp2_op", "log_op", "log2_op", "log10_op", "sin_op", "cos_op", "tan_op",
+    "sqrt_op", "reciprocal_op", "tanh_op", "sinh_op", "cosh_op", "div_op", "pow_op",
+})
+
 # op_name -> mmp_ops.h function, for every unary / binary op
 UNARY_FN = {k: v[2] for k, v in UNARY_OPS.items()}
 UNARY_FN.update({k: v[1] for k, v in EXPR_UNARY_OPS.items()})

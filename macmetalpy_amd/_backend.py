@@ -8,9 +8,10 @@ method names and meanings, but
 
 * buffers are device allocations (HBM is not host-visible), so reading one
   is an explicit device-to-host copy;
-* kernels are typed C entry points (``unary``, ``binary``, ``reduce`` ...)
-  plus ``compile``/``launch`` for runtime-compiled HIP source, instead of
-  "compile this MSL text, pick a function, run it";
+* the library's own work goes through typed C entry points (``unary``,
+  ``binary``, ``reduce`` ...); ``execute_kernel(source, name, grid,
+  buffers)`` keeps the reference's "compile this source, pick a function,
+  run it" for HIP source (``compile`` / ``launch`` underneath);
 * every call checks the C status and raises with the library's message.
 
 There is no CPU fallback: if the library is missing or no GPU is present
@@ -28,7 +29,7 @@ import numpy as np
 from . import _abi
 
 __all__ = ["HipBackend", "DeviceBuffer", "HipError", "HipWaitTimeoutError", "lib_path",
-           "load_library"]
+           "load_library", "block_for_grid"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
@@ -191,6 +192,45 @@ class DeviceBuffer:
 
 _U32x3 = ctypes.c_uint32 * 3
 
+_BLOCK_BUDGET = 256
+
+
+def _largest_divisor(n: int, limit: int) -> int:
+    """Largest d <= limit dividing n, preferring multiples of 64."""
+    limit = max(1, min(limit, n))
+    best = 1
+    for d in range(limit, 0, -1):
+        if n % d == 0:
+            if d % 64 == 0:
+                return d
+            if best == 1:
+                best = d
+    return best
+
+
+def block_for_grid(grid) -> tuple:
+    """Uniform workgroup extents dividing the thread grid exactly (x first),
+    so that a kernel launched with exactly ``grid`` threads needs no bounds
+    check (Metal's dispatchThreads semantics)."""
+    bx = _largest_divisor(grid[0], _BLOCK_BUDGET)
+    by = _largest_divisor(grid[1], _BLOCK_BUDGET // bx) if len(grid) > 1 else 1
+    bz = _largest_divisor(grid[2], _BLOCK_BUDGET // (bx * by)) if len(grid) > 2 else 1
+    return (bx, by, bz)
+
+
+def _grid3(grid_size) -> tuple:
+    """int, 1-3 tuple or an object with width / height / depth (the
+    reference's MetalSize) -> a 3-tuple of thread counts."""
+    if isinstance(grid_size, (int, np.integer)):
+        return (int(grid_size), 1, 1)
+    if hasattr(grid_size, "width"):
+        return (int(grid_size.width), int(getattr(grid_size, "height", 1)),
+                int(getattr(grid_size, "depth", 1)))
+    g = tuple(int(v) for v in grid_size)
+    if not 1 <= len(g) <= 3:
+        raise ValueError("grid must have 1-3 dimensions")
+    return g + (1,) * (3 - len(g))
+
 
 class HipBackend:
     """Process-wide device context (one GPU, one stream)."""
@@ -206,6 +246,7 @@ class HipBackend:
             if cls._instance is None:
                 inst = super().__new__(cls)
                 inst._lib = load_library()
+                inst._exec_cache = {}
                 _check(inst._lib.mmp_init(int(os.environ.get("MMP_DEVICE", "0"))), "mmp_init")
                 cls._instance = inst
             return cls._instance
@@ -406,6 +447,54 @@ class HipBackend:
                C: int, ldc: int, sC: int) -> None:
         _check(self._lib.mmp_matmul(dcode, batch, M, N, K, A, lda, sA, B, ldb, sB,
                                     C, ldc, sC), "mmp_matmul")
+
+    # ------------------------------------------ reference kernel interface
+    def execute_kernel(self, shader_src: str, func_name, grid_size, buffers) -> None:
+        """Compile (cached), select and launch one kernel of ``shader_src``
+        with one thread per grid point (reference:
+        _metal_backend.py:313-357).  ``shader_src`` is HIP C++ (e.g. from
+        ``KernelCache().get_shader``); ``grid_size`` counts threads (int,
+        tuple or a MetalSize-like object); ``buffers`` are DeviceBuffers
+        (an ndarray's ``_buffer``), device ndarrays or None, bound in order.
+        The total thread count is passed as one extra trailing ``long long``
+        argument, which the cache's kernels bounds-check against and other
+        kernels may ignore.  Asynchronous, like the reference's
+        ``runFunction(wait=False)``; ``synchronize()`` waits."""
+        from ._fusion import RTC_OPTIONS
+        name = func_name.decode() if isinstance(func_name, bytes) else str(func_name)
+        key = (shader_src, name)
+        kern = self._exec_cache.get(key)
+        if kern is None:
+            kern = self.compile(shader_src, name, RTC_OPTIONS)
+            self._exec_cache[key] = kern
+        g = _grid3(grid_size)
+        total = g[0] * g[1] * g[2]
+        if total <= 0:
+            return
+        block = block_for_grid(g)
+        blocks = tuple(gi // bi for gi, bi in zip(g, block))
+        from ._elementwise import flush_lazy
+        args = []
+        for b in buffers:
+            if isinstance(b, DeviceBuffer):
+                dev = b
+                args.append(_c_vp(b.ptr))
+            elif hasattr(b, "_ensure_gpu"):  # an ndarray: upload / evaluate first
+                b._ensure_gpu()
+                dev = b._buffer
+                args.append(_c_vp(b._ptr))
+            elif b is None:
+                # the reference binds no buffer (-1); a kernel reading it here
+                # would fault, so refuse instead
+                raise ValueError("execute_kernel: buffer is None (the _buffer of a host-resident "
+                                 "array?); pass the array itself or a DeviceBuffer")
+            else:
+                raise TypeError(f"execute_kernel: unsupported buffer {type(b).__name__}")
+            if not dev.ptr:
+                raise ValueError("execute_kernel: buffer has been freed")
+            flush_lazy(dev)  # pending expressions reading it see the old data
+        args.append(_c_i64(total))
+        self.launch(kern, blocks, block, args)
 
     # -------------------------------------------------- runtime compile
     def compile(self, source: str, name: str, options: str = "") -> int:

@@ -37,6 +37,7 @@ import numpy as np
 
 from . import _abi
 from ._backend import HipBackend
+from ._config import get_config
 from ._dtypes import ctype_name, dtype_code
 
 __all__ = [
@@ -304,12 +305,25 @@ def _acc_type(dtype):
     return "mmp_i64", np.dtype(np.int64)
 
 
-def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode):
+_FAST_DTYPES = (np.dtype(np.float32), np.dtype(np.float16))
+
+
+def _op_fn(table, op_name, dtype, fast):
+    """mmp_ops.h function for ``op_name`` computing in ``dtype``; the
+    ``_fast`` form under fast_math for float32 / float16."""
+    fn = table[op_name]
+    if fast and op_name in _abi.FAST_MATH_OPS and dtype in _FAST_DTYPES:
+        return fn + "_fast"
+    return fn
+
+
+def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=False):
     """HIP source for ``prog``.
 
     kinds[k]: last-dim stride class of array leaf k ('c' unit, 'b' zero,
     's' general).  nouter: number of outer (row) dims (0 = 1-D launch).
     mode: 'map' (elementwise, contiguous output), 'sum' (row-sum epilogue).
+    fast: use the fast_math forms of the transcendentals.
     """
     nin, nsc = len(prog.arrays), len(prog.scalars)
     L = []
@@ -343,13 +357,13 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode):
                 src_t = ctype_name(prog.dtypes[step[1]])
                 rhs = f"mmp_convert<{t}, {src_t}>(t{step[1]})"
             elif kind == "unary":
-                rhs = f"{_abi.UNARY_FN[step[1]]}(t{step[2]})"
+                rhs = f"{_op_fn(_abi.UNARY_FN, step[1], prog.dtypes[i], fast)}(t{step[2]})"
             elif kind == "where":
                 rhs = f"(t{step[1]} ? t{step[2]} : t{step[3]})"
             elif step[1] in _abi.COMPARE_OPS:
                 rhs = f"(t{step[2]} {_abi.COMPARE_OPS[step[1]][1]} t{step[3]})"
             else:
-                rhs = f"{_abi.BINARY_FN[step[1]]}(t{step[2]}, t{step[3]})"
+                rhs = f"{_op_fn(_abi.BINARY_FN, step[1], prog.dtypes[i], fast)}(t{step[2]}, t{step[3]})"
             out.append(f"{indent}const {t} t{i} = {rhs};")
         return out
 
@@ -512,11 +526,12 @@ _struct_cache: dict = {}
 
 
 def _kernel_for_program(prog, kinds, nouter, out_dtype, vec, mode) -> int:
+    fast = get_config().fast_math
     key = (tuple(prog.steps), tuple(prog.dtypes), tuple(a._dtype for a in prog.arrays),
-           tuple(kinds), nouter, out_dtype, vec, mode)
+           tuple(kinds), nouter, out_dtype, vec, mode, fast)
     k = _struct_cache.get(key)
     if k is None:
-        k = _kernel_for(generate_source(prog, kinds, nouter, out_dtype, vec, mode))
+        k = _kernel_for(generate_source(prog, kinds, nouter, out_dtype, vec, mode, fast))
         with _cache_lock:
             _struct_cache[key] = k
     return k
@@ -669,6 +684,10 @@ def materialize_node(node: FusionNode, out_ptr: int) -> None:
     for s in node._shape:
         n *= s
     if n == 0:
+        return
+    if (get_config().fast_math and getattr(node, "_op_name", None) in _abi.FAST_MATH_OPS
+            and node._dtype in _FAST_DTYPES):
+        run_map(node, None, out_ptr)  # the generated kernel carries the fast form
         return
     if is_precompiled_unary(node):
         code = _abi.UNARY_OPS[node._op_name][0]

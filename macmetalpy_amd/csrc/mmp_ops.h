@@ -787,3 +787,69 @@ template <typename To, typename From> MMP_DI To mmp_convert(From v) {
     return (To)v;
   }
 }
+
+// =====================================================================
+// fast_math forms (set_config(fast_math=True); the reference switches its
+// elementwise shader to Metal's fast:: functions, _kernels.py:26-27).  For
+// float32 (and float16, computed in float32) they use the hardware
+// transcendental instructions -- v_exp_f32 / v_log_f32 (base 2), v_sin_f32
+// / v_cos_f32 (argument in revolutions), v_sqrt_f32, v_rcp_f32 -- instead of
+// the correctly rounded or 2-ULP library functions.  Bound (the reference's
+// unary-math tolerance, rtol = atol = 1e-5): exp [-80, 80], log / log2 /
+// log10 [1e-30, 1e30], sin / cos [-100, 100], tan [-1.4, 1.4], sqrt,
+// reciprocal, divide, tanh / sinh / cosh [-10, 10], power with a positive
+// base in (0, 100] and exponent in [-4, 4].  Denormal inputs and results
+// may flush to zero.  float64 and integer operands take the accurate ops.
+// =====================================================================
+MMP_DI float mm_fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+MMP_DI float mm_fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+MMP_DI float mm_fast_sin(float x) { return __builtin_amdgcn_sinf(x * 0.159154943091895336f); }
+MMP_DI float mm_fast_cos(float x) { return __builtin_amdgcn_cosf(x * 0.159154943091895336f); }
+MMP_DI float mm_fast_tanh(float x) {
+  // tanh|x| = 1 - 2 / (e^{2|x|} + 1); e = inf gives 1
+  const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(x) * 2.88539008177792682f);
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+  return __builtin_copysignf(t, x);
+}
+
+#define MMP_FAST_UNARY(NAME, FEXPR)                                           \
+  template <typename T> MMP_DI T op_##NAME##_fast(T x_) {                     \
+    if constexpr (__is_same(typename mmp_t<T>::C, float)) {                   \
+      const float x = (float)x_;                                              \
+      return (T)(FEXPR);                                                      \
+    } else {                                                                  \
+      return op_##NAME(x_);                                                   \
+    }                                                                         \
+  }
+MMP_FAST_UNARY(exp, mm_fast_exp(x))
+MMP_FAST_UNARY(exp2, __builtin_amdgcn_exp2f(x))
+MMP_FAST_UNARY(log, __builtin_amdgcn_logf(x) * 0.693147180559945309f)
+MMP_FAST_UNARY(log2, __builtin_amdgcn_logf(x))
+MMP_FAST_UNARY(log10, __builtin_amdgcn_logf(x) * 0.301029995663981195f)
+MMP_FAST_UNARY(sin, mm_fast_sin(x))
+MMP_FAST_UNARY(cos, mm_fast_cos(x))
+MMP_FAST_UNARY(tan, mm_fast_sin(x) * mm_fast_rcp(mm_fast_cos(x)))
+MMP_FAST_UNARY(sqrt, __builtin_amdgcn_sqrtf(x))
+MMP_FAST_UNARY(reciprocal, mm_fast_rcp(x))
+MMP_FAST_UNARY(tanh, mm_fast_tanh(x))
+MMP_FAST_UNARY(sinh, 0.5f * (mm_fast_exp(x) - mm_fast_rcp(mm_fast_exp(x))))
+MMP_FAST_UNARY(cosh, 0.5f * (mm_fast_exp(x) + mm_fast_rcp(mm_fast_exp(x))))
+
+template <typename T> MMP_DI T op_true_divide_fast(T a, T b) {
+  if constexpr (__is_same(typename mmp_t<T>::C, float)) {
+    return (T)((float)a * mm_fast_rcp((float)b));
+  } else {
+    return op_true_divide(a, b);
+  }
+}
+template <typename T> MMP_DI T op_power_fast(T a, T b) {
+  if constexpr (__is_same(typename mmp_t<T>::C, float)) {
+    const float x = (float)a, y = (float)b;
+    // positive finite base: 2^(y log2 x); anything else takes the exact pow
+    if (x > 0.0f && x < __builtin_inff())
+      return (T)__builtin_amdgcn_exp2f(y * __builtin_amdgcn_logf(x));
+    return op_power(a, b);
+  } else {
+    return op_power(a, b);
+  }
+}

@@ -73,6 +73,10 @@ struct RtcEntry {
   hipFunction_t fn;
 };
 std::unordered_map<std::string, RtcEntry> g_rtc;
+// Modules by (options, source): several kernels of one source share one
+// compilation (the reference's execute_kernel selects functions of one
+// library, _metal_backend.py:341-356).
+std::unordered_map<std::string, hipModule_t> g_rtc_mod;
 
 int init_locked(int device) {
   if (g_dev.ready) {
@@ -478,17 +482,27 @@ int mmp_rtc_compile(const char *src, const char *name, const char *options, void
   std::string arch = g_dev.arch;
   const size_t colon = arch.find(':');
   if (colon != std::string::npos) arch.resize(colon);
+  const std::string mkey = std::string(options ? options : "") + '\x01' + src;
+  hipModule_t mod = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_rtc_mod.find(mkey);
+    if (it != g_rtc_mod.end()) mod = it->second;
+  }
   std::vector<char> code;
-  if (int st = rtc_compile_code(src, options, arch.c_str(), &code)) return st;
-  hipModule_t mod;
-  if (int st = mmpi::check_hip(hipModuleLoadData(&mod, code.data()), "hipModuleLoadData"))
-    return st;
+  if (!mod) {
+    if (int st = rtc_compile_code(src, options, arch.c_str(), &code)) return st;
+    if (int st = mmpi::check_hip(hipModuleLoadData(&mod, code.data()), "hipModuleLoadData"))
+      return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_rtc_mod[mkey] = mod;
+  }
   hipFunction_t fn;
   hipError_t e = hipModuleGetFunction(&fn, mod, name);
   if (e != hipSuccess) {
-    // not extern "C": recompile asking hiprtc for the mangled name
+    // not extern "C": recompile asking hiprtc for the mangled name (the
+    // shared module stays loaded for the source's other kernels)
     (void)hipGetLastError();
-    (void)hipModuleUnload(mod);
     std::string expr = std::string("&") + name, lowered;
     if (int st = rtc_compile_code(src, options, arch.c_str(), &code, expr.c_str(), &lowered))
       return st;

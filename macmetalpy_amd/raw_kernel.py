@@ -23,7 +23,7 @@ from typing import Sequence, Union
 import numpy as np
 
 from . import _elementwise as ew
-from ._backend import HipBackend
+from ._backend import HipBackend, block_for_grid
 from .ndarray import ndarray
 
 __all__ = ["RawKernel"]
@@ -35,30 +35,6 @@ _CTYPES = {
     np.dtype(np.int16): ctypes.c_int16, np.dtype(np.uint16): ctypes.c_uint16,
     np.dtype(np.bool_): ctypes.c_bool,
 }
-
-_BUDGET = 256
-
-
-def _largest_divisor(n: int, limit: int) -> int:
-    """Largest d <= limit dividing n, preferring multiples of 64."""
-    limit = max(1, min(limit, n))
-    best = 1
-    for d in range(limit, 0, -1):
-        if n % d == 0:
-            if d % 64 == 0:
-                return d
-            if best == 1:
-                best = d
-    return best
-
-
-def block_for_grid(grid) -> tuple:
-    """Uniform workgroup extents dividing ``grid`` exactly (x first)."""
-    bx = _largest_divisor(grid[0], _BUDGET)
-    by = _largest_divisor(grid[1], _BUDGET // bx) if len(grid) > 1 else 1
-    bz = _largest_divisor(grid[2], _BUDGET // (bx * by)) if len(grid) > 2 else 1
-    return (bx, by, bz)
-
 
 class RawKernel:
     def __init__(self, source: str, func_name: str, options: str = "") -> None:

@@ -100,6 +100,9 @@ from .host_api import (
 )
 from .linalg_top import matmul, dot, vdot, inner
 from ._backend import HipBackend as MetalBackend  # the reference's backend class name
+from . import _gate as _gate_mod
+
+_gate_mod.setup()  # the native dispatch gate takes over the hot elementwise path
 from . import linalg
 from . import random
 from . import fft

@@ -141,7 +141,7 @@ def load_library():
         if not os.path.exists(path):
             raise HipError(
                 f"{path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
-                "or `python -m macmetalpy_amd.csrc.build`")
+                "or `python macmetalpy_amd/csrc/build.py`")
         lib = ctypes.CDLL(path)
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(lib, name)
@@ -164,30 +164,11 @@ def _i64_array(vals: Sequence[int]):
     return arr
 
 
-class DeviceBuffer:
-    """Owning handle to one device allocation (the reference's ``_Buffer``,
-    _metal_backend.py:121-165).  Freed back to the stream-ordered pool when
-    the last reference goes away."""
-
-    __slots__ = ("ptr", "nbytes", "lazy_dependents", "__weakref__")
-
-    def __init__(self, ptr: int, nbytes: int):
-        self.ptr = ptr
-        self.nbytes = nbytes
-        # lazy arrays whose expression reads this buffer (see _elementwise)
-        self.lazy_dependents = None
-
-    def __del__(self):
-        lib = _lib
-        if lib is not None and self.ptr:
-            try:
-                lib.mmp_free(self.ptr)
-            except Exception:  # interpreter shutdown
-                pass
-            self.ptr = 0
-
-    def __repr__(self):
-        return f"DeviceBuffer(0x{self.ptr:x}, {self.nbytes} bytes)"
+# Owning handle to one device allocation (the reference's ``_Buffer``,
+# _metal_backend.py:121-165), implemented in the native gate: attributes
+# ``ptr``, ``nbytes``, ``lazy_dependents``; freed to the stream-ordered pool
+# (mmp_free) when the last reference goes.
+from ._native import DeviceBuffer  # noqa: E402
 
 
 _U32x3 = ctypes.c_uint32 * 3
@@ -248,6 +229,8 @@ class HipBackend:
                 inst._lib = load_library()
                 inst._exec_cache = {}
                 _check(inst._lib.mmp_init(int(os.environ.get("MMP_DEVICE", "0"))), "mmp_init")
+                from ._gate import bind_library
+                bind_library(inst._lib)
                 cls._instance = inst
             return cls._instance
 

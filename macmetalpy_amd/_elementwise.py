@@ -79,7 +79,13 @@ def track_lazy(arr) -> None:
             continue
         deps.append(ref)
         if len(deps) > _PRUNE_AT:
-            deps[:] = [r for r in deps if _pending(r) is not None]
+            _prune_deps(deps)
+
+
+def _prune_deps(deps) -> None:
+    """Drop dead and already evaluated arrays from a buffer's dependents
+    list, in place."""
+    deps[:] = [r for r in deps if _pending(r) is not None]
 
 
 def _pending(ref):
@@ -161,7 +167,9 @@ def _unary_dtypes(op_name, dt):
     return hit
 
 
-def unary(op_name: str, x):
+def _unary_py(op_name: str, x):
+    """The Python path of a unary op (the native gate calls it for every
+    case it does not handle itself)."""
     if type(x) is not _ndarray():
         x = _asarray(x)
     rdt, idt = _unary_dtypes(op_name, x._dtype)
@@ -205,7 +213,9 @@ def _binary_dtypes(op_name, ka, kb):
     return rdt, rdt
 
 
-def binary(op_name: str, a, b):
+def _binary_py(op_name: str, a, b):
+    """The Python path of a binary op (the native gate calls it for every
+    case it does not handle itself)."""
     nd = _ndarray()
     a_arr = isinstance(a, nd)
     b_arr = isinstance(b, nd)
@@ -349,3 +359,10 @@ def power(a, b):
 
 def resolve(dtype):
     return resolve_dtype(dtype)
+
+
+# The native gate (macmetalpy_amd._native) takes over these names when the
+# package is set up; until then (and for what it hands back) the Python
+# paths run.
+unary = _unary_py
+binary = _binary_py

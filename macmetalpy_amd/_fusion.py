@@ -88,15 +88,24 @@ class InputNode(FusionNode):
 
 
 class ScalarNode(FusionNode):
-    __slots__ = ("_value",)
+    """A scalar kernel argument: its value converted to ``dtype`` (NumPy's
+    conversion), held as the little-endian bits of that value."""
+    __slots__ = ("_bits",)
 
     def __init__(self, value, dtype):
         self._dtype = np.dtype(dtype)
-        self._value = np.array(value, dtype=self._dtype)
+        raw = np.array(value, dtype=self._dtype).tobytes()
+        self._bits = int.from_bytes(raw.ljust(8, b"\0"), "little")
         self._shape = ()
         self._depth = 0
         self._buffers = ()
         self._nleaves = 0
+
+    @property
+    def _value(self):
+        """The value as a 0-d array of ``dtype``."""
+        raw = self._bits.to_bytes(8, "little")[:self._dtype.itemsize]
+        return np.frombuffer(raw, dtype=self._dtype).reshape(())
 
 
 def _merge_buffers(*nodes):
@@ -508,6 +517,13 @@ _kernel_cache: dict = {}
 _cache_lock = threading.Lock()
 
 
+def clear_kernel_caches() -> None:
+    """Forget every compiled-kernel handle (by source and by structure)."""
+    with _cache_lock:
+        _kernel_cache.clear()
+        _struct_cache.clear()
+
+
 def _kernel_for(src: str) -> int:
     k = _kernel_cache.get(src)
     if k is None:
@@ -542,8 +558,7 @@ def _leaf_ptr(node: InputNode) -> int:
 
 
 def _scalar_bits(sc: ScalarNode) -> int:
-    raw = sc._value.tobytes()
-    return int.from_bytes(raw.ljust(8, b"\0"), "little")
+    return sc._bits
 
 
 def _plan(prog: _Program, shape, keep_last):
@@ -716,10 +731,21 @@ def materialize_node(node: FusionNode, out_ptr: int) -> None:
     run_map(node, None, out_ptr)
 
 
-def materialize(arr) -> None:
+def compile_map_for_native(root, kinds, nouter, out_dtype, vec) -> int:
+    """Kernel handle of the 'map' kernel for ``root`` with the iteration
+    plan the native gate computed (leaf stride classes ``kinds``, ``nouter``
+    outer dims, output dtype, vector flag); the DAG is linearised here in
+    the same order as there."""
+    prog = _Program(root)
+    return _kernel_for_program(prog, list(kinds), nouter, np.dtype(out_dtype), bool(vec), "map")
+
+
+def _materialize_py(arr) -> None:
     """Evaluate a lazy ndarray in place (reference: _fusion.py:443-486):
     afterwards ``arr._buffer`` holds the result and ``arr._fusion_node`` is
-    None."""
+    None.  The native gate (``_native.materialize``, bound to
+    ``materialize`` by the package) handles the common cases and calls this
+    for the rest."""
     node = arr._fusion_node
     if node is None:
         return
@@ -731,3 +757,7 @@ def materialize(arr) -> None:
     arr._np_data = None
     arr._offset = 0
     arr._strides = _c_contig_strides(arr._shape)
+
+
+# Replaced by the native gate's materialize when the package is set up.
+materialize = _materialize_py

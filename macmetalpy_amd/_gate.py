@@ -1,0 +1,93 @@
+"""Binding of the native dispatch gate (``macmetalpy_amd._native``).
+
+``setup()`` hands the gate the Python classes it builds (ndarray, the
+fusion nodes), the Python paths it falls back to, the dtype-resolution
+functions that fill its result-dtype tables and the op tables; it then
+takes over ``_elementwise.unary`` / ``binary`` and ``_fusion.materialize``.
+``bind_library(lib)`` gives it the entry-point addresses of the loaded
+libmmp_hip.so (called when the device is initialised).  Reference: the
+reference's C gate ``_accelerator.c`` is set up the same way, from Python,
+with the ndarray class and dispatch tables (ndarray.py:2790-2882).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _abi
+from . import _elementwise as ew
+from . import _fusion
+from ._config import get_config
+
+try:
+    from . import _native
+except ImportError as exc:  # the product needs it: no silent Python-only mode
+    raise ImportError(
+        "macmetalpy_amd._native is not built; run `python -c 'import __graft_entry__ as g; "
+        "g.build()'` or `python macmetalpy_amd/csrc/build.py`") from exc
+
+__all__ = ["setup", "bind_library", "unbind_library", "stats"]
+
+_LIB_FUNCS = ("mmp_alloc", "mmp_free", "mmp_unary", "mmp_binary", "mmp_binary_scalar",
+              "mmp_rtc_launch")
+
+
+def _op_names():
+    names = []
+    for table in (_abi.UNARY_OPS, _abi.BINARY_OPS, _abi.EXPR_UNARY_OPS, _abi.EXPR_BINARY_OPS,
+                  _abi.COMPARE_OPS):
+        for k in table:
+            if k not in names:
+                names.append(k)
+    return names
+
+
+def _check(status: int, what: str) -> None:
+    from ._backend import _check as check
+    check(status, what)
+
+
+def setup() -> None:
+    from .ndarray import ndarray
+    dtypes = tuple(sorted(_abi.DTYPE_CODES, key=_abi.DTYPE_CODES.get))
+    _native.init({
+        "ndarray": ndarray,
+        "InputNode": _fusion.InputNode, "CastNode": _fusion.CastNode,
+        "UnaryOpNode": _fusion.UnaryOpNode, "BinaryOpNode": _fusion.BinaryOpNode,
+        "ScalarNode": _fusion.ScalarNode, "WhereNode": _fusion.WhereNode,
+        "unary_py": ew._unary_py, "binary_py": ew._binary_py,
+        "materialize_py": _fusion._materialize_py,
+        "compile_map": _fusion.compile_map_for_native,
+        "check": _check,
+        "unary_dtypes": ew._unary_dtypes, "binary_dtypes": ew._binary_dtypes,
+        "prune": ew._prune_deps,
+        "config": get_config(),
+        "dtypes": dtypes,
+        "max_depth": _fusion._MAX_DEPTH, "max_leaves": _fusion._MAX_LEAVES,
+        "op_names": _op_names(),
+        "unary_codes": {k: v[0] for k, v in _abi.UNARY_OPS.items()},
+        "binary_codes": {k: v[0] for k, v in _abi.BINARY_OPS.items()},
+        "fast_ops": set(_abi.FAST_MATH_OPS),
+    })
+    ew.unary = _native.unary
+    ew.binary = _native.binary
+    _fusion.materialize = _native.materialize
+
+
+def bind_library(lib) -> None:
+    _native.set_library({name: ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+                         for name in _LIB_FUNCS})
+
+
+def unbind_library() -> None:
+    """Detach the gate from the library and forget every compiled-kernel
+    handle (used by tests that bind a host-only stand-in)."""
+    _native.set_library(None)
+    _fusion.clear_kernel_caches()
+
+
+def stats() -> dict:
+    """Counters: ops built natively, arrays materialised natively, calls
+    handed to the Python path, generated kernels known to the gate."""
+    return _native.stats()

@@ -2,10 +2,12 @@
 
 Every ``*.hip`` file is compiled by hipcc into ``_build/<name>.o`` in
 parallel and the objects are linked into ``macmetalpy_amd/libmmp_hip.so``
-together with hiprtc.  Usage::
+together with hiprtc; ``native_gate.cpp`` is compiled by g++ into the
+CPython extension ``macmetalpy_amd/_native*.so``.  Run as a script (the
+package cannot be imported before these exist)::
 
-    python -m macmetalpy_amd.csrc.build            # full rebuild
-    python -m macmetalpy_amd.csrc.build --incremental
+    python macmetalpy_amd/csrc/build.py            # full rebuild
+    python macmetalpy_amd/csrc/build.py --incremental
 """
 from __future__ import annotations
 
@@ -72,6 +74,35 @@ def _compile(src: str, incremental: bool, hdr_time: float) -> tuple[str, float, 
     return src, time.time() - t, warn
 
 
+NATIVE_SRC = os.path.join(HERE, "native_gate.cpp")
+
+
+def native_path() -> str:
+    import sysconfig
+    return os.path.join(PKG, "_native" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_native(verbose: bool = True) -> str:
+    """The CPython extension of the dispatch gate (host code only: g++
+    against the Python headers; it reaches libmmp_hip.so through entry-point
+    addresses handed over at run time)."""
+    import sysconfig
+    out = native_path()
+    tmp = out + ".tmp"
+    cmd = [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-shared", "-fPIC",
+           "-fvisibility=hidden", "-Wall", "-Wno-missing-field-initializers",
+           "-Wno-cast-function-type", f"-I{sysconfig.get_paths()['include']}", NATIVE_SRC,
+           "-o", tmp]
+    t = time.time()
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"g++ failed for native_gate.cpp:\n{p.stdout}\n{p.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out} in {time.time() - t:.1f}s", flush=True)
+    return out
+
+
 def build(incremental: bool = False, jobs: int | None = None, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
@@ -94,6 +125,9 @@ def build(incremental: bool = False, jobs: int | None = None, verbose: bool = Tr
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} in {time.time() - t0:.1f}s", flush=True)
+    if not (incremental and os.path.exists(native_path())
+            and os.path.getmtime(native_path()) >= os.path.getmtime(NATIVE_SRC)):
+        build_native(verbose)
     return LIB
 
 

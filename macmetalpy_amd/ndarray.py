@@ -23,6 +23,7 @@ import numpy as np
 
 from . import _abi
 from . import _elementwise as ew
+from . import _fusion as _fusion_mod
 from ._backend import HipBackend
 from ._dtypes import dtype_code, resolve_dtype
 
@@ -120,8 +121,7 @@ class ndarray:
     # ------------------------------------------------------- residency
     def _materialize_if_lazy(self) -> None:
         if self._fusion_node is not None:
-            from ._fusion import materialize
-            materialize(self)
+            _fusion_mod.materialize(self)
 
     def _ensure_gpu(self) -> "ndarray":
         """Upload host-resident data (reference ndarray.py:352-368)."""

@@ -1,0 +1,234 @@
+"""The native dispatch gate on the CPU, against the Python path.
+
+The gate (macmetalpy_amd/csrc/native_gate.cpp) is bound to a host-only stub
+of the five library entry points it calls (tests/native_stub/stub_mmp.c,
+built here with gcc); the stub records calls and copies the parameter
+block of each generated-kernel launch.  Checked: the gate builds the same
+lazy DAGs and result dtypes as the Python path, hands back what it does not
+handle, calls the precompiled kernels with the right codes and pointers,
+and packs exactly the parameter block the Python path packs (_fill_params)
+for the same program -- what the generated kernel reads on the device.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import macmetalpy_amd as cp
+from macmetalpy_amd import _abi, _backend, _elementwise as ew, _fusion, _gate
+from macmetalpy_amd.ndarray import ndarray
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def stub(tmp_path_factory):
+    out = str(tmp_path_factory.mktemp("stub") / "libstub_mmp.so")
+    subprocess.run(["gcc", "-O1", "-shared", "-fPIC", "-std=c11",
+                    os.path.join(HERE, "native_stub", "stub_mmp.c"), "-o", out], check=True)
+    lib = ctypes.CDLL(out)
+    lib.stub_call.restype = ctypes.c_int64
+    lib.stub_params.restype = ctypes.c_void_p
+    lib.stub_live.restype = ctypes.c_longlong
+    lib.mmp_last_error.restype = ctypes.c_char_p
+    for name, argt in (("mmp_rtc_compile", [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                            ctypes.POINTER(ctypes.c_void_p)]),
+                       ("mmp_alloc", [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+                       ("mmp_free", [ctypes.c_void_p]),
+                       ("mmp_h2d", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+                       ("mmp_d2h", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+                       ("mmp_rtc_launch", [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
+                                           ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32,
+                                           ctypes.POINTER(ctypes.c_void_p)])):
+        getattr(lib, name).argtypes = argt
+        getattr(lib, name).restype = ctypes.c_int
+    saved = (_backend.HipBackend._instance, _backend._lib)
+    _gate.unbind_library()
+    inst = object.__new__(_backend.HipBackend)
+    inst._lib = lib
+    inst._exec_cache = {}
+    _backend.HipBackend._instance = inst
+    _backend._lib = lib
+    _gate.bind_library(lib)
+    # generated-kernel compiles only produce a handle (nothing runs)
+    saved_compile = _backend.HipBackend.compile
+    _backend.HipBackend.compile = lambda self, src, name, opts="": 0x4000
+    yield lib
+    _backend.HipBackend.compile = saved_compile
+    # forget the stand-in's handles and pointers; rebind a real device, if any
+    _gate.unbind_library()
+    _backend.HipBackend._instance, _backend._lib = saved
+    if saved[0] is not None:
+        _gate.bind_library(saved[0]._lib)
+
+
+def _dev(stub, a):
+    """A device-resident ndarray over stub host memory holding ``a``."""
+    a = np.ascontiguousarray(a)
+    p = ctypes.c_void_p()
+    assert stub.mmp_alloc(max(a.nbytes, 1), ctypes.byref(p)) == 0
+    ctypes.memmove(p.value, a.ctypes.data, a.nbytes)
+    buf = _backend.DeviceBuffer(p.value, a.nbytes)
+    return ndarray(buf, a.shape, a.dtype)
+
+
+def _same_dag(x, y):
+    if type(x) is not type(y):
+        return False
+    if x._dtype != y._dtype or x._shape != y._shape or x._depth != y._depth \
+            or x._nleaves != y._nleaves or x._buffers != y._buffers:
+        return False
+    t = type(x)
+    if t is _fusion.InputNode:
+        return (x._buffer is y._buffer and x._offset == y._offset and x._strides == y._strides)
+    if t is _fusion.ScalarNode:
+        return x._bits == y._bits
+    if t is _fusion.CastNode:
+        return _same_dag(x._input, y._input)
+    if t is _fusion.UnaryOpNode:
+        return x._op_name == y._op_name and _same_dag(x._input, y._input)
+    if t is _fusion.BinaryOpNode:
+        return (x._op_name == y._op_name and _same_dag(x._lhs, y._lhs)
+                and _same_dag(x._rhs, y._rhs))
+    return False
+
+
+def test_gate_builds_the_python_dags(stub):
+    g = np.random.default_rng(1)
+    a = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
+    b = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
+    i = _dev(stub, g.integers(-9, 9, (4, 6)).astype(np.int32))
+    cases = [
+        ("unary", "sin_op", a), ("unary", "neg_op", i), ("unary", "sqrt_op", i),
+        ("unary", "isnan_op", a), ("binary", "add_op", a, b), ("binary", "mul_op", i, a),
+        ("binary", "div_op", i, i), ("binary", "lt_op", a, b), ("binary", "sub_op", a, 2.5),
+        ("binary", "sub_op", 2.5, a), ("binary", "mul_op", i, 3), ("binary", "add_op", i, 1.5),
+        ("binary", "floor_divide_op", i, -7), ("binary", "pow_op", a, 2.0),
+    ]
+    before = _gate.stats()["native_ops"]
+    for kind, op, *args in cases:
+        if kind == "unary":
+            got, want = _gate._native.unary(op, *args), ew._unary_py(op, *args)
+        else:
+            got, want = _gate._native.binary(op, *args), ew._binary_py(op, *args)
+        assert type(got) is ndarray and got._dtype == want._dtype, (op, got._dtype, want._dtype)
+        assert got._shape == want._shape and got._strides == want._strides
+        assert _same_dag(got._fusion_node, want._fusion_node), op
+        # the result is registered with the buffers it reads
+        for buf in got._fusion_node._buffers:
+            assert any(r() is got for r in buf.lazy_dependents)
+    assert _gate.stats()["native_ops"] - before == len(cases)
+    # chains: a lazy operand is extended, not re-read
+    c = _gate._native.binary("add_op", _gate._native.unary("abs_op", a), b)
+    assert c._fusion_node._lhs._op_name == "abs_op" and c._fusion_node._depth == 2
+
+
+def test_gate_hands_back_what_it_does_not_handle(stub):
+    g = np.random.default_rng(2)
+    a = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
+    row = _dev(stub, g.standard_normal((1, 6)).astype(np.float32))
+    host = cp.array(g.standard_normal((4, 6)).astype(np.float32))  # host-resident
+    i16 = _dev(stub, g.integers(-9, 9, (4, 6)).astype(np.int16))
+    before = _gate.stats()["fallbacks"]
+    r = _gate._native.binary("add_op", a, row)               # broadcasting
+    assert r._shape == (4, 6)
+    with pytest.raises(OverflowError):                        # NumPy's error, from Python
+        _gate._native.binary("add_op", i16, 100000)
+    h = _gate._native.binary("mul_op", host, 2.0)             # host data uploads in Python
+    assert h._fusion_node is not None
+    assert _gate._native.binary("add_op", a, np.float32(1)) is not None  # NumPy scalar
+    assert _gate._native.binary("pow_op", i16, 2) is not None            # int power check
+    assert _gate.stats()["fallbacks"] - before >= 5
+
+
+def _expected_block(root, out_ptr):
+    """The parameter block the Python path packs for ``root``."""
+    prog = _fusion._Program(root)
+    shape = root._shape
+    cshape, outer, cols, leaf_str, kinds = _fusion._plan(prog, shape, keep_last=False)
+    vec = _fusion._vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, root._dtype.itemsize, "map")
+    tile = _fusion._BLOCK * _fusion._ELEMS * _fusion._UNROLL
+    colblocks = -(-cols // tile)
+    P = _fusion._param_struct(len(prog.arrays), len(prog.scalars), len(outer))
+    p, rows = _fusion._fill_params(prog, P, outer, cols, leaf_str, out_ptr, colblocks, 1.0)
+    return bytes(p), rows * colblocks, vec
+
+
+@pytest.mark.parametrize("case", ["c1", "chain_scalars", "strided", "int_cast", "where_like"])
+def test_gate_packs_the_python_parameter_block(stub, case):
+    g = np.random.default_rng(3)
+    x = _dev(stub, g.standard_normal(5000).astype(np.float32))
+    m = _dev(stub, g.standard_normal((64, 48)).astype(np.float32))
+    i = _dev(stub, g.integers(-5, 5, 5000).astype(np.int32))
+    n = _gate._native
+    if case == "c1":
+        y = n.binary("add_op", n.unary("sqrt_op", n.unary("abs_op", x)),
+                     n.unary("exp_op", n.unary("neg_op", n.unary("square_op", x))))
+    elif case == "chain_scalars":
+        y = n.binary("sub_op", n.binary("mul_op", x, 3.0), n.binary("add_op", x, -1.25))
+    elif case == "strided":
+        mt = m.transpose()
+        y = n.binary("add_op", n.unary("sin_op", mt), mt)
+    elif case == "int_cast":
+        y = n.binary("add_op", n.binary("mul_op", i, 2), x)  # int32 -> float64 cast leaves
+    else:
+        y = n.binary("mul_op", n.binary("gt_op", x, 0.0), x)
+    root = y._fusion_node
+    out_probe = ctypes.c_void_p()
+    # the block holds the output pointer, which the gate allocates itself:
+    # compare everything else, then check that field against the new buffer
+    want, nblocks, vec = _expected_block(root, 0)
+    stub.stub_reset(len(want))
+    n.materialize(y)
+    assert y._fusion_node is None and y._buffer is not None
+    calls = [[stub.stub_call(k, j) for j in range(8)] for k in range(stub.stub_ncalls())]
+    assert len(calls) == 1 and calls[0][0] == 4, calls
+    assert calls[0][2] == nblocks and calls[0][5] == 256
+    got = ctypes.string_at(stub.stub_params(), len(want))
+    nin = len(_fusion._Program(root).arrays)
+    off = 8 * max(1, nin)  # outp follows ptr[nin]
+    assert got[:off] == want[:off] and got[off + 8:] == want[off + 8:]
+    assert int.from_bytes(got[off:off + 8], "little") == y._buffer.ptr
+    del out_probe
+
+
+def test_gate_calls_precompiled_kernels(stub):
+    g = np.random.default_rng(4)
+    a = _dev(stub, g.standard_normal(1000).astype(np.float32))
+    b = _dev(stub, g.standard_normal(1000).astype(np.float32))
+    n = _gate._native
+    f32 = _abi.DTYPE_CODES[np.dtype(np.float32)]
+    for y, expect in ((n.unary("sin_op", a), (1, _abi.UNARY_OPS["sin_op"][0], f32, 1000, a._ptr)),
+                      (n.binary("add_op", a, b),
+                       (2, _abi.BINARY_OPS["add_op"][0], f32, 1000, a._ptr, b._ptr)),
+                      (n.binary("mul_op", a, 2.0),
+                       (3, _abi.BINARY_OPS["mul_op"][0], f32, 1000, a._ptr,
+                        int.from_bytes(np.float32(2.0).tobytes(), "little"), 1)),
+                      (n.binary("sub_op", 0.5, b),
+                       (3, _abi.BINARY_OPS["sub_op"][0], f32, 1000, b._ptr,
+                        int.from_bytes(np.float32(0.5).tobytes(), "little"), 0))):
+        stub.stub_reset(0)
+        n.materialize(y)
+        call = tuple(stub.stub_call(0, j) for j in range(len(expect)))
+        assert stub.stub_ncalls() == 1 and call == expect, (call, expect)
+    # fast_math: a fast-form op skips the precompiled kernel
+    cp.set_config(fast_math=True)
+    try:
+        y = n.unary("exp_op", a)
+        stub.stub_reset(8)
+        n.materialize(y)
+        assert stub.stub_call(0, 0) == 4
+    finally:
+        cp.set_config(fast_math=False)
+
+
+def test_buffers_are_freed(stub):
+    live = stub.stub_live()
+    x = _dev(stub, np.ones(100, np.float32))
+    y = _gate._native.unary("neg_op", x)
+    _gate._native.materialize(y)
+    assert stub.stub_live() == live + 2
+    del x, y
+    assert stub.stub_live() == live

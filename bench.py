@@ -131,7 +131,22 @@ def _mat(r):
 
 
 # --------------------------------------------------------------- C1
+def _call_us(cp, f, n_calls):
+    """Host-inclusive time per call: ``n_calls`` back-to-back calls (each
+    result evaluated), one synchronisation at the end."""
+    t = time.perf_counter()
+    for _ in range(n_calls):
+        f()
+    cp.synchronize()
+    return (time.perf_counter() - t) / n_calls * 1e6
+
+
 def bench_c1(cp, be, reps=50):
+    """C1 y = sqrt(abs(x)) + exp(-x**2): ``kernel_ms`` is the event time per
+    call (at 2^20 it includes the host gaps between launches: the device
+    waits for the host), ``call_us`` the host-inclusive time per call of
+    back-to-back calls; both count the whole call (6 lazy ops, one fused
+    kernel)."""
     from macmetalpy_amd.workloads import c1_inputs
     res = {}
     for label, n in (("2^20", 1 << 20), ("2^28", N28)):
@@ -149,7 +164,31 @@ def bench_c1(cp, be, reps=50):
         timer.close()
         res[label] = {"kernel_ms": round(ms, 4), "gbs": round(8 * n / ms / 1e6, 1),
                       "frac_of_peak": round(8 * n / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        if n < N28:
+            res[label]["call_us"] = round(_call_us(cp, f, 2000), 2)
         del x
+    return res
+
+
+def bench_small_ops(cp, be, n=1 << 20, calls=2000):
+    """Per-call time of single small ops on 2^20 float32 (host dispatch
+    included; the reference's bench_vs_numpy.py:30-45 times these calls
+    end to end): back-to-back calls, one synchronisation at the end."""
+    g = np.random.default_rng(0)
+    x = cp.array(g.standard_normal(n, dtype=np.float32))
+    y = cp.array(g.standard_normal(n, dtype=np.float32))
+    x._ensure_gpu()
+    y._ensure_gpu()
+    cases = {"add": lambda: _mat(x + y), "mul_scalar": lambda: _mat(x * 2.5),
+             "sin": lambda: _mat(cp.sin(x)), "sum": lambda: cp.sum(x),
+             "argmax": lambda: cp.argmax(x), "cumsum": lambda: cp.cumsum(x),
+             "c1_fused": lambda: _mat(cp.sqrt(cp.abs(x)) + cp.exp(-x ** 2))}
+    res = {}
+    for name, f in cases.items():
+        for _ in range(50):
+            f()
+        cp.synchronize()
+        res[name] = {"call_us": round(_call_us(cp, f, calls), 2)}
     return res
 
 
@@ -437,9 +476,9 @@ def bench_c5(cp, be, reps=10):
         return cp.sum(cp.tanh(x * r + 1.0) * cp.exp(-cp.abs(x)) - cp.log1p(x * x), axis=1)
 
     res = {}
-    for mode in ("fused", "unfused"):
+    for mode in ("fused", "fused_fast_math", "unfused"):
         try:
-            cp.set_config(fusion=(mode == "fused"))
+            cp.set_config(fusion=(mode != "unfused"), fast_math=(mode == "fused_fast_math"))
             chain()
             cp.synchronize()
             timer = EventTimer(be)
@@ -454,7 +493,11 @@ def bench_c5(cp, be, reps=10):
         except Exception as e:
             res[mode] = {"error": f"{type(e).__name__}: {e}"[:300]}
         finally:
-            cp.set_config(fusion=True)
+            cp.set_config(fusion=True, fast_math=False)
+    if "ms" in res.get("fused_fast_math", {}):
+        ms = res["fused_fast_math"]["ms"]
+        res["fused_fast_math"].update({"gbs": round(nbytes / ms / 1e6, 1),
+                                       "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)})
     if "ms" in res.get("fused", {}):
         ms = res["fused"]["ms"]
         res["fused"].update({"gbs": round(nbytes / ms / 1e6, 1),
@@ -465,34 +508,125 @@ def bench_c5(cp, be, reps=10):
 
 
 # ------------------------------------------------------- CPU baseline
+def _median_time(fn, reps, warm):
+    """Median wall time of ``fn`` over ``reps`` runs after ``warm`` warm-ups
+    (the reference's method, benchmarks/bench_vs_numpy.py:30-45)."""
+    times = []
+    for i in range(warm + reps):
+        t = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t
+        if i >= warm:
+            times.append(dt)
+    return statistics.median(times)
+
+
+def _host_info():
+    info = {"nproc": os.cpu_count()}
+    try:
+        with open("/proc/cpuinfo") as f:
+            info["cpu_model"] = next((l.split(":", 1)[1].strip() for l in f
+                                      if l.startswith("model name")), "")
+    except OSError:
+        pass
+    try:
+        from threadpoolctl import threadpool_info
+        info["blas"] = [{k: d.get(k) for k in ("internal_api", "version", "num_threads",
+                                                 "threading_layer", "architecture")}
+                        for d in threadpool_info() if d.get("user_api") == "blas"]
+    except Exception as e:  # report, keep going
+        info["blas"] = f"unavailable: {type(e).__name__}"
+    info["OPENBLAS_NUM_THREADS"] = os.environ.get("OPENBLAS_NUM_THREADS", "unset (all cores)")
+    info["numpy"] = np.__version__
+    return info
+
+
+def _cpu_entry(value, unit, cores, sample, extra=None):
+    d = {"value": round(value, 3), "unit": unit, "cores": cores, "kind": "port",
+         "sample": sample}
+    if extra:
+        d.update(extra)
+    return d
+
+
 def cpu_baseline(sample_log2=25, reps=10, warm=2):
-    """The reference's CPU path (NumPy ufuncs, single-threaded) on the first
-    2^sample_log2 elements of the C2 inputs; median of ``reps`` runs after
-    ``warm`` warm-ups, as the reference's bench_vs_numpy.py:30-45."""
-    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    """The reference's CPU path -- NumPy, the oracle's restatement
+    (oracle/reference_cpu.py) -- timed on this host: the headline C2 step on
+    the first 2^sample_log2 elements of the 2^28 inputs, and one bounded
+    sample of every other configuration (``per_config``).  NumPy ufuncs
+    are single-threaded; np.matmul uses all host cores through BLAS."""
+    from macmetalpy_amd import workloads as W
     from oracle import reference_cpu as ref
     n = 1 << sample_log2
-    a, b = c2_float_inputs(N28)
+    a, b = W.c2_float_inputs(N28)
     a, b = a[:n].copy(), b[:n].copy()
-    ai, bi = c2_int_inputs(N28)
+    ai, bi = W.c2_int_inputs(N28)
     ai, bi = ai[:n].copy(), bi[:n].copy()
     ops = [(lambda: ref.binary("add_op", a, b), 12), (lambda: ref.unary("sin_op", a), 8),
            (lambda: ref.floor_divide(ai, bi), 12), (lambda: ref.mod(ai, bi), 12)]
     total_bytes = sum(bpe for _, bpe in ops) * n
-    times = []
-    for i in range(warm + reps):
-        t = time.perf_counter()
-        for fn, _ in ops:
-            fn()
-        dt = time.perf_counter() - t
-        if i >= warm:
-            times.append(dt)
-    med = statistics.median(times)
-    return {"value": round(total_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": (f"a+b, sin(a) float32 and floor_divide, mod int32 on the first 2^{sample_log2} "
-                       f"elements of the 2^28 inputs; NumPy {np.__version__} single-threaded "
-                       f"ufuncs; median of {reps} after {warm} warm-ups ({med:.3f} s/step)")}
+    med = _median_time(lambda: [fn() for fn, _ in ops], reps, warm)
+    out = _cpu_entry(total_bytes / med / 1e9, "GB/s", 1,
+                     f"a+b, sin(a) float32 and floor_divide, mod int32 on the first 2^{sample_log2} "
+                     f"elements of the 2^28 inputs; NumPy {np.__version__} single-threaded "
+                     f"ufuncs; median of {reps} after {warm} warm-ups ({med:.3f} s/step)")
+    del a, b, ai, bi
+    per = {}
+    # C1 at its full size, 2^20
+    x = W.c1_inputs(1 << 20)
+    t = _median_time(lambda: ref.fused_elementwise(x), reps, warm)
+    per["c1_fused_elementwise_2^20"] = _cpu_entry(
+        8 * x.size / t / 1e9, "GB/s", 1, "full 2^20 config, op by op in float32",
+        {"call_us": round(t * 1e6, 1)})
+    # C2 per op (same sample as the headline)
+    per["c2_binary"] = {k: v for k, v in out.items()}
+    # C3: reductions on the first 4096 rows of the 16384^2 matrix, scans on 2^25
+    A = W.c3_matrix(4096, 16384)
+    nb = A.nbytes
+    c3 = {}
+    for name, fn in (("sum_all", lambda: ref.sum(A)), ("mean_all", lambda: ref.mean(A)),
+                     ("sum_axis1", lambda: ref.sum(A, axis=1)),
+                     ("mean_axis1", lambda: ref.mean(A, axis=1)),
+                     ("argmax_all", lambda: ref.argmax(A)),
+                     ("argmax_axis1", lambda: ref.argmax(A, axis=1))):
+        t = _median_time(fn, reps, warm)
+        c3[name] = _cpu_entry(nb / t / 1e9, "GB/s", 1, "4096 x 16384 float32 (first quarter of "
+                              "the 16384^2 config)", {"ms": round(t * 1e3, 2)})
+    del A
+    ci, cf = W.c3_scan_inputs(1 << 25)
+    for name, arr, bpe in (("cumsum_i32_to_i64", ci, 12), ("cumsum_f32", cf, 8)):
+        t = _median_time(lambda arr=arr: ref.cumsum(arr), reps, warm)
+        c3[name] = _cpu_entry(bpe * arr.size / t / 1e9, "GB/s", 1,
+                              "2^25 elements (1/8 of the 2^28 config)", {"ms": round(t * 1e3, 2)})
+    per["c3_reduce_scan"] = c3
+    del ci, cf
+    # C4: BLAS float32 at full size (all host cores), float16 scaled down
+    c4 = {}
+    for kind, label in (("f32", "4096^3 float32"), ("batched", "64 x 1024^3 float32")):
+        p, q = W.c4_inputs(kind)
+        flops = 2.0 * p.shape[-2] * p.shape[-1] * q.shape[-1] * (p.shape[0] if p.ndim == 3 else 1)
+        t = _median_time(lambda p=p, q=q: ref.matmul(p, q), 3, 1)
+        c4[kind] = _cpu_entry(flops / t / 1e9, "GFLOP/s", os.cpu_count(),
+                              f"full {label}, np.matmul (BLAS, all host cores); median of 3 after 1",
+                              {"ms": round(t * 1e3, 1)})
+        del p, q
+    p, q = W.c4_inputs("f16", 1024)
+    t = _median_time(lambda: ref.matmul(p, q), 2, 0)
+    c4["f16"] = _cpu_entry(2.0 * 1024 ** 3 / t / 1e9, "GFLOP/s", 1,
+                           "scaled: 1024^3 float16 (NumPy's non-BLAS float16 loop; the 8192^3 "
+                           "config would take about an hour); median of 2",
+                           {"ms": round(t * 1e3, 1)})
+    per["c4_matmul"] = c4
+    # C5 on the first 2048 rows
+    xx, rr = W.c5_inputs(2048, 8192)
+    t = _median_time(lambda: ref.fusion_chain(xx, rr), reps, warm)
+    per["c5_fusion_chain"] = _cpu_entry(
+        (xx.nbytes + rr.nbytes + 4 * xx.shape[0]) / t / 1e9, "GB/s", 1,
+        "2048 x 8192 rows of the 8192^2 config, op by op in float32",
+        {"ms": round(t * 1e3, 2)})
+    out["per_config"] = per
+    out["host"] = _host_info()
+    return out
 
 
 def _env(be):
@@ -652,7 +786,8 @@ def bench_routines(cp, be, reps=5):
 
 
 CONFIG_SECTIONS = {
-    "c1_fused_elementwise": bench_c1, "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
+    "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
+    "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
     "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
     "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,
     "indexing_manipulation": bench_indexing, "linalg": bench_linalg,

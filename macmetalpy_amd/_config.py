@@ -1,11 +1,18 @@
 """Global configuration (reference: src/macmetalpy/_config.py:11-64).
 
-Same singleton and ``set_config`` keywords as the reference, plus two
+Same singleton and ``set_config`` keywords as the reference, plus the
 switches this implementation adds:
 
 * ``fusion`` -- build lazy expression DAGs and compile one kernel per DAG
   (default True).  False evaluates op by op with precompiled kernels, the
   "unfused" baseline of the fusion benchmark.
+* ``native_dispatch`` -- route elementwise ops, their materialisation and
+  fused row sums through the native gate (macmetalpy_amd._native; default
+  True).  False runs the Python path for everything (same kernels, same
+  results, more host time per op).  This is the counterpart of the
+  reference's dispatch policy (its C gate plus the size thresholds of
+  ndarray.py:41-44 that send small CPU-resident arrays to NumPy); there are
+  no size thresholds here because nothing is computed on the host.
 * ``float64_behavior`` keeps the reference's two values.  ``"cpu_fallback"``
   (the reference's default) keeps float64 precision; on MI355X float64 runs
   natively on the GPU, so nothing falls back to the CPU.  ``"downcast"``
@@ -32,6 +39,7 @@ class MacMetalConfig:
                 inst.default_float_dtype = "float32"
                 inst.fast_math = False
                 inst.fusion = True
+                inst.native_dispatch = True
                 cls._instance = inst
             return cls._instance
 
@@ -48,6 +56,7 @@ def set_config(
     default_float_dtype: str | None = None,
     fast_math: bool | None = None,
     fusion: bool | None = None,
+    native_dispatch: bool | None = None,
 ) -> None:
     """Update configuration values (reference: _config.py:43-64)."""
     cfg = get_config()
@@ -64,3 +73,7 @@ def set_config(
         cfg.fast_math = bool(fast_math)
     if fusion is not None:
         cfg.fusion = bool(fusion)
+    if native_dispatch is not None and bool(native_dispatch) != cfg.native_dispatch:
+        cfg.native_dispatch = bool(native_dispatch)
+        from . import _gate
+        _gate.apply(cfg.native_dispatch)

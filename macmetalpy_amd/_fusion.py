@@ -639,7 +639,7 @@ def run_map(root: FusionNode, out_buffer, out_ptr: int) -> None:
     HipBackend().launch(kern, (nblocks, 1, 1), (_BLOCK, 1, 1), [p])
 
 
-def run_sum(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean: bool):
+def _run_sum_py(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean: bool):
     """Fused reduction epilogue: sum (or mean) of ``root`` over its last axis
     (axis_last=True) or over all elements, written to ``out_ptr``."""
     from ._backend import HipBackend as _HB
@@ -731,13 +731,13 @@ def materialize_node(node: FusionNode, out_ptr: int) -> None:
     run_map(node, None, out_ptr)
 
 
-def compile_map_for_native(root, kinds, nouter, out_dtype, vec) -> int:
-    """Kernel handle of the 'map' kernel for ``root`` with the iteration
-    plan the native gate computed (leaf stride classes ``kinds``, ``nouter``
-    outer dims, output dtype, vector flag); the DAG is linearised here in
-    the same order as there."""
+def compile_for_native(root, kinds, nouter, out_dtype, vec, mode="map") -> int:
+    """Kernel handle of the generated kernel for ``root`` ('map' or 'sum'
+    mode) with the iteration plan the native gate computed (leaf stride
+    classes ``kinds``, ``nouter`` outer dims, output dtype, vector flag);
+    the DAG is linearised here in the same order as there."""
     prog = _Program(root)
-    return _kernel_for_program(prog, list(kinds), nouter, np.dtype(out_dtype), bool(vec), "map")
+    return _kernel_for_program(prog, list(kinds), nouter, np.dtype(out_dtype), bool(vec), mode)
 
 
 def _materialize_py(arr) -> None:
@@ -759,5 +759,6 @@ def _materialize_py(arr) -> None:
     arr._strides = _c_contig_strides(arr._shape)
 
 
-# Replaced by the native gate's materialize when the package is set up.
+# Replaced by the native gate's versions when the package is set up.
 materialize = _materialize_py
+run_sum = _run_sum_py

@@ -3,7 +3,8 @@
 ``setup()`` hands the gate the Python classes it builds (ndarray, the
 fusion nodes), the Python paths it falls back to, the dtype-resolution
 functions that fill its result-dtype tables and the op tables; it then
-takes over ``_elementwise.unary`` / ``binary`` and ``_fusion.materialize``.
+takes over ``_elementwise.unary`` / ``binary`` and ``_fusion.materialize`` /
+``run_sum``.
 ``bind_library(lib)`` gives it the entry-point addresses of the loaded
 libmmp_hip.so (called when the device is initialised).  Reference: the
 reference's C gate ``_accelerator.c`` is set up the same way, from Python,
@@ -27,10 +28,10 @@ except ImportError as exc:  # the product needs it: no silent Python-only mode
         "macmetalpy_amd._native is not built; run `python -c 'import __graft_entry__ as g; "
         "g.build()'` or `python macmetalpy_amd/csrc/build.py`") from exc
 
-__all__ = ["setup", "bind_library", "unbind_library", "stats"]
+__all__ = ["setup", "apply", "bind_library", "unbind_library", "stats"]
 
 _LIB_FUNCS = ("mmp_alloc", "mmp_free", "mmp_unary", "mmp_binary", "mmp_binary_scalar",
-              "mmp_rtc_launch")
+              "mmp_rtc_launch", "mmp_reduce")
 
 
 def _op_names():
@@ -58,7 +59,8 @@ def setup() -> None:
         "ScalarNode": _fusion.ScalarNode, "WhereNode": _fusion.WhereNode,
         "unary_py": ew._unary_py, "binary_py": ew._binary_py,
         "materialize_py": _fusion._materialize_py,
-        "compile_map": _fusion.compile_map_for_native,
+        "run_sum_py": _fusion._run_sum_py,
+        "compile_map": _fusion.compile_for_native,
         "check": _check,
         "unary_dtypes": ew._unary_dtypes, "binary_dtypes": ew._binary_dtypes,
         "prune": ew._prune_deps,
@@ -70,9 +72,17 @@ def setup() -> None:
         "binary_codes": {k: v[0] for k, v in _abi.BINARY_OPS.items()},
         "fast_ops": set(_abi.FAST_MATH_OPS),
     })
-    ew.unary = _native.unary
-    ew.binary = _native.binary
-    _fusion.materialize = _native.materialize
+    apply(get_config().native_dispatch)
+
+
+def apply(native: bool) -> None:
+    """Route the hot path through the gate (True) or the Python path."""
+    if native:
+        ew.unary, ew.binary = _native.unary, _native.binary
+        _fusion.materialize, _fusion.run_sum = _native.materialize, _native.run_sum
+    else:
+        ew.unary, ew.binary = ew._unary_py, ew._binary_py
+        _fusion.materialize, _fusion.run_sum = _fusion._materialize_py, _fusion._run_sum_py
 
 
 def bind_library(lib) -> None:

@@ -48,6 +48,7 @@ typedef int (*fn_unary_t)(int, int, int64_t, const void *, void *);
 typedef int (*fn_binary_t)(int, int, int64_t, const void *, const void *, void *);
 typedef int (*fn_binary_scalar_t)(int, int, int64_t, const void *, const void *, int, void *);
 typedef int (*fn_launch_t)(void *, const uint32_t *, const uint32_t *, uint32_t, void **);
+typedef int (*fn_reduce_t)(int, int, int, int64_t, int64_t, int64_t, const void *, void *);
 
 fn_alloc_t p_alloc = nullptr;
 fn_free_t p_free = nullptr;
@@ -55,6 +56,7 @@ fn_unary_t p_unary = nullptr;
 fn_binary_t p_binary = nullptr;
 fn_binary_scalar_t p_binary_scalar = nullptr;
 fn_launch_t p_launch = nullptr;
+fn_reduce_t p_reduce = nullptr;
 
 // ------------------------------------------------------------ DeviceBuffer
 struct DevBuf {
@@ -123,7 +125,8 @@ PyTypeObject DevBufType = {PyVarObject_HEAD_INIT(nullptr, 0)};
 // ------------------------------------------------------------- state
 PyTypeObject *T_ndarray = nullptr, *T_input = nullptr, *T_cast = nullptr, *T_unary = nullptr,
              *T_binary = nullptr, *T_scalar = nullptr, *T_where = nullptr;
-PyObject *py_unary_fb = nullptr, *py_binary_fb = nullptr, *py_materialize_fb = nullptr;
+PyObject *py_unary_fb = nullptr, *py_binary_fb = nullptr, *py_materialize_fb = nullptr,
+         *py_run_sum_fb = nullptr;
 PyObject *py_compile_map = nullptr, *py_check = nullptr, *py_unary_dt = nullptr,
          *py_binary_dt = nullptr, *py_prune = nullptr;
 PyObject *cfg_obj = nullptr;
@@ -617,6 +620,32 @@ bool scalar_bits(PyObject *v, int kind, int dt, unsigned long long *bits) {
   }
 }
 
+// NumPy broadcasting of two shape tuples; NULL (exception set) if they
+// do not broadcast.
+PyObject *broadcast_shape(PyObject *sa, PyObject *sb) {
+  const Py_ssize_t na = PyTuple_GET_SIZE(sa), nb = PyTuple_GET_SIZE(sb);
+  const Py_ssize_t nd = na > nb ? na : nb;
+  PyObject *t = PyTuple_New(nd);
+  if (!t) return nullptr;
+  for (Py_ssize_t i = 0; i < nd; ++i) {
+    const Py_ssize_t ia = i - (nd - na), ib = i - (nd - nb);
+    const long long x = ia >= 0 ? PyLong_AsLongLong(PyTuple_GET_ITEM(sa, ia)) : 1;
+    const long long y = ib >= 0 ? PyLong_AsLongLong(PyTuple_GET_ITEM(sb, ib)) : 1;
+    if (x != y && x != 1 && y != 1) {
+      Py_DECREF(t);
+      PyErr_SetString(PyExc_ValueError, "shapes do not broadcast");
+      return nullptr;
+    }
+    PyObject *v = PyLong_FromLongLong(x == 1 ? y : x);
+    if (!v) {
+      Py_DECREF(t);
+      return nullptr;
+    }
+    PyTuple_SET_ITEM(t, i, v);
+  }
+  return t;
+}
+
 // ------------------------------------------------------------- binary
 PyObject *gate_binary(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
   if (nargs != 3) {
@@ -636,10 +665,23 @@ PyObject *gate_binary(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
     long long n = 0;
     if (ia < 0 || ib < 0 || !sa || !sb || !shape_size(sa, &n) || n == 0)
       return fallback3(py_binary_fb, op, a, b);
+    PyObject *shape = sa;  // borrowed, or the new broadcast shape below
+    PyObject *bshape = nullptr;
     if (sa != sb) {
       const int eq = PyObject_RichCompareBool(sa, sb, Py_EQ);
       if (eq < 0) return nullptr;
-      if (!eq) return fallback3(py_binary_fb, op, a, b);  // broadcasting: Python
+      if (!eq) {
+        bshape = broadcast_shape(sa, sb);
+        if (!bshape) {
+          PyErr_Clear();  // incompatible: Python raises NumPy's error
+          return fallback3(py_binary_fb, op, a, b);
+        }
+        if (!shape_size(bshape, &n) || n == 0) {
+          Py_DECREF(bshape);
+          return fallback3(py_binary_fb, op, a, b);
+        }
+        shape = bshape;
+      }
     }
     if (bin_rdt[id][ia][ib] < 0) {
       PyObject *r = PyObject_CallFunctionObjArgs(py_binary_dt, op, dta, dtb, nullptr);
@@ -655,34 +697,40 @@ PyObject *gate_binary(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
       bin_odt[id][ia][ib] = (int8_t)od;
     }
     const int rd = bin_rdt[id][ia][ib], od = bin_odt[id][ia][ib];
+    PyObject *an = nullptr, *bn = nullptr, *node = nullptr, *arr = nullptr;
+    int st;
     // integer powers need the host's negative-exponent check
-    if (binary_code[id] == 6 && rd != D_F16 && rd != D_F32 && rd != D_F64)
-      return fallback3(py_binary_fb, op, a, b);
-    PyObject *an = nullptr, *bn = nullptr;
-    int st = operand_node(ad, od, &an);
+    if (binary_code[id] == 6 && rd != D_F16 && rd != D_F32 && rd != D_F64) goto back;
+    st = operand_node(ad, od, &an);
     if (st <= 0) {
-      if (st < 0) return nullptr;
-      return fallback3(py_binary_fb, op, a, b);
+      if (st < 0) goto err;
+      goto back;
     }
     st = operand_node(bd, od, &bn);
     if (st <= 0) {
-      Py_DECREF(an);
-      if (st < 0) return nullptr;
-      return fallback3(py_binary_fb, op, a, b);
+      if (st < 0) goto err;
+      goto back;
     }
-    if (dget_ll(d_nleaves, an) + dget_ll(d_nleaves, bn) > max_leaves) {
-      Py_DECREF(an);
-      Py_DECREF(bn);
-      return fallback3(py_binary_fb, op, a, b);
-    }
-    PyObject *node = new_binary(op, an, bn, sa, dtypes[rd]);
-    Py_DECREF(an);
-    Py_DECREF(bn);
-    if (!node) return nullptr;
-    PyObject *arr = new_lazy_array(node, sa, dtypes[rd]);
+    if (dget_ll(d_nleaves, an) + dget_ll(d_nleaves, bn) > max_leaves) goto back;
+    node = new_binary(op, an, bn, shape, dtypes[rd]);
+    if (!node) goto err;
+    arr = new_lazy_array(node, shape, dtypes[rd]);
     Py_DECREF(node);
-    ++stat_native_ops;
+    Py_XDECREF(an);
+    Py_XDECREF(bn);
+    Py_XDECREF(bshape);
+    if (arr) ++stat_native_ops;
     return arr;
+  back:
+    Py_XDECREF(an);
+    Py_XDECREF(bn);
+    Py_XDECREF(bshape);
+    return fallback3(py_binary_fb, op, a, b);
+  err:
+    Py_XDECREF(an);
+    Py_XDECREF(bn);
+    Py_XDECREF(bshape);
+    return nullptr;
   }
   // one array and a Python int / float
   PyObject *arr_o = a_arr ? a : b, *sc = a_arr ? b : a;
@@ -893,14 +941,19 @@ int visit(Prog &p, PyObject *node) {
   return idx;
 }
 
-// Collapse the iteration space (the Python _collapse with keep_last=False).
+// Collapse the iteration space (the Python _collapse): merge adjacent dims
+// contiguous for every operand, drop size-1 dims; with keep_last the last
+// dim stays separate (the reduced axis of a row reduction).
 void collapse(const std::vector<long long> &shape, std::vector<std::vector<long long>> &st,
-              std::vector<long long> *cshape, std::vector<std::vector<long long>> *cst) {
+              bool keep_last, std::vector<long long> *cshape,
+              std::vector<std::vector<long long>> *cst) {
   cshape->clear();
   cst->assign(st.size(), {});
-  for (size_t d = 0; d < shape.size(); ++d) {
-    if (shape[d] == 1) continue;
-    bool merge = !cshape->empty();
+  const size_t n = shape.size();
+  for (size_t d = 0; d < n; ++d) {
+    const bool is_last = keep_last && d == n - 1;
+    if (shape[d] == 1 && !is_last) continue;
+    bool merge = !cshape->empty() && !is_last;
     for (size_t k = 0; merge && k < st.size(); ++k)
       merge = (*cst)[k].back() == st[k][d] * shape[d];
     if (merge) {
@@ -975,6 +1028,153 @@ int finish(PyObject *arr, PyObject *arrd, PyObject *buf, PyObject *shape) {
 }
 
 constexpr int kBlock = 256, kTile = 256 * 4 * 4;
+
+// Linearised program plus its iteration plan (the Python _Program + _plan).
+struct Plan {
+  Prog p;
+  std::vector<long long> cshape;
+  std::vector<std::vector<long long>> cst;  // collapsed strides per leaf
+  std::string kinds;                        // last-dim stride class per leaf
+  long long cols = 1, rows = 1;
+  size_t nouter = 0;
+};
+
+// 1 = planned, 0 = not handled here (fall back), -1 = error set.
+int make_plan(PyObject *root, PyObject *shape, bool keep_last, Plan *pl) {
+  Prog &p = pl->p;
+  p.key.reserve(128);
+  visit(p, root);
+  if (!p.ok || PyErr_Occurred()) {
+    PyErr_Clear();
+    return 0;
+  }
+  std::vector<long long> oshape;
+  if (!tuple_ll(shape, &oshape)) return -1;
+  const size_t nin = p.leaves.size();
+  std::vector<std::vector<long long>> st(nin + 1);
+  for (size_t k = 0; k < nin; ++k) {
+    const Leaf &L = p.leaves[k];
+    if (L.shape.size() > oshape.size()) return 0;
+    const size_t diff = oshape.size() - L.shape.size();
+    st[k].assign(diff, 0);
+    for (size_t d = 0; d < L.shape.size(); ++d) {
+      const long long sz = L.shape[d], tt = oshape[diff + d];
+      st[k].push_back((sz == tt && sz != 1) ? L.strides[d] : 0);
+    }
+  }
+  st[nin].assign(oshape.size(), 0);
+  long long acc = 1;
+  for (size_t d = oshape.size(); d-- > 0;) {
+    st[nin][d] = acc;
+    acc *= oshape[d];
+  }
+  collapse(oshape, st, keep_last, &pl->cshape, &pl->cst);
+  pl->cst.resize(nin);  // the output's collapsed strides are not needed
+  if (pl->cshape.empty()) {
+    pl->cshape.push_back(1);
+    for (size_t k = 0; k < nin; ++k) pl->cst[k].assign(1, 0);
+  }
+  pl->cols = pl->cshape.back();
+  pl->nouter = pl->cshape.size() - 1;
+  pl->rows = 1;
+  for (size_t d = 0; d < pl->nouter; ++d) pl->rows *= pl->cshape[d];
+  pl->kinds.clear();
+  for (size_t k = 0; k < nin; ++k) {
+    const long long ls = pl->cst[k].empty() ? 0 : pl->cst[k].back();
+    pl->kinds.push_back(ls == 1 ? 'c' : (ls == 0 ? 'b' : 's'));
+  }
+  return 1;
+}
+
+// Whether every leaf can be read 4 elements at a time with aligned vector
+// loads (the Python _vec_ok); `out_ok` covers the output for map mode.
+bool vec_ok(const Plan &pl, bool out_ok) {
+  if (pl.cols % 4 || !out_ok) return false;
+  for (size_t k = 0; k < pl.p.leaves.size(); ++k) {
+    if (pl.kinds[k] == 's') return false;
+    if (pl.kinds[k] == 'c') {
+      if (pl.p.leaves[k].ptr % (4ull * itemsize[pl.p.leaves[k].dt])) return false;
+      for (size_t d = 0; d + 1 < pl.cst[k].size(); ++d)
+        if (pl.cst[k][d] % 4) return false;
+    }
+  }
+  return true;
+}
+
+// Kernel for the plan (mode 'm' map, 's' row sum), by structure; compiled
+// through the Python code generator the first time.
+void *kernel_for(const Plan &pl, PyObject *root, int out_dt, bool vec, char mode, bool fast) {
+  std::string key = pl.p.key;
+  key.push_back('|');
+  for (const Leaf &L : pl.p.leaves) key.push_back((char)L.dt);
+  key += pl.kinds;
+  key.push_back((char)pl.nouter);
+  key.push_back((char)out_dt);
+  key.push_back(vec ? 'v' : 's');
+  key.push_back(fast ? 'f' : 'e');
+  key.push_back(mode);
+  auto it = g_kernels.find(key);
+  if (it != g_kernels.end()) return it->second;
+  PyObject *kt = PyUnicode_FromStringAndSize(pl.kinds.data(), (Py_ssize_t)pl.kinds.size());
+  PyObject *r = kt ? PyObject_CallFunction(py_compile_map, "OOiOOs", root, kt, (int)pl.nouter,
+                                           dtypes[out_dt], vec ? Py_True : Py_False,
+                                           mode == 'm' ? "map" : "sum")
+                   : nullptr;
+  Py_XDECREF(kt);
+  if (!r) return nullptr;
+  void *kern = PyLong_AsVoidPtr(r);
+  Py_DECREF(r);
+  if (PyErr_Occurred()) return nullptr;
+  if (!kern) {
+    PyErr_SetString(PyExc_RuntimeError, "null kernel handle");
+    return nullptr;
+  }
+  g_kernels.emplace(key, kern);
+  return kern;
+}
+
+// Pack the generated kernel's parameter block (struct P: 8-byte fields
+// ptr[nin], outp, sbits[nsc], n, rows, cols, colblocks, oshape[nouter],
+// ostride[nin * nouter], lstride[nin], scale) and launch rows * colblocks
+// workgroups of kBlock threads.  0 or -1 with an exception set.
+int launch_plan(const Plan &pl, void *kern, unsigned long long outp, long long colblocks,
+                double scale) {
+  const size_t nin = pl.p.leaves.size(), nsc = pl.p.sbits.size(), nouter = pl.nouter;
+  const size_t nin1 = nin ? nin : 1, nsc1 = nsc ? nsc : 1, nout1 = nouter ? nouter : 1,
+               nio1 = (nin * nouter) != 0 ? nin * nouter : 1;
+  std::vector<unsigned long long> P(nin1 + 1 + nsc1 + 4 + nout1 + nio1 + nin1 + 1, 0ull);
+  size_t o = 0;
+  const size_t o_ptr = o; o += nin1;
+  const size_t o_out = o; o += 1;
+  const size_t o_sb = o; o += nsc1;
+  const size_t o_n = o; o += 4;
+  const size_t o_osh = o; o += nout1;
+  const size_t o_ost = o; o += nio1;
+  const size_t o_lst = o; o += nin1;
+  const size_t o_scale = o;
+  for (size_t k = 0; k < nin; ++k) {
+    P[o_ptr + k] = pl.p.leaves[k].ptr;
+    P[o_lst + k] = (unsigned long long)(pl.cst[k].empty() ? 0 : pl.cst[k].back());
+    for (size_t d = 0; d < nouter; ++d) P[o_ost + k * nouter + d] = (unsigned long long)pl.cst[k][d];
+  }
+  for (size_t j = 0; j < nsc; ++j) P[o_sb + j] = pl.p.sbits[j];
+  for (size_t d = 0; d < nouter; ++d) P[o_osh + d] = (unsigned long long)pl.cshape[d];
+  P[o_out] = outp;
+  P[o_n + 0] = (unsigned long long)(pl.rows * pl.cols);
+  P[o_n + 1] = (unsigned long long)pl.rows;
+  P[o_n + 2] = (unsigned long long)pl.cols;
+  P[o_n + 3] = (unsigned long long)colblocks;
+  std::memcpy(&P[o_scale], &scale, 8);
+  const unsigned long long nblocks = (unsigned long long)(pl.rows * colblocks);
+  if (nblocks > 0xffffffffull) {
+    PyErr_SetString(PyExc_ValueError, "fused launch too large");
+    return -1;
+  }
+  if (nblocks == 0) return 0;
+  uint32_t grid[3] = {(uint32_t)nblocks, 1, 1}, block[3] = {kBlock, 1, 1};
+  void *argv[1] = {P.data()};
+  return check_status(p_launch(kern, grid, block, 0, argv), "mmp_rtc_launch");
+}
 
 PyObject *gate_materialize(PyObject *, PyObject *arr) {
   if (Py_TYPE(arr) != T_ndarray) return PyObject_CallOneArg(py_materialize_fb, arr);
@@ -1057,124 +1257,22 @@ PyObject *gate_materialize(PyObject *, PyObject *arr) {
   if (!result) {
     if (buf) goto fail;  // allocated but failed: error already set
     // ---- generated kernel
-    Prog p;
-    p.key.reserve(128);
-    visit(p, node);
-    if (!p.ok || PyErr_Occurred()) {
-      PyErr_Clear();
+    Plan pl;
+    const int pst = make_plan(node, shape, false, &pl);
+    if (pst <= 0) {
+      if (pst < 0) goto fail;
       Py_DECREF(shape);
       Py_DECREF(node);
       return PyObject_CallOneArg(py_materialize_fb, arr);
     }
-    std::vector<long long> oshape;
-    if (!tuple_ll(shape, &oshape)) goto fail;
-    const size_t nin = p.leaves.size(), nsc = p.sbits.size();
-    std::vector<std::vector<long long>> st(nin + 1);
-    for (size_t k = 0; k < nin; ++k) {
-      const Leaf &L = p.leaves[k];
-      const size_t diff = oshape.size() - L.shape.size();
-      st[k].assign(diff, 0);
-      for (size_t d = 0; d < L.shape.size(); ++d) {
-        const long long s = L.shape[d], tt = oshape[diff + d];
-        st[k].push_back((s == tt && s != 1) ? L.strides[d] : 0);
-      }
-    }
-    st[nin].assign(oshape.size(), 0);
-    {
-      long long acc = 1;
-      for (size_t d = oshape.size(); d-- > 0;) {
-        st[nin][d] = acc;
-        acc *= oshape[d];
-      }
-    }
-    std::vector<long long> cshape;
-    std::vector<std::vector<long long>> cst;
-    collapse(oshape, st, &cshape, &cst);
-    if (cshape.empty()) {
-      cshape.push_back(1);
-      for (size_t k = 0; k < nin; ++k) cst[k].assign(1, 0);
-    }
-    const long long cols = cshape.back();
-    const size_t nouter = cshape.size() - 1;
-    long long rows = 1;
-    for (size_t d = 0; d < nouter; ++d) rows *= cshape[d];
-    std::string kinds;
-    for (size_t k = 0; k < nin; ++k) {
-      const long long ls = cst[k].empty() ? 0 : cst[k].back();
-      kinds.push_back(ls == 1 ? 'c' : (ls == 0 ? 'b' : 's'));
-    }
     buf = new_devbuf(n * itemsize[odt]);
     if (!buf) goto fail;
     const unsigned long long outp = ((DevBuf *)buf)->ptr;
-    bool vec = cols % 4 == 0 && outp % (4ull * itemsize[odt]) == 0;
-    for (size_t k = 0; vec && k < nin; ++k) {
-      if (kinds[k] == 's') vec = false;
-      if (kinds[k] == 'c') {
-        if (p.leaves[k].ptr % (4ull * itemsize[p.leaves[k].dt])) vec = false;
-        for (size_t d = 0; d + 1 < cst[k].size(); ++d)
-          if (cst[k][d] % 4) vec = false;
-      }
-    }
-    std::string key = p.key;
-    key.push_back('|');
-    for (size_t k = 0; k < nin; ++k) key.push_back((char)p.leaves[k].dt);
-    key += kinds;
-    key.push_back((char)nouter);
-    key.push_back((char)odt);
-    key.push_back(vec ? 'v' : 's');
-    key.push_back(fast ? 'f' : 'e');
-    void *kern = nullptr;
-    auto it = g_kernels.find(key);
-    if (it != g_kernels.end()) {
-      kern = it->second;
-    } else {
-      PyObject *kt = PyUnicode_FromStringAndSize(kinds.data(), (Py_ssize_t)kinds.size());
-      PyObject *r = kt ? PyObject_CallFunction(py_compile_map, "OOiOO", node, kt, (int)nouter,
-                                               dtypes[odt], vec ? Py_True : Py_False)
-                       : nullptr;
-      Py_XDECREF(kt);
-      if (!r) goto fail;
-      kern = PyLong_AsVoidPtr(r);
-      Py_DECREF(r);
-      if (PyErr_Occurred()) goto fail;
-      g_kernels.emplace(key, kern);
-    }
-    // parameter block: the generated kernel's struct P, 8-byte fields
-    const size_t nin1 = nin ? nin : 1, nsc1 = nsc ? nsc : 1, nout1 = nouter ? nouter : 1,
-                 nio1 = (nin * nouter) != 0 ? nin * nouter : 1;
-    std::vector<unsigned long long> P(nin1 + 1 + nsc1 + 4 + nout1 + nio1 + nin1 + 1, 0ull);
-    size_t o = 0;
-    const size_t o_ptr = o; o += nin1;
-    const size_t o_out = o; o += 1;
-    const size_t o_sb = o; o += nsc1;
-    const size_t o_n = o; o += 4;
-    const size_t o_osh = o; o += nout1;
-    const size_t o_ost = o; o += nio1;
-    const size_t o_lst = o; o += nin1;
-    const size_t o_scale = o;
-    const long long colblocks = (cols + kTile - 1) / kTile;
-    for (size_t k = 0; k < nin; ++k) {
-      P[o_ptr + k] = p.leaves[k].ptr;
-      P[o_lst + k] = (unsigned long long)(cst[k].empty() ? 0 : cst[k].back());
-      for (size_t d = 0; d < nouter; ++d) P[o_ost + k * nouter + d] = (unsigned long long)cst[k][d];
-    }
-    for (size_t j = 0; j < nsc; ++j) P[o_sb + j] = p.sbits[j];
-    for (size_t d = 0; d < nouter; ++d) P[o_osh + d] = (unsigned long long)cshape[d];
-    P[o_out] = outp;
-    P[o_n + 0] = (unsigned long long)(rows * cols);
-    P[o_n + 1] = (unsigned long long)rows;
-    P[o_n + 2] = (unsigned long long)cols;
-    P[o_n + 3] = (unsigned long long)colblocks;
-    const double one = 1.0;
-    std::memcpy(&P[o_scale], &one, 8);
-    const unsigned long long nblocks = (unsigned long long)(rows * colblocks);
-    if (nblocks > 0xffffffffull) {
-      PyErr_SetString(PyExc_ValueError, "fused launch too large");
-      goto fail;
-    }
-    uint32_t grid[3] = {(uint32_t)nblocks, 1, 1}, block[3] = {kBlock, 1, 1};
-    void *argv[1] = {P.data()};
-    if (check_status(p_launch(kern, grid, block, 0, argv), "mmp_rtc_launch")) goto fail;
+    const bool vec = vec_ok(pl, outp % (4ull * itemsize[odt]) == 0);
+    void *kern = kernel_for(pl, node, odt, vec, 'm', fast);
+    if (!kern) goto fail;
+    const long long colblocks = (pl.cols + kTile - 1) / kTile;
+    if (launch_plan(pl, kern, outp, colblocks, 1.0)) goto fail;
     result = Py_None;
   }
   if (finish(arr, arrd, buf, shape)) goto fail;
@@ -1189,6 +1287,82 @@ fail:
   Py_DECREF(node);
   if (!PyErr_Occurred()) PyErr_SetString(PyExc_RuntimeError, "materialize failed");
   return nullptr;
+}
+
+// ------------------------------------------------------ fused row sum
+// run_sum(root, axis_last, out_dtype, out_ptr, mean): the sum (or mean) of
+// the lazy expression `root` over its last axis (axis_last) or over all of
+// it, written to out_ptr -- the Python run_sum: generated kernel with a
+// float64 / 64-bit integer row-sum epilogue, split over column blocks when
+// there are few rows, then the precompiled reduction over the partials.
+// Returns the partials' DeviceBuffer (kept alive by the caller until the
+// stream passes it) or None.
+PyObject *gate_run_sum(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
+  if (nargs != 5) {
+    PyErr_SetString(PyExc_TypeError, "run_sum(root, axis_last, out_dtype, out_ptr, mean)");
+    return nullptr;
+  }
+  PyObject *root = args[0], *out_dtype = args[2];
+  const int axis_last = PyObject_IsTrue(args[1]), mean = PyObject_IsTrue(args[4]);
+  const unsigned long long out_ptr = PyLong_AsUnsignedLongLong(args[3]);
+  if (axis_last < 0 || mean < 0 || PyErr_Occurred()) return nullptr;
+  const int odt = dtype_index(out_dtype);
+  PyTypeObject *t = Py_TYPE(root);
+  if (!p_launch || !p_reduce || odt < 0 ||
+      (t != T_unary && t != T_binary && t != T_where && t != T_cast && t != T_input)) {
+    ++stat_fallback;
+    return PyObject_Vectorcall(py_run_sum_fb, args, 5, nullptr);
+  }
+  PyObject *shape = dget(d_shape, root), *rdto = dget(d_dtype, root);
+  const int rdt = rdto ? dtype_index(rdto) : -1;
+  Py_XDECREF(rdto);
+  long long total = 0;
+  Plan pl;
+  int pst = (shape && rdt >= 0 && shape_size(shape, &total)) ? make_plan(root, shape, axis_last, &pl)
+                                                             : 0;
+  Py_XDECREF(shape);
+  if (pst <= 0) {
+    if (pst < 0) return nullptr;
+    PyErr_Clear();
+    ++stat_fallback;
+    return PyObject_Vectorcall(py_run_sum_fb, args, 5, nullptr);
+  }
+  const long long count = axis_last ? pl.cols : (total > 1 ? total : 1);
+  const double scale = mean ? 1.0 / (double)count : 1.0;
+  const int acc = (rdt == D_F16 || rdt == D_F32 || rdt == D_F64)
+                      ? D_F64
+                      : ((rdt == D_U16 || rdt == D_U32 || rdt == D_U64) ? D_U64 : D_I64);
+  long long want = 2048 / (pl.rows > 1 ? pl.rows : 1);
+  if (want < 1) want = 1;
+  long long colblocks = (pl.cols + 4095) / 4096;
+  if (colblocks > want) colblocks = want;
+  if (colblocks < 1) colblocks = 1;
+  const bool final_direct = axis_last && colblocks == 1;
+  const bool vec = vec_ok(pl, true);
+  void *kern = kernel_for(pl, root, final_direct ? odt : acc, vec, 's', cfg_flag(s_fast_math));
+  if (!kern) return nullptr;
+  if (final_direct) {
+    if (launch_plan(pl, kern, out_ptr, 1, scale)) return nullptr;
+    ++stat_native_mat;
+    Py_RETURN_NONE;
+  }
+  PyObject *part = new_devbuf(pl.rows * colblocks * 8);
+  if (!part) return nullptr;
+  const unsigned long long pp = ((DevBuf *)part)->ptr;
+  if (launch_plan(pl, kern, pp, colblocks, scale)) {
+    Py_DECREF(part);
+    return nullptr;
+  }
+  const long long outer_n = axis_last ? pl.rows : 1;
+  const long long length = axis_last ? colblocks : pl.rows * colblocks;
+  if (check_status(p_reduce(0 /* MMP_R_SUM */, acc, odt, outer_n, length, 1,
+                            (const void *)(uintptr_t)pp, (void *)(uintptr_t)out_ptr),
+                   "mmp_reduce")) {
+    Py_DECREF(part);
+    return nullptr;
+  }
+  ++stat_native_mat;
+  return part;
 }
 
 // ------------------------------------------------------------ setup
@@ -1228,6 +1402,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   GETCFG(py_unary_fb, "unary_py");
   GETCFG(py_binary_fb, "binary_py");
   GETCFG(py_materialize_fb, "materialize_py");
+  GETCFG(py_run_sum_fb, "run_sum_py");
   GETCFG(py_compile_map, "compile_map");
   GETCFG(py_check, "check");
   GETCFG(py_unary_dt, "unary_dtypes");
@@ -1312,6 +1487,7 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
     p_binary = nullptr;
     p_binary_scalar = nullptr;
     p_launch = nullptr;
+    p_reduce = nullptr;
     g_kernels.clear();
     Py_RETURN_NONE;
   }
@@ -1329,8 +1505,10 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
   p_binary = (fn_binary_t)addr("mmp_binary");
   p_binary_scalar = (fn_binary_scalar_t)addr("mmp_binary_scalar");
   p_launch = (fn_launch_t)addr("mmp_rtc_launch");
+  p_reduce = (fn_reduce_t)addr("mmp_reduce");
   if (PyErr_Occurred()) return nullptr;
-  if (!p_alloc || !p_free || !p_unary || !p_binary || !p_binary_scalar || !p_launch) {
+  if (!p_alloc || !p_free || !p_unary || !p_binary || !p_binary_scalar || !p_launch ||
+      !p_reduce) {
     p_launch = nullptr;
     PyErr_SetString(PyExc_ValueError, "set_library: missing entry points");
     return nullptr;
@@ -1359,6 +1537,8 @@ PyMethodDef methods[] = {
      "binary(op_name, a, b): lazy elementwise result (falls back to the Python path)."},
     {"materialize", (PyCFunction)gate_materialize, METH_O,
      "Evaluate a lazy array in place (falls back to the Python path)."},
+    {"run_sum", (PyCFunction)(void (*)(void))gate_run_sum, METH_FASTCALL,
+     "run_sum(root, axis_last, out_dtype, out_ptr, mean): fused sum epilogue."},
     {"stats", (PyCFunction)gate_stats, METH_NOARGS, "Counters of the native and fallback paths."},
     {"clear_kernels", (PyCFunction)gate_clear_kernels, METH_NOARGS,
      "Forget the generated kernels known by structure."},

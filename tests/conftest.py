@@ -22,9 +22,11 @@ def _reset_config():
     """Each test starts from the default configuration (the reference's
     tests reset float64 handling the same way, tests/conftest.py:135-142)."""
     from macmetalpy_amd._config import set_config
-    set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True)
+    set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True,
+               fast_math=False, native_dispatch=True)
     yield
-    set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True)
+    set_config(float64_behavior="cpu_fallback", fusion=True, warn_on_downcast=True,
+               fast_math=False, native_dispatch=True)
 
 
 @pytest.fixture(autouse=True)

@@ -33,16 +33,10 @@ def stub(tmp_path_factory):
     lib.stub_params.restype = ctypes.c_void_p
     lib.stub_live.restype = ctypes.c_longlong
     lib.mmp_last_error.restype = ctypes.c_char_p
-    for name, argt in (("mmp_rtc_compile", [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
-                                            ctypes.POINTER(ctypes.c_void_p)]),
-                       ("mmp_alloc", [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
-                       ("mmp_free", [ctypes.c_void_p]),
-                       ("mmp_h2d", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
-                       ("mmp_d2h", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
-                       ("mmp_rtc_launch", [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
-                                           ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32,
-                                           ctypes.POINTER(ctypes.c_void_p)])):
-        getattr(lib, name).argtypes = argt
+    # the library's own ctypes signatures, for the entry points the stub has
+    for name in ("mmp_rtc_compile", "mmp_alloc", "mmp_free", "mmp_h2d", "mmp_d2h",
+                 "mmp_rtc_launch", "mmp_reduce", "mmp_unary", "mmp_binary", "mmp_binary_scalar"):
+        getattr(lib, name).argtypes = _backend._SIGNATURES[name]
         getattr(lib, name).restype = ctypes.c_int
     saved = (_backend.HipBackend._instance, _backend._lib)
     _gate.unbind_library()
@@ -100,12 +94,16 @@ def test_gate_builds_the_python_dags(stub):
     a = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
     b = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
     i = _dev(stub, g.integers(-9, 9, (4, 6)).astype(np.int32))
+    row = _dev(stub, g.standard_normal((1, 6)).astype(np.float32))
+    col = _dev(stub, g.standard_normal((4, 1)).astype(np.float32))
     cases = [
         ("unary", "sin_op", a), ("unary", "neg_op", i), ("unary", "sqrt_op", i),
         ("unary", "isnan_op", a), ("binary", "add_op", a, b), ("binary", "mul_op", i, a),
         ("binary", "div_op", i, i), ("binary", "lt_op", a, b), ("binary", "sub_op", a, 2.5),
         ("binary", "sub_op", 2.5, a), ("binary", "mul_op", i, 3), ("binary", "add_op", i, 1.5),
         ("binary", "floor_divide_op", i, -7), ("binary", "pow_op", a, 2.0),
+        ("binary", "mul_op", a, row), ("binary", "add_op", col, row),
+        ("binary", "sub_op", i, row),
     ]
     before = _gate.stats()["native_ops"]
     for kind, op, *args in cases:
@@ -131,9 +129,10 @@ def test_gate_hands_back_what_it_does_not_handle(stub):
     row = _dev(stub, g.standard_normal((1, 6)).astype(np.float32))
     host = cp.array(g.standard_normal((4, 6)).astype(np.float32))  # host-resident
     i16 = _dev(stub, g.integers(-9, 9, (4, 6)).astype(np.int16))
+    bad = _dev(stub, g.standard_normal((5, 6)).astype(np.float32))
     before = _gate.stats()["fallbacks"]
-    r = _gate._native.binary("add_op", a, row)               # broadcasting
-    assert r._shape == (4, 6)
+    with pytest.raises(ValueError):                           # shapes do not broadcast
+        _gate._native.binary("add_op", a, bad)
     with pytest.raises(OverflowError):                        # NumPy's error, from Python
         _gate._native.binary("add_op", i16, 100000)
     h = _gate._native.binary("mul_op", host, 2.0)             # host data uploads in Python
@@ -156,7 +155,8 @@ def _expected_block(root, out_ptr):
     return bytes(p), rows * colblocks, vec
 
 
-@pytest.mark.parametrize("case", ["c1", "chain_scalars", "strided", "int_cast", "where_like"])
+@pytest.mark.parametrize("case", ["c1", "chain_scalars", "strided", "int_cast", "where_like",
+                                  "c5_broadcast"])
 def test_gate_packs_the_python_parameter_block(stub, case):
     g = np.random.default_rng(3)
     x = _dev(stub, g.standard_normal(5000).astype(np.float32))
@@ -173,8 +173,14 @@ def test_gate_packs_the_python_parameter_block(stub, case):
         y = n.binary("add_op", n.unary("sin_op", mt), mt)
     elif case == "int_cast":
         y = n.binary("add_op", n.binary("mul_op", i, 2), x)  # int32 -> float64 cast leaves
-    else:
+    elif case == "where_like":
         y = n.binary("mul_op", n.binary("gt_op", x, 0.0), x)
+    else:  # tanh(x*r + 1.0) * exp(-abs(x)) - log1p(x*x) with a (1, 48) row r
+        r = _dev(stub, g.uniform(0.5, 2.0, (1, 48)).astype(np.float32))
+        y = n.binary("sub_op",
+                     n.binary("mul_op", n.unary("tanh_op", n.binary("add_op", n.binary("mul_op", m, r), 1.0)),
+                              n.unary("exp_op", n.unary("neg_op", n.unary("abs_op", m)))),
+                     n.unary("log1p_op", n.binary("mul_op", m, m)))
     root = y._fusion_node
     out_probe = ctypes.c_void_p()
     # the block holds the output pointer, which the gate allocates itself:
@@ -232,3 +238,50 @@ def test_buffers_are_freed(stub):
     assert stub.stub_live() == live + 2
     del x, y
     assert stub.stub_live() == live
+
+
+def _record(stub, fn, nbytes):
+    stub.stub_reset(nbytes)
+    keep = fn()
+    calls = [[stub.stub_call(k, j) for j in range(8)] for k in range(stub.stub_ncalls())]
+    return calls, ctypes.string_at(stub.stub_params(), nbytes), keep
+
+
+@pytest.mark.parametrize("shape,axis_last,mean", [((64, 48), True, False), ((2, 20000), True, True),
+                                                  ((64, 48), False, False), ((3, 7, 40), True, False)])
+def test_gate_run_sum_matches_python(stub, shape, axis_last, mean):
+    g = np.random.default_rng(5)
+    x = _dev(stub, g.standard_normal(shape).astype(np.float32))
+    r = _dev(stub, g.uniform(0.5, 2.0, (1,) * (len(shape) - 1) + (shape[-1],)).astype(np.float32))
+    n = _gate._native
+    y = n.binary("sub_op", n.unary("tanh_op", n.binary("mul_op", x, r)), n.unary("log1p_op", x))
+    root = y._fusion_node
+    f32 = np.dtype(np.float32)
+    out = _dev(stub, np.zeros(64, np.float32))
+    prog = _fusion._Program(root)
+    nin, nsc = len(prog.arrays), len(prog.scalars)
+    _, outer, _, _, _ = _fusion._plan(prog, root._shape, keep_last=axis_last)
+    nbytes = ctypes.sizeof(_fusion._param_struct(nin, nsc, len(outer)))
+    want = _record(stub, lambda: _fusion._run_sum_py(root, axis_last, f32, out._ptr, mean), nbytes)
+    got = _record(stub, lambda: n.run_sum(root, axis_last, f32, out._ptr, mean), nbytes)
+    assert len(got[0]) == len(want[0]) and got[0][0][0] == 4
+    assert got[0][0][1:] == want[0][0][1:]  # kernel, grid, block
+    off = 8 * max(1, nin)
+    assert got[1][:off] == want[1][:off] and got[1][off + 8:] == want[1][off + 8:]
+    if len(want[0]) == 2:  # partials, then the reduction over them into out
+        assert got[0][1][:7] == want[0][1][:7] and got[0][1][7] == want[0][1][7] == out._ptr
+        assert int.from_bytes(got[1][off:off + 8], "little") == got[2].ptr
+    else:
+        assert int.from_bytes(got[1][off:off + 8], "little") == out._ptr
+
+
+def test_native_dispatch_switch():
+    from macmetalpy_amd._config import set_config
+    assert ew.unary is _gate._native.unary
+    set_config(native_dispatch=False)
+    try:
+        assert ew.unary is ew._unary_py and _fusion.materialize is _fusion._materialize_py
+        assert _fusion.run_sum is _fusion._run_sum_py
+    finally:
+        set_config(native_dispatch=True)
+    assert ew.binary is _gate._native.binary and _fusion.run_sum is _gate._native.run_sum

@@ -31,7 +31,7 @@ except ImportError as exc:  # the product needs it: no silent Python-only mode
 __all__ = ["setup", "apply", "bind_library", "unbind_library", "stats"]
 
 _LIB_FUNCS = ("mmp_alloc", "mmp_free", "mmp_unary", "mmp_binary", "mmp_binary_scalar",
-              "mmp_rtc_launch", "mmp_reduce")
+              "mmp_rtc_launch", "mmp_reduce", "mmp_argreduce", "mmp_d2h")
 
 
 def _op_names():
@@ -49,6 +49,18 @@ def _check(status: int, what: str) -> None:
     check(status, what)
 
 
+def _reduce_dtype(code: int, dt):
+    """Result dtype of the gate's reduction ``code`` on ``dt`` (the Python
+    path's rule)."""
+    from .reductions import _np_out_dtype
+    if code in (_abi.REDUCE_ARGMAX, _abi.REDUCE_ARGMIN):
+        return np.dtype(np.int64)
+    if code in (_abi.REDUCE_MAX, _abi.REDUCE_MIN):
+        return dt
+    kind = {_abi.REDUCE_SUM: "sum", _abi.REDUCE_PROD: "prod", _abi.REDUCE_MEAN: "mean"}[code]
+    return _np_out_dtype(kind, dt)
+
+
 def setup() -> None:
     from .ndarray import ndarray
     dtypes = tuple(sorted(_abi.DTYPE_CODES, key=_abi.DTYPE_CODES.get))
@@ -64,6 +76,7 @@ def setup() -> None:
         "check": _check,
         "unary_dtypes": ew._unary_dtypes, "binary_dtypes": ew._binary_dtypes,
         "prune": ew._prune_deps,
+        "reduce_dtype": _reduce_dtype,
         "config": get_config(),
         "dtypes": dtypes,
         "max_depth": _fusion._MAX_DEPTH, "max_leaves": _fusion._MAX_LEAVES,
@@ -77,12 +90,15 @@ def setup() -> None:
 
 def apply(native: bool) -> None:
     """Route the hot path through the gate (True) or the Python path."""
+    from . import reductions
     if native:
         ew.unary, ew.binary = _native.unary, _native.binary
         _fusion.materialize, _fusion.run_sum = _native.materialize, _native.run_sum
+        reductions._native_reduce = _native.reduce
     else:
         ew.unary, ew.binary = ew._unary_py, ew._binary_py
         _fusion.materialize, _fusion.run_sum = _fusion._materialize_py, _fusion._run_sum_py
+        reductions._native_reduce = None
 
 
 def bind_library(lib) -> None:

@@ -49,6 +49,8 @@ typedef int (*fn_binary_t)(int, int, int64_t, const void *, const void *, void *
 typedef int (*fn_binary_scalar_t)(int, int, int64_t, const void *, const void *, int, void *);
 typedef int (*fn_launch_t)(void *, const uint32_t *, const uint32_t *, uint32_t, void **);
 typedef int (*fn_reduce_t)(int, int, int, int64_t, int64_t, int64_t, const void *, void *);
+typedef int (*fn_argreduce_t)(int, int, int64_t, int64_t, int64_t, const void *, int64_t *);
+typedef int (*fn_d2h_t)(void *, const void *, size_t);
 
 fn_alloc_t p_alloc = nullptr;
 fn_free_t p_free = nullptr;
@@ -57,6 +59,8 @@ fn_binary_t p_binary = nullptr;
 fn_binary_scalar_t p_binary_scalar = nullptr;
 fn_launch_t p_launch = nullptr;
 fn_reduce_t p_reduce = nullptr;
+fn_argreduce_t p_argreduce = nullptr;
+fn_d2h_t p_d2h = nullptr;
 
 // ------------------------------------------------------------ DeviceBuffer
 struct DevBuf {
@@ -126,7 +130,7 @@ PyTypeObject DevBufType = {PyVarObject_HEAD_INIT(nullptr, 0)};
 PyTypeObject *T_ndarray = nullptr, *T_input = nullptr, *T_cast = nullptr, *T_unary = nullptr,
              *T_binary = nullptr, *T_scalar = nullptr, *T_where = nullptr;
 PyObject *py_unary_fb = nullptr, *py_binary_fb = nullptr, *py_materialize_fb = nullptr,
-         *py_run_sum_fb = nullptr;
+         *py_run_sum_fb = nullptr, *py_reduce_dt = nullptr;
 PyObject *py_compile_map = nullptr, *py_check = nullptr, *py_unary_dt = nullptr,
          *py_binary_dt = nullptr, *py_prune = nullptr;
 PyObject *cfg_obj = nullptr;
@@ -1365,6 +1369,112 @@ PyObject *gate_run_sum(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
   return part;
 }
 
+// ------------------------------------------------------------ reductions
+// reduce(code, x, axis): sum / prod / max / min / mean (MMP_R_* codes 0-4)
+// or argmax / argmin (5, 6) of a device-resident C-contiguous array over
+// all elements (axis None) or its last axis, straight to mmp_reduce /
+// mmp_argreduce -- the reference's fast_reduce gate (_accelerator.c:
+// 549-858).  Returns None (the caller takes the Python path) for anything
+// else: lazy or host-resident input, other axes, empty reductions.  argmax
+// / argmin over everything return a Python int, as the Python path does.
+constexpr int kRedCodes = 7;
+int8_t red_odt[kRedCodes][kNDT];
+
+PyObject *gate_reduce(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
+  if (nargs != 3) {
+    PyErr_SetString(PyExc_TypeError, "reduce(code, x, axis)");
+    return nullptr;
+  }
+  const long code = PyLong_AsLong(args[0]);
+  PyObject *x = args[1], *axis = args[2];
+  if (code < 0 || code >= kRedCodes || !p_reduce || Py_TYPE(x) != T_ndarray) {
+    PyErr_Clear();
+    Py_RETURN_NONE;
+  }
+  PyObject *xd = inst_dict(x);
+  PyObject *node = iget(xd, s_fnode), *np = iget(xd, s_np_data), *buf = iget(xd, s_buffer);
+  PyObject *shape = iget(xd, s_shape), *strides = iget(xd, s_strides), *dto = iget(xd, s_dtype);
+  PyObject *off = iget(xd, s_offset);
+  if ((node && node != Py_None) || (np && np != Py_None) || !buf || Py_TYPE(buf) != &DevBufType ||
+      !shape || !strides || !dto || !off || !PyTuple_CheckExact(shape))
+    Py_RETURN_NONE;
+  const int dt = dtype_index(dto);
+  long long n = 0;
+  if (dt < 0 || !shape_size(shape, &n) || n == 0 || !is_contig(shape, strides)) {
+    PyErr_Clear();
+    Py_RETURN_NONE;
+  }
+  const Py_ssize_t nd = PyTuple_GET_SIZE(shape);
+  long long outer = 1, len = n;
+  bool all = axis == Py_None;
+  if (!all) {
+    if (!PyLong_CheckExact(axis) || nd == 0) Py_RETURN_NONE;
+    const long a = PyLong_AsLong(axis);
+    if (a != -1 && a != nd - 1) Py_RETURN_NONE;
+    len = PyLong_AsLongLong(PyTuple_GET_ITEM(shape, nd - 1));
+    if (len == 0) Py_RETURN_NONE;
+    outer = n / len;
+  }
+  if (red_odt[code][dt] < 0) {
+    PyObject *c = PyLong_FromLong(code);
+    PyObject *r = c ? PyObject_CallFunctionObjArgs(py_reduce_dt, c, dto, nullptr) : nullptr;
+    Py_XDECREF(c);
+    const int od = r ? dtype_index(r) : -1;
+    Py_XDECREF(r);
+    if (od < 0) {
+      PyErr_Clear();
+      Py_RETURN_NONE;
+    }
+    red_odt[code][dt] = (int8_t)od;
+  }
+  const int odt = red_odt[code][dt];
+  const long long o = PyLong_AsLongLong(off);
+  const unsigned long long src = ((DevBuf *)buf)->ptr + (unsigned long long)o * itemsize[dt];
+  PyObject *res = new_devbuf(outer * itemsize[odt]);
+  if (!res) return nullptr;
+  void *dst = (void *)(uintptr_t)((DevBuf *)res)->ptr;
+  const int st = code <= 4 ? p_reduce((int)code, dt, odt, outer, len, 1, (const void *)(uintptr_t)src, dst)
+                           : p_argreduce((int)code, dt, outer, len, 1, (const void *)(uintptr_t)src,
+                                         (int64_t *)dst);
+  if (check_status(st, code <= 4 ? "mmp_reduce" : "mmp_argreduce")) {
+    Py_DECREF(res);
+    return nullptr;
+  }
+  ++stat_native_ops;
+  if (all && code >= 5) {  // a Python int (synchronises, like the Python path)
+    int64_t idx = 0;
+    const int st2 = p_d2h(&idx, dst, 8);
+    Py_DECREF(res);
+    if (check_status(st2, "mmp_d2h")) return nullptr;
+    return PyLong_FromLongLong(idx);
+  }
+  PyObject *oshape = all ? PyTuple_New(0) : PyTuple_GetSlice(shape, 0, nd - 1);
+  PyObject *arr = oshape ? T_ndarray->tp_alloc(T_ndarray, 0) : nullptr;
+  PyObject *d = arr ? PyDict_New() : nullptr;
+  PyObject *ost = d ? contig_strides(oshape) : nullptr;
+  PyObject *zero = ost ? PyLong_FromLong(0) : nullptr;
+  int bad = !zero;
+  if (!bad) {
+    *_PyObject_GetDictPtr(arr) = d;
+    d = nullptr;
+    PyObject *ad = inst_dict(arr);
+    bad = PyDict_SetItem(ad, s_buffer, res) || PyDict_SetItem(ad, s_np_data, Py_None) ||
+          PyDict_SetItem(ad, s_shape, oshape) || PyDict_SetItem(ad, s_dtype, dtypes[odt]) ||
+          PyDict_SetItem(ad, s_strides, ost) || PyDict_SetItem(ad, s_offset, zero) ||
+          PyDict_SetItem(ad, s_base, Py_None) || PyDict_SetItem(ad, s_fnode, Py_None);
+  }
+  Py_XDECREF(d);
+  Py_XDECREF(ost);
+  Py_XDECREF(zero);
+  Py_XDECREF(oshape);
+  Py_DECREF(res);
+  if (bad) {
+    Py_XDECREF(arr);
+    return nullptr;
+  }
+  return arr;
+}
+
 // ------------------------------------------------------------ setup
 PyObject *descr(PyObject *cls, const char *name) {
   PyObject *d = PyObject_GetAttrString(cls, name);
@@ -1403,6 +1513,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   GETCFG(py_binary_fb, "binary_py");
   GETCFG(py_materialize_fb, "materialize_py");
   GETCFG(py_run_sum_fb, "run_sum_py");
+  GETCFG(py_reduce_dt, "reduce_dtype");
   GETCFG(py_compile_map, "compile_map");
   GETCFG(py_check, "check");
   GETCFG(py_unary_dt, "unary_dtypes");
@@ -1444,6 +1555,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   std::memset(bin_odt, -1, sizeof bin_odt);
   std::memset(bsc_rdt, -1, sizeof bsc_rdt);
   std::memset(bsc_odt, -1, sizeof bsc_odt);
+  std::memset(red_odt, -1, sizeof red_odt);
   for (Py_ssize_t i = 0; i < nops; ++i) {
     PyObject *name = PySequence_GetItem(ops, i);
     PyObject *idv = PyLong_FromSsize_t(i);
@@ -1488,6 +1600,8 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
     p_binary_scalar = nullptr;
     p_launch = nullptr;
     p_reduce = nullptr;
+    p_argreduce = nullptr;
+    p_d2h = nullptr;
     g_kernels.clear();
     Py_RETURN_NONE;
   }
@@ -1506,9 +1620,11 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
   p_binary_scalar = (fn_binary_scalar_t)addr("mmp_binary_scalar");
   p_launch = (fn_launch_t)addr("mmp_rtc_launch");
   p_reduce = (fn_reduce_t)addr("mmp_reduce");
+  p_argreduce = (fn_argreduce_t)addr("mmp_argreduce");
+  p_d2h = (fn_d2h_t)addr("mmp_d2h");
   if (PyErr_Occurred()) return nullptr;
   if (!p_alloc || !p_free || !p_unary || !p_binary || !p_binary_scalar || !p_launch ||
-      !p_reduce) {
+      !p_reduce || !p_argreduce || !p_d2h) {
     p_launch = nullptr;
     PyErr_SetString(PyExc_ValueError, "set_library: missing entry points");
     return nullptr;
@@ -1539,6 +1655,8 @@ PyMethodDef methods[] = {
      "Evaluate a lazy array in place (falls back to the Python path)."},
     {"run_sum", (PyCFunction)(void (*)(void))gate_run_sum, METH_FASTCALL,
      "run_sum(root, axis_last, out_dtype, out_ptr, mean): fused sum epilogue."},
+    {"reduce", (PyCFunction)(void (*)(void))gate_reduce, METH_FASTCALL,
+     "reduce(code, x, axis): whole-array or last-axis reduction, or None."},
     {"stats", (PyCFunction)gate_stats, METH_NOARGS, "Counters of the native and fallback paths."},
     {"clear_kernels", (PyCFunction)gate_clear_kernels, METH_NOARGS,
      "Forget the generated kernels known by structure."},

@@ -31,6 +31,12 @@ __all__ = ["sum", "mean", "prod", "max", "min", "amax", "amin", "argmax", "argmi
 
 _OUT_DTYPE_CACHE: dict = {}
 
+# The native gate's reduction (macmetalpy_amd._native.reduce), bound by the
+# package when native dispatch is on: reduce(code, x, axis) does a plain
+# whole-array or last-axis reduction of a device-resident contiguous array
+# in C and returns None for everything else.
+_native_reduce = None
+
 
 def _np_out_dtype(kind: str, dt: np.dtype) -> np.dtype:
     key = (kind, dt)
@@ -183,6 +189,11 @@ def sum(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
         where=np._NoValue):
     """Sum of elements (reference reductions.py:74-113); ``where`` masks
     elements out (they count as 0)."""
+    if (_native_reduce is not None and dtype is None and out is None and not keepdims
+            and initial is np._NoValue and where is np._NoValue):
+        r = _native_reduce(_abi.REDUCE_SUM, a, axis)
+        if r is not None:
+            return r
     if where is not np._NoValue:
         a = _masked(a, where, 0)
     r = _reduce(a, "sum", axis, dtype, None, keepdims)
@@ -197,6 +208,10 @@ def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
     ``where``: the masked sum over the number of selected elements (NaN
     where none is selected, as NumPy)."""
     if where is None or where is np._NoValue:
+        if _native_reduce is not None and dtype is None and out is None and not keepdims:
+            r = _native_reduce(_abi.REDUCE_MEAN, a, axis)
+            if r is not None:
+                return r
         return _reduce(a, "mean", axis, dtype, out, keepdims)
     a = _asarray(a)
     odt = _np_out_dtype("mean", a._dtype if dtype is None else resolve_dtype(dtype))
@@ -208,6 +223,11 @@ def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
 
 def prod(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue,
          where=np._NoValue):
+    if (_native_reduce is not None and dtype is None and out is None and not keepdims
+            and initial is np._NoValue and where is np._NoValue):
+        r = _native_reduce(_abi.REDUCE_PROD, a, axis)
+        if r is not None:
+            return r
     if where is not np._NoValue:
         a = _masked(a, where, 1)
     r = _reduce(a, "prod", axis, dtype, None, keepdims)
@@ -217,6 +237,11 @@ def prod(a, axis=None, dtype=None, out=None, keepdims=False, initial=np._NoValue
 
 
 def _extreme(a, kind, axis, out, keepdims, initial, where):
+    if (_native_reduce is not None and out is None and not keepdims
+            and initial is np._NoValue and where is np._NoValue):
+        r = _native_reduce(_abi.REDUCE_MAX if kind == "max" else _abi.REDUCE_MIN, a, axis)
+        if r is not None:
+            return r
     from .ufunc_ops import maximum, minimum
     if where is not np._NoValue:
         if initial is np._NoValue:
@@ -270,6 +295,11 @@ def all(a, axis=None, out=None, keepdims=False, where=np._NoValue):
 
 
 def _argreduce(a, op, axis, out, keepdims):
+    if (_native_reduce is not None and out is None and not keepdims
+            and op in (_abi.REDUCE_ARGMAX, _abi.REDUCE_ARGMIN)):
+        r = _native_reduce(op, a, axis)
+        if r is not None:
+            return r
     a = _asarray(a)
     name = {_abi.REDUCE_ARGMAX: "argmax", _abi.REDUCE_ARGMIN: "argmin",
             _abi.REDUCE_NANARGMAX: "nanargmax", _abi.REDUCE_NANARGMIN: "nanargmin"}[op]

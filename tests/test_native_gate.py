@@ -35,7 +35,8 @@ def stub(tmp_path_factory):
     lib.mmp_last_error.restype = ctypes.c_char_p
     # the library's own ctypes signatures, for the entry points the stub has
     for name in ("mmp_rtc_compile", "mmp_alloc", "mmp_free", "mmp_h2d", "mmp_d2h",
-                 "mmp_rtc_launch", "mmp_reduce", "mmp_unary", "mmp_binary", "mmp_binary_scalar"):
+                 "mmp_rtc_launch", "mmp_reduce", "mmp_argreduce", "mmp_unary", "mmp_binary",
+                 "mmp_binary_scalar"):
         getattr(lib, name).argtypes = _backend._SIGNATURES[name]
         getattr(lib, name).restype = ctypes.c_int
     saved = (_backend.HipBackend._instance, _backend._lib)
@@ -285,3 +286,36 @@ def test_native_dispatch_switch():
     finally:
         set_config(native_dispatch=True)
     assert ew.binary is _gate._native.binary and _fusion.run_sum is _gate._native.run_sum
+
+
+def test_gate_reductions_call_the_library_directly(stub):
+    """sum / mean / max / argmax of a device-resident contiguous array, over
+    everything or the last axis: one mmp_reduce / mmp_argreduce call with the
+    Python path's output dtype; anything else is handed back (None)."""
+    g = np.random.default_rng(6)
+    x = _dev(stub, g.standard_normal((6, 10)).astype(np.float32))
+    i = _dev(stub, g.integers(-5, 5, (6, 10)).astype(np.int32))
+    n = _gate._native
+    f32, i32 = _abi.DTYPE_CODES[np.dtype(np.float32)], _abi.DTYPE_CODES[np.dtype(np.int32)]
+    i64 = _abi.DTYPE_CODES[np.dtype(np.int64)]
+    f64 = _abi.DTYPE_CODES[np.dtype(np.float64)]
+    for code, arr, axis, want_call, shape, dt in (
+            (_abi.REDUCE_SUM, x, None, (5, _abi.REDUCE_SUM, f32, f32, 1, 60, 1), (), np.float32),
+            (_abi.REDUCE_SUM, i, -1, (5, _abi.REDUCE_SUM, i32, i64, 6, 10, 1), (6,), np.int64),
+            (_abi.REDUCE_MEAN, i, None, (5, _abi.REDUCE_MEAN, i32, f64, 1, 60, 1), (), np.float64),
+            (_abi.REDUCE_MAX, x, 1, (5, _abi.REDUCE_MAX, f32, f32, 6, 10, 1), (6,), np.float32),
+            (_abi.REDUCE_ARGMAX, x, 1, (6, _abi.REDUCE_ARGMAX, f32, 6, 10, 1), (6,), np.int64)):
+        stub.stub_reset(0)
+        r = n.reduce(code, arr, axis)
+        call = tuple(stub.stub_call(0, j) for j in range(len(want_call)))
+        assert stub.stub_ncalls() == 1 and call == want_call, (call, want_call)
+        assert type(r) is ndarray and r._shape == shape and r._dtype == np.dtype(dt)
+        assert r._fusion_node is None and r._buffer is not None
+    stub.stub_reset(0)
+    assert n.reduce(_abi.REDUCE_ARGMAX, x, None) == 7  # a Python int, read back
+    assert stub.stub_ncalls() == 1
+    # handed back: other axes, lazy or host-resident input, non-contiguous views
+    assert n.reduce(_abi.REDUCE_SUM, x, 0) is None
+    assert n.reduce(_abi.REDUCE_SUM, n.unary("neg_op", x), None) is None
+    assert n.reduce(_abi.REDUCE_SUM, cp.array(np.ones(4, np.float32)), None) is None
+    assert n.reduce(_abi.REDUCE_SUM, x.transpose(), None) is None

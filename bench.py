@@ -243,6 +243,84 @@ def bench_c3(cp, be, reps=10):
 
 
 # --------------------------------------------------------------- C4
+# Register-only MFMA loop with random (finite) float16 operands: the matrix
+# units' practical ceiling when they are fed with no data movement at all
+# (the clock falls with operand toggling, so this sits below the 2.5 PF/s
+# dense spec).  Eight independent 16x16x32 (or four 32x32x16) accumulators
+# per wave, operands rotated so that consecutive MFMAs see different bits.
+_MFMA_CEILING_SRC = r"""
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+__device__ inline h8 operand(unsigned s) {
+  u4 u;
+  u.x = s * 2654435761u; u.y = u.x * 2246822519u + 7u;
+  u.z = u.y * 3266489917u + 11u; u.w = u.z * 668265263u + 13u;
+  u &= 0xbfffbfffu;  // clear each half's top exponent bit: finite values
+  return __builtin_bit_cast(h8, u);
+}
+extern "C" __global__ __launch_bounds__(256) void mfma16(float* out, int iters, unsigned seed) {
+  const unsigned t = blockIdx.x * 256 + threadIdx.x;
+  h8 a[4], b[4];
+  for (int i = 0; i < 4; ++i) { a[i] = operand(seed + t * 8 + i); b[i] = operand(seed ^ (t * 8 + i + 4)); }
+  f4 c[8];
+  for (int i = 0; i < 8; ++i) c[i] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        c[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i & 3], b[(i + p) & 3], c[i], 0, 0, 0);
+  }
+  float s = 0.f;
+  for (int i = 0; i < 8; ++i) s += c[i].x + c[i].y + c[i].z + c[i].w;
+  out[t] = s;
+}
+extern "C" __global__ __launch_bounds__(256) void mfma32(float* out, int iters, unsigned seed) {
+  const unsigned t = blockIdx.x * 256 + threadIdx.x;
+  h8 a[4], b[4];
+  for (int i = 0; i < 4; ++i) { a[i] = operand(seed + t * 8 + i); b[i] = operand(seed ^ (t * 8 + i + 4)); }
+  f16v c[4];
+  for (int i = 0; i < 4; ++i) for (int j = 0; j < 16; ++j) c[i][j] = 0.f;
+  for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        c[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[(i + p) & 3], c[i], 0, 0, 0);
+  }
+  float s = 0.f;
+  for (int i = 0; i < 4; ++i) for (int j = 0; j < 16; ++j) s += c[i][j];
+  out[t] = s;
+}
+"""
+
+
+def mfma_ceiling(cp, be, iters=16000, reps=3):
+    """TFLOP/s of the register-only float16 MFMA loops (2048 workgroups of
+    four waves, ``iters`` steps; best of ``reps`` after one warm-up)."""
+    nwg = 2048
+    out = cp.zeros(nwg * 256, dtype=np.float32)
+    out._ensure_gpu()
+    res = {}
+    for name in ("mfma16", "mfma32"):
+        k = cp.RawKernel(_MFMA_CEILING_SRC, name)
+        k((nwg * 256,), (out, np.int32(iters), np.uint32(1)))
+        best = None
+        for rep in range(reps):
+            s, e = be.event(), be.event()
+            be.record(s)
+            k((nwg * 256,), (out, np.int32(iters), np.uint32(2 + rep)))
+            be.record(e)
+            cp.synchronize()
+            ms = be.elapsed_ms(s, e)
+            best = ms if best is None else min(best, ms)
+        flops = nwg * 4 * iters * 131072  # 8 x 16x16x32 or 4 x 32x32x16 per step
+        res[name] = {"ms": round(best, 3), "tflops": round(flops / best / 1e9, 1)}
+    return res
+
+
 def bench_c4(cp, be, reps=20, warm=10):
     from macmetalpy_amd.workloads import c4_inputs
     res = {}
@@ -274,6 +352,10 @@ def bench_c4(cp, be, reps=20, warm=10):
             del a, b
         except Exception as e:
             res[kind] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    try:
+        res["fp16_mfma_practical_ceiling"] = mfma_ceiling(cp, be)
+    except Exception as e:
+        res["fp16_mfma_practical_ceiling"] = {"error": f"{type(e).__name__}: {e}"[:300]}
     return res
 
 
@@ -649,7 +731,7 @@ def _env(be):
 
 ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
             "cumsum_f32", "matmul_f16", "sort_f32", "c5_fused", "sum_all", "sum_axis1",
-            "argmax_all", "argmax_axis1", "c1_2p20")
+            "argmax_all", "argmax_axis1", "c1_2p20", "mfma_ceiling")
 
 
 def run_only(cp, be, name, steps):
@@ -658,6 +740,9 @@ def run_only(cp, be, name, steps):
     (1 GiB read + 1 GiB written) used to calibrate the byte counters."""
     from macmetalpy_amd.workloads import (c1_inputs, c2_float_inputs, c2_int_inputs, c3_matrix,
                                           c3_scan_inputs, c4_inputs, c5_inputs)
+    if name == "mfma_ceiling":
+        print(json.dumps({"only": name, **mfma_ceiling(cp, be)}), flush=True)
+        return
     if name in ("add_f32", "sin_f32", "copy_f32"):
         a, b = (cp.array(x) for x in c2_float_inputs(N28))
     elif name in ("floor_divide_i32", "mod_i32"):

@@ -392,13 +392,19 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
         for k in range(nin):
             L.append(f"  const long long ro{k} = 0;")
     else:
-        L.append("  const long long row = (long long)blockIdx.x / p.colblocks;")
-        L.append("  const long long cb = (long long)blockIdx.x - row * p.colblocks;")
+        # workgroup ids, colblocks and the outer extents are below 2^31
+        # (HIP's grid limit), so the index splits divide in 32 bits: a
+        # 64-bit division is ~130 scalar instructions per wave
+        L.append("  const unsigned cbk = (unsigned)p.colblocks;")
+        L.append("  const unsigned rowu = blockIdx.x / cbk;")
+        L.append("  const long long row = rowu;")
+        L.append("  const long long cb = blockIdx.x - rowu * cbk;")
         for k in range(nin):
             L.append(f"  long long ro{k} = 0;")
-        L.append("  { long long r = row;")
+        L.append("  { unsigned r = rowu;")
         for d in range(nouter - 1, -1, -1):
-            L.append(f"    {{ const long long q = r / p.oshape[{d}]; const long long ix = r - q * p.oshape[{d}];")
+            L.append(f"    {{ const unsigned q = r / (unsigned)p.oshape[{d}]; "
+                     f"const long long ix = r - q * (unsigned)p.oshape[{d}];")
             for k in range(nin):
                 L.append(f"      ro{k} += ix * p.ostride[{k * nouter + d}];")
             L.append("      r = q; }")
@@ -455,12 +461,17 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
         L.append("}")
     else:  # row-sum epilogue
         L.append(f"  {acc_ct} acc = 0;")
+        L.append("  const unsigned cbk_ = (unsigned)p.colblocks;")
         if vec:
             # column ranges are multiples of 4 elements, so every 16-byte
             # (or narrower) vector load of a contiguous leaf is aligned
-            L.append("  const long long per = ((cols + p.colblocks - 1) / p.colblocks + 3) & ~3LL;")
+            L.append("  const long long span = cols + p.colblocks - 1;")
+            L.append("  const long long per = ((span < 0x100000000LL ? (long long)((unsigned)span / cbk_) "
+                     ": span / p.colblocks) + 3) & ~3LL;")
         else:
-            L.append("  const long long per = (cols + p.colblocks - 1) / p.colblocks;")
+            L.append("  const long long span = cols + p.colblocks - 1;")
+            L.append("  const long long per = span < 0x100000000LL ? (long long)((unsigned)span / cbk_) "
+                     ": span / p.colblocks;")
         L.append("  const long long c0 = cb * per;")
         L.append("  const long long c1 = c0 + per < cols ? c0 + per : cols;")
         if vec:
@@ -621,6 +632,13 @@ def _vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, out_itemsize, mode):
     return True
 
 
+def _check_grid(nblocks: int) -> None:
+    """HIP counts at most 2^32 - 1 work-items per grid dimension; the
+    generated kernels also split workgroup ids in 32-bit arithmetic."""
+    if nblocks * _BLOCK > 0xFFFFFFFF:
+        raise ValueError("fused launch too large")
+
+
 def run_map(root: FusionNode, out_buffer, out_ptr: int) -> None:
     """Evaluate ``root`` into the C-contiguous output at ``out_ptr``."""
     prog = _Program(root)
@@ -636,6 +654,7 @@ def run_map(root: FusionNode, out_buffer, out_ptr: int) -> None:
     nblocks = rows * colblocks
     if nblocks == 0:
         return
+    _check_grid(nblocks)
     HipBackend().launch(kern, (nblocks, 1, 1), (_BLOCK, 1, 1), [p])
 
 
@@ -668,8 +687,10 @@ def _run_sum_py(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean
                                vec, "sum")
     if final_direct:
         p, rows = _fill_params(prog, P, outer, cols, leaf_str, out_ptr, 1, scale)
+        _check_grid(rows)
         be.launch(kern, (rows, 1, 1), (_BLOCK, 1, 1), [p])
         return None
+    _check_grid(rows * colblocks)
     part = be.create_buffer(rows * colblocks, acc_dt)
     p, rows = _fill_params(prog, P, outer, cols, leaf_str, part.ptr, colblocks, scale)
     be.launch(kern, (rows * colblocks, 1, 1), (_BLOCK, 1, 1), [p])

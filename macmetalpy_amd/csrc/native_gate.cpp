@@ -1170,7 +1170,7 @@ int launch_plan(const Plan &pl, void *kern, unsigned long long outp, long long c
   P[o_n + 3] = (unsigned long long)colblocks;
   std::memcpy(&P[o_scale], &scale, 8);
   const unsigned long long nblocks = (unsigned long long)(pl.rows * colblocks);
-  if (nblocks > 0xffffffffull) {
+  if (nblocks * kBlock > 0xffffffffull) {  // HIP's limit on work-items per grid dimension
     PyErr_SetString(PyExc_ValueError, "fused launch too large");
     return -1;
   }

@@ -165,7 +165,10 @@ MMP_DI float mm_log1p(float x) {
   float r = __builtin_fmaf(kf, ln2_hi, __builtin_fmaf(kf, ln2_lo, p));
   const float inf = __builtin_inff();
   r = (x == 0.0f || x == inf) ? x : r;  // keeps -0.0; +inf -> +inf
-  return x > -1.0f ? r : (x == -1.0f ? -inf : __builtin_nanf(""));
+  // x <= -1 (r is finite or NaN there): adding -inf or NaN gives log1p's
+  // value; elsewhere -0.0 changes nothing.  An add rather than a select of
+  // r keeps the compiler from guarding the whole evaluation by a branch.
+  return r + (x > -1.0f ? -0.0f : (x == -1.0f ? -inf : __builtin_nanf("")));
 }
 MMP_DI double mm_log1p(double x) { return log1p(x); }
 

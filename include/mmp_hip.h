@@ -442,6 +442,17 @@ int mmp_rtc_build(const char *src, const char *options, const char *arch,
 int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
                    uint32_t shared_bytes, void **args);
 
+/* Launch exactly threads3 work-items (Metal's dispatchThreads, as the
+ * reference's RawKernel and MetalBackend.execute_kernel dispatch:
+ * raw_kernel.py:46-59, _metal_backend.py:313-357) in workgroups of block3;
+ * a dimension that block3 does not divide gets a partial last workgroup
+ * whose missing work-items do not run.  Kernels compiled by mmp_rtc_compile
+ * assume uniform workgroups, so blockDim is the full block3 extent in every
+ * workgroup and blockIdx * blockDim + threadIdx is the global index.
+ * block3's product must be 1..1024. */
+int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3, const uint32_t *block3,
+                           uint32_t shared_bytes, void **args);
+
 /* ---- device-side wait status ------------------------------------------ */
 /* Split reductions and scans combine results across workgroups with
  * bounded waits; a wait that runs out records a flag (pinned host memory,

@@ -197,7 +197,7 @@ EXPORTS = (
     "mmp_sort", "mmp_searchsorted", "mmp_take", "mmp_gather", "mmp_scatter", "mmp_nonzero",
     "mmp_bincount", "mmp_histogram",
     "mmp_lu", "mmp_lu_solve", "mmp_cholesky", "mmp_qr", "mmp_qr_q", "mmp_eigh", "mmp_svd",
-    "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch",
+    "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch", "mmp_rtc_launch_threads",
     "mmp_wait_status",
     "mmp_debug_fail_next",
 )

@@ -121,6 +121,7 @@ _SIGNATURES = {
     "mmp_rtc_build": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_vp, _c_sz,
                       ctypes.POINTER(_c_sz)],
     "mmp_rtc_launch": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
+    "mmp_rtc_launch_threads": [_c_vp, _c_u32p, _c_u32p, ctypes.c_uint32, ctypes.POINTER(_c_vp)],
     "mmp_wait_status": [ctypes.POINTER(ctypes.c_uint32)],
     "mmp_debug_fail_next": [_c_int, _c_int],
 }
@@ -197,6 +198,41 @@ def block_for_grid(grid) -> tuple:
     by = _largest_divisor(grid[1], _BLOCK_BUDGET // bx) if len(grid) > 1 else 1
     bz = _largest_divisor(grid[2], _BLOCK_BUDGET // (bx * by)) if len(grid) > 2 else 1
     return (bx, by, bz)
+
+
+# User kernels (RawKernel, execute_kernel) run exactly the requested number
+# of threads.  When no uniform workgroup tiles that count well, the last
+# workgroup of a dimension is partial; a kernel marked uniform-workgroup
+# (hiprtc's default) may not be dispatched that way, so these sources are
+# compiled without that mark, and blockDim is read from the dispatch's
+# workgroup size, which is the full extent in every workgroup, so that
+# blockIdx * blockDim + threadIdx stays the global index (HIP's own
+# blockDim reports the partial extent in a partial workgroup).
+DISPATCH_OPTIONS = "-fno-offload-uniform-block"
+DISPATCH_PRELUDE = (
+    "#define blockDim (dim3(__builtin_amdgcn_workgroup_size_x(), "
+    "__builtin_amdgcn_workgroup_size_y(), __builtin_amdgcn_workgroup_size_z()))\n"
+    "#define hipBlockDim_x (__builtin_amdgcn_workgroup_size_x())\n"
+    "#define hipBlockDim_y (__builtin_amdgcn_workgroup_size_y())\n"
+    "#define hipBlockDim_z (__builtin_amdgcn_workgroup_size_z())\n"
+    "#line 1\n")
+
+
+def dispatch_shape(grid) -> tuple:
+    """(uniform, block) for a launch of exactly ``grid`` threads (1-3
+    dims).  Uniform workgroups dividing the grid are used when they hold at
+    least one wave64; otherwise (a prime thread count would get one-thread
+    workgroups) full workgroups with a partial last one per dimension."""
+    g = tuple(grid) + (1,) * (3 - len(grid))
+    if any(x > 0xFFFFFFFF for x in g):
+        raise ValueError("grid dimension exceeds 2^32 - 1 threads")
+    block = block_for_grid(g)
+    if block[0] * block[1] * block[2] >= 64 or g[0] * g[1] * g[2] <= block[0] * block[1] * block[2]:
+        return True, block
+    bx = min(g[0], _BLOCK_BUDGET)
+    by = min(g[1], _BLOCK_BUDGET // bx)
+    bz = min(g[2], _BLOCK_BUDGET // (bx * by))
+    return False, (bx, by, bz)
 
 
 def _grid3(grid_size) -> tuple:
@@ -448,14 +484,14 @@ class HipBackend:
         key = (shader_src, name)
         kern = self._exec_cache.get(key)
         if kern is None:
-            kern = self.compile(shader_src, name, RTC_OPTIONS)
+            kern = self.compile(DISPATCH_PRELUDE + shader_src, name,
+                                RTC_OPTIONS + " " + DISPATCH_OPTIONS)
             self._exec_cache[key] = kern
         g = _grid3(grid_size)
         total = g[0] * g[1] * g[2]
         if total <= 0:
             return
-        block = block_for_grid(g)
-        blocks = tuple(gi // bi for gi, bi in zip(g, block))
+        uniform, block = dispatch_shape(g)
         from ._elementwise import flush_lazy
         args = []
         for b in buffers:
@@ -477,7 +513,10 @@ class HipBackend:
                 raise ValueError("execute_kernel: buffer has been freed")
             flush_lazy(dev)  # pending expressions reading it see the old data
         args.append(_c_i64(total))
-        self.launch(kern, blocks, block, args)
+        if uniform:
+            self.launch(kern, tuple(gi // bi for gi, bi in zip(g, block)), block, args)
+        else:
+            self.launch_threads(kern, g, block, args)
 
     # -------------------------------------------------- runtime compile
     def compile(self, source: str, name: str, options: str = "") -> int:
@@ -498,6 +537,18 @@ class HipBackend:
         st = self._lib.mmp_rtc_launch(kernel, g, b, shared, ptrs)
         if st:
             _check(st, "mmp_rtc_launch")
+
+    def launch_threads(self, kernel: int, threads: Sequence[int], block: Sequence[int],
+                       args: Sequence, shared: int = 0) -> None:
+        """Launch exactly ``threads`` work-items (per dimension) in
+        workgroups of ``block``; a dimension that ``block`` does not divide
+        ends in a partial workgroup (Metal's dispatchThreads)."""
+        t = _U32x3(*(tuple(threads) + (1, 1, 1))[:3])
+        b = _U32x3(*(tuple(block) + (1, 1, 1))[:3])
+        ptrs = (_c_vp * max(1, len(args)))(*[ctypes.addressof(a) for a in args])
+        st = self._lib.mmp_rtc_launch_threads(kernel, t, b, shared, ptrs)
+        if st:
+            _check(st, "mmp_rtc_launch_threads")
 
 
 def rtc_build(source: str, options: str = "", arch: str = "gfx950") -> bytes:

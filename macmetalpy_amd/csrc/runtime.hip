@@ -13,6 +13,7 @@
 //  * kernels are precompiled gfx950 code objects; only fused expressions and
 //    user RawKernels go through hiprtc, cached by source text.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hiprtc.h>
 
 #include <cstdarg>
@@ -533,6 +534,25 @@ int mmp_rtc_launch(void *kernel, const uint32_t *grid3, const uint32_t *block3,
                                        block3[0], block3[1], block3[2], shared_bytes,
                                        g_dev.stream, args, nullptr);
   return mmpi::check_hip(e, "hipModuleLaunchKernel");
+}
+
+int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3, const uint32_t *block3,
+                           uint32_t shared_bytes, void **args) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (!kernel || !threads3 || !block3) return mmpi::fail(MMP_E_ARG, "null argument");
+  if (threads3[0] == 0 || threads3[1] == 0 || threads3[2] == 0) return MMP_OK;
+  if (block3[0] == 0 || block3[1] == 0 || block3[2] == 0 ||
+      (uint64_t)block3[0] * block3[1] * block3[2] > 1024)
+    return mmpi::fail(MMP_E_ARG, "mmp_rtc_launch_threads: bad workgroup %ux%ux%u", block3[0],
+                      block3[1], block3[2]);
+  if (mmpi::inject(3)) return mmpi::fail(MMP_E_INJECTED, "mmp_rtc_launch_threads: injected failure");
+  // The dispatch packet counts work-items, so a grid that is not a multiple
+  // of the workgroup gets a partial last workgroup per dimension: exactly
+  // threads3 work-items run, no more.
+  hipError_t e = hipExtModuleLaunchKernel((hipFunction_t)kernel, threads3[0], threads3[1],
+                                          threads3[2], block3[0], block3[1], block3[2],
+                                          shared_bytes, g_dev.stream, args, nullptr);
+  return mmpi::check_hip(e, "hipExtModuleLaunchKernel");
 }
 
 int mmp_wait_status(uint32_t *flags) {

@@ -7,12 +7,13 @@ source is HIP C++ (compiled by hiprtc for gfx950) instead of MSL; the
 kernel reads its index as ``blockIdx.x * blockDim.x + threadIdx.x`` and,
 because exactly ``grid`` threads are launched, needs no bounds check.
 
-Exactness with uniform workgroups: the workgroup extent in each dimension
-is the largest divisor of the thread count that fits the block budget
-(256 threads), so the grid is a whole number of workgroups and HIP's
-``blockDim`` keeps its usual meaning.  Thread counts with a divisor that is
-a multiple of 64 fill whole wave64s; a prime count runs one thread per
-workgroup (correct, slow).  Scalars (NumPy scalar objects, Python
+Exactly ``grid`` threads run.  When a divisor of the thread count that
+holds at least one wave64 fits the block budget (256 threads), workgroups
+of that extent tile the grid uniformly; otherwise (a prime count, say)
+workgroups of up to 256 threads are used and the last one in each
+dimension is partial: its missing threads do not run, and ``blockDim``
+still reports the full extent, so ``blockIdx * blockDim + threadIdx`` is
+the global index either way.  Scalars (NumPy scalar objects, Python
 int/float) may be passed by value.
 """
 from __future__ import annotations
@@ -23,7 +24,7 @@ from typing import Sequence, Union
 import numpy as np
 
 from . import _elementwise as ew
-from ._backend import HipBackend, block_for_grid
+from ._backend import DISPATCH_OPTIONS, DISPATCH_PRELUDE, HipBackend, dispatch_shape
 from .ndarray import ndarray
 
 __all__ = ["RawKernel"]
@@ -50,8 +51,9 @@ class RawKernel:
     @property
     def kernel(self) -> int:
         if self._kernel is None:
-            self._kernel = HipBackend().compile(self._source, self._func_name,
-                                                ("-O3 -std=c++17 " + self._options).strip())
+            self._kernel = HipBackend().compile(
+                DISPATCH_PRELUDE + self._source, self._func_name,
+                ("-O3 -std=c++17 " + DISPATCH_OPTIONS + " " + self._options).strip())
         return self._kernel
 
     def __call__(self, grid: Union[int, tuple], args: Sequence, shared_mem: int = 0) -> None:
@@ -62,8 +64,7 @@ class RawKernel:
             raise ValueError("grid tuple must have 1-3 elements")
         if any(g <= 0 for g in grid):
             return
-        block = block_for_grid(grid)
-        blocks = tuple(g // b for g, b in zip(grid, block))
+        uniform, block = dispatch_shape(grid)
         cargs = []
         arrays = []
         for a in args:
@@ -81,4 +82,8 @@ class RawKernel:
                 raise TypeError(f"unsupported RawKernel argument type {type(a).__name__}")
         for a in arrays:  # the kernel may write any of them
             ew.flush_lazy(a._buffer)
-        HipBackend().launch(self.kernel, blocks, block, cargs, shared_mem)
+        if uniform:
+            HipBackend().launch(self.kernel, tuple(g // b for g, b in zip(grid + (1, 1), block)),
+                                block, cargs, shared_mem)
+        else:
+            HipBackend().launch_threads(self.kernel, grid, block, cargs, shared_mem)

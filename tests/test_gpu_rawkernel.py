@@ -102,6 +102,41 @@ def test_exact_thread_count_leaves_tail_untouched():
     assert np.all(got[n:] == -7.0)
 
 
+BLOCKDIM = r'''
+extern "C" __global__ void block_extent(int* out) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  out[i] = (int)(blockDim.x * 1000 + gridDim.x);
+}'''
+
+
+def test_prime_thread_count_runs_in_full_workgroups():
+    """A prime count has no divisor that fills a wave64: it runs in
+    256-thread workgroups with a partial last one (blockDim stays 256 there
+    too), exactly n threads, and the tail past n is untouched."""
+    n, pad = 1_000_003, 512
+    a = cp.array(np.arange(n + pad, dtype=np.float32))
+    out = cp.array(np.full(n + pad, -7.0, np.float32))
+    RawKernel(DBL_F32, "dbl")(n, (a, out))
+    got = out.get()
+    npt.assert_array_equal(got[:n], 2 * np.arange(n, dtype=np.float32))
+    assert np.all(got[n:] == -7.0)
+    ext = cp.array(np.full(n + pad, -1, np.int32))
+    RawKernel(BLOCKDIM, "block_extent")(n, (ext,))
+    got = ext.get()
+    assert np.all(got[:n] == 256 * 1000 + (n + 255) // 256)
+    assert np.all(got[n:] == -1)
+
+
+def test_prime_2d_grid():
+    w, h = 1009, 7
+    o = cp.array(np.full(1024 * 8 + 4096, -1, np.int32))
+    RawKernel(GRID2D, "fill2d")((w, h), (o, np.int32(w)))
+    got = o.get()
+    yy, xx = np.mgrid[0:h, 0:w]
+    npt.assert_array_equal(got[:w * h].reshape(h, w), yy * 1000 + xx)
+    assert np.all(got[w * h:] == -1)
+
+
 def test_eight_buffers_reuse_two_kernels():
     bufs = [cp.array([float(i + 1)], dtype=np.float32) for i in range(8)]
     out = cp.empty(1, dtype=np.float32)

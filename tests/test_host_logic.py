@@ -158,3 +158,35 @@ def test_jacobi_convergence_check():
         LA._check_converged(np.array([3, LA._MAX_SWEEPS, 12]), "SVD did not converge")
     src = open(os.path.join(os.path.dirname(LA.__file__), "csrc", "linalg.hip")).read()
     assert f"constexpr int kMaxSweeps = {LA._MAX_SWEEPS};" in src
+
+
+@pytest.mark.parametrize("grid", [(1,), (7,), (64,), (1000,), (100_000,), (1_000_003,), (65537,),
+                                  (37, 23), (1009, 7), (7, 11, 13), (4, 1, 1), (2, 3, 5),
+                                  (1 << 20, 3), (97, 89, 83)])
+def test_dispatch_shape_covers_exactly_the_grid(grid):
+    """RawKernel / execute_kernel launch shape: uniform workgroups of at
+    least one wave64 that divide the grid when such a divisor exists (or a
+    single workgroup), else full workgroups with a partial last one; the
+    workgroup never exceeds 256 threads and, in the uniform case, tiles the
+    grid exactly."""
+    from macmetalpy_amd._backend import dispatch_shape
+    uniform, block = dispatch_shape(grid)
+    g = tuple(grid) + (1,) * (3 - len(grid))
+    assert len(block) == 3 and all(b >= 1 for b in block)
+    assert block[0] * block[1] * block[2] <= 256
+    assert all(b <= x for b, x in zip(block, g))
+    if uniform:
+        assert all(x % b == 0 for x, b in zip(g, block))
+        assert block[0] * block[1] * block[2] >= 64 or block == g
+    else:
+        # a partial last workgroup only where no uniform wave-sized split exists
+        assert block[0] * block[1] * block[2] >= 64
+        assert any(x % b for x, b in zip(g, block))
+
+
+def test_dispatch_shape_prime_counts_use_full_workgroups():
+    from macmetalpy_amd._backend import dispatch_shape
+    assert dispatch_shape((1_000_003,)) == (False, (256, 1, 1))
+    assert dispatch_shape((1000,)) == (True, (250, 1, 1))
+    with pytest.raises(ValueError):
+        dispatch_shape((1 << 32,))

@@ -319,3 +319,53 @@ def test_gate_reductions_call_the_library_directly(stub):
     assert n.reduce(_abi.REDUCE_SUM, n.unary("neg_op", x), None) is None
     assert n.reduce(_abi.REDUCE_SUM, cp.array(np.ones(4, np.float32)), None) is None
     assert n.reduce(_abi.REDUCE_SUM, x.transpose(), None) is None
+
+
+def test_gate_leaks_no_references(stub):
+    """Thousands of gate calls (elementwise ops with arrays and Python
+    scalars, materialisation through the precompiled and the generated
+    paths, reductions, calls handed back to Python, errors) leave the
+    reference counts of the shared objects they touch, the number of live
+    Python objects and the stub's live allocations where they were."""
+    import gc
+    import sys
+    n = _gate._native
+    g = np.random.default_rng(9)
+    x = _dev(stub, g.standard_normal((8, 16)).astype(np.float32))
+    w = _dev(stub, g.standard_normal((8, 16)).astype(np.float32))
+    i = _dev(stub, g.integers(-5, 5, (8, 16)).astype(np.int32))
+    f32, i64 = np.dtype(np.float32), np.dtype(np.int64)
+    watched = [f32, i64, np.dtype(np.int32), np.dtype(np.float64), ndarray, "add_op", "neg_op",
+               "mul_op", "tanh_op", x, w, i, x._buffer, w._buffer, None, True, False]
+
+    def work():
+        a = n.binary("add_op", x, w)
+        n.materialize(a)                                   # precompiled binary kernel
+        b = n.unary("neg_op", n.binary("mul_op", x, 2.5))  # generated kernel
+        n.materialize(b)
+        c = n.binary("add_op", i, 3)                       # int array + Python int
+        n.materialize(c)
+        d = n.unary("tanh_op", n.binary("mul_op", x, w))
+        n.run_sum(d._fusion_node, True, f32, x._ptr, False)
+        r = n.reduce(_abi.REDUCE_SUM, x, None)
+        r2 = n.reduce(_abi.REDUCE_MAX, i, -1)
+        h = n.binary("add_op", x, cp.array(np.ones((8, 16), np.float32)))  # handed back
+        assert n.reduce(_abi.REDUCE_SUM, x, 0) is None
+        try:
+            n.binary("add_op", x, _dev(stub, np.ones((3, 5), np.float32)))
+        except ValueError:
+            pass
+        return a, b, c, r, r2, h
+
+    for _ in range(20):  # warm the caches, result-dtype tables and kernel table
+        work()
+    gc.collect()
+    refs = [sys.getrefcount(o) for o in watched]
+    nobj = len(gc.get_objects())
+    live = stub.stub_live()
+    for _ in range(2000):
+        work()
+    gc.collect()
+    assert [sys.getrefcount(o) for o in watched] == refs
+    assert len(gc.get_objects()) <= nobj + 50
+    assert stub.stub_live() == live

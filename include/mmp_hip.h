@@ -185,6 +185,15 @@ int mmp_h2d(void *dst, const void *src, size_t bytes);
 int mmp_d2h(void *dst, const void *src, size_t bytes);
 int mmp_d2d(void *dst, const void *src, size_t bytes);
 
+/* Page-locked host blocks (cached by size) for arrays copied back to the
+ * host: mmp_d2h into one runs at the link rate instead of being staged
+ * through the runtime's bounce buffers.  The reference's get() reads
+ * unified memory (ndarray.py:576-603), so it has no counterpart.
+ * MMP_E_OOM when more than 4 GiB would be handed out at once (callers
+ * then use pageable memory). */
+int mmp_host_alloc(size_t bytes, void **ptr);
+int mmp_host_free(void *ptr);
+
 /* Wait for all enqueued work.  Replaces MetalBackend.synchronize
  * (_metal_backend.py:359-372: dispatch of `_sync` with wait=True).  Returns
  * MMP_E_WAIT when a device-side bounded wait ran out since the last check

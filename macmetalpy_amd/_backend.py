@@ -85,6 +85,8 @@ _SIGNATURES = {
     "mmp_h2d": [_c_vp, _c_vp, _c_sz],
     "mmp_d2h": [_c_vp, _c_vp, _c_sz],
     "mmp_d2d": [_c_vp, _c_vp, _c_sz],
+    "mmp_host_alloc": [_c_sz, ctypes.POINTER(_c_vp)],
+    "mmp_host_free": [_c_vp],
     "mmp_sync": [],
     "mmp_event_create": [ctypes.POINTER(_c_vp)],
     "mmp_event_record": [_c_vp],
@@ -173,6 +175,32 @@ from ._native import DeviceBuffer  # noqa: E402
 
 
 _U32x3 = ctypes.c_uint32 * 3
+
+# Results of 64 KiB .. 256 MiB come back into page-locked host blocks.
+_PINNED_MIN = 64 << 10
+_PINNED_MAX = 256 << 20
+
+
+class _PinnedBlock:
+    """Owner of one page-locked host block, exposed to NumPy as bytes; the
+    block goes back to the library's cache when the last array viewing it
+    is released."""
+
+    __slots__ = ("_lib", "_ptr", "__array_interface__", "__weakref__")
+
+    def __init__(self, lib, ptr: int, nbytes: int) -> None:
+        self._lib = lib
+        self._ptr = ptr
+        self.__array_interface__ = {"data": (ptr, False), "shape": (nbytes,), "typestr": "|u1",
+                                    "version": 3}
+
+    def __del__(self) -> None:
+        ptr, self._ptr = self._ptr, 0
+        if ptr:
+            try:
+                self._lib.mmp_host_free(ptr)
+            except Exception:  # interpreter shutdown
+                pass
 
 _BLOCK_BUDGET = 256
 
@@ -316,6 +344,22 @@ class HipBackend:
             _check(self._lib.mmp_d2h(out.ctypes.data, buf.ptr + byte_offset, out.nbytes),
                    "mmp_d2h")
         return out
+
+    def host_empty(self, shape, dtype) -> np.ndarray:
+        """A C-contiguous NumPy array in page-locked host memory (a cached
+        block, returned to the cache when the array is released), or an
+        ordinary array when the size is outside the pinned range or the
+        pinned budget is used up.  Copies from the device into it run at
+        the link rate."""
+        dtype = np.dtype(dtype)
+        nbytes = int(np.prod(shape, dtype=np.int64)) * dtype.itemsize
+        if not _PINNED_MIN <= nbytes <= _PINNED_MAX:
+            return np.empty(shape, dtype)
+        p = _c_vp()
+        if self._lib.mmp_host_alloc(nbytes, ctypes.byref(p)) or not p.value:
+            return np.empty(shape, dtype)
+        block = _PinnedBlock(self._lib, p.value, nbytes)
+        return np.asarray(block).view(dtype).reshape(shape)
 
     def copy_buffer(self, dst: int, src: int, nbytes: int) -> None:
         if nbytes:

@@ -366,6 +366,62 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   return check_waits();
 }
 
+// ---------------------------------------------------- pinned host blocks
+// Page-locked host memory for results copied back to the host: a DMA into
+// it runs at the link rate, where a copy into pageable memory is staged by
+// the runtime.  Blocks are cached by their rounded size (hipHostMalloc is
+// expensive); at most kHostCacheMax bytes stay cached, and at most
+// kHostLiveMax bytes may be handed out at once (callers fall back to
+// pageable memory beyond that).
+namespace {
+constexpr size_t kHostRound = 64 << 10;
+constexpr size_t kHostCacheMax = 1ull << 30;
+constexpr size_t kHostLiveMax = 4ull << 30;
+std::multimap<size_t, void *> g_host_free;          // rounded size -> block
+std::unordered_map<void *, size_t> g_host_live;     // block -> rounded size
+size_t g_host_cached = 0, g_host_out = 0;
+}  // namespace
+
+int mmp_host_alloc(size_t bytes, void **ptr) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (!ptr) return mmpi::fail(MMP_E_ARG, "null pointer");
+  *ptr = nullptr;
+  const size_t r = ((bytes ? bytes : 1) + kHostRound - 1) / kHostRound * kHostRound;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_host_out + r > kHostLiveMax)
+    return mmpi::fail(MMP_E_OOM, "pinned host blocks in use exceed %zu bytes", kHostLiveMax);
+  void *p = nullptr;
+  auto it = g_host_free.find(r);
+  if (it != g_host_free.end()) {
+    p = it->second;
+    g_host_free.erase(it);
+    g_host_cached -= r;
+  } else if (hipHostMalloc(&p, r, hipHostMallocDefault) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return mmpi::fail(MMP_E_OOM, "hipHostMalloc(%zu) failed", r);
+  }
+  g_host_live[p] = r;
+  g_host_out += r;
+  *ptr = p;
+  return MMP_OK;
+}
+
+int mmp_host_free(void *ptr) {
+  if (!ptr) return MMP_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_host_live.find(ptr);
+  if (it == g_host_live.end()) return mmpi::fail(MMP_E_ARG, "not a pinned host block");
+  const size_t r = it->second;
+  g_host_live.erase(it);
+  g_host_out -= r;
+  if (g_host_cached + r <= kHostCacheMax) {
+    g_host_free.emplace(r, ptr);
+    g_host_cached += r;
+    return MMP_OK;
+  }
+  return mmpi::check_hip(hipHostFree(ptr), "hipHostFree");
+}
+
 int mmp_d2d(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;

@@ -184,8 +184,9 @@ class ndarray:
             d = self._np_data
             return d.copy() if _force_copy else d
         src = self if self._is_c_contiguous() else self._contiguous_copy()
-        out = np.empty(self._shape, dtype=self._dtype)
-        HipBackend().read_buffer(src._buffer, src._offset * self._dtype.itemsize, out)
+        be = HipBackend()
+        out = be.host_empty(self._shape, self._dtype)
+        be.read_buffer(src._buffer, src._offset * self._dtype.itemsize, out)
         return out
 
     def _get_view(self) -> np.ndarray:

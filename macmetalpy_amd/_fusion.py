@@ -326,6 +326,51 @@ def _op_fn(table, op_name, dtype, fast):
     return fn
 
 
+_NONNEG_UNARY = frozenset(("abs_op", "absolute_op", "fabs_op", "square_op", "sqrt_op", "exp_op",
+                           "exp2_op", "cosh_op"))
+
+
+def _sign_facts(prog: _Program):
+    """Per SSA value, (never below zero, never above zero) as far as the
+    expression shows it, NaN aside: |x|, x*x, exp(...) are >= 0, their
+    negations <= 0, products and sums of known signs follow (scalar leaves
+    count as unknown: kernels are cached by structure, and a scalar's value
+    is a launch parameter).  Lets the
+    code generator call the forms of exp and log1p without the cases their
+    argument cannot reach (bit for bit the same results)."""
+    facts, canon = [], []
+    for i, step in enumerate(prog.steps):
+        kind, f = step[0], (False, False)
+        canon.append(("load", step[1]) if kind == "load" else i)
+        if prog.dtypes[i].kind != "f":
+            facts.append(f)
+            continue
+        if kind == "cast":
+            f = facts[step[1]] if prog.dtypes[step[1]].kind == "f" else f
+        elif kind == "unary":
+            a = facts[step[2]]
+            if step[1] in _NONNEG_UNARY:
+                f = (True, False)
+            elif step[1] in ("neg_op", "negative_op"):
+                f = (a[1], a[0])
+        elif kind == "where":
+            a, b = facts[step[2]], facts[step[3]]
+            f = (a[0] and b[0], a[1] and b[1])
+        elif kind == "binary":
+            op, a, b = step[1], facts[step[2]], facts[step[3]]
+            if op == "mul_op":
+                if canon[step[2]] == canon[step[3]]:
+                    f = (True, False)
+                else:
+                    f = ((a[0] and b[0]) or (a[1] and b[1]), (a[0] and b[1]) or (a[1] and b[0]))
+            elif op == "add_op":
+                f = (a[0] and b[0], a[1] and b[1])
+            elif op == "sub_op":
+                f = (a[0] and b[1], a[1] and b[0])
+        facts.append(f)
+    return facts
+
+
 def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=False):
     """HIP source for ``prog``.
 
@@ -352,6 +397,8 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
             vtypes[t] = vt
             L.append(f"typedef {st} {vt} __attribute__((ext_vector_type(4)));")
 
+    signs = _sign_facts(prog)
+
     def expr_lines(load_expr, indent):
         """Statements computing every SSA value; load_expr(k) -> leaf k."""
         out = []
@@ -366,7 +413,12 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
                 src_t = ctype_name(prog.dtypes[step[1]])
                 rhs = f"mmp_convert<{t}, {src_t}>(t{step[1]})"
             elif kind == "unary":
-                rhs = f"{_op_fn(_abi.UNARY_FN, step[1], prog.dtypes[i], fast)}(t{step[2]})"
+                fn = _op_fn(_abi.UNARY_FN, step[1], prog.dtypes[i], fast)
+                if fn == "op_exp" and signs[step[2]][1]:
+                    fn = "op_exp_nonpos"
+                elif fn == "op_log1p" and signs[step[2]][0]:
+                    fn = "op_log1p_nonneg"
+                rhs = f"{fn}(t{step[2]})"
             elif kind == "where":
                 rhs = f"(t{step[1]} ? t{step[2]} : t{step[3]})"
             elif step[1] in _abi.COMPARE_OPS:

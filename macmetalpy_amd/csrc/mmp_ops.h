@@ -103,7 +103,6 @@ template <> struct mmp_t<bool> {
 
 MMP_MATH1(sqrt, sqrtf, sqrt)
 MMP_MATH1(cbrt, cbrtf, cbrt)
-MMP_MATH1(exp, expf, exp)
 MMP_MATH1(exp2, exp2f, exp2)
 MMP_MATH1(expm1, expm1f, expm1)
 MMP_MATH1(log, logf, log)
@@ -144,7 +143,7 @@ MMP_MATH2(nextafter, nextafterf, nextafter)
 // exact for |k| <= 128) and a tail.  k = 0 needs no special case (f = x and
 // k ln2 adds zero) except for -0.0, which the final select returns as is.
 // Max error over every float32 input: 1.27 ULP of the exact value.
-MMP_DI float mm_log1p(float x) {
+MMP_DI float mm_log1p_core(float x) {
   const float m = 1.0f + x;
   const int k = (int)(__builtin_bit_cast(unsigned, m) - 0x3f400000u) >> 23;
   const float f = ldexpf(x, -k) + (ldexpf(1.0f, -k) - 1.0f);
@@ -164,13 +163,44 @@ MMP_DI float mm_log1p(float x) {
   const float ln2_lo = 3.1946183e-05f;                          // ln2 - ln2_hi
   float r = __builtin_fmaf(kf, ln2_hi, __builtin_fmaf(kf, ln2_lo, p));
   const float inf = __builtin_inff();
-  r = (x == 0.0f || x == inf) ? x : r;  // keeps -0.0; +inf -> +inf
-  // x <= -1 (r is finite or NaN there): adding -inf or NaN gives log1p's
-  // value; elsewhere -0.0 changes nothing.  An add rather than a select of
-  // r keeps the compiler from guarding the whole evaluation by a branch.
-  return r + (x > -1.0f ? -0.0f : (x == -1.0f ? -inf : __builtin_nanf("")));
+  return (x == 0.0f || x == inf) ? x : r;  // keeps -0.0; +inf -> +inf
 }
+MMP_DI float mm_log1p(float x) {
+  const float inf = __builtin_inff();
+  // x <= -1 (the core value is finite or NaN there): adding -inf or NaN
+  // gives log1p's value; elsewhere -0.0 changes nothing.  An add rather than
+  // a select keeps the compiler from guarding the evaluation by a branch.
+  return mm_log1p_core(x) + (x > -1.0f ? -0.0f : (x == -1.0f ? -inf : __builtin_nanf("")));
+}
+// The same function for arguments known to be >= 0 or NaN (x*x, |x|, ...):
+// bit for bit mm_log1p there (NaN payloads aside), without the x <= -1
+// cases.
+MMP_DI float mm_log1p_nonneg(float x) { return mm_log1p_core(x); }
 MMP_DI double mm_log1p(double x) { return log1p(x); }
+MMP_DI double mm_log1p_nonneg(double x) { return log1p(x); }
+
+// exp for float32 (the standard reduction: e^x = 2^n 2^f with
+// x log2(e) = n + f + l carried as a head and an fma-recovered tail,
+// |f| <= 1/2; v_exp_f32 of f + l, v_ldexp_f32 by n, which also rounds
+// denormal results).  Written here rather than taken from the device
+// library so that the same arithmetic exists without the overflow case
+// (mm_exp_nonpos, for arguments known to be <= 0 or NaN: exp(-|x|),
+// exp(-x*x)), bit for bit mm_exp there (NaN payloads aside).  Max error
+// over every float32 input: 0.89 ULP of the exact value (the device
+// library's expf: 1.0).
+MMP_DI float mm_exp_core(float x) {
+  const float l2e = __builtin_bit_cast(float, 0x3fb8aa3bu);     // log2(e) rounded
+  const float l2e_lo = __builtin_bit_cast(float, 0x32a5705fu);  // log2(e) - l2e
+  const float ph = x * l2e;
+  const float pl = __builtin_fmaf(x, l2e_lo, __builtin_fmaf(x, l2e, -ph));
+  const float n = __builtin_rintf(ph);
+  const float r = ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
+  return x < -104.0f ? 0.0f : r;  // below half the least denormal; also -inf
+}
+MMP_DI float mm_exp(float x) { return x > 89.0f ? __builtin_inff() : mm_exp_core(x); }
+MMP_DI float mm_exp_nonpos(float x) { return mm_exp_core(x); }
+MMP_DI double mm_exp(double x) { return exp(x); }
+MMP_DI double mm_exp_nonpos(double x) { return exp(x); }
 
 // tanh for float32, branch-free (the device library's tanhf branches on
 // |x| < 0.625, and in a fused loop over random data both sides run with
@@ -322,12 +352,14 @@ template <typename T> MMP_DI T op_reciprocal(T x) {
 MMP_FLOAT_UNARY(sqrt, mm_sqrt(x))
 MMP_FLOAT_UNARY(cbrt, mm_cbrt(x))
 MMP_FLOAT_UNARY(exp, mm_exp(x))
+MMP_FLOAT_UNARY(exp_nonpos, mm_exp_nonpos(x))
 MMP_FLOAT_UNARY(exp2, mm_exp2_acc(x))
 MMP_FLOAT_UNARY(expm1, mm_expm1(x))
 MMP_FLOAT_UNARY(log, mm_log(x))
 MMP_FLOAT_UNARY(log2, mm_log2(x))
 MMP_FLOAT_UNARY(log10, mm_log10_acc(x))
 MMP_FLOAT_UNARY(log1p, mm_log1p(x))
+MMP_FLOAT_UNARY(log1p_nonneg, mm_log1p_nonneg(x))
 MMP_FLOAT_UNARY(sin, mm_sin(x))
 MMP_FLOAT_UNARY(cos, mm_cos(x))
 MMP_FLOAT_UNARY(tan, mm_tan(x))

@@ -1,6 +1,6 @@
 """Every float32 bit pattern through this build's own float32 functions.
 
-`mm_tanh` and `mm_log1p` (csrc/mmp_ops.h) are written here rather than
+`mm_tanh`, `mm_log1p` and `mm_exp` (csrc/mmp_ops.h) are written here rather than
 taken from the device math library, so their accuracy is checked over all
 2^32 inputs: a kernel evaluates each one next to the library's float64
 function of the same input and records the error in units in the last
@@ -38,6 +38,15 @@ __device__ __forceinline__ double ulp_err(float c, double r) {
 template <int F> __device__ __forceinline__ void eval(float x, float& c, double& r) {
   if (F == 0) { c = mm_tanh(x); r = tanh((double)x); }
   if (F == 1) { c = mm_log1p(x); r = log1p((double)x); }
+  if (F == 2) { c = mm_exp(x); r = exp((double)x); }
+}
+// The sign-specialised forms equal the general ones bit for bit on the
+// inputs they are used for (exp: x <= 0 or NaN; log1p: x >= 0 or NaN; two
+// NaNs count as equal whatever their payloads): a mismatch counts as an
+// error of 1e30 ULP.
+__device__ __forceinline__ double same_bits(float a, float b) {
+  if (a != a && b != b) return 0.0;
+  return __builtin_bit_cast(unsigned, a) == __builtin_bit_cast(unsigned, b) ? 0.0 : 1e30;
 }
 template <int F> __device__ void sweep(unsigned* out) {
   const unsigned long long t = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -45,9 +54,16 @@ template <int F> __device__ void sweep(unsigned* out) {
   unsigned wbits = 0, n1 = 0, n2 = 0;
   for (unsigned j = 0; j < PER; ++j) {
     const unsigned bits = (unsigned)(t * PER + j);
-    float c; double r;
-    eval<F>(__builtin_bit_cast(float, bits), c, r);
-    const double e = ulp_err(c, r);
+    const float x = __builtin_bit_cast(float, bits);
+    double e;
+    if (F == 3) {
+      e = (x <= 0.0f || x != x) ? same_bits(mm_exp_nonpos(x), mm_exp(x)) : 0.0;
+      e += (x >= 0.0f || x != x) ? same_bits(mm_log1p_nonneg(x), mm_log1p(x)) : 0.0;
+    } else {
+      float c; double r;
+      eval<F>(x, c, r);
+      e = ulp_err(c, r);
+    }
     const float ef = e > 1e9 ? 1e9f : (float)e;
     if (ef > worst) { worst = ef; wbits = bits; }
     n1 += e > 1.0;
@@ -60,6 +76,8 @@ template <int F> __device__ void sweep(unsigned* out) {
 }
 extern "C" __global__ __launch_bounds__(256) void sweep_tanh(unsigned* out) { sweep<0>(out); }
 extern "C" __global__ __launch_bounds__(256) void sweep_log1p(unsigned* out) { sweep<1>(out); }
+extern "C" __global__ __launch_bounds__(256) void sweep_exp(unsigned* out) { sweep<2>(out); }
+extern "C" __global__ __launch_bounds__(256) void sweep_sign_forms(unsigned* out) { sweep<3>(out); }
 """
 
 
@@ -86,6 +104,7 @@ def _host_ulp(got, want):
 @pytest.mark.parametrize("name,op,fn,bound", [
     ("sweep_tanh", cp.tanh, np.tanh, 1.6),
     ("sweep_log1p", cp.log1p, np.log1p, 1.3),
+    ("sweep_exp", cp.exp, np.exp, 1.1),
 ])
 def test_every_float32_input(name, op, fn, bound):
     worst, wbits, n_gt1, n_gt2 = _sweep(name)
@@ -96,6 +115,15 @@ def test_every_float32_input(name, op, fn, bound):
     got = op(cp.array(x)).get()[0]
     want = float(fn(x.astype(np.float64))[0])
     assert abs(_host_ulp(got, want) - worst) < 1e-3
+
+
+def test_sign_specialised_forms_match_bit_for_bit():
+    """exp without its overflow case and log1p without its x <= -1 cases
+    (what the code generator calls for exp(-|x|), log1p(x*x), ...) give the
+    general functions' bits on every input they are used for (NaN for NaN,
+    payloads aside)."""
+    worst, wbits, n_gt1, _ = _sweep("sweep_sign_forms")
+    assert worst == 0.0 and n_gt1 == 0, f"first mismatch at bits {wbits:#010x}"
 
 
 def test_tanh_and_log1p_special_values():

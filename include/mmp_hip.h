@@ -294,7 +294,8 @@ int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len,
 
 /* Inclusive scan along the middle axis of (outer, len, inner).
  * MMP_S_CUMSUM / MMP_S_CUMPROD.  out_dtype follows numpy (int32 -> int64,
- * float32 -> float32); floating scans carry a float64 running value. */
+ * float32 -> float32); floating scans carry a float64 running value.  out
+ * must not overlap x (MMP_E_ARG): a tile may read its predecessors' input. */
 int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
              int64_t inner, const void *x, void *out);
 
@@ -467,7 +468,7 @@ int mmp_rtc_launch_threads(void *kernel, const uint32_t *threads3, const uint32_
  * bounded waits; a wait that runs out records a flag (pinned host memory,
  * written by the kernel) and lets the kernel finish instead of hanging.
  * Waits for the library stream, stores the flags raised since the last
- * check in *flags (bit 0: scan look-back, bit 1: reduction combine) and
+ * check in *flags (bit 0: a scan row tail found no prefix, bit 1: reduction combine) and
  * clears them.  Non-zero means a result produced since the last check may
  * be wrong; mmp_sync and mmp_d2h report the same flags as MMP_E_WAIT.  No
  * counterpart in the reference (its Metal scan and reductions use
@@ -478,9 +479,11 @@ int mmp_wait_status(uint32_t *flags);
 /* Make the next `count`-th call of kind (1 = mmp_alloc, 2 = mmp_rtc_compile,
  * 3 = kernel launch) fail with MMP_E_INJECTED.  Kind 4: the `count`-th next
  * split reduction or scan waits for a tag that its writers never write,
- * with a spin limit of 64, so its bounded wait runs out at once (the
+ * with a spin limit of 64: a reduction's bounded wait runs out at once (the
  * kernel still finishes) and the next mmp_sync / mmp_d2h returns
- * MMP_E_WAIT.  count 0 disables. */
+ * MMP_E_WAIT; a scan's tiles find no predecessor descriptor and sum their
+ * predecessors' inputs themselves (the result stays exact).  count 0
+ * disables. */
 int mmp_debug_fail_next(int kind, int count);
 
 #ifdef __cplusplus

@@ -370,7 +370,8 @@ class HipBackend:
 
     def wait_status(self) -> int:
         """Flags of device-side bounded waits that ran out since the last
-        call (bit 0 scan look-back, bit 1 reduction combine), then cleared.
+        call (bit 0 a scan row tail found no prefix, bit 1 reduction combine),
+        then cleared.
         Non-zero means a scan or reduction result may be wrong."""
         f = ctypes.c_uint32()
         _check(self._lib.mmp_wait_status(ctypes.byref(f)), "mmp_wait_status")

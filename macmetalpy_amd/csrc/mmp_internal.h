@@ -47,16 +47,19 @@ uint32_t next_generation();
 // word 1 reduction combine.  Read (and cleared) by the host after a stream
 // synchronisation, so checking them costs no device round trip.
 unsigned *wait_flags();
-// Flags raised since the last call (bit 0 scan, bit 1 reduction), cleared.
+// Flags raised since the last call (bit 0 scan row tail, bit 1 reduction),
+// cleared.
 // Only meaningful after the stream has been synchronised.
 uint32_t take_wait_flags();
 
 // Parameters of the next bounded cross-workgroup wait.  Normally the spin
 // limit is large and readers expect the call's own tag (tag_offset 0).
 // mmp_debug_fail_next(4, n) makes the n-th next split reduction or scan
-// wait for a tag its writers never write, with a spin limit of 64, so the
-// wait runs out at once and the kernel still finishes (a test of the
-// timeout reporting that needs no hung or faulting kernel).
+// wait for a tag its writers never write, with a spin limit of 64: a split
+// reduction's wait runs out at once and the kernel still finishes (a test
+// of the timeout reporting that needs no hung or faulting kernel); a scan
+// finds no predecessor's descriptor, so every tile sums its predecessors'
+// inputs itself (a test of that path: the result stays exact).
 struct WaitParams {
   long long spin_limit;
   unsigned tag_offset;

@@ -239,7 +239,7 @@ int check_waits() {
   return mmpi::fail(MMP_E_WAIT,
                     "a device-side bounded wait ran out (%s%s): a %s result computed since the "
                     "last synchronisation may be wrong",
-                    (f & 1u) ? "scan look-back" : "", f == 3u ? ", reduction combine" : (f == 2u ? "reduction combine" : ""),
+                    (f & 1u) ? "scan row tail prefix" : "", f == 3u ? ", reduction combine" : (f == 2u ? "reduction combine" : ""),
                     f == 1u ? "cumsum / cumprod" : (f == 2u ? "reduction" : "scan or reduction"));
 }
 }  // namespace

@@ -6,9 +6,10 @@
 //
 // Here a contiguous scan (any number of rows of length len) is a single
 // pass of decoupled look-back:
-//  * workgroups take tile ids from an atomic counter in launch order, so a
-//    tile only ever waits for tiles that are already running (AMD gives no
-//    forward-progress guarantee to workgroups that have not started);
+//  * a tile's id is its workgroup id; a tile never waits without bound for
+//    a predecessor (whose workgroup may not have started: AMD gives no
+//    forward-progress guarantee to workgroups that have not started) --
+//    after a few polls it sums that predecessor's input itself;
 //  * a tile (16384 elements: 4 sub-tiles of 256 threads x 16 consecutive
 //    elements) is loaded with 128-bit loads, all issued up front, and
 //    redistributed through LDS into registers, scanned serially per thread
@@ -18,8 +19,7 @@
 //    descriptors at once and combines aggregates up to the nearest
 //    inclusive prefix, then publishes its own inclusive prefix;
 //  * descriptors carry a per-call generation tag, so they are never
-//    cleared between calls; waits are bounded and a timeout is recorded
-//    instead of hanging;
+//    cleared between calls;
 //  * rows whose byte length is a multiple of 16 (and 16-byte aligned
 //    operands) run their whole tiles through a guard-free kernel and each
 //    row's partial tail through a second small launch; other layouts run a
@@ -101,11 +101,10 @@ __device__ __forceinline__ void publish(unsigned long long *d, A v, unsigned tag
 }
 
 struct ScanScratch {
-  unsigned *counter;          // tile ticket (left at 0 by the last tile)
   unsigned long long *desc;   // 2 words per tile
-  unsigned *timeout;          // pinned host word, set to 1 if a look-back wait ran out
+  unsigned *timeout;          // pinned host word, set to 1 if a tail's prefix was missing
   unsigned read_gen;          // generation look-back readers expect (== gen unless forced)
-  long long spin_limit;       // bound of every look-back wait
+  long long spin_limit;       // look-back polls before a tile sums a predecessor itself
 };
 
 template <bool B> struct Bool { static constexpr bool value = B; };
@@ -133,21 +132,43 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 // Decoupled look-back by wave 0: lanes 0..kLook-1 read the descriptors of
 // the kLook (8) nearest predecessors at once (lane 0 = tile - 1).  The window is
 // usable when every lane nearer than the nearest inclusive prefix holds a
-// valid aggregate; otherwise it is re-read (bounded).  Tiles before the
-// row's first tile count as an inclusive identity.  Returns the exclusive
-// prefix of `tile` (lane 0's value is the one used).  The descriptor reads
-// are agent-scope loads that contend with the other tiles' publications;
+// valid aggregate; otherwise it is re-read.  Tiles before the row's first
+// tile count as an inclusive identity.  Returns the exclusive prefix of
+// `tile` (lane 0's value is the one used).  The descriptor reads are
+// agent-scope loads that contend with the other tiles' publications;
 // measured on MI355X at 2^28 elements, int32 -> int64: 64 tiles per round
 // 0.72 ms, 32: 0.64, 16: 0.60, 8: 0.58, 4: 0.57 (float32 best at 8), and
 // 256 per round 1.03 ms.
+//
+// Tiles are numbered by workgroup id, so a predecessor may belong to a
+// workgroup that has not started (nothing in the hardware promises that a
+// lower id runs first, although dispatch is in id order in practice).  A
+// tile therefore never waits for one without bound: after sc.spin_limit
+// polls it reads the nearest missing predecessor's input and sums it
+// itself (64 KiB for a float32 tile, a few microseconds), and goes on.
+// Forward progress needs no other workgroup, and no atomic ticket is
+// drawn (a same-address ticket per workgroup cost 6 % of the float32 scan).
 #ifndef MMP_SCAN_LOOK
 #define MMP_SCAN_LOOK 8
 #endif
 constexpr int kLook = MMP_SCAN_LOOK;
+constexpr long long kPollsBeforeSum = 256;
 
-template <typename S>
+// Aggregate of n elements at p by one wave (coalesced, lane-strided).
+template <typename S, typename Ti>
+__device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int n, int lane) {
+  typename S::A acc = S::ident();
+  for (int i = lane; i < n; i += 64) acc = S::comb(acc, S::map(p[i]));
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) acc = S::comb(acc, shfl_xor64(acc, m));
+  return acc;
+}
+
+template <typename S, typename Ti>
 __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long long t,
-                                   typename S::A total, unsigned gen, int lane) {
+                                   typename S::A total, unsigned gen, int lane,
+                                   const Ti *__restrict__ xrow, int tile_len,
+                                   typename S::A *own_val) {
   typedef typename S::A A;
   A prefix = S::ident();
   unsigned long long *d = sc.desc;
@@ -157,6 +178,8 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
     const unsigned long long in_window = kLook >= 64 ? ~0ull : ((1ull << kLook) - 1);
     long long top = tile - 1;
     long long spins = 0;
+    // lanes whose predecessor was summed here (wave-uniform), values in LDS
+    unsigned long long own = 0;
     while (true) {
       const long long j = top - lane;
       unsigned state = 2u;
@@ -167,17 +190,26 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
         const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
         state = (t0 == t1 && (t0 >> 2) == sc.read_gen) ? (t0 & 3u) : 0u;
         val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
+        if (state == 0u && ((own >> lane) & 1ull)) {
+          state = 1u;
+          val = own_val[lane];
+        }
       }
       const unsigned long long incl = __ballot(state == 2u) & in_window;
       const unsigned long long bad = __ballot(state == 0u) & in_window;
       const int p = incl ? __ffsll((long long)incl) - 1 : kLook;  // nearest inclusive lane
       const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
       if (bad & nearer) {
-        if (++spins > sc.spin_limit) {
-          if (lane == 0) __hip_atomic_store(sc.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-          break;
+        if (++spins <= sc.spin_limit) {
+          __builtin_amdgcn_s_sleep(1);
+          continue;
         }
-        __builtin_amdgcn_s_sleep(1);
+        // the nearest predecessor still missing: sum its input here
+        const int b = __ffsll((long long)(bad & nearer)) - 1;
+        const A agg = wave_aggregate<S>(xrow + (top - b - first) * (long long)tile_len, tile_len,
+                                        lane);
+        if (lane == b) own_val[b] = agg;
+        own |= 1ull << b;
         continue;
       }
       A part = lane <= p && lane < kLook ? val : S::ident();
@@ -186,6 +218,8 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
       prefix = S::comb(part, prefix);
       if (p < kLook) break;
       top -= kLook;
+      own = 0;
+      spins = 0;
     }
   }
   if (lane == 0) publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
@@ -226,22 +260,16 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
   __shared__ __attribute__((aligned(16))) unsigned char stage[(kSubTile + kPad) * kStage];
   __shared__ A wsum[Q][kBlock / 64];
   __shared__ A s_prefix;
-  __shared__ unsigned s_tile;
+  __shared__ A s_own[kLook];  // predecessor aggregates the look-back summed itself
+  __shared__ A s_excl[Q][kBlock];
   Ti *sx = reinterpret_cast<Ti *>(stage);
   To *sy = reinterpret_cast<To *>(stage);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  if (MODE != 2 && tid == 0) {
-    const unsigned t = __hip_atomic_fetch_add(sc.counter, 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    s_tile = t;
-    // every other workgroup has already drawn its id: re-arm for the next call
-    if ((long long)t == ntiles - 1)
-      __hip_atomic_store(sc.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (MODE != 2) __syncthreads();
-  // MODE 2: tile = the row's tail, one past its last whole tile
-  const long long tile = MODE == 2 ? (long long)blockIdx.x * tiles_per_row + tiles_per_row : s_tile;
+  // tile = workgroup id (rows x tiles per row, row-major); MODE 2: the
+  // row's tail, one past its last whole tile
+  const long long tile = MODE == 2 ? (long long)blockIdx.x * tiles_per_row + tiles_per_row
+                                   : (long long)blockIdx.x;
   const long long row = MODE == 2 ? (long long)blockIdx.x : tile / tiles_per_row;
   const long long t = tile - row * tiles_per_row;
   const long long base = t * kTile;
@@ -331,7 +359,9 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
         if (w < wave) wpre = S::comb(wpre, wsum[q][w]);
         qtot = S::comb(qtot, wsum[q][w]);
       }
-      excl[q] = S::comb(total, S::comb(wpre, excl[q]));  // prefix within the tile
+      // prefix within the tile, parked in LDS (this thread's slot) so that
+      // it holds no registers across the look-back
+      s_excl[q][tid] = S::comb(total, S::comb(wpre, excl[q]));
       total = S::comb(total, qtot);
     }
 
@@ -339,7 +369,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
     if constexpr (MODE == 2) {
       if (tid == 0) s_prefix = t > 0 ? tail_prefix<S>(sc, tile - 1, gen) : S::ident();
     } else if (wave == 0) {
-      const A prefix = look_back<S>(sc, tile, t, total, gen, lane);
+      const A prefix = look_back<S>(sc, tile, t, total, gen, lane, x + row * len, kTile, s_own);
       if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();
@@ -349,7 +379,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
       const int qn = count(q);
-      A run = S::comb(s_prefix, excl[q]);
+      A run = S::comb(s_prefix, s_excl[q][tid]);
 #pragma unroll
       for (int j = 0; j < kItems; ++j) {
         const int i = tid * kItems + j;
@@ -459,6 +489,13 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
     return mmpi::fail(MMP_E_UNSUPPORTED, "scan: unsupported output dtype");
   } else {
     typedef typename ScanOp<OP, Ti>::A A;
+    {  // a tile may read its predecessors' inputs, so out must not overlap in
+      const uintptr_t xb = (uintptr_t)x, yb = (uintptr_t)y;
+      const uintptr_t xe = xb + (uintptr_t)(outer * len * inner) * sizeof(Ti);
+      const uintptr_t ye = yb + (uintptr_t)(outer * len * inner) * sizeof(To);
+      if (outer * len * inner > 0 && xb < ye && yb < xe)
+        return mmpi::fail(MMP_E_ARG, "scan: output overlaps the input");
+    }
     if (inner == 1) {
       constexpr long long kTile = (long long)sub_tiles<Ti>() * kSubTile;
       // streaming layout: every row starts 16-byte aligned in input and output
@@ -471,8 +508,6 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
         return mmpi::fail(MMP_E_ARG, "scan too large");
       int st = MMP_OK;
       ScanScratch sc;
-      sc.counter = (unsigned *)mmpi::scratch(mmpi::SCRATCH_SCAN_COUNTER, 64, &st);
-      if (st) return st;
       sc.timeout = mmpi::wait_flags();
       sc.desc = (unsigned long long *)mmpi::scratch(mmpi::SCRATCH_SCAN_VALUES,
                                                       16ull * (ntiles > 0 ? ntiles : 1), &st);
@@ -480,7 +515,9 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
       const unsigned gen = mmpi::next_generation();
       const mmpi::WaitParams wp = mmpi::wait_params();
       sc.read_gen = (gen + wp.tag_offset) & 0x3fffffffu;
-      sc.spin_limit = wp.spin_limit;
+      // polls of a missing predecessor before summing it here: it normally
+      // publishes within a few (its loads are in flight when we start)
+      sc.spin_limit = wp.spin_limit < kPollsBeforeSum ? wp.spin_limit : kPollsBeforeSum;
       if (!vec) {
         hipLaunchKernelGGL((k_scan_rows<OP, Ti, To, 1>), dim3((unsigned)ntiles), dim3(kBlock), 0,
                            mmpi::stream(), (const Ti *)x, (To *)y, len, tpr, ntiles, sc, gen);

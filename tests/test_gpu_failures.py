@@ -3,8 +3,9 @@
 Every case makes a call fail without a faulting or hung kernel: allocation,
 runtime-compile and launch failures are injected by the library's test hook
 (``mmp_debug_fail_next``), and a bounded cross-workgroup wait of a split
-reduction or scan is made to give up at once by having its readers expect
-a tag that no writer produces (the kernel still finishes).  The reference
+reduction is made to give up at once by having its readers expect a tag
+that no writer produces (the kernel still finishes); a scan in that state
+sums its tiles' predecessors itself and stays exact.  The reference
 has no error channel below Python (its metalgpu calls return void,
 _metal_backend.py:221-263); its Python-level errors (``ndarray.py:355-359``,
 ``_dtypes.py:133-134``) are covered by the host-logic tests.
@@ -57,15 +58,34 @@ def test_forced_reduction_wait_timeout_raises_on_get(be):
     assert be.wait_status() == 0
 
 
-def test_forced_scan_wait_timeout_raises(be):
-    x_np = np.random.default_rng(42).integers(-100, 100, 1 << 22, dtype=np.int32)
+@pytest.mark.parametrize("n", [1 << 22, 3 * 16384 + 4096])
+def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
+    """A scan whose tiles find no predecessor's descriptor (every reader
+    expects a tag no writer produces) sums each missing predecessor's input
+    itself: the result is exact and no wait is reported."""
+    g = np.random.default_rng(42)
+    x_np = g.integers(-100, 100, n, dtype=np.int32)
     x = cp.array(x_np)
     be.debug_fail_next(4, 1)
     c = cp.cumsum(x)
-    with pytest.raises(HipWaitTimeoutError, match="scan"):
-        c.get()
+    if n % 16384:  # the row tail's prefix comes from the last whole tile
+        with pytest.raises(HipWaitTimeoutError, match="scan"):
+            c.get()
+    else:
+        assert np.array_equal(c.get(), np.cumsum(x_np))
     assert be.wait_status() == 0
     assert np.array_equal(cp.cumsum(x).get(), np.cumsum(x_np))
+    f_np = g.random(n, dtype=np.float32)
+    f = cp.array(f_np)
+    be.debug_fail_next(4, 1)
+    cf = cp.cumsum(f)
+    if n % 16384 == 0:
+        ref = np.cumsum(f_np, dtype=np.float64)
+        assert np.all(np.abs(cf.get() - ref) <= 1e-5 * ref + 1e-6)
+    else:
+        with pytest.raises(HipWaitTimeoutError, match="scan"):
+            cf.get()
+    assert be.wait_status() == 0
 
 
 def test_injected_allocation_failure_leaks_nothing(be):

@@ -130,7 +130,7 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 }
 
 // Decoupled look-back by wave 0: lanes 0..kLook-1 read the descriptors of
-// the kLook (8) nearest predecessors at once (lane 0 = tile - 1).  The window is
+// the kLook (4 or 8, below) nearest predecessors at once (lane 0 = tile - 1).  The window is
 // usable when every lane nearer than the nearest inclusive prefix holds a
 // valid aggregate; otherwise it is re-read.  Tiles before the row's first
 // tile count as an inclusive identity.  Returns the exclusive prefix of
@@ -148,10 +148,13 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 // itself (64 KiB for a float32 tile, a few microseconds), and goes on.
 // Forward progress needs no other workgroup, and no atomic ticket is
 // drawn (a same-address ticket per workgroup cost 6 % of the float32 scan).
-#ifndef MMP_SCAN_LOOK
-#define MMP_SCAN_LOOK 8
-#endif
-constexpr int kLook = MMP_SCAN_LOOK;
+// Window per type, measured at 2^28 elements with the ticket-free look-back:
+// int32 -> int64 (8-byte outputs) 4 (6.0 TB/s; 8: 5.9, 16: 5.8), float32 8
+// (5.6; 4: 5.1, 16: 5.6).
+template <typename Ti, typename To> constexpr int scan_look() {
+  return (sizeof(Ti) == 4 && sizeof(To) == 8) ? 4 : 8;
+}
+constexpr int kLookMax = 8;
 constexpr long long kPollsBeforeSum = 256;
 
 // Aggregate of n elements at p by one wave (coalesced, lane-strided).
@@ -164,7 +167,7 @@ __device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int n, int lan
   return acc;
 }
 
-template <typename S, typename Ti>
+template <typename S, int kLook, typename Ti>
 __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long long t,
                                    typename S::A total, unsigned gen, int lane,
                                    const Ti *__restrict__ xrow, int tile_len,
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
   __shared__ __attribute__((aligned(16))) unsigned char stage[(kSubTile + kPad) * kStage];
   __shared__ A wsum[Q][kBlock / 64];
   __shared__ A s_prefix;
-  __shared__ A s_own[kLook];  // predecessor aggregates the look-back summed itself
+  __shared__ A s_own[kLookMax];  // predecessor aggregates the look-back summed itself
   __shared__ A s_excl[Q][kBlock];
   Ti *sx = reinterpret_cast<Ti *>(stage);
   To *sy = reinterpret_cast<To *>(stage);
@@ -369,7 +372,8 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
     if constexpr (MODE == 2) {
       if (tid == 0) s_prefix = t > 0 ? tail_prefix<S>(sc, tile - 1, gen) : S::ident();
     } else if (wave == 0) {
-      const A prefix = look_back<S>(sc, tile, t, total, gen, lane, x + row * len, kTile, s_own);
+      const A prefix = look_back<S, scan_look<Ti, To>()>(sc, tile, t, total, gen, lane,
+                                                         x + row * len, kTile, s_own);
       if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();

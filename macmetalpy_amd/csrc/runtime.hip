@@ -415,7 +415,9 @@ int mmp_host_free(void *ptr) {
   g_host_live.erase(it);
   g_host_out -= r;
   if (g_host_cached + r <= kHostCacheMax) {
-    g_host_free.emplace(r, ptr);
+    // Insert ahead of the blocks of the same size, so find() hands back the
+    // most recently released (still mapped in the TLB) block first.
+    g_host_free.emplace_hint(g_host_free.lower_bound(r), r, ptr);
     g_host_cached += r;
     return MMP_OK;
   }

@@ -196,6 +196,42 @@ def _scalar_operand(v):
 
 
 _BINARY_DTYPES: dict = {}
+_LOGICAL_OPS = frozenset({"logical_and_op", "logical_or_op", "logical_xor_op"})
+# (array OP scalar) when the scalar exceeds every value of the array's
+# integer dtype; below every value the answers flip except == / !=
+_ABOVE = {"lt_op": True, "le_op": True, "gt_op": False, "ge_op": False, "eq_op": False,
+          "ne_op": True}
+_FLIP = {"lt_op": "gt_op", "le_op": "ge_op", "gt_op": "lt_op", "ge_op": "le_op",
+         "eq_op": "eq_op", "ne_op": "ne_op"}
+
+
+def _out_of_range_compare(op_name, s, dtype, array_left):
+    """The constant result of comparing an integer array with a Python int
+    outside its dtype's range (NumPy compares by value), or None when the
+    int is in range or not an int."""
+    if type(s) is not int:
+        return None
+    info = np.iinfo(dtype)
+    if info.min <= s <= info.max:
+        return None
+    op = op_name if array_left else _FLIP[op_name]
+    if s > info.max:
+        return _ABOVE[op]
+    return op in ("gt_op", "ge_op", "ne_op")
+
+
+def _logical_int_scalar(a, b, ka, kb, b_arr):
+    """Replace a Python int operand of a logical op by its truth value when
+    it fits int64 (NumPy then accepts it whatever the array's dtype; beyond
+    int64 NumPy raises OverflowError, which the conversion below keeps)."""
+    s = a if b_arr else b
+    if -2 ** 63 <= s < 2 ** 63:
+        s = bool(s)
+        if b_arr:
+            a, ka = s, s
+        else:
+            b, kb = s, s
+    return a, b, ka, kb
 
 
 def _binary_dtypes(op_name, ka, kb):
@@ -237,6 +273,9 @@ def _binary_py(op_name: str, a, b):
             hit = _BINARY_DTYPES[key] = _binary_dtypes(op_name, ka, kb)
         rdt, odt = hit
     else:
+        if type(a if b_arr else b) is int and op_name in _LOGICAL_OPS:
+            # only the truth of an int counts; NumPy accepts any int64 value
+            a, b, ka, kb = _logical_int_scalar(a, b, ka, kb, b_arr)
         rdt, odt = _binary_dtypes(op_name, ka, kb)
     sa = a._shape if a_arr else ()
     sb = b._shape if b_arr else ()
@@ -246,6 +285,10 @@ def _binary_py(op_name: str, a, b):
         size *= s
     if size == 0:
         return _empty(shape, rdt)
+    if not (a_arr and b_arr) and op_name in _abi.COMPARE_OPS and odt.kind in "iu":
+        const = _out_of_range_compare(op_name, b if a_arr else a, odt, a_arr)
+        if const is not None:
+            return _creation().full(shape, const, dtype=np.bool_)
     if op_name == "pow_op" and rdt.kind in "iu":
         _check_int_power(b if b_arr else None, None if b_arr else b)
 

@@ -190,3 +190,38 @@ def test_dispatch_shape_prime_counts_use_full_workgroups():
     assert dispatch_shape((1000,)) == (True, (250, 1, 1))
     with pytest.raises(ValueError):
         dispatch_shape((1 << 32,))
+
+
+@pytest.mark.parametrize("dt", [np.int16, np.uint16, np.int32, np.uint32, np.int64, np.uint64])
+def test_out_of_range_int_comparisons_are_constant(dt):
+    """Comparing an integer array with a Python int outside its dtype's
+    range: NumPy compares by value, so every element gives the same answer
+    (the library fills the result instead of converting the int)."""
+    from macmetalpy_amd._elementwise import _out_of_range_compare
+    info = np.iinfo(dt)
+    a = np.array([info.min, info.min + 1, 0, info.max - 1, info.max], dt)
+    ops = {"lt_op": np.less, "le_op": np.less_equal, "gt_op": np.greater,
+           "ge_op": np.greater_equal, "eq_op": np.equal, "ne_op": np.not_equal}
+    for s in (info.max + 1, info.min - 1, 2 ** 70, -2 ** 70, 0, info.max):
+        for name, uf in ops.items():
+            for left in (True, False):
+                c = _out_of_range_compare(name, s, np.dtype(dt), left)
+                if info.min <= s <= info.max:
+                    assert c is None
+                    continue
+                want = uf(a, s) if left else uf(s, a)
+                assert np.all(want == c), (s, name, left)
+    assert _out_of_range_compare("lt_op", 2.5, np.dtype(dt), True) is None
+
+
+def test_logical_ops_read_int_scalars_as_truth_values():
+    from macmetalpy_amd._elementwise import _logical_int_scalar
+    arr = object()
+    assert _logical_int_scalar(arr, 300000, np.dtype(np.int16), 300000, False)[1] is True
+    assert _logical_int_scalar(0, arr, 0, np.dtype(np.int16), True)[0] is False
+    # beyond int64 NumPy raises OverflowError; the int is left for the
+    # conversion to raise it
+    assert _logical_int_scalar(arr, 2 ** 64, np.dtype(np.int16), 2 ** 64, False)[1] == 2 ** 64
+    with pytest.raises(OverflowError):
+        np.logical_or(np.zeros(2, np.int16), 2 ** 64)
+    assert np.logical_or(np.zeros(2, np.int16), 300000).tolist() == [True, True]

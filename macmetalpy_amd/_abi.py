@@ -50,6 +50,19 @@ CTYPE_NAMES: dict[np.dtype, str] = {
     np.dtype(np.float64): "double",
 }
 
+# Ops the precompiled unary kernels (mmp_unary) also define for integer
+# dtypes; they define every op for float dtypes and none for bool (the
+# generated kernels cover the rest).  Mirrors UnaryOk in elementwise.hip.
+INT_UNARY_OPS = frozenset({"negative_op", "positive_op", "abs_op", "sign_op", "square_op",
+                           "reciprocal_op", "floor_op", "ceil_op", "rint_op", "trunc_op"})
+
+
+def precompiled_unary_ok(op_name: str, dtype) -> bool:
+    """True if mmp_unary defines ``op_name`` for ``dtype``."""
+    kind = np.dtype(dtype).kind
+    return op_name in UNARY_OPS and (kind == "f" or (kind in "iu" and op_name in INT_UNARY_OPS))
+
+
 # op_name -> (code, numpy ufunc, mmp_ops.h function)
 UNARY_OPS: dict[str, tuple[int, np.ufunc, str]] = {
     "neg_op": (0, np.negative, "op_neg"),

@@ -753,7 +753,7 @@ def _run_sum_py(root: FusionNode, axis_last: bool, out_dtype, out_ptr: int, mean
 
 
 def is_precompiled_unary(node) -> bool:
-    return (isinstance(node, UnaryOpNode) and node._op_name in _abi.UNARY_OPS
+    return (isinstance(node, UnaryOpNode) and _abi.precompiled_unary_ok(node._op_name, node._dtype)
             and isinstance(node._input, InputNode)
             and node._input._dtype == node._dtype
             and node._input._shape == node._shape

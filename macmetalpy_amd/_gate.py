@@ -84,6 +84,7 @@ def setup() -> None:
         "unary_codes": {k: v[0] for k, v in _abi.UNARY_OPS.items()},
         "binary_codes": {k: v[0] for k, v in _abi.BINARY_OPS.items()},
         "fast_ops": set(_abi.FAST_MATH_OPS),
+        "int_unary_ops": set(_abi.INT_UNARY_OPS),
     })
     apply(get_config().native_dispatch)
 

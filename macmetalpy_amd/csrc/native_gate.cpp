@@ -156,6 +156,7 @@ PyObject *op_ids = nullptr;  // dict name -> id
 int n_ops = 0;
 int unary_code[kMaxOps], binary_code[kMaxOps];
 bool fast_op[kMaxOps];
+bool int_unary_op[kMaxOps];  // mmp_unary also defines the op for integer dtypes
 int8_t un_rdt[kMaxOps][kNDT], un_idt[kMaxOps][kNDT];
 int8_t bin_rdt[kMaxOps][kNDT][kNDT], bin_odt[kMaxOps][kNDT][kNDT];
 // array dtype x scalar kind (0 float, 1 int) x scalar side (0 left, 1 right):
@@ -1211,7 +1212,11 @@ PyObject *gate_materialize(PyObject *, PyObject *arr) {
     Py_XDECREF(op);
   }
   const bool fast_form = fast && oid >= 0 && fast_op[oid] && (odt == D_F32 || odt == D_F16);
-  if (!fast_form && t == T_unary && oid >= 0 && unary_code[oid] >= 0) {
+  // mmp_unary defines every op for floats, the integer set for integers and
+  // nothing for bool; the generated kernel covers the rest
+  const bool unary_ok = oid >= 0 && unary_code[oid] >= 0 &&
+                        (odt >= D_F16 || (odt != D_BOOL && int_unary_op[oid]));
+  if (!fast_form && t == T_unary && unary_ok) {
     PyObject *in = dget(d_un_input, node);
     if (in && contig_leaf(in, shape, odt)) {
       const unsigned long long src = leaf_ptr(in, odt);
@@ -1535,11 +1540,12 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   GETCFG(ml, "max_leaves");
   max_depth = PyLong_AsLong(md);
   max_leaves = PyLong_AsLong(ml);
-  PyObject *ops, *ucodes, *bcodes, *fastset;
+  PyObject *ops, *ucodes, *bcodes, *fastset, *intset;
   GETCFG(ops, "op_names");
   GETCFG(ucodes, "unary_codes");
   GETCFG(bcodes, "binary_codes");
   GETCFG(fastset, "fast_ops");
+  GETCFG(intset, "int_unary_ops");
 #undef GETCFG
   const Py_ssize_t nops = PySequence_Size(ops);
   if (nops < 0 || nops > kMaxOps) {
@@ -1564,6 +1570,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
     unary_code[i] = uc ? (int)PyLong_AsLong(uc) : -1;
     binary_code[i] = bc ? (int)PyLong_AsLong(bc) : -1;
     fast_op[i] = PySet_Contains(fastset, name) == 1;
+    int_unary_op[i] = PySet_Contains(intset, name) == 1;
     Py_DECREF(name);
     Py_DECREF(idv);
   }

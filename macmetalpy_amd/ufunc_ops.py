@@ -36,6 +36,25 @@ def _binary(name, op_name, doc):
     return f
 
 
+def fabs(x, /, out=None, **kwargs):
+    """Element-wise absolute value in NumPy's result dtype for fabs, which
+    has float loops only: integers and bool are converted to float16 /
+    float32 / float64 first (as np.fabs does), then the absolute value is
+    taken."""
+    import numpy as np
+    from ._dtypes import ufunc_result_dtype
+    from .ndarray import ndarray
+    if not isinstance(x, ndarray):
+        x = ew._asarray(x)
+    rdt = ufunc_result_dtype(np.fabs, x.dtype)
+    if rdt != x.dtype:
+        x = x.astype(rdt)
+    return _to_out(ew.unary("abs_op", x), out)
+
+
+__all__.append("fabs")
+
+
 def _to_out(r, out):
     if out is None:
         return r
@@ -49,7 +68,6 @@ for _name, _op, _doc in [
     ("positive", "positive_op", "Element-wise +x."),
     ("absolute", "abs_op", "Element-wise absolute value."),
     ("abs", "abs_op", "Element-wise absolute value."),
-    ("fabs", "abs_op", "Element-wise absolute value (floats)."),
     ("sign", "sign_op", "Element-wise sign."),
     ("square", "square_op", "Element-wise square."),
     ("reciprocal", "reciprocal_op", "Element-wise 1/x."),

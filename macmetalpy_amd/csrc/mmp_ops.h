@@ -332,8 +332,11 @@ template <typename T> MMP_DI T op_reciprocal(T x) {
     typedef typename mmp_t<T>::C C;
     return (T)((C)1 / (C)x);
   } else {
-    // numpy's integer reciprocal evaluates 1/x; 1/0 yields the lowest value
-    if (x == 0) return mmp_t<T>::lowest;
+    // numpy's integer reciprocal converts 1.0 / x to the type: for x == 0 the
+    // conversion of inf gives the lowest value of a 32- or 64-bit signed
+    // type, and 0 for narrower signed types and every unsigned type (whose
+    // conversions go through a wider signed integer and keep its low bits)
+    if (x == 0) return (mmp_t<T>::is_signed && sizeof(T) >= 4) ? mmp_t<T>::lowest : (T)0;
     if constexpr (mmp_t<T>::is_signed) {
       return (T)(x == 1 ? 1 : (x == -1 ? -1 : 0));
     } else {

@@ -107,6 +107,9 @@ def _make_leaves(rng, R, C, dtypes, n):
         else:
             base = draw((C, R)); h = base.T; d = cp.array(base).T
         leaves.append((h, d))
+    if all(np.ndim(h) == 0 for h, _ in leaves):            # at least one array leaf
+        h = draw((R, C))
+        leaves[0] = (h, cp.array(h))
     return leaves
 
 

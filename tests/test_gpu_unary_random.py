@@ -52,9 +52,7 @@ def _values(rng, shape, dtype, op):
     if dt.kind in "iu":
         info = np.iinfo(dt)
         if op == "reciprocal":                 # NumPy's integer reciprocal divides 1 by x
-            v = rng.integers(max(info.min, -3), 4, shape).astype(dt)
-            v[v == 0] = 1
-            return v
+            return rng.integers(max(info.min, -3), 4, shape).astype(dt)
         v = rng.integers(info.min, info.max, shape, dtype=dt, endpoint=True)
         flat = v.reshape(-1)
         k = min(flat.size, 4)

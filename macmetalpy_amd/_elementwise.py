@@ -345,6 +345,10 @@ def where(cond, x, y):
 
     def leaf(v, is_arr, dt):
         if not is_arr:
+            if type(v) is int and dt.kind in "biu":
+                # np.where converts a Python int with a plain cast, which
+                # wraps (and warns) where the strict conversion would raise
+                v = np.asarray(v).astype(dt)
             return ScalarNode(v, dt)
         if unfused:
             return _node_of(_materialise_operand(v, shape, dt), dt)

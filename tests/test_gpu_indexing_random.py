@@ -58,9 +58,8 @@ def _key(rng, shape, for_set):
             items.append(("slice", slice(lo, hi, step)))
         else:
             items.append(("all", slice(None)))
-    # drop trailing whole-axis items, put an Ellipsis over a run of them
-    while items and items[-1][0] == "all" and rng.random() < 0.5:
-        items.pop()
+    # put an Ellipsis over a run of whole-axis items, or drop trailing ones
+    # (not both: after an Ellipsis the items align with the last axes)
     runs = [i for i, it in enumerate(items) if it[0] == "all"]
     if runs and rng.random() < 0.4:
         i = runs[int(rng.integers(len(runs)))]
@@ -68,6 +67,9 @@ def _key(rng, shape, for_set):
         while j + 1 < len(items) and items[j + 1][0] == "all":
             j += 1
         items[i:j + 1] = [("ell", Ellipsis)]
+    else:
+        while items and items[-1][0] == "all" and rng.random() < 0.5:
+            items.pop()
     # newaxis
     if rng.random() < 0.25:
         items.insert(int(rng.integers(len(items) + 1)), ("none", None))

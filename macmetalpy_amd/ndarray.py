@@ -484,6 +484,10 @@ class ndarray:
         if not np.can_cast(result._dtype, self._dtype, casting="same_kind"):
             raise TypeError(f"Cannot cast ufunc output from {result._dtype} to {self._dtype} "
                             "with casting rule 'same_kind'")
+        if result._shape != self._shape:
+            # the result has the broadcast shape of this array and the operand
+            raise ValueError(f"non-broadcastable output operand with shape {self._shape} "
+                             f"doesn't match the broadcast shape {result._shape}")
         if self._np_data is not None:
             self._ensure_gpu()
         ew.flush_lazy(self._buffer)

@@ -118,6 +118,16 @@ def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
         a = a.astype(dtype)
     if kind in ("max", "min", "nanmax", "nanmin"):
         odt = a._dtype
+    elif dtype is not None:
+        odt = a._dtype          # NumPy accumulates in, and returns, the requested dtype
+        if odt.kind in "biu" and (odt.itemsize < 8 or kind in ("mean", "nanmean")):
+            # 64-bit accumulation, then the cast: the low bits of an integer
+            # sum / product are NumPy's wrapping accumulation in the narrow
+            # type; an integer mean is the float mean truncated, as NumPy's
+            wide = (np.float64 if kind in ("mean", "nanmean")
+                    else np.uint64 if odt.kind in "bu" else np.int64)
+            r = _reduce(a, kind, axis, wide, None, keepdims)
+            return _finish(r.astype(odt), out)
     else:
         odt = _np_out_dtype(_BASE_KIND.get(kind, kind), a._dtype)
     oshape = _out_shape(a._shape, axes, keepdims)
@@ -214,7 +224,7 @@ def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
                 return r
         return _reduce(a, "mean", axis, dtype, out, keepdims)
     a = _asarray(a)
-    odt = _np_out_dtype("mean", a._dtype if dtype is None else resolve_dtype(dtype))
+    odt = _np_out_dtype("mean", a._dtype) if dtype is None else resolve_dtype(dtype)
     tot = _reduce(_masked(a, where, 0).astype(np.float64), "sum", axis, None, None, keepdims)
     everywhere = (a == a) | (a != a)          # True with a's shape (NaN included)
     cnt = _reduce(_masked(everywhere, where, False), "sum", axis, None, None, keepdims)
@@ -346,7 +356,16 @@ def _scan(a, op, kind, axis, dtype, out):
     a = _asarray(a)
     if dtype is not None:
         a = a.astype(dtype)
-    odt = _np_out_dtype(kind, a._dtype)
+        want = a._dtype
+        if want.kind in "biu" and want.itemsize < 8:
+            # accumulate in 64 bits: the low bits are NumPy's wrapping
+            # accumulation in the requested integer type
+            wide = np.dtype(np.uint64 if want.kind in "bu" else np.int64)
+            r = _scan(a, op, kind, axis, wide, None)
+            return _finish(r.astype(want), out)
+        odt = want
+    else:
+        odt = _np_out_dtype(kind, a._dtype)
     x = a._ensure_contiguous()
     if axis is None:
         x = x.reshape(-1)

@@ -224,6 +224,8 @@ def mean(a, axis=None, dtype=None, out=None, keepdims=False, where=np._NoValue):
                 return r
         return _reduce(a, "mean", axis, dtype, out, keepdims)
     a = _asarray(a)
+    if dtype is not None:
+        a = a.astype(dtype)                   # NumPy converts the elements first
     odt = _np_out_dtype("mean", a._dtype) if dtype is None else resolve_dtype(dtype)
     tot = _reduce(_masked(a, where, 0).astype(np.float64), "sum", axis, None, None, keepdims)
     everywhere = (a == a) | (a != a)          # True with a's shape (NaN included)

@@ -184,7 +184,8 @@ def test_random_reduction_kwargs(seed):
     if want.dtype.kind != "f" or op in ("max", "min"):
         np.testing.assert_array_equal(got, want)
         return
-    x64 = x.astype(np.float64)
+    # the elements are first converted to the requested dtype, as NumPy does
+    x64 = (x.astype(kw["dtype"]) if "dtype" in kw else x).astype(np.float64)
     kw64 = {k: v for k, v in kw.items() if k != "dtype"}
     with np.errstate(all="ignore"):
         ref = np.asarray(getattr(np, op)(x64, axis=axis, **kw64), dtype=np.float64)

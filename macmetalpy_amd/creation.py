@@ -95,14 +95,19 @@ def arange(start, stop=None, step=1, dtype=None, *, like=None, device=None) -> n
 
 
 def linspace(start, stop, num=50, endpoint=True, retstep=False, dtype=None, axis=0):
+    """NumPy's linspace; without ``dtype`` the result keeps NumPy's dtype
+    (float64 for real bounds), as the reference's does (creation.py:159-173)."""
     r = np.linspace(start, stop, num, endpoint=endpoint, retstep=retstep, axis=axis)
+    arr, step = r if retstep else (r, None)
+    arr = arr.astype(resolve_dtype(arr.dtype if dtype is None else dtype), copy=False)
     if retstep:
-        arr, step = r
-        return ndarray._from_np_direct(arr.astype(resolve_dtype(dtype))), step
-    return ndarray._from_np_direct(r.astype(resolve_dtype(dtype)))
+        return ndarray._from_np_direct(arr), step
+    return ndarray._from_np_direct(arr)
 
 
 def eye(N, M=None, k=0, dtype=None) -> ndarray:
+    """Ones on diagonal k; without ``dtype`` the library's default float, as
+    the reference's eye (creation.py:176-181)."""
     return ndarray._from_np_direct(np.eye(N, M, k, dtype=resolve_dtype(dtype)))
 
 
@@ -113,6 +118,12 @@ def array(obj, dtype=None, copy=True) -> ndarray:
             out = obj.copy() if dtype is None else obj.astype(dtype)
             return out
         data = obj._np_data
+    elif dtype is not None:
+        # NumPy's own conversion: Python ints outside the dtype raise
+        data = np.asarray(obj, dtype=resolve_dtype(dtype))
+        if copy and data is obj:
+            data = data.copy()
+        return ndarray._from_np_direct(data)
     else:
         data = np.asarray(obj)
     if dtype is not None:
@@ -127,9 +138,7 @@ def asarray(obj, dtype=None) -> ndarray:
         if dtype is None or np.dtype(dtype) == obj._dtype:
             return obj
         return obj.astype(dtype)
-    data = np.asarray(obj)
-    if dtype is not None:
-        data = data.astype(resolve_dtype(dtype))
+    data = np.asarray(obj) if dtype is None else np.asarray(obj, dtype=resolve_dtype(dtype))
     return ndarray._from_np_direct(data)
 
 

@@ -67,9 +67,11 @@ def dispatch(ufunc, method, inputs, kwargs):
                            for x in inputs)
         res = fn(*inputs)
         if out is None:
-            if where is not True:
-                return NotImplemented  # NumPy leaves the unselected outputs undefined
-            return res
+            if where is True:
+                return res
+            # NumPy leaves the outputs outside ``where`` undefined: here they
+            # are whatever a new array holds
+            out = creation.empty(res.shape, dtype=res.dtype)
         return _write_out(out, res, casting, where)
     name = ufunc.__name__
     if method == "reduce" and name in _REDUCE and len(inputs) == 1:

@@ -16,6 +16,8 @@ __all__: list[str] = []
 
 def _unary(name, op_name, doc):
     def f(x, /, out=None, **kwargs):
+        if kwargs:
+            return _with_kwargs(name, (x,), out, kwargs)
         r = ew.unary(op_name, x)
         return _to_out(r, out)
     f.__name__ = f.__qualname__ = name
@@ -27,6 +29,8 @@ def _unary(name, op_name, doc):
 
 def _binary(name, op_name, doc):
     def f(x1, x2, /, out=None, **kwargs):
+        if kwargs:
+            return _with_kwargs(name, (x1, x2), out, kwargs)
         r = ew.binary(op_name, x1, x2)
         return _to_out(r, out)
     f.__name__ = f.__qualname__ = name
@@ -34,6 +38,24 @@ def _binary(name, op_name, doc):
     globals()[name] = f
     __all__.append(name)
     return f
+
+
+def _with_kwargs(name, inputs, out, kwargs):
+    """A ufunc call with keyword arguments (``where=``, ``dtype=``,
+    ``casting=``, ``order`` / ``subok``), evaluated as NumPy's ufunc call
+    does, by the same code as the NumPy ufunc protocol.  Without ``out``,
+    the elements outside ``where`` are left as a new array holds them
+    (NumPy leaves them undefined)."""
+    import numpy as np
+    from . import _ufunc_table
+    uf = getattr(np, name)
+    kw = dict(kwargs)
+    if out is not None:
+        kw["out"] = out
+    res = _ufunc_table.dispatch(uf, "__call__", inputs, kw)
+    if res is NotImplemented:
+        raise TypeError(f"{name}() got unsupported keyword arguments {sorted(kwargs)}")
+    return res
 
 
 def fabs(x, /, out=None, **kwargs):
@@ -44,6 +66,8 @@ def fabs(x, /, out=None, **kwargs):
     import numpy as np
     from ._dtypes import ufunc_result_dtype
     from .ndarray import ndarray
+    if kwargs:
+        return _with_kwargs("fabs", (x,), out, kwargs)
     if not isinstance(x, ndarray):
         x = ew._asarray(x)
     rdt = ufunc_result_dtype(np.fabs, x.dtype)

@@ -7,6 +7,8 @@ square, negative, mod, isnan, ...) plus ``dot``, and defines ``where``,
 """
 from __future__ import annotations
 
+import numpy as np
+
 from .linalg_top import dot  # noqa: F401
 from .ufunc_ops import (  # noqa: F401
     abs, arccos, arcsin, arctan, ceil, cos, cosh, exp, floor, log, log2, log10, mod,
@@ -40,6 +42,14 @@ def clip(a, a_min=None, a_max=None, out=None, *, min=None, max=None):
         a_max = max
     from .creation import asarray
     r = asarray(a)
+    if r.dtype.kind in "iu":
+        # a Python int bound beyond the dtype on its own side clips nothing
+        # (NumPy ignores it); beyond the other side it raises OverflowError
+        info = np.iinfo(r.dtype)
+        if type(a_min) is int and a_min < info.min:
+            a_min = None
+        if type(a_max) is int and a_max > info.max:
+            a_max = None
     if a_min is None and a_max is None:
         r = r.copy()
     if a_min is not None:

@@ -144,3 +144,20 @@ def test_random_sort_argsort_searchsorted(seed):
     side = "left" if rng.random() < 0.5 else "right"
     _same(cp.searchsorted(cp.array(s), cp.array(q), side=side).get(),
           np.searchsorted(s, q, side=side))
+
+
+def test_clip_python_int_bounds_beyond_dtype():
+    """NumPy's clip ignores a Python int bound beyond the dtype on its own
+    side and raises OverflowError for one beyond the other side."""
+    for dt, lo, hi in ((np.uint16, -5, 5), (np.uint16, -5, None), (np.uint16, 0, 70000),
+                       (np.int16, -40000, 2), (np.int16, -2, 40000),
+                       (np.uint16, 70000, 80000), (np.uint16, None, -5), (np.int16, 40000, 50000)):
+        x = np.array([1, 2, 600, 0], dt)
+        try:
+            want = np.clip(x, lo, hi)
+        except OverflowError:
+            with pytest.raises(OverflowError):
+                cp.clip(cp.array(x), lo, hi).get()
+            continue
+        _same(cp.clip(cp.array(x), lo, hi).get(), want)
+        _same(cp.array(x).clip(lo, hi).get(), want)

@@ -274,9 +274,10 @@ int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
  * partials: they always fit); strided reductions lower their split count
  * until the partials fit, so a floating sum may round differently from
  * mmp_reduce there.  A layout whose partials still do not fit is rejected
- * with MMP_E_ARG.  Every call on a device shares its array: calls must not
- * overlap on one device (they are ordered when issued from one thread on
- * the library stream). */
+ * with MMP_E_ARG.  Every call on a device shares its array: direct calls,
+ * from any host thread, are serialised and run in order on the library
+ * stream; work that replays a captured call on another stream must not
+ * overlap another use of the array on that device. */
 int mmp_reduce_noalloc(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
                        int64_t inner, const void *x, void *out);
 

@@ -1,5 +1,6 @@
 // mmp_internal.h -- shared host-side helpers of libmmp_hip.so (not ABI).
 #pragma once
+#include <mutex>
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -39,8 +40,16 @@ enum { SCRATCH_REDUCE_PARTIALS = 0, SCRATCH_REDUCE_TICKETS = 1,
        SCRATCH_SCAN_FLAGS = 2, SCRATCH_SCAN_VALUES = 3,
        SCRATCH_SCAN_COUNTER = 4, SCRATCH_NSLOTS = 5 };
 // Monotone call counter used to tag scan tile flags with a generation, so
-// the flag array never needs clearing between calls.
+// the flag array never needs clearing between calls (atomic: concurrent
+// callers never share a generation).
 uint32_t next_generation();
+
+// Held by every entry point that uses the shared scratch slots, from the
+// slot lookup through the kernel launches: a concurrent call on another
+// host thread could otherwise grow (free and replace) a slot between this
+// call's lookup and its launch.  Launches of all callers go to the one
+// library stream, so the kernels themselves run in enqueue order.
+std::mutex &launch_mutex();
 
 // Flags of device-side bounded waits that ran out, in pinned host memory
 // that kernels write with system-scope stores: word 0 scan look-back,

@@ -946,6 +946,7 @@ extern "C" int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64
   if (int st = mmpi::ensure_init()) return st;
   if (int st = check_view(outer, len, inner, x, out)) return st;
   if (outer * inner == 0) return MMP_OK;
+  std::lock_guard<std::mutex> lk(mmpi::launch_mutex());
   return reduce_dispatch(op, dtype, out_dtype, outer, len, inner, x, out, false);
 }
 
@@ -956,6 +957,7 @@ extern "C" int mmp_reduce_noalloc(int op, int dtype, int out_dtype, int64_t oute
     return mmpi::fail(MMP_E_ARG, "mmp_reduce_noalloc: call mmp_init first");
   if (int st = check_view(outer, len, inner, x, out)) return st;
   if (outer * inner == 0) return MMP_OK;
+  std::lock_guard<std::mutex> lk(mmpi::launch_mutex());
   return reduce_dispatch(op, dtype, out_dtype, outer, len, inner, x, out, true);
 }
 
@@ -964,6 +966,7 @@ extern "C" int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len, int6
   if (int st = mmpi::ensure_init()) return st;
   if (int st = check_view(outer, len, inner, x, out)) return st;
   if (outer * inner == 0) return MMP_OK;
+  std::lock_guard<std::mutex> lk(mmpi::launch_mutex());
   MMP_DISPATCH_ALL(dtype, {
     if (op == MMP_R_ARGMAX)
       return launch_argreduce<MMP_R_ARGMAX, T>(outer, len, inner, x, (long long *)out);

@@ -27,6 +27,8 @@
 
 #include "mmp_internal.h"
 
+#include <atomic>
+
 namespace {
 
 struct Device {
@@ -62,7 +64,8 @@ size_t round_size(size_t b) {
 // ---- scratch -------------------------------------------------------------
 void *g_scratch[mmpi::SCRATCH_NSLOTS] = {};
 size_t g_scratch_size[mmpi::SCRATCH_NSLOTS] = {};
-uint32_t g_generation = 0;
+std::atomic<uint32_t> g_generation{0};
+std::mutex g_launch_mu;
 unsigned *g_wait_flags = nullptr;  // pinned host words written by kernels
 
 // ---- fault injection (mmp_debug_fail_next) -------------------------------
@@ -224,10 +227,14 @@ WaitParams wait_params() {
 uint32_t next_generation() {
   // 30 usable bits (flags keep 2 state bits); 0 is never used so that
   // zero-filled scratch never matches a live generation.
-  g_generation = (g_generation + 1) & 0x3fffffffu;
-  if (g_generation == 0) g_generation = 1;
-  return g_generation;
+  uint32_t g;
+  do {
+    g = (g_generation.fetch_add(1, std::memory_order_relaxed) + 1) & 0x3fffffffu;
+  } while (g == 0);
+  return g;
 }
+
+std::mutex &launch_mutex() { return g_launch_mu; }
 
 }  // namespace mmpi
 

@@ -585,6 +585,7 @@ extern "C" int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t
   if (outer < 0 || len < 0 || inner < 0) return mmpi::fail(MMP_E_ARG, "negative extent");
   if (outer * len * inner == 0) return MMP_OK;
   if (!x || !out) return mmpi::fail(MMP_E_ARG, "null pointer");
+  std::lock_guard<std::mutex> lk(mmpi::launch_mutex());
   MMP_DISPATCH_ALL(dtype, {
     if (op == MMP_S_CUMSUM) return scan_out<MMP_S_CUMSUM, T>(out_dtype, outer, len, inner, x, out);
     if (op == MMP_S_CUMPROD) return scan_out<MMP_S_CUMPROD, T>(out_dtype, outer, len, inner, x, out);

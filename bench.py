@@ -212,6 +212,8 @@ def bench_c3(cp, be, reps=10):
         "sum_axis1": lambda: cp.sum(A, axis=1), "mean_axis1": lambda: cp.mean(A, axis=1),
         "argmax_axis1": lambda: cp.argmax(A, axis=1),
         "argmax_all": lambda: cp.argmax(A, axis=None, keepdims=True),
+        # the same matrix reduced over its strided axis
+        "sum_axis0": lambda: cp.sum(A, axis=0), "argmax_axis0": lambda: cp.argmax(A, axis=0),
     }
     for name, f in cases.items():
         try:
@@ -745,7 +747,8 @@ def _env(be):
 
 ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
             "cumsum_f32", "matmul_f16", "sort_f32", "c5_fused", "sum_all", "sum_axis1",
-            "argmax_all", "argmax_axis1", "c1_2p20", "mfma_ceiling")
+            "argmax_all", "argmax_axis1", "sum_axis0", "argmax_axis0", "c1_2p20",
+            "mfma_ceiling")
 
 
 def run_only(cp, be, name, steps):
@@ -769,7 +772,8 @@ def run_only(cp, be, name, steps):
         a = b = cp.array(np.random.default_rng(12).standard_normal(N28, dtype=np.float32))
     elif name == "c5_fused":
         a, b = (cp.array(x) for x in c5_inputs())
-    elif name in ("sum_all", "sum_axis1", "argmax_all", "argmax_axis1"):
+    elif name in ("sum_all", "sum_axis1", "argmax_all", "argmax_axis1", "sum_axis0",
+                  "argmax_axis0"):
         a = b = cp.array(c3_matrix())
     elif name == "c1_2p20":
         a = b = cp.array(c1_inputs(1 << 20))
@@ -787,6 +791,7 @@ def run_only(cp, be, name, steps):
           "sum_all": lambda: cp.sum(a), "sum_axis1": lambda: cp.sum(a, axis=1),
           "argmax_all": lambda: cp.argmax(a, axis=None, keepdims=True),
           "argmax_axis1": lambda: cp.argmax(a, axis=1),
+          "sum_axis0": lambda: cp.sum(a, axis=0), "argmax_axis0": lambda: cp.argmax(a, axis=0),
           "c1_2p20": lambda: cp.sqrt(cp.abs(a)) + cp.exp(-a ** 2)}[name]
     timer = EventTimer(be)
     for _ in range(steps):

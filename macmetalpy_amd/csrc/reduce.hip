@@ -460,6 +460,50 @@ struct ReduceScratch {
   long long spin_limit;       // bound of every wait
 };
 
+// Combines S tagged partials, slot j at base + j * stride words, in index
+// order (deterministic).  The loads of kBatch partials go out before any of
+// them is checked, so one thread pays the atomic-load latency once per
+// batch rather than once per partial; a partial whose tag is not there yet
+// is waited for as get_tagged does.
+template <typename R>
+__device__ __forceinline__ typename R::A combine_tagged(const unsigned long long *base,
+                                                        long long stride, int S,
+                                                        const ReduceScratch &sc) {
+  typedef typename R::A A;
+  constexpr int W = words_of<A>();
+  constexpr int kBatch = 8;
+  A acc = R::ident();
+  for (int j0 = 0; j0 < S; j0 += kBatch) {
+    unsigned long long w[kBatch][W];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+      for (int k = 0; k < W; ++k)
+        w[b][k] = j0 + b < S ? __hip_atomic_load(base + (long long)(j0 + b) * stride + k,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0ull;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (j0 + b >= S) break;
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < W; ++k) ok = ok && (unsigned)(w[b][k] >> 32) == sc.read_tag;
+      A part;
+      if (ok) {
+        unsigned buf[W];
+#pragma unroll
+        for (int k = 0; k < W; ++k) buf[k] = (unsigned)w[b][k];
+        __builtin_memcpy(&part, buf, sizeof(A));
+      } else {
+        part = get_tagged<A>(base + (long long)(j0 + b) * stride, sc.read_tag, sc.timeout,
+                             sc.spin_limit);
+      }
+      acc = R::comb(acc, part);
+    }
+  }
+  return acc;
+}
+
 // Last-arrival combine of the S partials of one row.  Returns true in the
 // workgroup that finishes the row; its thread 0 then holds the result in
 // *out.  Partials are combined in index order (deterministic).
@@ -619,10 +663,7 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const T *__restrict__ x,
   }
   __syncthreads();
   if (!is_last) return;
-  A acc = R::ident();
-  for (int k = 0; k < S; ++k)
-    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.read_tag,
-                                     sc.timeout, sc.spin_limit));
+  const A acc = combine_tagged<R>(grp + (long long)threadIdx.x * W, (long long)kBlock * W, S, sc);
   if (c < inner) out[o * inner + c] = finalize<OP, T, To>(acc, len);
   if (threadIdx.x == 0)
     __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -675,20 +716,145 @@ __global__ __launch_bounds__(kBlock) void k_argreduce_cols(const T *__restrict__
   }
   __syncthreads();
   if (!is_last) return;
-  A acc = R::ident();
-  for (int k = 0; k < S; ++k)
-    acc = R::comb(acc, get_tagged<A>(grp + ((long long)k * kBlock + threadIdx.x) * W, sc.read_tag,
-                                     sc.timeout, sc.spin_limit));
+  const A acc = combine_tagged<R>(grp + (long long)threadIdx.x * W, (long long)kBlock * W, S, sc);
   if (c < inner) out[o * inner + c] = acc.i;
   if (threadIdx.x == 0)
     __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Strided axis with 16-byte column vectors (element size 2, 4 or 8 bytes,
+// inner extent a multiple of the vector, 16-byte aligned base): grid
+// (ceil(inner / CW), outer, S) with CW = 64 x VI columns per workgroup.
+// A lane owns VI adjacent columns and each wave takes every fourth row of
+// the split (one 1 KiB row segment per wave load, kColUnroll loads in
+// flight); the four waves' partials meet in LDS in wave order, then one
+// partial per (split, column) is combined in split order by the last
+// workgroup to arrive, as in k_reduce_cols.  Sums accumulate in the same
+// types; only the order of additions inside a split differs.
+template <typename T> constexpr int col_vec() { return 16 / (int)sizeof(T); }
+template <typename T> constexpr int col_width() { return 64 * col_vec<T>(); }
+
+template <typename R, typename T, typename MapF, typename StoreF>
+__device__ __forceinline__ void cols_vec_body(const T *__restrict__ x, long long len,
+                                              long long inner, int S, const ReduceScratch &sc,
+                                              MapF map, StoreF store) {
+  typedef typename R::A A;
+  constexpr int W = words_of<A>();
+  constexpr int VI = col_vec<T>();
+  constexpr int CW = col_width<T>();
+  constexpr int KC = (CW + kBlock - 1) / kBlock;  // columns per thread in the combine
+  __shared__ A part[kWaves][CW];
+  __shared__ int is_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long o = blockIdx.y;
+  const int s = blockIdx.z;
+  const long long c0 = (long long)blockIdx.x * CW;
+  const long long c = c0 + (long long)lane * VI;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  A v[VI];
+#pragma unroll
+  for (int e = 0; e < VI; ++e) v[e] = R::ident();
+  if (c < inner) {
+    const T *p = x + o * len * inner + c;
+    long long l = b0 + wave;
+    for (; l + (long long)kWaves * (kColUnroll - 1) < b1; l += (long long)kWaves * kColUnroll) {
+      u32x4 q[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u)
+        q[u] = *reinterpret_cast<const u32x4 *>(p + (l + (long long)kWaves * u) * inner);
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) {
+        Pack<T> pk;
+        pk.v = q[u];
+#pragma unroll
+        for (int e = 0; e < VI; ++e) v[e] = R::comb(v[e], map(pk.e[e], l + (long long)kWaves * u));
+      }
+    }
+    for (; l < b1; l += kWaves) {
+      Pack<T> pk;
+      pk.v = *reinterpret_cast<const u32x4 *>(p + l * inner);
+#pragma unroll
+      for (int e = 0; e < VI; ++e) v[e] = R::comb(v[e], map(pk.e[e], l));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VI; ++e) part[wave][lane * VI + e] = v[e];
+  __syncthreads();
+  A acc[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int cc = threadIdx.x + k * kBlock;
+    acc[k] = R::ident();
+    if (cc < CW) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) acc[k] = R::comb(acc[k], part[w][cc]);
+    }
+  }
+  if (S == 1) {
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int cc = threadIdx.x + k * kBlock;
+      if (cc < CW && c0 + cc < inner) store(o * inner + c0 + cc, acc[k]);
+    }
+    return;
+  }
+  // one tagged partial per (o, column block, s, column); ticket per (o, cb)
+  const long long cb = blockIdx.x, ncb = gridDim.x;
+  unsigned long long *grp = sc.words + (o * ncb + cb) * (long long)S * CW * W;
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int cc = threadIdx.x + k * kBlock;
+    if (cc < CW) put_tagged(grp + ((long long)s * CW + cc) * W, acc[k], sc.tag);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(sc.tickets + o * ncb + cb, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == (unsigned)(S - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int cc = threadIdx.x + k * kBlock;
+    if (cc >= CW) continue;
+    const A tot = combine_tagged<R>(grp + (long long)cc * W, (long long)CW * W, S, sc);
+    if (c0 + cc < inner) store(o * inner + c0 + cc, tot);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(sc.tickets + o * ncb + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int OP, typename T, typename To>
+__global__ __launch_bounds__(kBlock) void k_reduce_cols_vec(const T *__restrict__ x,
+                                                           To *__restrict__ out, long long len,
+                                                           long long inner, int S,
+                                                           ReduceScratch sc) {
+  typedef Red<OP, T> R;
+  cols_vec_body<R, T>(
+      x, len, inner, S, sc, [](T q, long long) { return R::map(q); },
+      [&](long long i, const typename R::A &a) { out[i] = finalize<OP, T, To>(a, len); });
+}
+
+// Whether a strided reduction can take the column-vector kernel.
+template <typename T> bool cols_vec_ok(long long inner, const void *x) {
+  if (sizeof(T) < 2) return false;  // one-byte types keep the column-per-thread kernels
+  return inner % col_vec<T>() == 0 && ((uintptr_t)x & 15) == 0;
+}
+
 // ------------------------------------------------------------ launch
 // Strided layouts: split the reduced axis so that the launch has about
-// 2 x kTargetBlocks workgroups, each reading at least 64 rows.
-int col_splits(long long col_blocks, long long len) {
-  long long want = (2 * kTargetBlocks + col_blocks - 1) / col_blocks;
+// `target` workgroups, each reading at least 64 rows.  Measured on 16384^2
+// float32 over axis 0 (the splits' partials combined in batched loads):
+// the column-vector sum runs best with one workgroup per CU (256: 6.2 TB/s;
+// 128: 5.3, 512: 5.8, 1024: 5.4, 2048: 5.3), the column-per-thread
+// kernels with 1024 (argmax 4.76 TB/s; 512: 3.2, 2048: 4.45).
+constexpr long long kColVecTargetBlocks = 256;
+constexpr long long kColTargetBlocks = 1024;
+int col_splits(long long col_blocks, long long len, long long target) {
+  long long want = (target + col_blocks - 1) / col_blocks;
   long long maxs = len / 64 > 0 ? len / 64 : 1;
   long long s = want < maxs ? want : maxs;
   if (s < 1) s = 1;
@@ -737,8 +903,8 @@ constexpr size_t kNoAllocTicketBytes = 16u << 10;
 // Splits of a strided reduction for mmp_reduce_noalloc: the library's
 // choice, lowered until the partials fit the static scratch (S = 1 needs
 // none).
-template <typename A> int noalloc_col_splits(int S, long long groups) {
-  const long long per_split = groups * (long long)kBlock * words_of<A>() * 8;
+template <typename A> int noalloc_col_splits(int S, long long groups, int cols_per_group) {
+  const long long per_split = groups * (long long)cols_per_group * words_of<A>() * 8;
   const long long fit = (long long)(kNoAllocBytes - kNoAllocTicketBytes) / per_split;
   if (S > fit) S = fit > 1 ? (int)fit : 1;
   return S;
@@ -765,17 +931,27 @@ int launch_reduce(long long outer, long long len, long long inner, const void *x
                        mmpi::stream(), (const T *)x, (To *)out, len, S, sc);
     return mmpi::check_launch("mmp_reduce(rows)");
   }
-  const long long ncb = mmpi::ceil_div(inner, kBlock);
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided reduction: outer extent %lld > 65535", outer);
-  int S = col_splits(outer * ncb, len);
-  if (noalloc) S = noalloc_col_splits<A>(S, outer * ncb);
+  const bool vec = cols_vec_ok<T>(inner, x);
+  const int cw = vec ? col_width<T>() : kBlock;  // columns per workgroup
+  const long long ncb = mmpi::ceil_div(inner, cw);
+  int S = col_splits(outer * ncb, len, vec ? kColVecTargetBlocks : kColTargetBlocks);
+  if (noalloc) S = noalloc_col_splits<A>(S, outer * ncb, cw);
   if (S > 1) {
-    if (int st = noalloc ? noalloc_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)
-                         : reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc))
+    if (int st = noalloc ? noalloc_scratch<A>(outer * ncb * S * cw, outer * ncb, &sc)
+                         : reduce_scratch<A>(outer * ncb * S * cw, outer * ncb, &sc))
       return st;
   }
-  hipLaunchKernelGGL((k_reduce_cols<OP, T, To>), dim3((unsigned)ncb, (unsigned)outer, (unsigned)S),
-                     dim3(kBlock), 0, mmpi::stream(), (const T *)x, (To *)out, len, inner, S, sc);
+  const dim3 grid((unsigned)ncb, (unsigned)outer, (unsigned)S);
+  if constexpr (sizeof(T) >= 2) {
+    if (vec) {
+      hipLaunchKernelGGL((k_reduce_cols_vec<OP, T, To>), grid, dim3(kBlock), 0, mmpi::stream(),
+                         (const T *)x, (To *)out, len, inner, S, sc);
+      return mmpi::check_launch("mmp_reduce(cols)");
+    }
+  }
+  hipLaunchKernelGGL((k_reduce_cols<OP, T, To>), grid, dim3(kBlock), 0, mmpi::stream(),
+                     (const T *)x, (To *)out, len, inner, S, sc);
   return mmpi::check_launch("mmp_reduce(cols)");
 }
 
@@ -796,7 +972,7 @@ int launch_argreduce(long long outer, long long len, long long inner, const void
   }
   if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided argreduce: outer extent %lld > 65535", outer);
   const long long ncb = mmpi::ceil_div(inner, kBlock);
-  const int S = col_splits(outer * ncb, len);
+  const int S = col_splits(outer * ncb, len, kColTargetBlocks);
   if (S > 1) {
     if (int st = reduce_scratch<A>(outer * ncb * S * kBlock, outer * ncb, &sc)) return st;
   }

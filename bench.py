@@ -214,8 +214,10 @@ def bench_c3(cp, be, reps=10):
         "argmax_all": lambda: cp.argmax(A, axis=None, keepdims=True),
         # the same matrix reduced over its strided axis
         "sum_axis0": lambda: cp.sum(A, axis=0), "argmax_axis0": lambda: cp.argmax(A, axis=0),
+        "cumsum_axis0": lambda: cp.cumsum(A, axis=0),       # 4 B read + 4 B written
     }
     for name, f in cases.items():
+        nb = 2 * nbytes if name == "cumsum_axis0" else nbytes
         try:
             f()
             cp.synchronize()
@@ -225,8 +227,8 @@ def bench_c3(cp, be, reps=10):
             cp.synchronize()
             ms, _ = timer.ms(name)
             timer.close()
-            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1),
-                         "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nb / ms / 1e6, 1),
+                         "frac_of_peak": round(nb / ms / 1e6 / HBM_PEAK_GBS, 4)}
         except Exception as e:  # report, keep going
             res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
     del A

@@ -481,10 +481,174 @@ __global__ __launch_bounds__(kBlock) void k_scan_cols(const Ti *__restrict__ x, 
   }
 }
 
+// Strided axis with 16-byte column vectors (input element of 2, 4 or 8
+// bytes, inner extent a multiple of the vector, 16-byte aligned input and
+// output): a thread owns VI = 16 / sizeof(Ti) adjacent columns, so a
+// workgroup reads 256 x 16 bytes of every row and each lane keeps 16 bytes
+// in flight per row.  Phase 1 writes the VI chunk totals, a carry pass turns
+// each column's totals into exclusive prefixes in place, phase 2 rescans
+// each chunk from its prefix.
+template <typename Ti> constexpr int scan_col_vec() { return 16 / (int)sizeof(Ti); }
+
+template <int OP, typename Ti>
+__global__ __launch_bounds__(kBlock) void k_scan_cols_part_vec(
+    const Ti *__restrict__ x, typename ScanOp<OP, Ti>::A *__restrict__ part, long long len,
+    long long inner, int S) {
+  typedef ScanOp<OP, Ti> Sc;
+  typedef typename Sc::A A;
+  constexpr int VI = scan_col_vec<Ti>();
+  const long long o = blockIdx.y;
+  const int s = blockIdx.z;
+  const long long c = ((long long)blockIdx.x * kBlock + threadIdx.x) * VI;
+  if (c >= inner) return;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  const Ti *p = x + o * len * inner + c;
+  A acc[VI];
+#pragma unroll
+  for (int e = 0; e < VI; ++e) acc[e] = Sc::ident();
+  long long l = b0;
+  for (; l + kColUnroll <= b1; l += kColUnroll) {
+    u32x4 q[kColUnroll];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) q[u] = *reinterpret_cast<const u32x4 *>(p + (l + u) * inner);
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      union { u32x4 v; Ti e[VI]; } w;
+      w.v = q[u];
+#pragma unroll
+      for (int e = 0; e < VI; ++e) acc[e] = Sc::comb(acc[e], Sc::map(w.e[e]));
+    }
+  }
+  for (; l < b1; ++l) {
+    union { u32x4 v; Ti e[VI]; } w;
+    w.v = *reinterpret_cast<const u32x4 *>(p + l * inner);
+#pragma unroll
+    for (int e = 0; e < VI; ++e) acc[e] = Sc::comb(acc[e], Sc::map(w.e[e]));
+  }
+  A *dst = part + ((long long)o * S + s) * inner + c;
+#pragma unroll
+  for (int e = 0; e < VI; ++e) dst[e] = acc[e];
+}
+
+// Chunk totals -> exclusive chunk prefixes, per column, in place.
+template <int OP, typename Ti>
+__global__ __launch_bounds__(kBlock) void k_scan_cols_carry(typename ScanOp<OP, Ti>::A *__restrict__ part,
+                                                           long long inner, int S) {
+  typedef ScanOp<OP, Ti> Sc;
+  typedef typename Sc::A A;
+  const long long o = blockIdx.y;
+  const long long c = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= inner) return;
+  A *p = part + (long long)o * S * inner + c;
+  A run = Sc::ident();
+  int k = 0;
+  for (; k + 8 <= S; k += 8) {
+    A v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(long long)(k + u) * inner];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      p[(long long)(k + u) * inner] = run;
+      run = Sc::comb(run, v[u]);
+    }
+  }
+  for (; k < S; ++k) {
+    const A v = p[(long long)k * inner];
+    p[(long long)k * inner] = run;
+    run = Sc::comb(run, v);
+  }
+}
+
+template <int OP, typename Ti, typename To>
+__global__ __launch_bounds__(kBlock) void k_scan_cols_vec(const Ti *__restrict__ x, To *__restrict__ y,
+                                                         const typename ScanOp<OP, Ti>::A *__restrict__ pre,
+                                                         long long len, long long inner, int S) {
+  typedef ScanOp<OP, Ti> Sc;
+  typedef typename Sc::A A;
+  constexpr int VI = scan_col_vec<Ti>();
+  constexpr int VO = 16 / (int)sizeof(To);  // outputs per 16-byte store
+  static_assert(VI % VO == 0, "a lane's outputs fill whole 16-byte stores");
+  const long long o = blockIdx.y;
+  const int s = blockIdx.z;
+  const long long c = ((long long)blockIdx.x * kBlock + threadIdx.x) * VI;
+  if (c >= inner) return;
+  const long long per = (len + S - 1) / S;
+  const long long b0 = s * per;
+  const long long b1 = b0 + per < len ? b0 + per : len;
+  A acc[VI];
+#pragma unroll
+  for (int e = 0; e < VI; ++e) acc[e] = pre ? pre[((long long)o * S + s) * inner + c + e] : Sc::ident();
+  const long long off = o * len * inner + c;
+  auto row = [&](const u32x4 &v, long long l) {
+    union { u32x4 v; Ti e[VI]; } w;
+    w.v = v;
+    union { u32x4 v[VI / VO]; To e[VI]; } r;
+#pragma unroll
+    for (int e = 0; e < VI; ++e) {
+      acc[e] = Sc::comb(acc[e], Sc::map(w.e[e]));
+      r.e[e] = mmp_convert<To, A>(acc[e]);
+    }
+    u32x4 *dst = reinterpret_cast<u32x4 *>(y + off + l * inner);
+#pragma unroll
+    for (int k = 0; k < VI / VO; ++k) dst[k] = r.v[k];
+  };
+  long long l = b0;
+  for (; l + kColUnroll <= b1; l += kColUnroll) {
+    u32x4 q[kColUnroll];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) q[u] = *reinterpret_cast<const u32x4 *>(x + off + (l + u) * inner);
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) row(q[u], l + u);
+  }
+  for (; l < b1; ++l) row(*reinterpret_cast<const u32x4 *>(x + off + l * inner), l);
+}
+
 template <int OP, typename Ti, typename To> constexpr bool scan_out_ok() {
   if (mmp_t<Ti>::is_float) return __is_same(Ti, To);
   if (mmp_t<Ti>::is_signed || mmp_t<Ti>::is_bool) return __is_same(To, mmp_i64);
   return __is_same(To, mmp_u64);
+}
+
+#ifndef MMP_SCAN_COL_TARGET
+#define MMP_SCAN_COL_TARGET 512
+#endif
+// The column-vector strided scan: splits of the axis for about
+// MMP_SCAN_COL_TARGET workgroups, each chunk at least 64 rows.
+template <int OP, typename Ti, typename To>
+int launch_scan_cols_vec(long long outer, long long len, long long inner, const void *x, void *y) {
+  typedef typename ScanOp<OP, Ti>::A A;
+  constexpr int VI = scan_col_vec<Ti>();
+  const long long ncb = mmpi::ceil_div(inner / VI, kBlock);
+  const long long want = (MMP_SCAN_COL_TARGET + outer * ncb - 1) / (outer * ncb);
+  const long long maxs = len / 64 > 0 ? len / 64 : 1;
+  long long S = want < maxs ? want : maxs;
+  if (S < 1) S = 1;
+  if (S > 256) S = 256;
+  const dim3 grid((unsigned)ncb, (unsigned)outer, (unsigned)S);
+  void *part = nullptr;
+  if (S > 1) {
+    if (int st = mmp_alloc((size_t)outer * S * inner * sizeof(A), &part)) return st;
+    hipLaunchKernelGGL((k_scan_cols_part_vec<OP, Ti>), grid, dim3(kBlock), 0, mmpi::stream(),
+                       (const Ti *)x, (A *)part, len, inner, (int)S);
+    int st = mmpi::check_launch("mmp_scan(cols, totals)");
+    if (!st) {
+      hipLaunchKernelGGL((k_scan_cols_carry<OP, Ti>),
+                         dim3((unsigned)mmpi::ceil_div(inner, kBlock), (unsigned)outer), dim3(kBlock), 0,
+                         mmpi::stream(), (A *)part, inner, (int)S);
+      st = mmpi::check_launch("mmp_scan(cols, carries)");
+    }
+    if (st) {
+      (void)mmp_free(part);
+      return st;
+    }
+  }
+  hipLaunchKernelGGL((k_scan_cols_vec<OP, Ti, To>), grid, dim3(kBlock), 0, mmpi::stream(),
+                     (const Ti *)x, (To *)y, (const A *)part, len, inner, (int)S);
+  const int st = mmpi::check_launch("mmp_scan(cols)");
+  if (part) (void)mmp_free(part);  // stream-ordered: reused only by later work
+  return st;
 }
 
 template <int OP, typename Ti, typename To>
@@ -540,6 +704,11 @@ int launch_scan(long long outer, long long len, long long inner, const void *x, 
       return MMP_OK;
     }
     if (outer > 65535) return mmpi::fail(MMP_E_ARG, "strided scan: outer extent %lld > 65535", outer);
+    if constexpr (sizeof(Ti) >= 2) {
+      constexpr int VI = scan_col_vec<Ti>();
+      if (inner % VI == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0)
+        return launch_scan_cols_vec<OP, Ti, To>(outer, len, inner, x, y);
+    }
     const long long ncb = mmpi::ceil_div(inner, kBlock);
     long long want = (2048 + outer * ncb - 1) / (outer * ncb);
     long long maxs = len / 64 > 0 ? len / 64 : 1;

@@ -111,3 +111,50 @@ def test_strided_axis_offset_base(dt):
     _check_sum(cp.sum(d, axis=0).get(), h, 0)
     assert np.array_equal(cp.argmax(d, axis=0).get(), np.argmax(h, axis=0))
     assert np.array_equal(cp.min(d, axis=0).get(), np.min(h, axis=0))
+
+
+SCAN_SHAPES = [((1000, 260), 0), ((5, 4096), 0), ((3000, 1024), 0), ((65, 12), 0),
+               ((7, 300, 520), 1), ((20000, 64), 0), ((999, 130), 0)]
+
+
+@pytest.mark.parametrize("shape_axis", SCAN_SHAPES, ids=lambda s: f"{s[0]}-ax{s[1]}")
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.float16, np.int16, np.int32, np.int64,
+                                np.uint16, np.bool_], ids=lambda d: np.dtype(d).name)
+def test_strided_axis_cumsum(shape_axis, dt):
+    """cumsum over a strided axis: 2-, 4- and 8-byte inputs with a
+    16-byte-multiple inner extent take the column-vector scan (chunk totals,
+    carries, rescan), the rest the column-per-thread scan.  Integers bit for
+    bit (64-bit accumulation as NumPy); floats within the float64 running
+    sum's rounding bound."""
+    shape, axis = shape_axis
+    rng = np.random.default_rng(43400 + shape[0] + shape[-1])
+    h = _data(rng, shape, dt)
+    got = cp.cumsum(cp.array(h), axis=axis).get()
+    want = np.cumsum(h, axis=axis)
+    assert got.dtype == want.dtype and got.shape == want.shape
+    if want.dtype.kind == "f":
+        ref = np.cumsum(h.astype(np.float64), axis=axis)
+        bound = np.cumsum(np.abs(h.astype(np.float64)), axis=axis)
+        tol = np.finfo(want.dtype).eps * (np.abs(ref) + 1e-3 * bound) + np.finfo(want.dtype).tiny
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= 2 * tol + 1e-12 * bound)
+    else:
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.float64, np.int16], ids=lambda d: np.dtype(d).name)
+def test_strided_axis_cumprod(dt):
+    rng = np.random.default_rng(43500)
+    h = rng.choice(np.array([-1, 1, 1, 2], dtype=dt), size=(40, 520))
+    got = cp.cumprod(cp.array(h), axis=0).get()
+    want = np.cumprod(h, axis=0)
+    assert got.dtype == want.dtype and np.array_equal(got, want)
+
+
+def test_strided_axis_cumsum_offset_base():
+    """Input one element into its buffer (not 16-byte aligned): the
+    column-per-thread scan; same answer."""
+    rng = np.random.default_rng(43600)
+    flat = rng.integers(-1000, 1000, 1 + 3000 * 256).astype(np.int32)
+    h = flat[1:].reshape(3000, 256)
+    got = cp.cumsum(cp.array(flat)[1:].reshape(3000, 256), axis=0).get()
+    assert np.array_equal(got, np.cumsum(h, axis=0))

@@ -80,6 +80,7 @@ def setup() -> None:
         "config": get_config(),
         "dtypes": dtypes,
         "max_depth": _fusion._MAX_DEPTH, "max_leaves": _fusion._MAX_LEAVES,
+        "sum_blocks": _fusion._SUM_BLOCKS,
         "op_names": _op_names(),
         "unary_codes": {k: v[0] for k, v in _abi.UNARY_OPS.items()},
         "binary_codes": {k: v[0] for k, v in _abi.BINARY_OPS.items()},

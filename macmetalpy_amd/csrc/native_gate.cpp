@@ -139,6 +139,7 @@ PyObject *dtypes[kNDT] = {};
 int itemsize[kNDT] = {1, 2, 2, 4, 4, 8, 8, 2, 4, 8};
 enum { D_BOOL = 0, D_I16, D_U16, D_I32, D_U32, D_I64, D_U64, D_F16, D_F32, D_F64 };
 long max_depth = 16, max_leaves = 24;
+long sum_blocks = 1024;  // workgroups of a fused row-sum launch (init key "sum_blocks")
 
 // slot descriptors of the fusion node classes
 PyObject *d_shape, *d_dtype, *d_depth, *d_buffers, *d_nleaves;
@@ -1341,7 +1342,7 @@ PyObject *gate_run_sum(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
   const int acc = (rdt == D_F16 || rdt == D_F32 || rdt == D_F64)
                       ? D_F64
                       : ((rdt == D_U16 || rdt == D_U32 || rdt == D_U64) ? D_U64 : D_I64);
-  long long want = 2048 / (pl.rows > 1 ? pl.rows : 1);
+  long long want = sum_blocks / (pl.rows > 1 ? pl.rows : 1);
   if (want < 1) want = 1;
   long long colblocks = (pl.cols + 4095) / 4096;
   if (colblocks > want) colblocks = want;
@@ -1540,6 +1541,10 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   GETCFG(ml, "max_leaves");
   max_depth = PyLong_AsLong(md);
   max_leaves = PyLong_AsLong(ml);
+  PyObject *sb;
+  GETCFG(sb, "sum_blocks");
+  sum_blocks = PyLong_AsLong(sb);
+  if (sum_blocks < 1) sum_blocks = 1;
   PyObject *ops, *ucodes, *bcodes, *fastset, *intset;
   GETCFG(ops, "op_names");
   GETCFG(ucodes, "unary_codes");

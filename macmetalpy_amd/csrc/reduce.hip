@@ -691,14 +691,37 @@ __global__ __launch_bounds__(kBlock) void k_argreduce_cols(const T *__restrict__
   if (c < inner) {
     const T *p = x + o * len * inner + c;
     long long l = b0;
-    for (; l + kColUnroll <= b1; l += kColUnroll) {
-      T q[kColUnroll];
+    if (b1 - b0 < 0xffffffffLL) {
+      // rows are visited in order: the sequential update rule with 32-bit
+      // offsets from b0 (as slice_argreduce) instead of the index-comparing
+      // combine per element
+      constexpr unsigned kNone = 0xffffffffu;
+      C bv = R::ident().v;
+      unsigned bi = kNone;
+      auto visit = [&](C e, unsigned off) {
+        const bool upd = (R::seq_better(e, bv) | (bi == kNone)) & R::eligible(e);
+        bv = upd ? e : bv;
+        bi = upd ? off : bi;
+      };
+      for (; l + kColUnroll <= b1; l += kColUnroll) {
+        T q[kColUnroll];
 #pragma unroll
-      for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
+        for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
 #pragma unroll
-      for (int u = 0; u < kColUnroll; ++u) v = R::comb(v, A{(C)q[u], l + u});
+        for (int u = 0; u < kColUnroll; ++u) visit((C)q[u], (unsigned)(l + u - b0));
+      }
+      for (; l < b1; ++l) visit((C)p[l * inner], (unsigned)(l - b0));
+      if (bi != kNone) v = A{bv, b0 + (long long)bi};
+    } else {
+      for (; l + kColUnroll <= b1; l += kColUnroll) {
+        T q[kColUnroll];
+#pragma unroll
+        for (int u = 0; u < kColUnroll; ++u) q[u] = p[(l + u) * inner];
+#pragma unroll
+        for (int u = 0; u < kColUnroll; ++u) v = R::comb(v, A{(C)q[u], l + u});
+      }
+      for (; l < b1; ++l) v = R::comb(v, A{(C)p[l * inner], l});
     }
-    for (; l < b1; ++l) v = R::comb(v, A{(C)p[l * inner], l});
   }
   if (S == 1) {
     if (c < inner) out[o * inner + c] = v.i;
@@ -851,8 +874,11 @@ template <typename T> bool cols_vec_ok(long long inner, const void *x) {
 // the column-vector sum runs best with one workgroup per CU (256: 6.2 TB/s;
 // 128: 5.3, 512: 5.8, 1024: 5.4, 2048: 5.3), the column-per-thread
 // kernels with 1024 (argmax 4.76 TB/s; 512: 3.2, 2048: 4.45).
+#ifndef MMP_COL_TARGET_BLOCKS
+#define MMP_COL_TARGET_BLOCKS 1024
+#endif
 constexpr long long kColVecTargetBlocks = 256;
-constexpr long long kColTargetBlocks = 1024;
+constexpr long long kColTargetBlocks = MMP_COL_TARGET_BLOCKS;
 int col_splits(long long col_blocks, long long len, long long target) {
   long long want = (target + col_blocks - 1) / col_blocks;
   long long maxs = len / 64 > 0 ? len / 64 : 1;

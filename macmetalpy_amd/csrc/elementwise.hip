@@ -367,6 +367,54 @@ __global__ __launch_bounds__(kBlock) void k_copy_transpose(const Ti *__restrict_
   }
 }
 
+// The same permuted copy for whole 64 x 64 tiles of 2-, 4- or 8-byte
+// elements (no conversion) whose rows start 16-byte aligned on both sides:
+// every global access is one 16-byte vector (VEC elements) -- a lane reads
+// VEC consecutive p of one q row and writes VEC consecutive q of one p row
+// -- and per-thread addresses are formed once, then advanced by constant
+// steps.  LDS pitch 65 elements: the transposed reads of a wave hit 64
+// distinct banks.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_copy_transpose_vec(const T *__restrict__ x,
+                                                              T *__restrict__ y, TransDesc t) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int VPR = 64 / VEC;          // vectors per 64-element tile row
+  constexpr int RPP = kBlock / VPR;      // tile rows per pass
+  __shared__ T tile[64][65];
+  long long b = blockIdx.x;
+  const long long jq = b % t.tq;
+  b /= t.tq;
+  const long long jp = b % t.tp;
+  b /= t.tp;
+  long long so = 0, dof = 0;
+  for (int k = t.nb - 1; k >= 0; --k) {
+    const long long q = b / t.bshape[k];
+    const long long i = b - q * t.bshape[k];
+    so += i * t.bs[k];
+    dof += i * t.bd[k];
+    b = q;
+  }
+  const int v = threadIdx.x % VPR, r0 = threadIdx.x / VPR;
+  const long long p0 = jp * 64, q0 = jq * 64;
+  const T *src = x + so + p0 + v * VEC + (q0 + r0) * t.sq;
+#pragma unroll
+  for (int i = 0; i < 64 / RPP; ++i) {
+    union { u32x4 u; T e[VEC]; } w;
+    w.u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + (long long)i * RPP * t.sq));
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) tile[r0 + i * RPP][v * VEC + e] = w.e[e];
+  }
+  __syncthreads();
+  T *dst = y + dof + (p0 + r0) * t.dp + q0 + v * VEC;
+#pragma unroll
+  for (int i = 0; i < 64 / RPP; ++i) {
+    union { u32x4 u; T e[VEC]; } w;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) w.e[e] = tile[v * VEC + e][r0 + i * RPP];
+    __builtin_nontemporal_store(w.u, reinterpret_cast<u32x4 *>(dst + (long long)i * RPP * t.dp));
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_fill(T *__restrict__ y, long long n, T v) {
   const long long stride = (long long)gridDim.x * kBlock;
@@ -475,6 +523,16 @@ bool transpose_desc(const StrideDesc &d, TransDesc *t) {
   return true;
 }
 
+// Whole tiles and 16-byte aligned rows on both sides for the vector
+// transpose: extents multiples of 64, every stride other than the two unit
+// ones a multiple of the vector, aligned bases.
+bool transpose_vec_ok(const TransDesc &t, const void *x, const void *y, int vec) {
+  if (t.np % 64 || t.nq % 64 || t.sq % vec || t.dp % vec) return false;
+  for (int k = 0; k < t.nb; ++k)
+    if (t.bs[k] % vec || t.bd[k] % vec) return false;
+  return aligned16(x) && aligned16(y);
+}
+
 template <typename Ti>
 int copy_from(int dst_dtype, long long n, const void *x, void *y,
               const StrideDesc &d, int mode) {
@@ -495,6 +553,16 @@ int copy_from(int dst_dtype, long long n, const void *x, void *y,
     long long nbatch = 1;
     for (int k = 0; k < t.nb; ++k) nbatch *= t.bshape[k];
     const long long blocks = nbatch * t.tp * t.tq;
+    if (blocks <= 0x7fffffffLL && transpose_vec_ok(t, x, y, 16 / (int)sizeof(Ti))) {
+      MMP_DISPATCH_ALL(dst_dtype, {
+        if constexpr (__is_same(T, Ti) && sizeof(Ti) >= 2) {  // a plain copy of the bits
+          hipLaunchKernelGGL((k_copy_transpose_vec<Ti>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                             mmpi::stream(), (const Ti *)x, (Ti *)y, t);
+          return mmpi::check_launch("mmp_copy(transpose)");
+        }
+        break;  // leave the dtype switch: the converting kernel below
+      })
+    }
     if (blocks <= 0x7fffffffLL) {
       MMP_DISPATCH_ALL(dst_dtype, {
         hipLaunchKernelGGL((k_copy_transpose<Ti, T>), dim3((unsigned)blocks), dim3(kBlock), 0,

@@ -76,7 +76,9 @@ def test_column_scans_chunked(shape, ax):
                                    np.int64])
 @pytest.mark.parametrize("shape,perm", [((1000, 777), (1, 0)), ((64, 64), (1, 0)),
                                         ((5, 130, 70), (0, 2, 1)), ((70, 5, 130), (2, 1, 0)),
-                                        ((33, 17, 3), (1, 0, 2)), ((300, 20), (1, 0))])
+                                        ((33, 17, 3), (1, 0, 2)), ((300, 20), (1, 0)),
+                                        ((192, 256), (1, 0)), ((3, 128, 192), (0, 2, 1)),
+                                        ((128, 3, 256), (2, 1, 0))])
 def test_transpose_copies(dtype, shape, perm):
     rng = np.random.default_rng(8)
     x = (rng.standard_normal(shape) * 100).astype(dtype)
@@ -90,6 +92,25 @@ def test_transpose_copies(dtype, shape, perm):
     inv = tuple(range(nsl.ndim))[::-1]
     got2 = sl.transpose(inv).astype(np.float32).get()
     assert np.array_equal(got2, np.ascontiguousarray(nsl.transpose(inv)).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.float16, np.int16, np.int32])
+def test_transpose_copies_whole_tiles(dtype):
+    """Whole 64 x 64 tiles with 16-byte aligned rows take the vector
+    transpose (one 16-byte access per lane on both sides): sliced views whose
+    offsets and strides keep that alignment, reversed and stepped views, a
+    batch dimension, and a view whose offset breaks it (the element kernel)."""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((320, 512)) * 100).astype(dtype)
+    cx = cp.array(x)
+    for sl in ((slice(64, None), slice(128, None)), (slice(None), slice(None, None, 2)),
+               (slice(None, None, -1), slice(None)), (slice(1, 257), slice(None)),
+               (slice(None), slice(8, 392))):
+        got = cx[sl].T.copy().get()
+        assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(x[sl].T).view(np.uint8)), sl
+    b = (rng.standard_normal((4, 128, 192)) * 100).astype(dtype)
+    got = cp.ascontiguousarray(cp.array(b).transpose(2, 0, 1)).get()
+    assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(b.transpose(2, 0, 1)).view(np.uint8))
 
 
 def test_device_creation_large():

@@ -261,6 +261,23 @@ __global__ __launch_bounds__(kBlock) void k_copy_rows(const Ti *__restrict__ x,
     rem = q;
   }
   const long long ss = d.sstride[last], ds = d.dstride[last];
+  if (ss == 1 && ds == 1) {
+    // rows contiguous on both sides (slices, tiles, concatenations): row
+    // pointers once, 32-bit offsets within the tile, all loads first
+    const Ti *xs = x + so + c0;
+    To *yd = y + dof + c0;
+    const int n = len - c0 < kRowTile ? (int)(len - c0) : kRowTile;
+    if (n == kRowTile) {
+      Ti v[kRowItems];
+#pragma unroll
+      for (int u = 0; u < kRowItems; ++u) v[u] = xs[u * kBlock + threadIdx.x];
+#pragma unroll
+      for (int u = 0; u < kRowItems; ++u) yd[u * kBlock + threadIdx.x] = mmp_convert<To, Ti>(v[u]);
+    } else {
+      for (int c = threadIdx.x; c < n; c += kBlock) yd[c] = mmp_convert<To, Ti>(xs[c]);
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < kRowItems; ++u) {
     const long long c = c0 + u * kBlock + threadIdx.x;

@@ -357,6 +357,22 @@ int mmp_scatter(int word, void *dst, int64_t dst_bytes, const int64_t *offsets, 
  * position of the k-th selected element, k < count. */
 int mmp_nonzero(int64_t n, const int64_t *incl, int64_t count, int64_t *out);
 
+/* Boolean-mask compaction straight from the mask's bytes (any nonzero byte
+ * selects), by tiles of 4096 elements.  Replaces the same NumPy nonzero the
+ * reference's mask indexing and nonzero / flatnonzero / argwhere run on the
+ * host (ndarray.py:874-891, indexing.py:370-391).
+ * mmp_mask_tile_counts: tile_incl[t] = number of selected elements in tiles
+ * 0..t (ceil(n / 4096) entries); the last entry is the total.
+ * mmp_mask_positions: out[k] = position of the k-th selected element, given
+ * tile_incl from the first call on the same mask (out holds the total). */
+int mmp_mask_tile_counts(int64_t n, const void *mask, uint64_t *tile_incl);
+int mmp_mask_positions(int64_t n, const void *mask, const uint64_t *tile_incl, int64_t *out);
+/* The selected elements (word = 1, 2, 4 or 8 bytes each) of src, a
+ * contiguous array of the mask's n elements, packed in order into out:
+ * a[mask] for a mask of a's shape (reference ndarray.py:874-891). */
+int mmp_mask_compact(int word, int64_t n, const void *mask, const uint64_t *tile_incl,
+                     const void *src, void *out);
+
 /* Integer counts (replace the NumPy host calls behind bincount / histogram,
  * math_ext.py).  counts (int64) are zeroed first, then:
  * mmp_bincount: counts[v] = number of integer elements equal to v, for v in

@@ -208,6 +208,7 @@ EXPORTS = (
     "mmp_copy_strided", "mmp_fill",
     "mmp_reduce", "mmp_reduce_noalloc", "mmp_argreduce", "mmp_scan", "mmp_matmul",
     "mmp_sort", "mmp_searchsorted", "mmp_take", "mmp_gather", "mmp_scatter", "mmp_nonzero",
+    "mmp_mask_tile_counts", "mmp_mask_positions", "mmp_mask_compact",
     "mmp_bincount", "mmp_histogram",
     "mmp_lu", "mmp_lu_solve", "mmp_cholesky", "mmp_qr", "mmp_qr_q", "mmp_eigh", "mmp_svd",
     "mmp_rtc_compile", "mmp_rtc_build", "mmp_rtc_launch", "mmp_rtc_launch_threads",

@@ -108,6 +108,9 @@ _SIGNATURES = {
     "mmp_gather": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp],
     "mmp_scatter": [_c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64],
     "mmp_nonzero": [_c_i64, _c_vp, _c_i64, _c_vp],
+    "mmp_mask_tile_counts": [_c_i64, _c_vp, _c_vp],
+    "mmp_mask_positions": [_c_i64, _c_vp, _c_vp, _c_vp],
+    "mmp_mask_compact": [_c_int, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp],
     "mmp_bincount": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp],
     "mmp_histogram": [_c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp],
     "mmp_lu": [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp],
@@ -478,6 +481,15 @@ class HipBackend:
 
     def nonzero(self, n: int, incl: int, count: int, out: int) -> None:
         _check(self._lib.mmp_nonzero(n, incl, count, out), "mmp_nonzero")
+
+    def mask_tile_counts(self, n: int, mask: int, tile_incl: int) -> None:
+        _check(self._lib.mmp_mask_tile_counts(n, mask, tile_incl), "mmp_mask_tile_counts")
+
+    def mask_positions(self, n: int, mask: int, tile_incl: int, out: int) -> None:
+        _check(self._lib.mmp_mask_positions(n, mask, tile_incl, out), "mmp_mask_positions")
+
+    def mask_compact(self, word: int, n: int, mask: int, tile_incl: int, src: int, out: int) -> None:
+        _check(self._lib.mmp_mask_compact(word, n, mask, tile_incl, src, out), "mmp_mask_compact")
 
     def bincount(self, dcode, n, x, nbins, counts) -> None:
         _check(self._lib.mmp_bincount(dcode, n, x, nbins, counts), "mmp_bincount")

@@ -16,6 +16,12 @@
 //  * mmp_nonzero turns the inclusive int64 count of a mask (its cumsum)
 //    into the positions of the nonzero elements: element i is selected
 //    where incl[i] != incl[i - 1], and lands at incl[i] - 1.
+//  * mmp_mask_tile_counts / mmp_mask_positions do the same from the mask
+//    bytes themselves, by tiles of 4096 elements: a tile's selected count,
+//    the inclusive count over tiles (the library scan), then each tile
+//    writes its positions from its tile's start offset and an in-tile
+//    exclusive count.  The mask is read twice (1 byte per element each) and
+//    nothing per element is written besides the positions.
 #include "mmp_ops.h"
 #include "mmp_internal.h"
 
@@ -93,6 +99,99 @@ __global__ __launch_bounds__(kBlock) void k_nonzero(const long long *__restrict_
     const long long v = incl[i];
     const long long prev = i > 0 ? incl[i - 1] : 0;
     if (v != prev && v >= 1 && v <= count) out[v - 1] = i;
+  }
+}
+
+// Mask compaction by tiles of kMaskTile elements; thread t of a tile owns
+// elements 16 t .. 16 t + 15 (one 16-byte load when the tile is whole and
+// aligned).  Any nonzero byte selects.
+constexpr int kMaskItems = 16;
+constexpr int kMaskTile = kBlock * kMaskItems;
+
+// This thread's 16 selection flags as a bit mask.
+__device__ __forceinline__ unsigned mask_bits(const unsigned char *__restrict__ m, long long n,
+                                              long long t0) {
+  const long long i0 = t0 + (long long)threadIdx.x * kMaskItems;
+  unsigned bits = 0;
+  if (i0 + kMaskItems <= n && (((uintptr_t)(m + i0)) & 15u) == 0) {
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(m + i0);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bits |= (((v[w] >> (8 * b)) & 0xffu) != 0u ? 1u : 0u) << (4 * w + b);
+  } else {
+    for (int k = 0; k < kMaskItems; ++k)
+      if (i0 + k < n && m[i0 + k] != 0) bits |= 1u << k;
+  }
+  return bits;
+}
+
+// Workgroup exclusive sum of one value per thread (wave shuffles, then the
+// wave totals through LDS); *total = the workgroup's sum.
+__device__ __forceinline__ unsigned block_excl_sum(unsigned v, unsigned *total) {
+  __shared__ unsigned wsum[kBlock / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  unsigned pre = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) {
+    if (w < wave) pre += wsum[w];
+    tot += wsum[w];
+  }
+  *total = tot;
+  return pre + inc - v;
+}
+
+__global__ __launch_bounds__(kBlock) void k_mask_counts(const unsigned char *__restrict__ m,
+                                                        long long n, unsigned *__restrict__ counts) {
+  const long long t0 = (long long)blockIdx.x * kMaskTile;
+  unsigned total;
+  block_excl_sum((unsigned)__builtin_popcount(mask_bits(m, n, t0)), &total);
+  if (threadIdx.x == 0) counts[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kBlock) void k_mask_positions(const unsigned char *__restrict__ m,
+                                                           long long n,
+                                                           const unsigned long long *__restrict__ incl,
+                                                           long long *__restrict__ out) {
+  const long long t0 = (long long)blockIdx.x * kMaskTile;
+  unsigned bits = mask_bits(m, n, t0);
+  unsigned total;
+  const unsigned ex = block_excl_sum((unsigned)__builtin_popcount(bits), &total);
+  // the tile's first output slot: inclusive count through this tile minus its own
+  long long o = (long long)incl[blockIdx.x] - (long long)total + ex;
+  const long long i0 = t0 + (long long)threadIdx.x * kMaskItems;
+  while (bits) {
+    const int k = __builtin_ctz(bits);
+    out[o++] = i0 + k;
+    bits &= bits - 1;
+  }
+}
+
+// The selected elements themselves (W bytes each) of a contiguous source
+// of the mask's shape, in order: a[mask] without the positions.
+template <typename W>
+__global__ __launch_bounds__(kBlock) void k_mask_compact(const unsigned char *__restrict__ m,
+                                                         long long n,
+                                                         const unsigned long long *__restrict__ incl,
+                                                         const W *__restrict__ src, W *__restrict__ out) {
+  const long long t0 = (long long)blockIdx.x * kMaskTile;
+  unsigned bits = mask_bits(m, n, t0);
+  unsigned total;
+  const unsigned ex = block_excl_sum((unsigned)__builtin_popcount(bits), &total);
+  long long o = (long long)incl[blockIdx.x] - (long long)total + ex;
+  const long long i0 = t0 + (long long)threadIdx.x * kMaskItems;
+  while (bits) {
+    const int k = __builtin_ctz(bits);
+    out[o++] = src[i0 + k];
+    bits &= bits - 1;
   }
 }
 
@@ -182,4 +281,60 @@ extern "C" int mmp_nonzero(int64_t n, const int64_t *incl, int64_t count, int64_
   hipLaunchKernelGGL(k_nonzero, dim3(grid_for(n)), dim3(kBlock), 0, mmpi::stream(),
                      (const long long *)incl, (long long)n, (long long)count, (long long *)out);
   return mmpi::check_launch("mmp_nonzero");
+}
+
+extern "C" int mmp_mask_tile_counts(int64_t n, const void *mask, uint64_t *tile_incl) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (n < 0) return mmpi::fail(MMP_E_ARG, "mmp_mask_tile_counts: negative extent");
+  if (n == 0) return MMP_OK;
+  if (!mask || !tile_incl) return mmpi::fail(MMP_E_ARG, "mmp_mask_tile_counts: null pointer");
+  const long long tiles = mmpi::ceil_div(n, kMaskTile);
+  if (tiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "mmp_mask_tile_counts: mask too large");
+  void *counts = nullptr;
+  if (int st = mmp_alloc((size_t)tiles * sizeof(unsigned), &counts)) return st;
+  hipLaunchKernelGGL(k_mask_counts, dim3((unsigned)tiles), dim3(kBlock), 0, mmpi::stream(),
+                     (const unsigned char *)mask, (long long)n, (unsigned *)counts);
+  int st = mmpi::check_launch("mmp_mask_tile_counts");
+  if (!st) st = mmp_scan(MMP_S_CUMSUM, MMP_U32, MMP_U64, 1, tiles, 1, counts, tile_incl);
+  (void)mmp_free(counts);  // stream-ordered: reused only by later work
+  return st;
+}
+
+extern "C" int mmp_mask_positions(int64_t n, const void *mask, const uint64_t *tile_incl,
+                                  int64_t *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (n < 0) return mmpi::fail(MMP_E_ARG, "mmp_mask_positions: negative extent");
+  if (n == 0) return MMP_OK;
+  if (!mask || !tile_incl || !out) return mmpi::fail(MMP_E_ARG, "mmp_mask_positions: null pointer");
+  const long long tiles = mmpi::ceil_div(n, kMaskTile);
+  if (tiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "mmp_mask_positions: mask too large");
+  hipLaunchKernelGGL(k_mask_positions, dim3((unsigned)tiles), dim3(kBlock), 0, mmpi::stream(),
+                     (const unsigned char *)mask, (long long)n, (const unsigned long long *)tile_incl,
+                     (long long *)out);
+  return mmpi::check_launch("mmp_mask_positions");
+}
+
+extern "C" int mmp_mask_compact(int word, int64_t n, const void *mask, const uint64_t *tile_incl,
+                                const void *src, void *out) {
+  if (int st = mmpi::ensure_init()) return st;
+  if (n < 0) return mmpi::fail(MMP_E_ARG, "mmp_mask_compact: negative extent");
+  if (n == 0) return MMP_OK;
+  if (!mask || !tile_incl || !src || !out) return mmpi::fail(MMP_E_ARG, "mmp_mask_compact: null pointer");
+  const long long tiles = mmpi::ceil_div(n, kMaskTile);
+  if (tiles > 0x7fffffffLL) return mmpi::fail(MMP_E_ARG, "mmp_mask_compact: mask too large");
+  const dim3 grid((unsigned)tiles);
+  const auto *m = (const unsigned char *)mask;
+  const auto *ti = (const unsigned long long *)tile_incl;
+  switch (word) {
+    case 1: hipLaunchKernelGGL((k_mask_compact<unsigned char>), grid, dim3(kBlock), 0, mmpi::stream(),
+                               m, (long long)n, ti, (const unsigned char *)src, (unsigned char *)out); break;
+    case 2: hipLaunchKernelGGL((k_mask_compact<unsigned short>), grid, dim3(kBlock), 0, mmpi::stream(),
+                               m, (long long)n, ti, (const unsigned short *)src, (unsigned short *)out); break;
+    case 4: hipLaunchKernelGGL((k_mask_compact<unsigned>), grid, dim3(kBlock), 0, mmpi::stream(),
+                               m, (long long)n, ti, (const unsigned *)src, (unsigned *)out); break;
+    case 8: hipLaunchKernelGGL((k_mask_compact<unsigned long long>), grid, dim3(kBlock), 0, mmpi::stream(),
+                               m, (long long)n, ti, (const unsigned long long *)src, (unsigned long long *)out); break;
+    default: return mmpi::fail(MMP_E_ARG, "mmp_mask_compact: element size %d not 1, 2, 4 or 8", word);
+  }
+  return mmpi::check_launch("mmp_mask_compact");
 }

@@ -55,19 +55,43 @@ def _int_scalar(k) -> bool:
 
 
 # ------------------------------------------------------------- nonzero
+_MASK_TILE = 4096  # elements per tile of mmp_mask_tile_counts / mmp_mask_positions
+
+
 def _flat_nonzero(mask: ndarray) -> ndarray:
     """int64 positions of the nonzero elements of ``mask`` in C order."""
-    from . import reductions
     m = mask if mask._dtype == np.bool_ else (mask != 0)
-    m = m.ravel()
+    m = m.ravel()._ensure_contiguous()
     n = m.size
     if n == 0:
         return ndarray._empty_device((0,), _I64)
-    incl = reductions.cumsum(m)._ensure_contiguous()  # bool -> int64 inclusive count
-    count = int(incl[n - 1])
+    be = HipBackend()
+    tiles = -(-n // _MASK_TILE)
+    incl = ndarray._empty_device((tiles,), np.dtype(np.uint64))  # selected count through each tile
+    be.mask_tile_counts(n, m._ptr, incl._ptr)
+    count = int(incl[tiles - 1])
     out = ndarray._empty_device((count,), _I64)
     if count:
-        HipBackend().nonzero(n, incl._ptr, count, out._ptr)
+        be.mask_positions(n, m._ptr, incl._ptr, out._ptr)
+    return out
+
+
+def _mask_compact(a: ndarray, mask: ndarray) -> ndarray:
+    """``a[mask]`` for a boolean mask of a's shape: the selected elements
+    in C order, packed on the device straight from the mask and the data."""
+    m = mask.ravel()._ensure_contiguous()
+    src = a.ravel()._ensure_contiguous()
+    n = m.size
+    if n == 0:
+        return ndarray._empty_device((0,), a._dtype)
+    be = HipBackend()
+    tiles = -(-n // _MASK_TILE)
+    incl = ndarray._empty_device((tiles,), np.dtype(np.uint64))
+    be.mask_tile_counts(n, m._ptr, incl._ptr)
+    count = int(incl[tiles - 1])
+    out = ndarray._empty_device((count,), a._dtype)
+    if count:
+        be.mask_compact(a._dtype.itemsize, n, m._ptr, incl._ptr, src._ptr, out._ptr)
     return out
 
 
@@ -354,6 +378,9 @@ def getitem(a: ndarray, key, mode: str = "raise") -> ndarray:
     ``mode`` treats out-of-range indices as np.take does."""
     a._materialize_if_lazy()
     a._ensure_gpu()
+    if (mode == "raise" and isinstance(key, ndarray) and key._dtype == np.bool_ and key.ndim
+            and tuple(key.shape) == tuple(a.shape) and a._dtype.itemsize in (1, 2, 4, 8)):
+        return _mask_compact(a, key)
     if mode == "raise":
         idx = _row_index(a, key)
         if idx is not None:

@@ -195,3 +195,40 @@ def test_routines():
     gy = cp.array(x)
     cp.put_along_axis(gy, cp.array(first), -7.0, axis=1)
     _same(gy, y)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.float16, np.int16, np.int64, np.bool_])
+@pytest.mark.parametrize("n", [1, 4095, 4096, 4097, (1 << 20) + 3])
+def test_full_shape_mask_compaction(dt, n):
+    """a[mask] for a mask of a's shape packs the selected elements on the
+    device straight from the mask (tiles of 4096: counts, their scan, then
+    each tile writes from its offset); nonzero / flatnonzero use the same
+    tile counts.  Tile boundaries, every density, views and element sizes
+    against NumPy bit for bit."""
+    rng = np.random.default_rng(44000 + n)
+    x = (rng.standard_normal(n) * 50).astype(dt) if dt != np.bool_ else rng.random(n) < 0.5
+    gx = cp.array(x)
+    for density in (0.0, 0.01, 0.5, 1.0):
+        m = rng.random(n) < density
+        gm = cp.array(m)
+        got = gx[gm].get()
+        assert got.dtype == x.dtype and np.array_equal(got.view(np.uint8), x[m].view(np.uint8))
+        assert np.array_equal(cp.flatnonzero(gm).get(), np.flatnonzero(m))
+    # 2-D, a mask view one element into its buffer (unaligned) and a transposed source
+    if n >= 4096:
+        r = 64
+        c = n // r
+        x2 = x[: r * c].reshape(r, c)
+        mb = rng.random(r * c + 1) < 0.3
+        gm2 = cp.array(mb)[1:].reshape(r, c)
+        want = x2[mb[1:].reshape(r, c)]
+        got = cp.array(x2)[gm2].get()
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+        mt = rng.random((c, r)) < 0.3
+        got = cp.array(x2).T[cp.array(mt)].get()
+        assert np.array_equal(got.view(np.uint8), x2.T[mt].view(np.uint8))
+
+
+def test_full_shape_mask_empty():
+    a = cp.zeros((0, 3), dtype=np.float32)
+    assert cp.zeros((0, 3), dtype=np.float32)[a > 0].get().shape == (0,)

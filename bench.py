@@ -527,8 +527,8 @@ def bench_indexing(cp, be, reps=5):
     cases = {
         "gather_a[idx]_2^26": (lambda: x[idx], 16 * n),
         # a > 0 (4 B read, 1 B written), tile counts (1 B), packing (1 B of
-        # mask + 4 B read and 4 B written per selected element)
-        "mask_a[a>0]_2^26": (lambda: x[x > 0], (5 + 1 + 1) * n + 8 * (n // 2)),
+        # mask and 4 B of data read per element, 4 B written per selected one)
+        "mask_a[a>0]_2^26": (lambda: x[x > 0], (5 + 1 + 5) * n + 4 * (n // 2)),
         "concatenate_2x2^25": (lambda: cp.concatenate([x[: n // 2], x[n // 2:]]), 8 * n),
         "tile_8192sq_2x2": (lambda: cp.tile(x.reshape(8192, 8192), (2, 2)), 4 * n + 16 * n),
         "transpose_copy_8192sq": (lambda: x.reshape(8192, 8192).T.copy(), 8 * n),

@@ -176,23 +176,40 @@ __global__ __launch_bounds__(kBlock) void k_mask_positions(const unsigned char *
 }
 
 // The selected elements themselves (W bytes each) of a contiguous source
-// of the mask's shape, in order: a[mask] without the positions.
+// of the mask's shape, in order: a[mask] without the positions.  The tile's
+// source is read coalesced into LDS, each thread takes its 16 elements from
+// there, writes the selected ones back packed (LDS slot = in-tile rank), and
+// the packed run leaves with coalesced stores.
 template <typename W>
 __global__ __launch_bounds__(kBlock) void k_mask_compact(const unsigned char *__restrict__ m,
                                                          long long n,
                                                          const unsigned long long *__restrict__ incl,
                                                          const W *__restrict__ src, W *__restrict__ out) {
+  __shared__ __attribute__((aligned(16))) W buf[kMaskTile];
   const long long t0 = (long long)blockIdx.x * kMaskTile;
+  const int tn = n - t0 < kMaskTile ? (int)(n - t0) : kMaskTile;  // elements in this tile
+  const W *s = src + t0;
+  constexpr int VW = 16 / (int)sizeof(W);
+  if (tn == kMaskTile && (((uintptr_t)s) & 15u) == 0) {
+    for (int v = threadIdx.x; v < kMaskTile / VW; v += kBlock)
+      *reinterpret_cast<u32x4 *>(&buf[v * VW]) = *reinterpret_cast<const u32x4 *>(s + v * VW);
+  } else {
+    for (int i = threadIdx.x; i < tn; i += kBlock) buf[i] = s[i];
+  }
   unsigned bits = mask_bits(m, n, t0);
   unsigned total;
-  const unsigned ex = block_excl_sum((unsigned)__builtin_popcount(bits), &total);
-  long long o = (long long)incl[blockIdx.x] - (long long)total + ex;
-  const long long i0 = t0 + (long long)threadIdx.x * kMaskItems;
-  while (bits) {
-    const int k = __builtin_ctz(bits);
-    out[o++] = src[i0 + k];
-    bits &= bits - 1;
-  }
+  const unsigned ex = block_excl_sum((unsigned)__builtin_popcount(bits), &total);  // syncs
+  W mine[kMaskItems];
+#pragma unroll
+  for (int k = 0; k < kMaskItems; ++k) mine[k] = buf[threadIdx.x * kMaskItems + k];
+  __syncthreads();
+  unsigned r = ex;
+#pragma unroll
+  for (int k = 0; k < kMaskItems; ++k)
+    if ((bits >> k) & 1u) buf[r++] = mine[k];
+  __syncthreads();
+  const long long o = (long long)incl[blockIdx.x] - (long long)total;
+  for (unsigned j = threadIdx.x; j < total; j += kBlock) out[o + j] = buf[j];
 }
 
 template <typename W>

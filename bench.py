@@ -200,6 +200,76 @@ def bench_small_ops(cp, be, n=1 << 20, calls=2000):
     return res
 
 
+SMALL_HOST_SIZES = (("1K", 1 << 10), ("64K", 1 << 16))
+
+
+def _small_host_cases(cp, a_np, b_np):
+    """The three calls on arrays created from host (NumPy) data each call:
+    the case the reference's C gate answers on the CPU (_accelerator.c:
+    549-712 fast_binary / fast_unary, :798-858 fast_reduce, below the
+    thresholds of ndarray.py:41-44)."""
+    return {"add_get": lambda: (cp.array(a_np) + cp.array(b_np)).get(),
+            "sin_get": lambda: cp.sin(cp.array(a_np)).get(),
+            "sum_float": lambda: float(cp.sum(cp.array(a_np)))}
+
+
+def bench_small_host_ops(cp, be, calls=1000):
+    """Per-call time of (a+b).get(), sin(a).get() and float(sum(a)) on
+    float32 arrays made from NumPy data in the call (host-resident until
+    the native gate uploads them through page-locked staging), end to end
+    with the result back on the host.  ``gate`` is the native gate's
+    counters per call: uploads, ops and materialisations done in C, calls
+    handed to the Python path.  The NumPy time of the same calls (the
+    reference's CPU path) is filled in beside each from ``cpu_baseline``."""
+    from macmetalpy_amd import _gate
+    res = {}
+    for label, n in SMALL_HOST_SIZES:
+        g = np.random.default_rng(n)
+        a_np = g.standard_normal(n, dtype=np.float32)
+        b_np = g.standard_normal(n, dtype=np.float32)
+        sec = {}
+        for name, f in _small_host_cases(cp, a_np, b_np).items():
+            for _ in range(50):
+                f()
+            k = calls if n <= 4096 else calls // 4
+            s0 = _gate.stats()
+            t = time.perf_counter()
+            for _ in range(k):
+                f()
+            dt = time.perf_counter() - t
+            s1 = _gate.stats()
+            per = {key: round((s1[key] - s0[key]) / k, 3)
+                   for key in ("native_uploads", "native_ops", "native_materialize", "fallbacks")}
+            sec[name] = {"call_us": round(dt / k * 1e6, 2), "gate_per_call": per}
+        res[label] = sec
+    return res
+
+
+def _small_host_cpu(reps=2000):
+    """NumPy time of the small host calls, as the reference's CPU path runs
+    them (the array copy of cp.array, then the NumPy ufunc / reduction);
+    the reference's Python wrapper around them is not included."""
+    out = {}
+    for label, n in SMALL_HOST_SIZES:
+        g = np.random.default_rng(n)
+        a_np = g.standard_normal(n, dtype=np.float32)
+        b_np = g.standard_normal(n, dtype=np.float32)
+        cases = {"add_get": lambda: np.add(a_np.copy(), b_np.copy()),
+                 "sin_get": lambda: np.sin(a_np.copy()),
+                 "sum_float": lambda: float(np.sum(a_np.copy()))}
+        sec = {}
+        for name, f in cases.items():
+            k = reps if n <= 4096 else reps // 4
+            for _ in range(50):
+                f()
+            t = time.perf_counter()
+            for _ in range(k):
+                f()
+            sec[name] = {"call_us": round((time.perf_counter() - t) / k * 1e6, 2)}
+        out[label] = sec
+    return out
+
+
 # --------------------------------------------------------------- C3
 def bench_c3(cp, be, reps=10):
     from macmetalpy_amd.workloads import c3_matrix, c3_scan_inputs
@@ -251,6 +321,118 @@ def bench_c3(cp, be, reps=10):
             del x
         except Exception as e:
             res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    return res
+
+
+# Copy kernels with the data movement of the contiguous scan (k_scan_rows,
+# scan.hip) and none of its arithmetic: the same 16384-element tile per
+# 256-thread workgroup, all 16-byte loads of the tile issued first, each
+# 4096-element sub-tile redistributed through LDS (padded rows) so that a
+# thread holds 16 consecutive elements, written back through LDS in the
+# output type and stored with 16-byte non-temporal stores, sub-tile by
+# sub-tile.  No in-tile scan, no look-back.  What the tile shape alone
+# allows, beside the scan.
+_SCAN_SHAPE_COPY_SRC = r"""
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int pad16(int i) { return i + i / 16; }
+template <typename Ti, typename To>
+__device__ __forceinline__ void tile_copy(const Ti* __restrict__ x, To* __restrict__ y,
+                                          unsigned char* stage) {
+  constexpr int kSub = 4096, VI = 16 / sizeof(Ti), VO = 16 / sizeof(To);
+  constexpr int NV = kSub / VI / 256, NO = kSub / VO / 256;
+  Ti* sx = (Ti*)stage;
+  To* sy = (To*)stage;
+  const int tid = threadIdx.x;
+  const long long base = (long long)blockIdx.x * 4 * kSub;
+  const u32x4* xv = (const u32x4*)(x + base);
+  u32x4 raw[4][NV];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      raw[q][k] = __builtin_nontemporal_load(xv + q * (kSub / VI) + k * 256 + tid);
+  Ti xin[4][16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q) __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      union { u32x4 v; Ti e[VI]; } u;
+      u.v = raw[q][k];
+#pragma unroll
+      for (int e = 0; e < VI; ++e) sx[pad16((k * 256 + tid) * VI + e)] = u.e[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xin[q][j] = sx[pad16(tid * 16 + j)];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sy[pad16(tid * 16 + j)] = (To)xin[q][j];
+    __syncthreads();
+    u32x4* yv = (u32x4*)(y + base + q * kSub);
+#pragma unroll
+    for (int k = 0; k < NO; ++k) {
+      union { u32x4 v; To e[VO]; } u;
+#pragma unroll
+      for (int e = 0; e < VO; ++e) u.e[e] = sy[pad16((k * 256 + tid) * VO + e)];
+      __builtin_nontemporal_store(u.v, yv + k * 256 + tid);
+    }
+    __syncthreads();
+  }
+}
+extern "C" __global__ __launch_bounds__(256) void tilecopy_f32(const float* x, float* y) {
+  __shared__ __attribute__((aligned(16))) unsigned char stage[8 * 4352];
+  tile_copy<float, float>(x, y, stage);
+}
+extern "C" __global__ __launch_bounds__(256) void tilecopy_i32_i64(const int* x, long long* y) {
+  __shared__ __attribute__((aligned(16))) unsigned char stage[8 * 4352];
+  tile_copy<int, long long>(x, y, stage);
+}
+"""
+
+
+def scan_shape_copy(cp, be, reps=10):
+    """GB/s of the scan-shaped copies at 2^28 elements (float32 -> float32,
+    int32 -> int64), the plain library copy beside them, each output
+    checked against its input."""
+    res = {}
+    for name, dt_in, dt_out, bpe in (("tilecopy_f32", np.float32, np.float32, 8),
+                                     ("tilecopy_i32_i64", np.int32, np.int64, 12)):
+        x_np = (np.arange(N28, dtype=np.int64) % 1000003).astype(dt_in)
+        x = cp.array(x_np)
+        x._ensure_gpu()
+        y = cp.empty(N28, dtype=dt_out)
+        y._ensure_gpu()
+        k = cp.RawKernel(_SCAN_SHAPE_COPY_SRC, name)
+        assert N28 % 16384 == 0
+        k((N28 // 16384 * 256,), (x, y))
+        cp.synchronize()
+        ok = bool(np.array_equal(y.get(), x_np.astype(dt_out)))
+        timer = EventTimer(be)
+        for _ in range(reps):
+            timer.run(name, lambda: k((N28 // 16384 * 256,), (x, y)))
+        cp.synchronize()
+        ms, _ = timer.ms(name)
+        timer.close()
+        res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
+                     "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "copy_exact": ok}
+        del x, y
+    x = cp.array(np.ones(N28, dtype=np.float32))
+    x._ensure_gpu()
+    x.copy()
+    cp.synchronize()
+    timer = EventTimer(be)
+    for _ in range(reps):
+        timer.run("copy", lambda: x.copy())
+    cp.synchronize()
+    ms, _ = timer.ms("copy")
+    timer.close()
+    res["library_copy_f32"] = {"kernel_ms": round(ms, 4), "gbs": round(8 * N28 / ms / 1e6, 1),
+                               "frac_of_peak": round(8 * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
     return res
 
 
@@ -727,6 +909,7 @@ def cpu_baseline(sample_log2=25, reps=10, warm=2):
         (xx.nbytes + rr.nbytes + 4 * xx.shape[0]) / t / 1e9, "GB/s", 1,
         "2048 x 8192 rows of the 8192^2 config, op by op in float32",
         {"ms": round(t * 1e3, 2)})
+    per["small_host_ops"] = _small_host_cpu()
     out["per_config"] = per
     out["host"] = _host_info()
     return out
@@ -896,6 +1079,8 @@ def bench_routines(cp, be, reps=5):
 
 CONFIG_SECTIONS = {
     "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
+    "small_host_ops": bench_small_host_ops,
+    "scan_shape_copy_2p28": scan_shape_copy,
     "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
     "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
     "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,
@@ -940,7 +1125,8 @@ def main():
     kernel_names = {"add_f32": "k_binary<MMP_B_ADD,float>", "sin_f32": "k_unary<MMP_U_SIN,float>",
                     "floor_divide_i32": "k_binary<MMP_B_FLOOR_DIVIDE,int>",
                     "mod_i32": "k_binary<MMP_B_MOD,int>"}
-    traffic = _traffic_table().get(f"{dominant}@2^28")
+    traffic_table = _traffic_table()
+    traffic = traffic_table.get(f"{dominant}@2^28")
     out = {
         "metric": "achieved HBM GB/s (fused elementwise/reduce/cumsum) + matmul TFLOPS, 1xMI355X",
         "value": round(value, 1),
@@ -961,6 +1147,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel_names[dominant], "op": dominant,
                      "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_table.get("_source"),
                      "algorithmic_bytes_per_launch": dom["bytes"],
                      "avg_launch_ms": dom["kernel_ms"]},
         "per_op": per_op,
@@ -979,6 +1166,13 @@ def main():
         t = time.time()
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_log2)
         _log(f"cpu baseline done in {time.time() - t:.1f}s")
+        # the CPU path's time of each small host call beside the device's
+        small = out.get("configs", {}).get("small_host_ops", {})
+        cpu_small = out["cpu_baseline"]["per_config"]["small_host_ops"]
+        for label, sec in small.items() if isinstance(small, dict) else ():
+            for name, d in sec.items() if isinstance(sec, dict) else ():
+                if name in cpu_small.get(label, {}):
+                    d["cpu_path_us"] = cpu_small[label][name]["call_us"]
     out["env"] = _env(be)
     print(json.dumps(out), flush=True)
 

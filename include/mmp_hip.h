@@ -178,7 +178,11 @@ int mmp_memory_stats(size_t *in_use, size_t *cached);
 /* Host<->device copies.  The reference reads unified memory through
  * getBufferPointer (_metal_backend.py:233-236, ndarray.py:576-618); HBM is
  * discrete, so get()/set() become explicit copies.  h2d/d2h are synchronous
- * with respect to the host buffer; d2d is stream-ordered.  mmp_d2h returns
+ * with respect to the host buffer (it may be reused as soon as they return);
+ * d2d is stream-ordered.  mmp_h2d of at most 1 MiB copies the bytes into
+ * page-locked staging memory and queues the transfer on the library stream
+ * without waiting for it (work queued later sees the data); larger copies
+ * wait for the transfer.  mmp_d2h returns
  * MMP_E_WAIT (after completing the copy) when a device-side bounded wait
  * ran out since the last check -- see mmp_wait_status. */
 int mmp_h2d(void *dst, const void *src, size_t bytes);
@@ -274,7 +278,11 @@ int mmp_reduce(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
  * partials: they always fit); strided reductions lower their split count
  * until the partials fit, so a floating sum may round differently from
  * mmp_reduce there.  A layout whose partials still do not fit is rejected
- * with MMP_E_ARG.  Every call on a device shares its array: direct calls,
+ * with MMP_E_ARG.  Each call first zeroes the partial words it will use
+ * with a small kernel on the stream (not a memset, so a capture records a
+ * kernel node): a captured call replays with the tag fixed at capture time,
+ * and the clear keeps the previous replay's partials, which carry the same
+ * tag, from being combined.  Every call on a device shares its array: direct calls,
  * from any host thread, are serialised and run in order on the library
  * stream; work that replays a captured call on another stream must not
  * overlap another use of the array on that device. */

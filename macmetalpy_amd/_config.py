@@ -60,6 +60,7 @@ def set_config(
 ) -> None:
     """Update configuration values (reference: _config.py:43-64)."""
     cfg = get_config()
+    policy = (cfg.float64_behavior, cfg.default_float_dtype)
     if float64_behavior is not None:
         if float64_behavior not in ("downcast", "cpu_fallback"):
             raise ValueError(
@@ -69,6 +70,8 @@ def set_config(
         cfg.warn_on_downcast = bool(warn_on_downcast)
     if default_float_dtype is not None:
         cfg.default_float_dtype = default_float_dtype
+    if (cfg.float64_behavior, cfg.default_float_dtype) != policy:
+        _forget_result_dtypes()
     if fast_math is not None:
         cfg.fast_math = bool(fast_math)
     if fusion is not None:
@@ -77,3 +80,21 @@ def set_config(
         cfg.native_dispatch = bool(native_dispatch)
         from . import _gate
         _gate.apply(cfg.native_dispatch)
+
+
+def _forget_result_dtypes() -> None:
+    """Drop every cached result dtype: they follow float64_behavior and
+    default_float_dtype (float64 results become float32 under "downcast"),
+    so a policy change must resolve them again -- in the Python tables and
+    in the native gate's C tables."""
+    import sys
+    pkg = __name__.rsplit(".", 1)[0]
+    for mod, names in (("_dtypes", ("_UFUNC_CACHE",)),
+                       ("_elementwise", ("_UNARY_DTYPES", "_BINARY_DTYPES")),
+                       ("reductions", ("_OUT_DTYPE_CACHE",))):
+        m = sys.modules.get(f"{pkg}.{mod}")
+        for name in names if m is not None else ():
+            getattr(m, name).clear()
+    native = sys.modules.get(f"{pkg}._native")
+    if native is not None:
+        native.forget_dtypes()

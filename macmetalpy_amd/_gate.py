@@ -31,7 +31,7 @@ except ImportError as exc:  # the product needs it: no silent Python-only mode
 __all__ = ["setup", "apply", "bind_library", "unbind_library", "stats"]
 
 _LIB_FUNCS = ("mmp_alloc", "mmp_free", "mmp_unary", "mmp_binary", "mmp_binary_scalar",
-              "mmp_rtc_launch", "mmp_reduce", "mmp_argreduce", "mmp_d2h")
+              "mmp_rtc_launch", "mmp_reduce", "mmp_argreduce", "mmp_d2h", "mmp_h2d")
 
 
 def _op_names():
@@ -61,6 +61,13 @@ def _reduce_dtype(code: int, dt):
     return _np_out_dtype(kind, dt)
 
 
+def _ensure_device() -> None:
+    """Set up the device (binds the library to the gate), as the Python
+    path's first upload would."""
+    from ._backend import HipBackend
+    HipBackend()
+
+
 def setup() -> None:
     from .ndarray import ndarray
     dtypes = tuple(sorted(_abi.DTYPE_CODES, key=_abi.DTYPE_CODES.get))
@@ -76,6 +83,7 @@ def setup() -> None:
         "check": _check,
         "unary_dtypes": ew._unary_dtypes, "binary_dtypes": ew._binary_dtypes,
         "prune": ew._prune_deps,
+        "ensure_device": _ensure_device,
         "reduce_dtype": _reduce_dtype,
         "config": get_config(),
         "dtypes": dtypes,
@@ -117,5 +125,6 @@ def unbind_library() -> None:
 
 def stats() -> dict:
     """Counters: ops built natively, arrays materialised natively, calls
-    handed to the Python path, generated kernels known to the gate."""
+    handed to the Python path, host-resident operands uploaded by the gate,
+    generated kernels known to the gate."""
     return _native.stats()

@@ -8,10 +8,16 @@
 // device runs every size, so the gate's job is the other half of that
 // contract -- do the common case natively, hand everything else back:
 //
-//  * unary(op, x) / binary(op, a, b): when the operands are device-resident
-//    (or lazy) ndarrays of one shape, or an array and a Python int / float,
-//    build the lazy fusion node and the result array in C (the result
-//    dtype comes from a table the Python path fills on first use);
+//  * unary(op, x) / binary(op, a, b): when the operands are ndarrays whose
+//    shapes broadcast, or an array and a Python int / float, build the lazy
+//    fusion node and the result array in C (the result dtype comes from a
+//    table the Python path fills on first use).  A host-resident operand
+//    (an array made from NumPy data, the case the reference's C gate
+//    answers on the CPU) with C-contiguous data is uploaded here first,
+//    through mmp_h2d's page-locked staging, so small host arrays reach the
+//    same device kernels without a pass through Python;
+//  * reduce(code, x, axis): whole-array or last-axis reductions of a
+//    contiguous array (host-resident ones uploaded the same way);
 //  * materialize(arr): evaluate a lazy array -- one precompiled kernel for
 //    a single op over contiguous operands (mmp_unary / mmp_binary /
 //    mmp_binary_scalar), else the generated fused kernel, looked up by the
@@ -20,13 +26,13 @@
 //  * DeviceBuffer: the owning handle of one device allocation, freed with
 //    mmp_free when the last reference goes.
 //
-// Anything else (broadcasting shapes, host-resident operands, depth or
-// leaf caps, casts of leaves to a new dtype at the root, float16 scalars,
-// unfused mode ...) calls the Python implementation, which stays the single
-// definition of the semantics.  The generated kernel for a structure seen
-// for the first time is compiled by a Python callback from the same DAG,
-// traversed in the same order as here, so leaves, scalars and the
-// parameter block agree.  Library functions are reached through pointers
+// Anything else (shapes that do not broadcast, host data that is not
+// C-contiguous, depth or leaf caps, casts of leaves to a new dtype at the
+// root, float16 scalars, unfused mode ...) calls the Python implementation,
+// which stays the single definition of the semantics.  The generated kernel
+// for a structure seen for the first time is compiled by a Python callback
+// from the same DAG, traversed in the same order as here, so leaves,
+// scalars and the parameter block agree.  Library functions are reached through pointers
 // handed over by the ctypes binding (one loaded copy of libmmp_hip.so).
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -51,6 +57,7 @@ typedef int (*fn_launch_t)(void *, const uint32_t *, const uint32_t *, uint32_t,
 typedef int (*fn_reduce_t)(int, int, int, int64_t, int64_t, int64_t, const void *, void *);
 typedef int (*fn_argreduce_t)(int, int, int64_t, int64_t, int64_t, const void *, int64_t *);
 typedef int (*fn_d2h_t)(void *, const void *, size_t);
+typedef int (*fn_h2d_t)(void *, const void *, size_t);
 
 fn_alloc_t p_alloc = nullptr;
 fn_free_t p_free = nullptr;
@@ -61,6 +68,7 @@ fn_launch_t p_launch = nullptr;
 fn_reduce_t p_reduce = nullptr;
 fn_argreduce_t p_argreduce = nullptr;
 fn_d2h_t p_d2h = nullptr;
+fn_h2d_t p_h2d = nullptr;
 
 // ------------------------------------------------------------ DeviceBuffer
 struct DevBuf {
@@ -132,7 +140,7 @@ PyTypeObject *T_ndarray = nullptr, *T_input = nullptr, *T_cast = nullptr, *T_una
 PyObject *py_unary_fb = nullptr, *py_binary_fb = nullptr, *py_materialize_fb = nullptr,
          *py_run_sum_fb = nullptr, *py_reduce_dt = nullptr;
 PyObject *py_compile_map = nullptr, *py_check = nullptr, *py_unary_dt = nullptr,
-         *py_binary_dt = nullptr, *py_prune = nullptr;
+         *py_binary_dt = nullptr, *py_prune = nullptr, *py_ensure_device = nullptr;
 PyObject *cfg_obj = nullptr;
 constexpr int kNDT = 10;
 PyObject *dtypes[kNDT] = {};
@@ -165,7 +173,7 @@ int8_t bin_rdt[kMaxOps][kNDT][kNDT], bin_odt[kMaxOps][kNDT][kNDT];
 int8_t bsc_rdt[kMaxOps][kNDT][2][2], bsc_odt[kMaxOps][kNDT][2][2];
 
 std::unordered_map<std::string, void *> g_kernels;  // structure key -> kernel handle
-unsigned long long stat_native_ops = 0, stat_native_mat = 0, stat_fallback = 0;
+unsigned long long stat_native_ops = 0, stat_native_mat = 0, stat_fallback = 0, stat_uploads = 0;
 
 // ------------------------------------------------------------ helpers
 inline PyObject *dget(PyObject *descr, PyObject *obj) {  // new reference
@@ -444,6 +452,84 @@ PyObject *new_lazy_array(PyObject *node, PyObject *shape, PyObject *dtype) {
   return arr;
 }
 
+int check_status(int st, const char *what) {
+  if (st == 0) return 0;
+  PyObject *r = PyObject_CallFunction(py_check, "is", st, what);
+  Py_XDECREF(r);
+  if (!PyErr_Occurred()) PyErr_Format(PyExc_RuntimeError, "%s failed (status %d)", what, st);
+  return -1;
+}
+
+PyObject *new_devbuf(long long nbytes) {
+  void *p = nullptr;
+  if (check_status(p_alloc((size_t)(nbytes > 0 ? nbytes : 1), &p), "mmp_alloc")) return nullptr;
+  DevBuf *b = PyObject_New(DevBuf, &DevBufType);
+  if (!b) {
+    p_free(p);
+    return nullptr;
+  }
+  b->ptr = (unsigned long long)(uintptr_t)p;
+  b->nbytes = nbytes;
+  b->owned = 1;
+  b->lazy_dependents = nullptr;
+  b->weakreflist = nullptr;
+  return (PyObject *)b;
+}
+
+// Host-resident ndarray (dict `xd`, `_np_data` set): upload its data into a
+// new device buffer and make the array device-resident in place, as
+// ndarray._ensure_gpu does (reference ndarray.py:352-368, where the first
+// GPU use of an array created from NumPy data copies it into the shared
+// buffer).  The data must be C-contiguous with the array's item size;
+// mmp_h2d stages small copies through page-locked memory and returns
+// without waiting for the device.  1 = uploaded, 0 = not handled here (the
+// Python path uploads), -1 = error.
+int upload_host(PyObject *xd) {
+  PyObject *np = iget(xd, s_np_data), *dtype = iget(xd, s_dtype), *shape = iget(xd, s_shape);
+  if (!np || np == Py_None || !dtype || !shape) return 0;
+  if (!p_h2d) {  // the device is not set up yet: set it up (that binds the library)
+    PyObject *r = PyObject_CallNoArgs(py_ensure_device);
+    if (!r) return -1;
+    Py_DECREF(r);
+    if (!p_h2d) return 0;
+  }
+  const int dt = dtype_index(dtype);
+  long long n = 0;
+  if (dt < 0 || !shape_size(shape, &n)) return 0;
+  Py_buffer view;
+  if (PyObject_GetBuffer(np, &view, PyBUF_C_CONTIGUOUS) != 0) {  // strided data: Python copies
+    PyErr_Clear();
+    return 0;
+  }
+  const long long bytes = n * itemsize[dt];
+  if (view.len != bytes || view.itemsize != itemsize[dt]) {
+    PyBuffer_Release(&view);
+    return 0;
+  }
+  PyObject *buf = new_devbuf(bytes);
+  if (!buf) {
+    PyBuffer_Release(&view);
+    return -1;
+  }
+  const int st =
+      bytes ? p_h2d((void *)(uintptr_t)((DevBuf *)buf)->ptr, view.buf, (size_t)bytes) : 0;
+  PyBuffer_Release(&view);
+  if (check_status(st, "mmp_h2d")) {
+    Py_DECREF(buf);
+    return -1;
+  }
+  PyObject *strides = contig_strides(shape), *zero = PyLong_FromLong(0);
+  const int bad = !strides || !zero || PyDict_SetItem(xd, s_buffer, buf) ||
+                  PyDict_SetItem(xd, s_np_data, Py_None) || PyDict_SetItem(xd, s_strides, strides) ||
+                  PyDict_SetItem(xd, s_offset, zero);
+  Py_XDECREF(strides);
+  Py_XDECREF(zero);
+  Py_DECREF(buf);
+  if (bad) return -1;
+  ++stat_uploads;
+  return 1;
+}
+
 // Operand node of ndarray `x` (dict `xd`) read as dtype index `want`:
 // 1 = ok (*out new ref), 0 = not handled here (fall back), -1 = error.
 int operand_node(PyObject *xd, int want, PyObject **out) {
@@ -463,8 +549,12 @@ int operand_node(PyObject *xd, int want, PyObject **out) {
     Py_INCREF(node);
   } else {
     PyObject *np = iget(xd, s_np_data);
+    if (np && np != Py_None) {
+      const int up = upload_host(xd);
+      if (up <= 0) return up;
+    }
     PyObject *buf = iget(xd, s_buffer);
-    if ((np && np != Py_None) || !buf || buf == Py_None) return 0;  // host data: upload in Python
+    if (!buf || buf == Py_None) return 0;
     PyObject *shape = iget(xd, s_shape), *strides = iget(xd, s_strides), *off = iget(xd, s_offset);
     if (!shape || !strides || !off) return 0;
     node = new_input(buf, shape, dtype, strides, off);
@@ -972,30 +1062,6 @@ void collapse(const std::vector<long long> &shape, std::vector<std::vector<long 
   }
 }
 
-int check_status(int st, const char *what) {
-  if (st == 0) return 0;
-  PyObject *r = PyObject_CallFunction(py_check, "is", st, what);
-  Py_XDECREF(r);
-  if (!PyErr_Occurred()) PyErr_Format(PyExc_RuntimeError, "%s failed (status %d)", what, st);
-  return -1;
-}
-
-PyObject *new_devbuf(long long nbytes) {
-  void *p = nullptr;
-  if (check_status(p_alloc((size_t)(nbytes > 0 ? nbytes : 1), &p), "mmp_alloc")) return nullptr;
-  DevBuf *b = PyObject_New(DevBuf, &DevBufType);
-  if (!b) {
-    p_free(p);
-    return nullptr;
-  }
-  b->ptr = (unsigned long long)(uintptr_t)p;
-  b->nbytes = nbytes;
-  b->owned = 1;
-  b->lazy_dependents = nullptr;
-  b->weakreflist = nullptr;
-  return (PyObject *)b;
-}
-
 bool contig_leaf(PyObject *n, PyObject *shape, int dt) {
   if (Py_TYPE(n) != T_input) return false;
   PyObject *dto = dget(d_dtype, n), *shp = dget(d_shape, n), *str = dget(d_in_strides, n);
@@ -1377,14 +1443,16 @@ PyObject *gate_run_sum(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
 
 // ------------------------------------------------------------ reductions
 // reduce(code, x, axis): sum / prod / max / min / mean (MMP_R_* codes 0-4)
-// or argmax / argmin (5, 6) of a device-resident C-contiguous array over
-// all elements (axis None) or its last axis, straight to mmp_reduce /
-// mmp_argreduce -- the reference's fast_reduce gate (_accelerator.c:
-// 549-858).  Returns None (the caller takes the Python path) for anything
-// else: lazy or host-resident input, other axes, empty reductions.  argmax
+// or argmax / argmin (5, 6) of a C-contiguous array over all elements
+// (axis None) or its last axis, straight to mmp_reduce / mmp_argreduce --
+// the reference's fast_reduce gate (_accelerator.c:549-858).  Host-resident
+// data is uploaded first (upload_host).  Returns None (the caller takes the
+// Python path) for anything else: lazy input, other axes, empty
+// reductions.  argmax
 // / argmin over everything return a Python int, as the Python path does.
 constexpr int kRedCodes = 7;
 int8_t red_odt[kRedCodes][kNDT];
+void clear_dtype_tables();
 
 PyObject *gate_reduce(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
   if (nargs != 3) {
@@ -1398,7 +1466,14 @@ PyObject *gate_reduce(PyObject *, PyObject *const *args, Py_ssize_t nargs) {
     Py_RETURN_NONE;
   }
   PyObject *xd = inst_dict(x);
-  PyObject *node = iget(xd, s_fnode), *np = iget(xd, s_np_data), *buf = iget(xd, s_buffer);
+  PyObject *node = iget(xd, s_fnode), *np = iget(xd, s_np_data);
+  if ((!node || node == Py_None) && np && np != Py_None) {  // host data: upload here
+    const int up = upload_host(xd);
+    if (up < 0) return nullptr;
+    if (up == 0) Py_RETURN_NONE;
+    np = iget(xd, s_np_data);
+  }
+  PyObject *buf = iget(xd, s_buffer);
   PyObject *shape = iget(xd, s_shape), *strides = iget(xd, s_strides), *dto = iget(xd, s_dtype);
   PyObject *off = iget(xd, s_offset);
   if ((node && node != Py_None) || (np && np != Py_None) || !buf || Py_TYPE(buf) != &DevBufType ||
@@ -1525,6 +1600,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   GETCFG(py_unary_dt, "unary_dtypes");
   GETCFG(py_binary_dt, "binary_dtypes");
   GETCFG(py_prune, "prune");
+  GETCFG(py_ensure_device, "ensure_device");
   GETCFG(cfg_obj, "config");
   PyObject *dts;
   GETCFG(dts, "dtypes");
@@ -1560,13 +1636,7 @@ PyObject *gate_init(PyObject *, PyObject *cfg) {
   Py_XDECREF(op_ids);
   op_ids = PyDict_New();
   n_ops = (int)nops;
-  std::memset(un_rdt, -1, sizeof un_rdt);
-  std::memset(un_idt, -1, sizeof un_idt);
-  std::memset(bin_rdt, -1, sizeof bin_rdt);
-  std::memset(bin_odt, -1, sizeof bin_odt);
-  std::memset(bsc_rdt, -1, sizeof bsc_rdt);
-  std::memset(bsc_odt, -1, sizeof bsc_odt);
-  std::memset(red_odt, -1, sizeof red_odt);
+  clear_dtype_tables();
   for (Py_ssize_t i = 0; i < nops; ++i) {
     PyObject *name = PySequence_GetItem(ops, i);
     PyObject *idv = PyLong_FromSsize_t(i);
@@ -1614,6 +1684,7 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
     p_reduce = nullptr;
     p_argreduce = nullptr;
     p_d2h = nullptr;
+    p_h2d = nullptr;
     g_kernels.clear();
     Py_RETURN_NONE;
   }
@@ -1634,13 +1705,32 @@ PyObject *gate_set_library(PyObject *, PyObject *fns) {
   p_reduce = (fn_reduce_t)addr("mmp_reduce");
   p_argreduce = (fn_argreduce_t)addr("mmp_argreduce");
   p_d2h = (fn_d2h_t)addr("mmp_d2h");
+  p_h2d = (fn_h2d_t)addr("mmp_h2d");
   if (PyErr_Occurred()) return nullptr;
   if (!p_alloc || !p_free || !p_unary || !p_binary || !p_binary_scalar || !p_launch ||
-      !p_reduce || !p_argreduce || !p_d2h) {
+      !p_reduce || !p_argreduce || !p_d2h || !p_h2d) {
     p_launch = nullptr;
     PyErr_SetString(PyExc_ValueError, "set_library: missing entry points");
     return nullptr;
   }
+  Py_RETURN_NONE;
+}
+
+// The result-dtype tables follow the float64 policy of the configuration
+// (set_config(float64_behavior=..., default_float_dtype=...)): a policy
+// change empties them, and the Python rules fill them again on first use.
+void clear_dtype_tables() {
+  std::memset(un_rdt, -1, sizeof un_rdt);
+  std::memset(un_idt, -1, sizeof un_idt);
+  std::memset(bin_rdt, -1, sizeof bin_rdt);
+  std::memset(bin_odt, -1, sizeof bin_odt);
+  std::memset(bsc_rdt, -1, sizeof bsc_rdt);
+  std::memset(bsc_odt, -1, sizeof bsc_odt);
+  std::memset(red_odt, -1, sizeof red_odt);
+}
+
+PyObject *gate_forget_dtypes(PyObject *, PyObject *) {
+  clear_dtype_tables();
   Py_RETURN_NONE;
 }
 
@@ -1650,9 +1740,9 @@ PyObject *gate_clear_kernels(PyObject *, PyObject *) {
 }
 
 PyObject *gate_stats(PyObject *, PyObject *) {
-  return Py_BuildValue("{s:K,s:K,s:K,s:n}", "native_ops", stat_native_ops, "native_materialize",
-                       stat_native_mat, "fallbacks", stat_fallback, "kernels",
-                       (Py_ssize_t)g_kernels.size());
+  return Py_BuildValue("{s:K,s:K,s:K,s:K,s:n}", "native_ops", stat_native_ops,
+                       "native_materialize", stat_native_mat, "fallbacks", stat_fallback,
+                       "native_uploads", stat_uploads, "kernels", (Py_ssize_t)g_kernels.size());
 }
 
 PyMethodDef methods[] = {
@@ -1670,6 +1760,8 @@ PyMethodDef methods[] = {
     {"reduce", (PyCFunction)(void (*)(void))gate_reduce, METH_FASTCALL,
      "reduce(code, x, axis): whole-array or last-axis reduction, or None."},
     {"stats", (PyCFunction)gate_stats, METH_NOARGS, "Counters of the native and fallback paths."},
+    {"forget_dtypes", (PyCFunction)gate_forget_dtypes, METH_NOARGS,
+     "Empty the result-dtype tables (after a float64 policy change)."},
     {"clear_kernels", (PyCFunction)gate_clear_kernels, METH_NOARGS,
      "Forget the generated kernels known by structure."},
     {nullptr, nullptr, 0, nullptr}};

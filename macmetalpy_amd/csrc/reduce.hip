@@ -22,6 +22,8 @@
 // (accuracy bar: 1e-5 relative to a float64-accumulated reference); integer
 // sums widen to 64 bits as NumPy does.  HBM-bound: algorithmic bytes =
 // sizeof(T) per input element (+ outputs).
+#include <algorithm>
+
 #include "mmp_ops.h"
 #include "mmp_internal.h"
 
@@ -1117,6 +1119,20 @@ int noalloc_scratch(long long count, long long nticket, ReduceScratch *sc) {
                       kNoAllocTicketBytes / 4);
   sc->tickets = static_cast<unsigned *>(base);
   sc->words = reinterpret_cast<unsigned long long *>(static_cast<char *>(base) + kNoAllocTicketBytes);
+  // Zero the partial words this call uses, on the stream, before its
+  // kernels.  A captured call replays with the tag fixed at capture time;
+  // without the clear the combining workgroup could accept a word of the
+  // previous replay that carries the same tag before this replay's store
+  // lands.  After it, only this launch can write a word with its tag (tags
+  // are never 0).  A kernel rather than hipMemsetAsync, so that a capture
+  // records a kernel node.
+  const long long nwords = (long long)(words_bytes / 8);
+  if (nwords > 0) {
+    const unsigned zblocks = (unsigned)std::min<long long>(256, (nwords + 255) / 256);
+    hipLaunchKernelGGL(k_zero_words, dim3(zblocks), dim3(256), 0, mmpi::stream(), sc->words,
+                       nwords);
+    if (int st = mmpi::check_launch("mmp_reduce_noalloc: partial clear")) return st;
+  }
   sc->timeout = mmpi::wait_flags() + 1;
   sc->tag = mmpi::next_generation();
   const mmpi::WaitParams wp = mmpi::wait_params();

@@ -351,10 +351,83 @@ int mmp_memory_stats(size_t *in_use, size_t *cached) {
   return MMP_OK;
 }
 
+// ---------------------------------------------------- upload staging
+// Host->device copies of up to kStageSeg bytes go through a page-locked
+// ring of kStageSegs segments: the bytes are copied into the ring on the
+// host and the DMA is queued on the stream without a host wait (a copy from
+// pageable memory makes the runtime stage it and block).  The ring leaves a
+// segment by recording an event on the stream; it re-enters that segment
+// only after the event has completed, so a staged source stays intact until
+// the device has read it.  Later work on the stream sees the copied bytes
+// (in-order stream).  For small host arrays this turns each upload from a
+// blocking round trip into a host memcpy plus a queued copy.
+namespace {
+constexpr size_t kStageSeg = 1 << 20;
+constexpr int kStageSegs = 8;
+constexpr size_t kStageAlign = 256;
+std::mutex g_stage_mu;
+char *g_stage = nullptr;  // kStageSegs * kStageSeg page-locked bytes
+hipEvent_t g_stage_ev[kStageSegs] = {};
+bool g_stage_pending[kStageSegs] = {};
+int g_stage_seg = 0;
+size_t g_stage_head = 0;  // bytes used in the current segment
+bool g_stage_off = false;  // set up failed: every copy takes the blocking path
+
+constexpr int kNotStaged = -1;
+
+// kNotStaged: the caller copies directly; else an mmp status.
+int stage_upload(void *dst, const void *src, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_stage_mu);
+  if (g_stage_off) return kNotStaged;
+  if (!g_stage) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, kStageSeg * kStageSegs, hipHostMallocDefault) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      g_stage_off = true;
+      return kNotStaged;
+    }
+    for (int i = 0; i < kStageSegs; ++i) {
+      if (hipEventCreateWithFlags(&g_stage_ev[i], hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        for (int j = 0; j < i; ++j) (void)hipEventDestroy(g_stage_ev[j]);
+        (void)hipHostFree(p);
+        g_stage_off = true;
+        return kNotStaged;
+      }
+    }
+    g_stage = static_cast<char *>(p);
+  }
+  const size_t span = (bytes + kStageAlign - 1) / kStageAlign * kStageAlign;
+  if (g_stage_head + span > kStageSeg) {  // leave the segment, enter the next one
+    if (int st = mmpi::check_hip(hipEventRecord(g_stage_ev[g_stage_seg], g_dev.stream),
+                                 "hipEventRecord(staging)"))
+      return st;
+    g_stage_pending[g_stage_seg] = true;
+    g_stage_seg = (g_stage_seg + 1) % kStageSegs;
+    g_stage_head = 0;
+    if (g_stage_pending[g_stage_seg]) {
+      if (int st = mmpi::check_hip(hipEventSynchronize(g_stage_ev[g_stage_seg]),
+                                   "hipEventSynchronize(staging)"))
+        return st;
+      g_stage_pending[g_stage_seg] = false;
+    }
+  }
+  char *slot = g_stage + (size_t)g_stage_seg * kStageSeg + g_stage_head;
+  std::memcpy(slot, src, bytes);
+  g_stage_head += span;
+  return mmpi::check_hip(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_dev.stream),
+                         "hipMemcpyAsync(H2D, staged)");
+}
+}  // namespace
+
 int mmp_h2d(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
+  if (bytes <= kStageSeg) {
+    const int st = stage_upload(dst, src, bytes);
+    if (st != kNotStaged) return st;
+  }
   if (int st = mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_dev.stream),
                                "hipMemcpyAsync(H2D)"))
     return st;

@@ -22,7 +22,6 @@ import numpy as np
 from .ndarray import ndarray
 
 _rng_gen = np.random.default_rng()
-_rng = np.random.RandomState()
 
 
 def _fnd(x):
@@ -30,9 +29,8 @@ def _fnd(x):
 
 
 def seed(s=None):
-    global _rng_gen, _rng
+    global _rng_gen
     _rng_gen = np.random.default_rng(s)
-    _rng = np.random.RandomState(s)
 
 
 def get_generator():

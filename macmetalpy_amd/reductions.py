@@ -120,10 +120,22 @@ def _reduce(a, kind, axis=None, dtype=None, out=None, keepdims=False):
         odt = a._dtype
     elif dtype is not None:
         odt = a._dtype          # NumPy accumulates in, and returns, the requested dtype
+        if kind in ("mean", "nanmean") and odt.kind in "iu":
+            # NumPy's mean with an integer dtype (numpy/_core/_methods.py
+            # _mean; nanmean of integers is mean): the sum accumulates in
+            # that dtype and wraps, then true_divide by the element count
+            # (float64) is cast back, truncating.  The 64-bit sum cast to
+            # the dtype has the wrapped sum's bits.
+            n_red = _prod(a._shape) if axes is None else _prod(a._shape[i] for i in axes)
+            if n_red and a.size:
+                wide = np.uint64 if odt.kind == "u" else np.int64
+                s = _reduce(a, "sum", axis, wide, None, keepdims).astype(odt)
+                q = (s.astype(np.float64) / float(n_red)).astype(odt)
+                return _finish(q, out)
         if odt.kind in "biu" and (odt.itemsize < 8 or kind in ("mean", "nanmean")):
             # 64-bit accumulation, then the cast: the low bits of an integer
             # sum / product are NumPy's wrapping accumulation in the narrow
-            # type; an integer mean is the float mean truncated, as NumPy's
+            # type; a bool mean is nonzero exactly when some element is
             wide = (np.float64 if kind in ("mean", "nanmean")
                     else np.uint64 if odt.kind in "bu" else np.int64)
             r = _reduce(a, kind, axis, wide, None, keepdims)

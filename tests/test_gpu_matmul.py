@@ -114,15 +114,27 @@ def test_matmul_shape_mismatch_message():
 
 @pytest.mark.parametrize("kind,dtype", [("f32", np.float32), ("f16", np.float16),
                                         ("batched", np.float32)])
-def test_c4_full_size_sampled(kind, dtype):
+def test_c4_full_size_whole(kind, dtype):
+    """The three matmul configurations at full size (float32 4096^2,
+    float16 8192^2, batched float32 64 x 1024^2), every element checked:
+    normwise error against the float64 product of the same inputs, and each
+    element within tol * (|A| @ |B|) of it."""
+    print(f"c4 {kind} full size", flush=True)
     a, b = c4_inputs(kind)
     got = (cp.array(a) @ cp.array(b)).get()
-    assert got.dtype == np.dtype(dtype)
-    rows = np.random.default_rng(3).choice(a.shape[-2], 64, replace=False)
-    if a.ndim == 3:
-        for bi in (0, 31, 63):
-            want = ref.matmul_f64(a[bi][rows], b[bi])
-            assert ref.normwise_rel_error(got[bi][rows], want) <= TOL[dtype]
-    else:
-        want = ref.matmul_f64(a[rows], b)
-        assert ref.normwise_rel_error(got[rows], want) <= TOL[dtype]
+    assert got.dtype == np.dtype(dtype) and got.shape == a.shape[:-1] + b.shape[-1:]
+    _check(a, b, got, dtype)
+
+
+def test_c4_f16_full_size_exact():
+    """The float16 8192^3 shape with operands in {-1, 0, 1}: every sum is an
+    integer of magnitude <= 8192, exact in the fp32 accumulators, so the
+    whole 32 x 32 grid of 256 x 256 tiles (XCD tile remap included) must
+    equal NumPy's float32 product rounded to float16."""
+    print("c4 f16 8192^3 exact", flush=True)
+    g = np.random.default_rng(8192)
+    a = g.integers(-1, 2, (8192, 8192)).astype(np.float16)
+    b = g.integers(-1, 2, (8192, 8192)).astype(np.float16)
+    got = (cp.array(a) @ cp.array(b)).get()
+    want = np.matmul(a.astype(np.float32), b.astype(np.float32)).astype(np.float16)
+    assert got.dtype == np.float16 and np.array_equal(got, want)

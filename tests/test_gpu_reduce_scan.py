@@ -164,6 +164,32 @@ def test_empty_and_errors():
         cp.argmax(e)
 
 
+def test_integer_mean_dtype_wraps_like_numpy():
+    """mean(x, dtype=<int>): NumPy sums in that dtype (wrapping), divides by
+    the count in float64 and truncates back (numpy/_core/_methods.py
+    _mean).  Known answers: 1000 x 100 in int16 sums to 100000 = 34464 mod
+    2^16 = -31072 as int16, / 1000 -> -31; 1000 x 3e6 in int32 sums to
+    3e9 -> -1294967296, / 1000 -> -1294967."""
+    print("integer mean dtypes", flush=True)
+    assert int(cp.mean(cp.array(np.full(1000, 100, np.int16)), dtype=np.int16)) == -31
+    assert int(cp.mean(cp.array(np.full(1000, 3_000_000, np.int32)), dtype=np.int32)) == -1294967
+    g = np.random.default_rng(11)
+    cases = [(g.integers(20000, 32767, (64, 300)).astype(np.int16), np.int16),
+             (g.integers(-2**31, 2**31 - 1, (16, 5000), dtype=np.int64).astype(np.int32), np.int32),
+             (g.integers(0, 65535, (8, 4000)).astype(np.uint16), np.uint16),
+             (g.integers(-2**62, 2**62, (4, 1000), dtype=np.int64), np.int64),
+             (g.integers(0, 2**31, (4, 1000)).astype(np.int32), np.int16)]
+    for x, dt in cases:
+        X = cp.array(x)
+        for axis in (None, 0, 1):
+            want = np.mean(x, axis=axis, dtype=dt)
+            got = cp.mean(X, axis=axis, dtype=dt)
+            assert got.dtype == want.dtype, (dt, axis, got.dtype)
+            assert np.array_equal(np.asarray(got.get()), want), (dt, axis)
+            nwant = np.nanmean(x, axis=axis, dtype=dt)
+            assert np.array_equal(np.asarray(cp.nanmean(X, axis=axis, dtype=dt).get()), nwant)
+
+
 def test_keepdims_and_var_std():
     x = np.random.default_rng(6).standard_normal((40, 50)).astype(np.float32)
     X = cp.array(x)

@@ -128,7 +128,6 @@ def test_gate_hands_back_what_it_does_not_handle(stub):
     g = np.random.default_rng(2)
     a = _dev(stub, g.standard_normal((4, 6)).astype(np.float32))
     row = _dev(stub, g.standard_normal((1, 6)).astype(np.float32))
-    host = cp.array(g.standard_normal((4, 6)).astype(np.float32))  # host-resident
     i16 = _dev(stub, g.integers(-9, 9, (4, 6)).astype(np.int16))
     bad = _dev(stub, g.standard_normal((5, 6)).astype(np.float32))
     before = _gate.stats()["fallbacks"]
@@ -136,11 +135,52 @@ def test_gate_hands_back_what_it_does_not_handle(stub):
         _gate._native.binary("add_op", a, bad)
     with pytest.raises(OverflowError):                        # NumPy's error, from Python
         _gate._native.binary("add_op", i16, 100000)
-    h = _gate._native.binary("mul_op", host, 2.0)             # host data uploads in Python
-    assert h._fusion_node is not None
+    strided = cp.asarray(g.standard_normal((4, 12)).astype(np.float32)[:, ::2])
+    assert strided._np_data is not None and not strided._np_data.flags.c_contiguous
+    h = _gate._native.binary("mul_op", strided, 2.0)          # strided host data: Python copies
+    assert h._fusion_node is not None and strided._np_data is None
     assert _gate._native.binary("add_op", a, np.float32(1)) is not None  # NumPy scalar
     assert _gate._native.binary("pow_op", i16, 2) is not None            # int power check
     assert _gate.stats()["fallbacks"] - before >= 5
+
+
+def test_gate_uploads_host_resident_operands(stub):
+    """Arrays made from NumPy data start host-resident; the gate uploads
+    contiguous data itself (mmp_h2d into a new buffer) and builds the same
+    DAG the Python path builds after its own upload."""
+    g = np.random.default_rng(5)
+    x_np = g.standard_normal(1000).astype(np.float32)
+    y_np = g.standard_normal(1000).astype(np.float32)
+    s0 = _gate.stats()
+    x, y = cp.array(x_np), cp.array(y_np)
+    assert x._np_data is not None and x._buffer is None
+    z = _gate._native.binary("add_op", x, y)
+    s1 = _gate.stats()
+    assert s1["native_uploads"] - s0["native_uploads"] == 2
+    assert s1["native_ops"] - s0["native_ops"] == 1 and s1["fallbacks"] == s0["fallbacks"]
+    for arr, ref in ((x, x_np), (y, y_np)):
+        assert arr._np_data is None and arr._buffer is not None and arr._offset == 0
+        assert arr._strides == (1,)
+        got = np.empty_like(ref)
+        ctypes.memmove(got.ctypes.data, arr._buffer.ptr, ref.nbytes)
+        assert np.array_equal(got, ref)
+    node = z._fusion_node
+    assert node._lhs._buffer is x._buffer and node._rhs._buffer is y._buffer
+    # the Python path over the now device-resident operands builds the same DAG
+    assert _same_dag(node, ew._binary_py("add_op", x, y)._fusion_node)
+    # unary and scalar forms, and a whole-array reduction of host data
+    u = cp.array(x_np.reshape(10, 100))
+    assert _gate._native.unary("sin_op", u)._fusion_node._input._buffer is u._buffer
+    w = cp.array(x_np)
+    assert _gate._native.binary("mul_op", 3.0, w)._fusion_node._rhs._buffer is w._buffer
+    r = cp.array(x_np.reshape(10, 100))
+    stub.stub_reset(0)
+    out = _gate._native.reduce(_abi.REDUCE_SUM, r, -1)
+    assert out is not None and out._shape == (10,) and r._np_data is None
+    call = [stub.stub_call(0, j) for j in range(8)]
+    assert call[:7] == [5, _abi.REDUCE_SUM, _abi.DTYPE_CODES[np.dtype(np.float32)],
+                        _abi.DTYPE_CODES[np.dtype(np.float32)], 10, 100, 1]
+    assert _gate.stats()["native_uploads"] - s0["native_uploads"] == 5
 
 
 def _expected_block(root, out_ptr):
@@ -314,11 +354,16 @@ def test_gate_reductions_call_the_library_directly(stub):
     stub.stub_reset(0)
     assert n.reduce(_abi.REDUCE_ARGMAX, x, None) == 7  # a Python int, read back
     assert stub.stub_ncalls() == 1
-    # handed back: other axes, lazy or host-resident input, non-contiguous views
+    # handed back: other axes, lazy input, non-contiguous views, strided host data
     assert n.reduce(_abi.REDUCE_SUM, x, 0) is None
     assert n.reduce(_abi.REDUCE_SUM, n.unary("neg_op", x), None) is None
-    assert n.reduce(_abi.REDUCE_SUM, cp.array(np.ones(4, np.float32)), None) is None
     assert n.reduce(_abi.REDUCE_SUM, x.transpose(), None) is None
+    assert n.reduce(_abi.REDUCE_SUM, cp.asarray(np.ones((4, 6), np.float32)[:, ::2]), None) is None
+    # contiguous host data is uploaded and reduced here
+    h = cp.array(np.ones(4, np.float32))
+    stub.stub_reset(0)
+    r = n.reduce(_abi.REDUCE_SUM, h, None)
+    assert type(r) is ndarray and h._np_data is None and stub.stub_call(0, 0) == 5
 
 
 def test_gate_leaks_no_references(stub):
@@ -369,3 +414,30 @@ def test_gate_leaks_no_references(stub):
     assert [sys.getrefcount(o) for o in watched] == refs
     assert len(gc.get_objects()) <= nobj + 50
     assert stub.stub_live() == live
+
+
+def test_gate_result_dtypes_follow_the_float64_policy(stub):
+    """The gate's result-dtype tables are filled on first use from the
+    Python rules, which depend on float64_behavior: switching the policy
+    mid-session must re-resolve them (the reference's tests switch to
+    "downcast" per test, and its test_config toggles it at run time)."""
+    import warnings
+    from macmetalpy_amd._config import set_config
+    g = np.random.default_rng(12)
+    i = _dev(stub, g.integers(1, 9, (4, 6)).astype(np.int32))
+    n = _gate._native
+    assert n.binary("div_op", i, i)._dtype == np.dtype(np.float64)
+    assert n.unary("sqrt_op", i)._dtype == np.dtype(np.float64)
+    assert n.binary("div_op", i, 2)._dtype == np.dtype(np.float64)
+    assert cp.mean(i).dtype == np.dtype(np.float64)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", UserWarning)
+        set_config(float64_behavior="downcast")
+        assert n.binary("div_op", i, i)._dtype == np.dtype(np.float32)
+        assert n.unary("sqrt_op", i)._dtype == np.dtype(np.float32)
+        assert n.binary("div_op", i, 2)._dtype == np.dtype(np.float32)
+        assert n.reduce(_abi.REDUCE_MEAN, i, None)._dtype == np.dtype(np.float32)
+        # and back
+        set_config(float64_behavior="cpu_fallback")
+    assert n.binary("div_op", i, i)._dtype == np.dtype(np.float64)
+    assert n.reduce(_abi.REDUCE_MEAN, i, None)._dtype == np.dtype(np.float64)

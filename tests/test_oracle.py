@@ -108,6 +108,31 @@ def test_ulp_distance_helper():
     assert ref.ulp_distance(np.array([-nxt]), np.array([nxt]))[0] == 2 * 0x3F800001
 
 
+@pytest.mark.parametrize("dt,one_bits", [(np.float16, 0x3C00), (np.float64, 0x3FF0000000000000)])
+def test_ulp_distance_helper_float16_float64(dt, one_bits):
+    """The float16 and float64 branches (the comparator of the float16 and
+    float64 GPU tests): adjacent values 1 apart, across zero and across a
+    binade; -0 vs +0 and NaN vs NaN 0; -x vs x twice x's bit pattern."""
+    one = dt(1.0)
+    nxt = np.nextafter(one, dt(2))
+    prv = np.nextafter(one, dt(0))
+    d = ref.ulp_distance
+    assert d(np.array([one], dt), np.array([nxt], dt))[0] == 1
+    assert d(np.array([prv], dt), np.array([nxt], dt))[0] == 2      # across the binade edge
+    tiny = np.nextafter(dt(0), dt(1))
+    assert d(np.array([-tiny], dt), np.array([tiny], dt))[0] == 2   # across zero
+    assert d(np.array([dt(-0.0)], dt), np.array([dt(0.0)], dt))[0] == 0
+    assert d(np.array([dt(np.nan)], dt), np.array([dt(np.nan)], dt))[0] == 0
+    assert d(np.array([-nxt], dt), np.array([nxt], dt))[0] == 2 * (one_bits + 1)
+    assert d(np.array([-one], dt), np.array([one], dt))[0] == 2 * one_bits
+    # symmetric, and counts every representable value in between
+    x = np.array([dt(0.75)], dt)
+    y = x.copy()
+    for _ in range(37):
+        y = np.nextafter(y, dt(2))
+    assert d(x, y)[0] == 37 and d(y, x)[0] == 37
+
+
 # ------------------------------------------------------------ reductions
 def test_sum_closed_forms():
     # tests/test_edge_shapes.py:367-378: sum of 1M ones is 1e6
@@ -321,6 +346,27 @@ def test_nan_reductions_against_python_loops():
         acc += 0.0 if v != v else v
         want.append(acc)
     assert cs.tolist() == want
+    # nanstd: the square root of the (pinned above) Python-loop variance
+    s1 = ref.nan_reduce("nanstd", x[[0, 3]], axis=1, ddof=1)
+    for g, r in zip(s1.tolist(), (rows[0], rows[3])):
+        c = clean(r)
+        m = sum(c) / len(c)
+        assert math.isclose(g, math.sqrt(sum((t - m) ** 2 for t in c) / (len(c) - 1)),
+                            rel_tol=1e-12)
+    s0 = ref.nan_reduce("nanstd", x[[0, 3]], axis=1)
+    for g, r in zip(s0.tolist(), (rows[0], rows[3])):
+        c = clean(r)
+        m = sum(c) / len(c)
+        assert math.isclose(g, math.sqrt(sum((t - m) ** 2 for t in c) / len(c)), rel_tol=1e-12)
+    assert math.isnan(ref.nan_reduce("nanstd", x[1]))                 # all NaN
+    # nancumprod: a running product with NaN taken as 1
+    for r in rows:
+        acc, want = 1.0, []
+        for v in r:
+            acc *= 1.0 if v != v else v
+            want.append(acc)
+        got = ref.nan_reduce("nancumprod", np.array(r, np.float64))
+        np.testing.assert_array_equal(got, want)
 
 
 # -------------------------------------------------------------- sorting

@@ -76,15 +76,18 @@ def test_noalloc_matches_reduce_twice(op, dt, odt, first, second):
 
 
 def test_noalloc_lowered_strided_split_within_tolerance():
-    """(65536, 2048) along axis 0: mmp_reduce splits the column sums into
-    more partials than the static scratch holds, so the no-alloc variant
-    uses fewer (float64 partials either way): float32 results within 1e-5
-    relative of the float64 sums, integer sums bit-exact; then a smaller
-    input."""
+    """Column sums along axis 0.  (65536, 2047) takes the column-per-thread
+    kernel (2047 is not a multiple of 4): 8 column blocks x 128 splits x 256
+    columns x 16 bytes of tagged slots is 4 MiB, more than the static
+    scratch's 4 MiB - 16 KiB of partials, so the no-alloc variant lowers the
+    split count to 127 (float64 partials either way): float32 results
+    within 1e-5 relative of the float64 sums, integer sums bit-exact.
+    (65536, 2048) takes the column-vector kernel (32 splits, 1 MiB: not
+    lowered); then a smaller input."""
     be = HipBackend()
     lib = load_library()
     rng = np.random.default_rng(95)
-    for rows, cols in ((65536, 2048), (8192, 512)):
+    for rows, cols in ((65536, 2047), (65536, 2048), (8192, 512)):
         xf = rng.standard_normal((rows, cols)).astype(np.float32)
         r1, r2, s0, s1 = _both(be, lib, _abi.REDUCE_SUM, xf, np.float32, 1, rows, cols)
         assert s0 == s1
@@ -95,6 +98,25 @@ def test_noalloc_lowered_strided_split_within_tolerance():
         xi = rng.integers(-50, 50, (rows, cols)).astype(np.int32)
         q1, q2, _, _ = _both(be, lib, _abi.REDUCE_SUM, xi, np.int64, 1, rows, cols)
         assert np.array_equal(q1, q2) and np.array_equal(q2, xi.sum(axis=0, dtype=np.int64))
+
+
+def test_noalloc_lowered_split_nanmean():
+    """nanmean along axis 0 of (65536, 3) float32: one column block, 1024
+    splits of (sum, count) pairs (32 bytes of tagged slots per column) need
+    8 MiB, so the no-alloc variant lowers the split count to 510; results
+    within 1e-5 relative of the float64 NaN-skipping means."""
+    be = HipBackend()
+    lib = load_library()
+    rng = np.random.default_rng(96)
+    for rows, cols in ((65536, 3), (4096, 5)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[::89, :] = np.nan
+        r1, r2, s0, s1 = _both(be, lib, _abi.REDUCE_NANMEAN, x, np.float32, 1, rows, cols)
+        assert s0 == s1
+        want = np.nanmean(x.astype(np.float64), axis=0)
+        scale = np.nanmean(np.abs(x).astype(np.float64), axis=0)
+        assert np.all(np.abs(r2 - want) <= 1e-5 * scale), (r2, want)
+        assert np.all(np.abs(r1 - want) <= 1e-5 * scale)
 
 
 def test_noalloc_rejects_bad_arguments():

@@ -330,7 +330,8 @@ def bench_c3(cp, be, reps=10):
 # 4096-element sub-tile redistributed through LDS (padded rows) so that a
 # thread holds 16 consecutive elements, written back through LDS in the
 # output type and stored with 16-byte non-temporal stores, sub-tile by
-# sub-tile.  No in-tile scan, no look-back.  What the tile shape alone
+# sub-tile.  No in-tile scan, no look-back; the LDS stage is sized for the
+# wider of the two types, as the scan's.  What the tile shape alone
 # allows, beside the scan.
 _SCAN_SHAPE_COPY_SRC = r"""
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -384,7 +385,7 @@ __device__ __forceinline__ void tile_copy(const Ti* __restrict__ x, To* __restri
   }
 }
 extern "C" __global__ __launch_bounds__(256) void tilecopy_f32(const float* x, float* y) {
-  __shared__ __attribute__((aligned(16))) unsigned char stage[8 * 4352];
+  __shared__ __attribute__((aligned(16))) unsigned char stage[4 * 4352];
   tile_copy<float, float>(x, y, stage);
 }
 extern "C" __global__ __launch_bounds__(256) void tilecopy_i32_i64(const int* x, long long* y) {
@@ -743,6 +744,72 @@ def bench_indexing(cp, be, reps=5):
 
 
 # --------------------------------------------------------------- C5
+# C5's per-element chain with its loads replaced by register values: the
+# row-sum kernel the fusion engine generates for C5 (same mmp_ops.h
+# functions, float64 accumulator, 4 elements per step, the same grid of
+# 8192 workgroups x 256 threads and 32 elements per thread), but each next
+# element is the previous one plus a constant instead of a load.  Its time
+# is the VALU-bound time of C5's instruction mix; "long" runs 4 times the
+# elements per thread on 2048 workgroups (8 per CU, resident at once: less
+# prologue / epilogue weight) for the sustained element rate.
+_C5_VALU_SRC = r"""
+extern "C" __global__ __launch_bounds__(256) void c5_valu(double* out, int iters, float dx) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  float x[4], r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = -2.0f + (float)((t * 4 + e) & 4095) * (4.0f / 4096.0f);
+    r[e] = 0.5f + 1.5f * (float)((t * 4 + e) & 255) * (1.0f / 256.0f);
+  }
+  const float s0 = 1.0f;
+  double acc = 0;
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t0 = x[e];
+      const float t1 = r[e];
+      const float t2 = op_multiply(t0, t1);
+      const float t4 = op_add(t2, s0);
+      const float t5 = op_tanh(t4);
+      const float t6 = op_abs(t0);
+      const float t7 = op_neg(t6);
+      const float t8 = op_exp_nonpos(t7);
+      const float t9 = op_multiply(t5, t8);
+      const float t10 = op_multiply(t0, t0);
+      const float t11 = op_log1p_nonneg(t10);
+      const float t12 = op_subtract(t9, t11);
+      acc += (double)t12;
+      x[e] = op_add(t0, dx);
+    }
+  }
+  out[t] = acc;
+}
+"""
+
+
+def c5_valu_ceiling(cp, be, reps=10):
+    """ms of the VALU-only C5 loop at C5's grid (8192 x 256 threads, 8
+    steps of 4 elements: 8192^2 elements) and Gelem/s of its long form."""
+    from macmetalpy_amd import _fusion
+    k = cp.RawKernel(_fusion._ops_header() + _C5_VALU_SRC, "c5_valu",
+                     options="-ffp-contract=off -Xclang -target-feature -Xclang -packed-fp32-ops")
+    out = cp.zeros(8192 * 256, dtype=np.float64)
+    out._ensure_gpu()
+    res = {}
+    for name, nwg, iters in (("c5_grid", 8192, 8), ("long", 2048, 32)):
+        k((nwg * 256,), (out, np.int32(iters), np.float32(1e-5)))
+        cp.synchronize()
+        timer = EventTimer(be)
+        for _ in range(reps):
+            timer.run(name, lambda: k((nwg * 256,), (out, np.int32(iters), np.float32(1e-5))))
+        cp.synchronize()
+        ms, _ = timer.ms(name)
+        timer.close()
+        elems = nwg * 256 * iters * 4
+        res[name] = {"ms": round(ms, 4), "gelem_s": round(elems / ms / 1e6, 1)}
+    return res
+
+
 def bench_c5(cp, be, reps=10):
     from macmetalpy_amd.workloads import c5_inputs
     x_np, r_np = c5_inputs()
@@ -783,6 +850,15 @@ def bench_c5(cp, be, reps=10):
                              "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)})
         if "ms" in res.get("unfused", {}):
             res["speedup_vs_unfused"] = round(res["unfused"]["ms"] / ms, 2)
+        # the VALU roof: the same chain with no memory traffic, timed now
+        try:
+            v = c5_valu_ceiling(cp, be)
+            v["c5_elements_gelem_s"] = round(x.size / ms / 1e6, 1)
+            v["valu_roof_frac"] = round(v["c5_grid"]["ms"] / ms, 4)
+            v["valu_roof_frac_sustained"] = round(x.size / ms / 1e6 / v["long"]["gelem_s"], 4)
+            res["valu_roof"] = v
+        except Exception as e:
+            res["valu_roof"] = {"error": f"{type(e).__name__}: {e}"[:300]}
     return res
 
 
@@ -936,7 +1012,7 @@ def _env(be):
 ONLY_OPS = ("add_f32", "sin_f32", "floor_divide_i32", "mod_i32", "copy_f32", "cumsum_i32",
             "cumsum_f32", "matmul_f16", "sort_f32", "c5_fused", "sum_all", "sum_axis1",
             "argmax_all", "argmax_axis1", "sum_axis0", "argmax_axis0", "c1_2p20",
-            "mfma_ceiling")
+            "c1_2p28", "matmul_f32", "matmul_batched", "mfma_ceiling")
 
 
 def run_only(cp, be, name, steps):
@@ -963,8 +1039,12 @@ def run_only(cp, be, name, steps):
     elif name in ("sum_all", "sum_axis1", "argmax_all", "argmax_axis1", "sum_axis0",
                   "argmax_axis0"):
         a = b = cp.array(c3_matrix())
-    elif name == "c1_2p20":
-        a = b = cp.array(c1_inputs(1 << 20))
+    elif name in ("c1_2p20", "c1_2p28"):
+        a = b = cp.array(c1_inputs(1 << 20 if name == "c1_2p20" else N28))
+    elif name == "matmul_f32":
+        a, b = (cp.array(x) for x in c4_inputs("f32"))
+    elif name == "matmul_batched":
+        a, b = (cp.array(x) for x in c4_inputs("batched"))
     else:  # matmul_f16
         a, b = (cp.array(x) for x in c4_inputs("f16"))
     a._ensure_gpu()
@@ -973,6 +1053,7 @@ def run_only(cp, be, name, steps):
           "floor_divide_i32": lambda: cp.floor_divide(a, b), "mod_i32": lambda: cp.mod(a, b),
           "copy_f32": lambda: a.copy(), "cumsum_i32": lambda: cp.cumsum(a),
           "cumsum_f32": lambda: cp.cumsum(a), "matmul_f16": lambda: a @ b,
+          "matmul_f32": lambda: a @ b, "matmul_batched": lambda: a @ b,
           "sort_f32": lambda: cp.sort(a),
           "c5_fused": lambda: cp.sum(cp.tanh(a * b + 1.0) * cp.exp(-cp.abs(a))
                                      - cp.log1p(a * a), axis=1),
@@ -980,7 +1061,8 @@ def run_only(cp, be, name, steps):
           "argmax_all": lambda: cp.argmax(a, axis=None, keepdims=True),
           "argmax_axis1": lambda: cp.argmax(a, axis=1),
           "sum_axis0": lambda: cp.sum(a, axis=0), "argmax_axis0": lambda: cp.argmax(a, axis=0),
-          "c1_2p20": lambda: cp.sqrt(cp.abs(a)) + cp.exp(-a ** 2)}[name]
+          "c1_2p20": lambda: cp.sqrt(cp.abs(a)) + cp.exp(-a ** 2),
+          "c1_2p28": lambda: cp.sqrt(cp.abs(a)) + cp.exp(-a ** 2)}[name]
     timer = EventTimer(be)
     for _ in range(steps):
         timer.run(name, lambda: _mat(fn()))

@@ -50,6 +50,27 @@ _MAX_LEAVES = 24
 _BLOCK = 256
 _UNROLL = 4
 _ELEMS = 4  # consecutive elements per thread per unroll step (vector path)
+
+
+def _map_unroll(kinds) -> int:
+    """Unroll steps of a map kernel's workgroup tile (_BLOCK * _ELEMS
+    elements each).  An expression with a single contiguous leaf and
+    nothing else to read streams best in 1024-element tiles; two or more
+    leaves (or a broadcast one) in 4096-element tiles.  Measured on MI355X
+    at 2^28 elements (GB/s, two runs; tiles of 1024 / 2048 / 4096 / 8192):
+    sqrt(|x|) + exp(-x*x) 6132-6487 / 6331-6400 / 6160-6214 / 5952-6066,
+    x >> 3 (int32) 6355-6388 / 5886-5967 / 6001-6067 / 5431-5511, isnan
+    6526-6581 / 6500-6518 / 6053-6191 / 6010-6074, clip 6373-6506 /
+    6212-6275 / 6005-6033 / 6115-6145; a & b 6190-6203 / 6082-6126 /
+    6354-6393 / 5798-5814, a * b + c 5938-5965 / 5998-6004 / 6100-6143 /
+    5818-5830, X * r with a broadcast row 5951-6035 / 5854-5904 / 6023-6030
+    / 5855-5912.  The native gate applies the same rule (native_gate.cpp,
+    map_tile)."""
+    return 1 if len(kinds) == 1 and kinds[0] == "c" else _UNROLL
+
+
+def _map_tile(kinds) -> int:
+    return _BLOCK * _ELEMS * _map_unroll(kinds)
 # Workgroups of a row-sum launch, split over its rows (a row gets at most
 # one per 4096 elements).  Measured on 2^28 float32 reduced whole:
 # any(a > 3) / count_nonzero 6.7 TB/s at 1024, 5.9-6.0 at 2048, 5.7 at 512;
@@ -468,7 +489,8 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
             L.append("      r = q; }")
         L.append("  }")
     L.append("  const long long cols = p.cols;")
-    tile = _BLOCK * _ELEMS * _UNROLL
+    tile = _map_tile(kinds)
+    unroll = _map_unroll(kinds)
 
     def scalar_load(k, col):
         if kinds[k] == "c":
@@ -486,8 +508,8 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
             L.append(f"  if (c0 + {tile}LL <= cols) {{")
             for k in range(nin):
                 if kinds[k] == "c":
-                    L.append(f"    {vtypes[ct[k]]} l{k}[{_UNROLL}];")
-            L.append(f"    #pragma unroll\n    for (int u = 0; u < {_UNROLL}; ++u) {{")
+                    L.append(f"    {vtypes[ct[k]]} l{k}[{unroll}];")
+            L.append(f"    #pragma unroll\n    for (int u = 0; u < {unroll}; ++u) {{")
             L.append(f"      const long long c = c0 + ((long long)u * {_BLOCK} + threadIdx.x) * {_ELEMS};")
             for k in range(nin):
                 if kinds[k] == "c":
@@ -496,7 +518,7 @@ def generate_source(prog: _Program, kinds, nouter, out_dtype, vec, mode, fast=Fa
             for k in range(nin):
                 if kinds[k] == "b":
                     L.append(f"    const {ct[k]} bc{k} = in{k}[ro{k}];")
-            L.append(f"    #pragma unroll\n    for (int u = 0; u < {_UNROLL}; ++u) {{")
+            L.append(f"    #pragma unroll\n    for (int u = 0; u < {unroll}; ++u) {{")
             L.append(f"      const long long c = c0 + ((long long)u * {_BLOCK} + threadIdx.x) * {_ELEMS};")
             L.append(f"      {vtypes[out_ct]} r;")
             L.append(f"      #pragma unroll\n      for (int e = 0; e < {_ELEMS}; ++e) {{")
@@ -705,7 +727,7 @@ def run_map(root: FusionNode, out_buffer, out_ptr: int) -> None:
     out_dtype = root._dtype
     vec = _vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, out_dtype.itemsize, "map")
     kern = _kernel_for_program(prog, kinds, len(outer), out_dtype, vec, "map")
-    tile = _BLOCK * _ELEMS * _UNROLL
+    tile = _map_tile(kinds)
     colblocks = -(-cols // tile)
     P = _param_struct(len(prog.arrays), len(prog.scalars), len(outer))
     p, rows = _fill_params(prog, P, outer, cols, leaf_str, out_ptr, colblocks, 1.0)

@@ -1099,7 +1099,7 @@ int finish(PyObject *arr, PyObject *arrd, PyObject *buf, PyObject *shape) {
   return bad ? -1 : 0;
 }
 
-constexpr int kBlock = 256, kTile = 256 * 4 * 4;
+constexpr int kBlock = 256;
 
 // Linearised program plus its iteration plan (the Python _Program + _plan).
 struct Plan {
@@ -1110,6 +1110,13 @@ struct Plan {
   long long cols = 1, rows = 1;
   size_t nouter = 0;
 };
+
+// Elements per workgroup of a generated map kernel: 1024 for a single
+// contiguous leaf, else 4096 -- the rule of _fusion._map_unroll, which
+// generates the kernel (its tile must match the launch).
+long long map_tile(const std::string &kinds) {
+  return kinds == "c" ? 256 * 4 * 1 : 256 * 4 * 4;
+}
 
 // 1 = planned, 0 = not handled here (fall back), -1 = error set.
 int make_plan(PyObject *root, PyObject *shape, bool keep_last, Plan *pl) {
@@ -1347,7 +1354,8 @@ PyObject *gate_materialize(PyObject *, PyObject *arr) {
     const bool vec = vec_ok(pl, outp % (4ull * itemsize[odt]) == 0);
     void *kern = kernel_for(pl, node, odt, vec, 'm', fast);
     if (!kern) goto fail;
-    const long long colblocks = (pl.cols + kTile - 1) / kTile;
+    const long long tile = map_tile(pl.kinds);
+    const long long colblocks = (pl.cols + tile - 1) / tile;
     if (launch_plan(pl, kern, outp, colblocks, 1.0)) goto fail;
     result = Py_None;
   }

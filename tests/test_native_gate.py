@@ -189,7 +189,7 @@ def _expected_block(root, out_ptr):
     shape = root._shape
     cshape, outer, cols, leaf_str, kinds = _fusion._plan(prog, shape, keep_last=False)
     vec = _fusion._vec_ok(prog, kinds, leaf_str, outer, cols, out_ptr, root._dtype.itemsize, "map")
-    tile = _fusion._BLOCK * _fusion._ELEMS * _fusion._UNROLL
+    tile = _fusion._map_tile(kinds)
     colblocks = -(-cols // tile)
     P = _fusion._param_struct(len(prog.arrays), len(prog.scalars), len(outer))
     p, rows = _fusion._fill_params(prog, P, outer, cols, leaf_str, out_ptr, colblocks, 1.0)

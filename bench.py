@@ -397,8 +397,8 @@ extern "C" __global__ __launch_bounds__(256) void tilecopy_i32_i64(const int* x,
 
 def scan_shape_copy(cp, be, reps=10):
     """GB/s of the scan-shaped copies at 2^28 elements (float32 -> float32,
-    int32 -> int64), the plain library copy beside them, each output
-    checked against its input."""
+    int32 -> int64), each output checked against its input, with the scan
+    (cumsum) of the same input and the plain library copy beside them."""
     res = {}
     for name, dt_in, dt_out, bpe in (("tilecopy_f32", np.float32, np.float32, 8),
                                      ("tilecopy_i32_i64", np.int32, np.int64, 12)):
@@ -421,7 +421,20 @@ def scan_shape_copy(cp, be, reps=10):
         res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
                      "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4),
                      "copy_exact": ok}
-        del x, y
+        # the scan itself on the same input, same session
+        del y
+        cp.cumsum(x)
+        cp.synchronize()
+        timer = EventTimer(be)
+        for _ in range(reps):
+            timer.run("scan", lambda: cp.cumsum(x))
+        cp.synchronize()
+        ms_scan, _ = timer.ms("scan")
+        timer.close()
+        res[name]["scan_kernel_ms"] = round(ms_scan, 4)
+        res[name]["scan_gbs"] = round(bpe * N28 / ms_scan / 1e6, 1)
+        res[name]["scan_vs_copy"] = round(ms / ms_scan, 4)
+        del x
     x = cp.array(np.ones(N28, dtype=np.float32))
     x._ensure_gpu()
     x.copy()

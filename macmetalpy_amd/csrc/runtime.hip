@@ -16,6 +16,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -362,11 +363,41 @@ int mmp_memory_stats(size_t *in_use, size_t *cached) {
 // (in-order stream).  For small host arrays this turns each upload from a
 // blocking round trip into a host memcpy plus a queued copy.
 namespace {
+// Copies of at most kKernelCopyMax bytes between device memory and the
+// mapped, coherent staging memory below run as a small kernel on the
+// library stream instead of a DMA transfer: a launch on the stream the
+// consuming kernels use costs less than handing the copy to a DMA engine
+// and back.
+constexpr size_t kKernelCopyMax = 64 << 10;
+
+__global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ dst,
+                                                    const unsigned char *__restrict__ src,
+                                                    size_t n) {
+  const size_t i0 = (size_t)blockIdx.x * 256 + threadIdx.x, step = (size_t)gridDim.x * 256;
+  size_t head = 0;
+  if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const size_t nv = n / 16;
+    for (size_t i = i0; i < nv; i += step)
+      reinterpret_cast<u4 *>(dst)[i] = reinterpret_cast<const u4 *>(src)[i];
+    head = nv * 16;
+  }
+  for (size_t i = head + i0; i < n; i += step) dst[i] = src[i];
+}
+
+int launch_copy_small(void *dst, const void *src, size_t n) {
+  const size_t blocks = std::min<size_t>(64, (n + 16 * 256 - 1) / (16 * 256));
+  hipLaunchKernelGGL(k_copy_small, dim3((unsigned)blocks), dim3(256), 0, g_dev.stream,
+                     static_cast<unsigned char *>(dst), static_cast<const unsigned char *>(src), n);
+  return mmpi::check_hip(hipGetLastError(), "small copy launch");
+}
+
 constexpr size_t kStageSeg = 1 << 20;
 constexpr int kStageSegs = 8;
 constexpr size_t kStageAlign = 256;
 std::mutex g_stage_mu;
-char *g_stage = nullptr;  // kStageSegs * kStageSeg page-locked bytes
+char *g_stage = nullptr;      // kStageSegs * kStageSeg page-locked bytes
+char *g_stage_dev = nullptr;  // the same bytes as the device addresses them
 hipEvent_t g_stage_ev[kStageSegs] = {};
 bool g_stage_pending[kStageSegs] = {};
 int g_stage_seg = 0;
@@ -381,7 +412,9 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
   if (g_stage_off) return kNotStaged;
   if (!g_stage) {
     void *p = nullptr;
-    if (hipHostMalloc(&p, kStageSeg * kStageSegs, hipHostMallocDefault) != hipSuccess || !p) {
+    if (hipHostMalloc(&p, kStageSeg * kStageSegs, hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        !p) {
       (void)hipGetLastError();
       g_stage_off = true;
       return kNotStaged;
@@ -395,7 +428,16 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
         return kNotStaged;
       }
     }
+    void *dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess || !dp) {
+      (void)hipGetLastError();
+      for (int j = 0; j < kStageSegs; ++j) (void)hipEventDestroy(g_stage_ev[j]);
+      (void)hipHostFree(p);
+      g_stage_off = true;
+      return kNotStaged;
+    }
     g_stage = static_cast<char *>(p);
+    g_stage_dev = static_cast<char *>(dp);
   }
   const size_t span = (bytes + kStageAlign - 1) / kStageAlign * kStageAlign;
   if (g_stage_head + span > kStageSeg) {  // leave the segment, enter the next one
@@ -412,11 +454,49 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
       g_stage_pending[g_stage_seg] = false;
     }
   }
-  char *slot = g_stage + (size_t)g_stage_seg * kStageSeg + g_stage_head;
+  const size_t at = (size_t)g_stage_seg * kStageSeg + g_stage_head;
+  char *slot = g_stage + at;
   std::memcpy(slot, src, bytes);
   g_stage_head += span;
+  if (bytes <= kKernelCopyMax) return launch_copy_small(dst, g_stage_dev + at, bytes);
   return mmpi::check_hip(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_dev.stream),
                          "hipMemcpyAsync(H2D, staged)");
+}
+
+// Small device -> host copies: a kernel writes the bytes into a mapped,
+// coherent page-locked block, the stream is synchronised, then the host
+// copies them out.
+std::mutex g_back_mu;
+char *g_back = nullptr, *g_back_dev = nullptr;
+bool g_back_off = false;
+
+int small_download(void *dst, const void *src, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_back_mu);
+  if (g_back_off) return kNotStaged;
+  if (!g_back) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, kKernelCopyMax, hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        !p) {
+      (void)hipGetLastError();
+      g_back_off = true;
+      return kNotStaged;
+    }
+    void *dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess || !dp) {
+      (void)hipGetLastError();
+      (void)hipHostFree(p);
+      g_back_off = true;
+      return kNotStaged;
+    }
+    g_back = static_cast<char *>(p);
+    g_back_dev = static_cast<char *>(dp);
+  }
+  if (int st = launch_copy_small(g_back_dev, src, bytes)) return st;
+  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+    return st;
+  std::memcpy(dst, g_back, bytes);
+  return MMP_OK;
 }
 }  // namespace
 
@@ -438,6 +518,11 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
+  if (bytes <= kKernelCopyMax) {
+    const int st = small_download(dst, src, bytes);
+    if (st == MMP_OK) return check_waits();
+    if (st != kNotStaged) return st;
+  }
   if (int st = mmpi::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_dev.stream),
                                "hipMemcpyAsync(D2H)"))
     return st;

@@ -80,6 +80,12 @@ template <typename A> __device__ __forceinline__ A shfl_xor64(A v, int m) {
   return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
 }
 
+template <typename A> __device__ __forceinline__ A shfl64(A v, int src) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  unsigned lo = __shfl((unsigned)u, src, 64), hi = __shfl((unsigned)(u >> 32), src, 64);
+  return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
+}
+
 template <typename A> __device__ __forceinline__ A shfl_up64(A v, int d) {
   unsigned long long u = __builtin_bit_cast(unsigned long long, v);
   unsigned lo = __shfl_up((unsigned)u, d, 64), hi = __shfl_up((unsigned)(u >> 32), d, 64);
@@ -157,21 +163,44 @@ template <typename Ti, typename To> constexpr int scan_look() {
 constexpr int kLookMax = 8;
 constexpr long long kPollsBeforeSum = 256;
 
-// Aggregate of n elements at p by one wave (coalesced, lane-strided).
-template <typename S, typename Ti>
-__device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int n, int lane) {
-  typename S::A acc = S::ident();
-  for (int i = lane; i < n; i += 64) acc = S::comb(acc, S::map(p[i]));
+// Aggregate of a whole tile (Q sub-tiles of kSubTile elements at p) by one
+// wave, combined in exactly the order the tile's own workgroup combines it
+// (k_scan_rows steps 1-2): thread t of wave w sums its 16 consecutive
+// elements from the identity, the wave's inclusive shuffle scan gives lane
+// 63's total, the four wave totals fold left from the identity per
+// sub-tile, the sub-tile totals fold left from the identity.  A floating
+// scan is then bit-identical whether a predecessor's aggregate came from
+// its descriptor or from here.  Lane 63's result is the one used (every
+// lane holds it after the final broadcast).
+template <typename S, int Q, typename Ti>
+__device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int lane) {
+  typedef typename S::A A;
+  A total = S::ident();
+  for (int q = 0; q < Q; ++q) {
+    A qtot = S::ident();
+    for (int w = 0; w < kBlock / 64; ++w) {
+      const Ti *e = p + q * kSubTile + (w * 64 + lane) * kItems;
+      A run = S::ident();
 #pragma unroll
-  for (int m = 32; m > 0; m >>= 1) acc = S::comb(acc, shfl_xor64(acc, m));
-  return acc;
+      for (int j = 0; j < kItems; ++j) run = S::comb(run, S::map(e[j]));
+      A inc = run;
+#pragma unroll
+      for (int dd = 1; dd < 64; dd <<= 1) {
+        const A o = shfl_up64(inc, dd);
+        if (lane >= dd) inc = S::comb(o, inc);
+      }
+      qtot = S::comb(qtot, shfl64(inc, 63));
+    }
+    total = S::comb(total, qtot);
+  }
+  return total;
 }
 
-template <typename S, int kLook, typename Ti>
+template <typename S, int kLook, int Q, typename Ti>
 __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long long t,
                                    typename S::A total, unsigned gen, int lane,
-                                   const Ti *__restrict__ xrow, int tile_len,
-                                   typename S::A *own_val) {
+                                   const Ti *__restrict__ xrow, typename S::A *own_val) {
+  constexpr long long tile_len = (long long)Q * kSubTile;
   typedef typename S::A A;
   A prefix = S::ident();
   unsigned long long *d = sc.desc;
@@ -209,8 +238,7 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
         }
         // the nearest predecessor still missing: sum its input here
         const int b = __ffsll((long long)(bad & nearer)) - 1;
-        const A agg = wave_aggregate<S>(xrow + (top - b - first) * (long long)tile_len, tile_len,
-                                        lane);
+        const A agg = wave_aggregate<S, Q>(xrow + (top - b - first) * tile_len, lane);
         if (lane == b) own_val[b] = agg;
         own |= 1ull << b;
         continue;
@@ -372,8 +400,8 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
     if constexpr (MODE == 2) {
       if (tid == 0) s_prefix = t > 0 ? tail_prefix<S>(sc, tile - 1, gen) : S::ident();
     } else if (wave == 0) {
-      const A prefix = look_back<S, scan_look<Ti, To>()>(sc, tile, t, total, gen, lane,
-                                                         x + row * len, kTile, s_own);
+      const A prefix = look_back<S, scan_look<Ti, To>(), Q>(sc, tile, t, total, gen, lane,
+                                                            x + row * len, s_own);
       if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();

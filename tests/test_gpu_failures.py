@@ -62,7 +62,9 @@ def test_forced_reduction_wait_timeout_raises_on_get(be):
 def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
     """A scan whose tiles find no predecessor's descriptor (every reader
     expects a tag no writer produces) sums each missing predecessor's input
-    itself: the result is exact and no wait is reported."""
+    itself: the result is exact and no wait is reported.  The fallback
+    combines a predecessor's elements in the order that tile's own
+    workgroup does, so a float scan is bit-identical to the normal run."""
     g = np.random.default_rng(42)
     x_np = g.integers(-100, 100, n, dtype=np.int32)
     x = cp.array(x_np)
@@ -81,7 +83,19 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
     cf = cp.cumsum(f)
     if n % 16384 == 0:
         ref = np.cumsum(f_np, dtype=np.float64)
-        assert np.all(np.abs(cf.get() - ref) <= 1e-5 * ref + 1e-6)
+        got = cf.get()
+        assert np.all(np.abs(got - ref) <= 1e-5 * ref + 1e-6)
+        assert np.array_equal(got, cp.cumsum(f).get())  # bit for bit
+        assert be.wait_status() == 0
+        d_np = g.random(n)                              # float64: 8192-element tiles
+        d = cp.array(d_np)
+        want = cp.cumsum(d).get()
+        be.debug_fail_next(4, 1)
+        assert np.array_equal(cp.cumsum(d).get(), want)
+        h = cp.array((g.random(n) + 0.5).astype(np.float32))
+        want = cp.cumprod(h[:16384 * 3]).get()        # products: the same order
+        be.debug_fail_next(4, 1)
+        assert np.array_equal(cp.cumprod(h[:16384 * 3]).get(), want)
     else:
         with pytest.raises(HipWaitTimeoutError, match="scan"):
             cf.get()

@@ -368,7 +368,7 @@ namespace {
 // library stream instead of a DMA transfer: a launch on the stream the
 // consuming kernels use costs less than handing the copy to a DMA engine
 // and back.
-constexpr size_t kKernelCopyMax = 64 << 10;
+constexpr size_t kKernelCopyMax = 1 << 20;
 
 __global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ dst,
                                                     const unsigned char *__restrict__ src,
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ 
 }
 
 int launch_copy_small(void *dst, const void *src, size_t n) {
-  const size_t blocks = std::min<size_t>(64, (n + 16 * 256 - 1) / (16 * 256));
+  const size_t blocks = std::min<size_t>(256, (n + 16 * 256 - 1) / (16 * 256));
   hipLaunchKernelGGL(k_copy_small, dim3((unsigned)blocks), dim3(256), 0, g_dev.stream,
                      static_cast<unsigned char *>(dst), static_cast<const unsigned char *>(src), n);
   return mmpi::check_hip(hipGetLastError(), "small copy launch");

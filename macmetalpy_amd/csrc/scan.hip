@@ -154,6 +154,12 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 // itself (64 KiB for a float32 tile, a few microseconds), and goes on.
 // Forward progress needs no other workgroup, and no atomic ticket is
 // drawn (a same-address ticket per workgroup cost 6 % of the float32 scan).
+// Integer prefixes are exact.  A floating prefix is the nearest inclusive
+// prefix combined with the aggregates after it, so which predecessor had
+// published its inclusive prefix decides the association of those float64
+// additions: the last bit of the accumulator can differ between runs
+// (float32 outputs rounded from it almost never do); every form is within
+// the accumulator's error bound.
 // Window per type, measured at 2^28 elements with the ticket-free look-back:
 // int32 -> int64 (8-byte outputs) 4 (6.0 TB/s; 8: 5.9, 16: 5.8), float32 8
 // (5.6; 4: 5.1, 16: 5.6).
@@ -176,12 +182,14 @@ template <typename S, int Q, typename Ti>
 __device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int lane) {
   typedef typename S::A A;
   A total = S::ident();
+#pragma unroll 1
   for (int q = 0; q < Q; ++q) {
     A qtot = S::ident();
+#pragma unroll 1
     for (int w = 0; w < kBlock / 64; ++w) {
       const Ti *e = p + q * kSubTile + (w * 64 + lane) * kItems;
       A run = S::ident();
-#pragma unroll
+#pragma unroll 1
       for (int j = 0; j < kItems; ++j) run = S::comb(run, S::map(e[j]));
       A inc = run;
 #pragma unroll

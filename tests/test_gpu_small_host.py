@@ -104,3 +104,88 @@ def test_uploads_of_changing_host_data_and_sizes():
     for i in range(5):
         d.set(np.full(1000, i, np.float32))
     assert np.array_equal((d + 0.0).get(), np.full(1000, 4, np.float32))
+
+
+_HOST_DTYPES = [np.bool_, np.int16, np.uint16, np.int32, np.uint32, np.int64, np.float16,
+                np.float32, np.float64]
+_UNARY = ["negative", "absolute", "sqrt", "exp", "sin", "floor", "square"]
+_BINARY = ["add", "subtract", "multiply", "maximum", "less", "floor_divide"]
+_REDUCE = ["sum", "max", "argmax", "mean"]
+
+
+def _host_values(rng, shape, dtype):
+    dt = np.dtype(dtype)
+    if dt == np.bool_:
+        return rng.random(shape) < 0.5
+    if dt.kind in "iu":
+        lo = -50 if dt.kind == "i" else 1
+        return rng.integers(lo, 50, shape).astype(dt)
+    return rng.standard_normal(shape).astype(dt)
+
+
+def _same(got, want, dtype):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    if np.dtype(dtype).kind == "f" and want.dtype.kind == "f":
+        if want.dtype == np.float16:
+            assert int(ref.ulp_distance(got.astype(np.float16), want).max(initial=0)) <= 2
+        else:
+            assert np.allclose(got, want, rtol=1e-5, atol=1e-6, equal_nan=True)
+    else:
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_calls_on_fresh_host_arrays(seed):
+    """Random unary / binary / reduction calls whose operands are arrays made
+    from NumPy data in the call (0-d to 3-D, broadcasting pairs, strided
+    host views that the gate hands to the Python path) match NumPy; every
+    contiguous operand is uploaded by the gate."""
+    print(f"fresh host arrays seed={seed}", flush=True)
+    rng = np.random.default_rng(1000 + seed)
+    shapes = [(), (1,), (7,), (3, 5), (2, 3, 4), (1000,)]
+    for _ in range(12):
+        dt = _HOST_DTYPES[rng.integers(len(_HOST_DTYPES))]
+        shape = shapes[rng.integers(len(shapes))]
+        x_np = _host_values(rng, shape, dt)
+        strided = len(shape) >= 1 and shape[-1] > 1 and rng.random() < 0.2
+        src = np.repeat(x_np, 2, axis=-1)[..., ::2] if strided else x_np
+        kind = rng.integers(3)
+        s0 = _gate.stats()["native_uploads"]
+        if kind == 0:
+            op = _UNARY[rng.integers(len(_UNARY))]
+            if dt == np.bool_ and op != "absolute":
+                continue
+            with np.errstate(all="ignore"):
+                want = getattr(np, op)(x_np)
+            got = getattr(cp, op)(cp.asarray(src)).get()
+            _same(got, want, want.dtype)
+            ups = 0 if strided else 1
+        elif kind == 1:
+            op = _BINARY[rng.integers(len(_BINARY))]
+            if dt == np.bool_ and op in ("subtract", "floor_divide"):
+                continue
+            other_shape = shape[-1:] if len(shape) >= 1 and rng.random() < 0.5 else shape
+            y_np = _host_values(rng, other_shape, dt)
+            if op == "floor_divide" and np.dtype(dt).kind in "iu":
+                y_np = np.where(y_np == 0, 1, y_np).astype(dt)
+            with np.errstate(all="ignore"):
+                want = getattr(np, op)(x_np, y_np)
+            got = getattr(cp, op)(cp.asarray(src), cp.array(y_np)).get()
+            _same(got, want, want.dtype)
+            ups = 0 if strided else 2
+        else:
+            op = _REDUCE[rng.integers(len(_REDUCE))]
+            axis = None if len(shape) == 0 or rng.random() < 0.5 else -1
+            if op == "mean" and dt == np.float16:
+                continue
+            if op == "sum" and np.dtype(dt).kind == "f":
+                # float sums accumulate in float64 and round once
+                want = np.sum(x_np.astype(np.float64), axis=axis).astype(dt)
+            else:
+                want = getattr(np, op)(x_np, axis=axis)
+            got = getattr(cp, op)(cp.asarray(src), axis=axis)
+            got = got.get() if hasattr(got, "get") else got
+            _same(got, want, np.asarray(want).dtype)
+            ups = 0 if strided else 1
+        assert _gate.stats()["native_uploads"] - s0 >= ups, (kind, op, dt, shape, strided)

@@ -130,6 +130,23 @@ def _mat(r):
     return r
 
 
+def _launch_ms(cp, be, f, reps):
+    """Mean device time per call over ``reps`` back-to-back calls between
+    one pair of events on the library stream: the queue stays ahead of the
+    host, so neither the per-call event overhead (a few microseconds) nor
+    host gaps enter a kernel's time."""
+    s, e = be.event(), be.event()
+    be.record(s)
+    for _ in range(reps):
+        f()
+    be.record(e)
+    cp.synchronize()
+    ms = be.elapsed_ms(s, e) / reps
+    be.destroy_event(s)
+    be.destroy_event(e)
+    return ms
+
+
 # --------------------------------------------------------------- C1
 def _call_us(cp, f, n_calls):
     """Host-inclusive time per call: ``n_calls`` back-to-back calls (each
@@ -142,11 +159,11 @@ def _call_us(cp, f, n_calls):
 
 
 def bench_c1(cp, be, reps=50):
-    """C1 y = sqrt(abs(x)) + exp(-x**2): ``kernel_ms`` is the event time per
-    call (at 2^20 it includes the host gaps between launches: the device
-    waits for the host), ``call_us`` the host-inclusive time per call of
-    back-to-back calls; both count the whole call (6 lazy ops, one fused
-    kernel)."""
+    """C1 y = sqrt(abs(x)) + exp(-x**2): ``kernel_ms`` is the device time per
+    call over back-to-back calls between one event pair (at 2^20 the device
+    waits for the host between launches, so it is the host's call rate),
+    ``call_us`` the host-inclusive time per call of back-to-back calls; both
+    count the whole call (6 lazy ops, one fused kernel)."""
     from macmetalpy_amd.workloads import c1_inputs
     res = {}
     for label, n in (("2^20", 1 << 20), ("2^28", N28)):
@@ -156,12 +173,7 @@ def bench_c1(cp, be, reps=50):
         for _ in range(3):
             f()
         cp.synchronize()
-        timer = EventTimer(be)
-        for _ in range(reps if n < N28 else 10):
-            timer.run("c1", f)
-        cp.synchronize()
-        ms, _ = timer.ms("c1")
-        timer.close()
+        ms = _launch_ms(cp, be, f, reps if n < N28 else 10)
         res[label] = {"kernel_ms": round(ms, 4), "gbs": round(8 * n / ms / 1e6, 1),
                       "frac_of_peak": round(8 * n / ms / 1e6 / HBM_PEAK_GBS, 4)}
         if n < N28:
@@ -291,12 +303,7 @@ def bench_c3(cp, be, reps=10):
         try:
             f()
             cp.synchronize()
-            timer = EventTimer(be)
-            for _ in range(reps):
-                timer.run(name, f)
-            cp.synchronize()
-            ms, _ = timer.ms(name)
-            timer.close()
+            ms = _launch_ms(cp, be, f, reps)
             res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nb / ms / 1e6, 1),
                          "frac_of_peak": round(nb / ms / 1e6 / HBM_PEAK_GBS, 4)}
         except Exception as e:  # report, keep going
@@ -310,12 +317,7 @@ def bench_c3(cp, be, reps=10):
             f = lambda: cp.cumsum(x)  # noqa: E731
             f()
             cp.synchronize()
-            timer = EventTimer(be)
-            for _ in range(reps):
-                timer.run(name, f)
-            cp.synchronize()
-            ms, _ = timer.ms(name)
-            timer.close()
+            ms = _launch_ms(cp, be, f, reps)
             res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
                          "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
             del x
@@ -412,12 +414,7 @@ def scan_shape_copy(cp, be, reps=10):
         k((N28 // 16384 * 256,), (x, y))
         cp.synchronize()
         ok = bool(np.array_equal(y.get(), x_np.astype(dt_out)))
-        timer = EventTimer(be)
-        for _ in range(reps):
-            timer.run(name, lambda: k((N28 // 16384 * 256,), (x, y)))
-        cp.synchronize()
-        ms, _ = timer.ms(name)
-        timer.close()
+        ms = _launch_ms(cp, be, lambda: k((N28 // 16384 * 256,), (x, y)), reps)
         res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
                      "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4),
                      "copy_exact": ok}
@@ -425,12 +422,7 @@ def scan_shape_copy(cp, be, reps=10):
         del y
         cp.cumsum(x)
         cp.synchronize()
-        timer = EventTimer(be)
-        for _ in range(reps):
-            timer.run("scan", lambda: cp.cumsum(x))
-        cp.synchronize()
-        ms_scan, _ = timer.ms("scan")
-        timer.close()
+        ms_scan = _launch_ms(cp, be, lambda: cp.cumsum(x), reps)
         res[name]["scan_kernel_ms"] = round(ms_scan, 4)
         res[name]["scan_gbs"] = round(bpe * N28 / ms_scan / 1e6, 1)
         res[name]["scan_vs_copy"] = round(ms / ms_scan, 4)
@@ -439,12 +431,7 @@ def scan_shape_copy(cp, be, reps=10):
     x._ensure_gpu()
     x.copy()
     cp.synchronize()
-    timer = EventTimer(be)
-    for _ in range(reps):
-        timer.run("copy", lambda: x.copy())
-    cp.synchronize()
-    ms, _ = timer.ms("copy")
-    timer.close()
+    ms = _launch_ms(cp, be, lambda: x.copy(), reps)
     res["library_copy_f32"] = {"kernel_ms": round(ms, 4), "gbs": round(8 * N28 / ms / 1e6, 1),
                                "frac_of_peak": round(8 * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
     return res
@@ -591,12 +578,7 @@ def bench_logic(cp, be, reps=10):
         try:
             f()
             cp.synchronize()
-            timer = EventTimer(be)
-            for _ in range(reps):
-                timer.run(name, f)
-            cp.synchronize()
-            ms, _ = timer.ms(name)
-            timer.close()
+            ms = _launch_ms(cp, be, f, reps)
             res[name] = {"kernel_ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1),
                          "frac_of_peak": round(bpe * N28 / ms / 1e6 / HBM_PEAK_GBS, 4)}
         except Exception as e:
@@ -625,12 +607,7 @@ def bench_nan(cp, be, reps=10):
         try:
             f()
             cp.synchronize()
-            timer = EventTimer(be)
-            for _ in range(reps):
-                timer.run(name, f)
-            cp.synchronize()
-            ms, _ = timer.ms(name)
-            timer.close()
+            ms = _launch_ms(cp, be, f, reps)
             res[name] = {"kernel_ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1),
                          "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
         except Exception as e:
@@ -840,14 +817,9 @@ def bench_c5(cp, be, reps=10):
             cp.set_config(fusion=(mode != "unfused"), fast_math=(mode == "fused_fast_math"))
             chain()
             cp.synchronize()
-            timer = EventTimer(be)
             t = time.perf_counter()
-            for _ in range(reps):
-                timer.run(mode, chain)
-            cp.synchronize()
+            ms = _launch_ms(cp, be, chain, reps)
             wall = (time.perf_counter() - t) / reps * 1e3
-            ms, _ = timer.ms(mode)
-            timer.close()
             res[mode] = {"ms": round(ms, 4), "wall_ms": round(wall, 4)}
         except Exception as e:
             res[mode] = {"error": f"{type(e).__name__}: {e}"[:300]}

@@ -134,8 +134,11 @@ def _launch_ms(cp, be, f, reps):
     """Mean device time per call over ``reps`` back-to-back calls between
     one pair of events on the library stream: the queue stays ahead of the
     host, so neither the per-call event overhead (a few microseconds) nor
-    host gaps enter a kernel's time."""
+    host gaps enter a kernel's time.  One untimed call is queued ahead of
+    the start event, so the device is busy when the window opens (else the
+    window would begin with the host's time to issue the first call)."""
     s, e = be.event(), be.event()
+    f()
     be.record(s)
     for _ in range(reps):
         f()

@@ -385,6 +385,18 @@ __global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ 
   for (size_t i = head + i0; i < n; i += step) dst[i] = src[i];
 }
 
+// The copy kernels address device memory directly; a pointer the runtime
+// does not know as device memory (host memory handed to mmp_h2d / mmp_d2h,
+// which DMA copies accept) takes the DMA path instead.
+bool is_device_memory(const void *p) {
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return a.type == hipMemoryTypeDevice;
+}
+
 int launch_copy_small(void *dst, const void *src, size_t n) {
   const size_t blocks = std::min<size_t>(256, (n + 16 * 256 - 1) / (16 * 256));
   hipLaunchKernelGGL(k_copy_small, dim3((unsigned)blocks), dim3(256), 0, g_dev.stream,
@@ -504,7 +516,7 @@ int mmp_h2d(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
-  if (bytes <= kStageSeg) {
+  if (bytes <= kStageSeg && is_device_memory(dst)) {
     const int st = stage_upload(dst, src, bytes);
     if (st != kNotStaged) return st;
   }
@@ -518,7 +530,7 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
-  if (bytes <= kKernelCopyMax) {
+  if (bytes <= kKernelCopyMax && is_device_memory(src)) {
     const int st = small_download(dst, src, bytes);
     if (st == MMP_OK) return check_waits();
     if (st != kNotStaged) return st;

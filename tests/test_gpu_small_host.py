@@ -189,3 +189,24 @@ def test_random_calls_on_fresh_host_arrays(seed):
             _same(got, want, np.asarray(want).dtype)
             ups = 0 if strided else 1
         assert _gate.stats()["native_uploads"] - s0 >= ups, (kind, op, dt, shape, strided)
+
+
+def test_small_copies_with_host_memory_pointers():
+    """mmp_h2d / mmp_d2h accept page-locked host memory on the device side
+    of the copy as DMA copies do: a pointer the runtime does not know as
+    device memory takes the DMA path, not the copy kernel."""
+    import ctypes
+    from macmetalpy_amd._backend import HipBackend, load_library
+    print("small copies with host memory pointers", flush=True)
+    HipBackend()
+    lib = load_library()
+    p = ctypes.c_void_p()
+    assert lib.mmp_host_alloc(4096, ctypes.byref(p)) == 0
+    try:
+        src = np.arange(1024, dtype=np.int32)
+        assert lib.mmp_h2d(p.value, src.ctypes.data, src.nbytes) == 0   # "device" side is host memory
+        got = np.empty(1024, np.int32)
+        assert lib.mmp_d2h(got.ctypes.data, p.value, got.nbytes) == 0
+        assert np.array_equal(got, src)
+    finally:
+        assert lib.mmp_host_free(p.value) == 0

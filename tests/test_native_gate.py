@@ -369,7 +369,8 @@ def test_gate_reductions_call_the_library_directly(stub):
 def test_gate_leaks_no_references(stub):
     """Thousands of gate calls (elementwise ops with arrays and Python
     scalars, materialisation through the precompiled and the generated
-    paths, reductions, calls handed back to Python, errors) leave the
+    paths, reductions, host-resident operands uploaded by the gate, calls
+    handed back to Python, errors) leave the
     reference counts of the shared objects they touch, the number of live
     Python objects and the stub's live allocations where they were."""
     import gc
@@ -394,13 +395,16 @@ def test_gate_leaks_no_references(stub):
         n.run_sum(d._fusion_node, True, f32, x._ptr, False)
         r = n.reduce(_abi.REDUCE_SUM, x, None)
         r2 = n.reduce(_abi.REDUCE_MAX, i, -1)
-        h = n.binary("add_op", x, cp.array(np.ones((8, 16), np.float32)))  # handed back
+        h = n.binary("add_op", x, cp.array(np.ones((8, 16), np.float32)))  # host: uploaded here
+        hu = n.unary("sin_op", cp.array(np.ones(16, np.float32)))
+        hr = n.reduce(_abi.REDUCE_SUM, cp.array(np.ones((8, 16), np.float32)), -1)
+        hs = n.binary("mul_op", cp.asarray(np.ones((8, 32), np.float32)[:, ::2]), 2.0)  # handed back
         assert n.reduce(_abi.REDUCE_SUM, x, 0) is None
         try:
             n.binary("add_op", x, _dev(stub, np.ones((3, 5), np.float32)))
         except ValueError:
             pass
-        return a, b, c, r, r2, h
+        return a, b, c, r, r2, h, hu, hr, hs
 
     for _ in range(20):  # warm the caches, result-dtype tables and kernel table
         work()

@@ -519,6 +519,112 @@ def mfma_ceiling(cp, be, iters=16000, reps=3):
     return res
 
 
+# The register-only float16 MFMA loop with the large GEMM's other traffic
+# added beside it at the GEMM's ratios, nothing waiting on that traffic: per
+# 16 MFMAs (262,144 flops) a wave reads READS x 1 KiB of LDS (ds_read_b128;
+# k_gemm16_dma reads 192 KiB per 8.4 MFLOP slab, 6 KiB per 16 MFMAs) and
+# issues DMAS x 1 KiB of global -> LDS copies (global_load_lds_dwordx4 from a
+# 2 MiB L2-resident buffer; the GEMM copies 64 KiB per slab, 2 KiB per 16
+# MFMAs).  Each wave reads the shader clock counter (s_memtime) and the
+# 100 MHz constant clock (s_memrealtime) around its loop, so the engine
+# clock under each load comes out beside the rate.
+_MFMA_LOAD_SRC = r"""
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+__device__ inline h8 operand(unsigned s) {
+  u4 u;
+  u.x = s * 2654435761u; u.y = u.x * 2246822519u + 7u;
+  u.z = u.y * 3266489917u + 11u; u.w = u.z * 668265263u + 13u;
+  u &= 0xbfffbfffu;  // clear each half's top exponent bit: finite values
+  return __builtin_bit_cast(h8, u);
+}
+extern "C" __global__ __launch_bounds__(256) void NAME(const unsigned char* g, float* out,
+                                                      unsigned long long* clk, int iters,
+                                                      unsigned seed) {
+  constexpr int R = READS, D = DMAS;
+  constexpr unsigned LDS = 32768u, GB = 2u << 20;
+  __shared__ __attribute__((aligned(16))) unsigned char s[LDS];
+  const unsigned t = blockIdx.x * 256 + threadIdx.x, lane = threadIdx.x & 63,
+                 wave = threadIdx.x >> 6;
+  for (unsigned i = threadIdx.x * 16; i < LDS; i += 4096) *(u4*)(s + i) = *(const u4*)(g + i);
+  h8 a[4], b[4];
+  for (int i = 0; i < 4; ++i) { a[i] = operand(seed + t * 8 + i); b[i] = operand(seed ^ (t * 8 + i + 4)); }
+  f4 c[8];
+  for (int i = 0; i < 8; ++i) c[i] = f4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      u4 v[R > 0 ? R : 1];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        v[r] = *(const u4*)(s + ((unsigned)(p * 8192 + r * 1024) + wave * 4096u + lane * 16u) % LDS);
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const unsigned go = (blockIdx.x * 131072u + wave * 32768u + (unsigned)(it + p) * 2048u +
+                             (unsigned)d * 1024u + lane * 16u) % GB;
+        __builtin_amdgcn_global_load_lds(g + go, (__attribute__((address_space(3))) void*)(
+            s + (wave * 8192u + (unsigned)d * 1024u) % LDS), 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        c[i & 7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i & 3], b[((i >> 2) + p) & 3], c[i & 7], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < R; ++r) asm volatile("" :: "v"(v[r]));
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  __syncthreads();  // no copy into LDS in flight when the workgroup ends
+  float sum = 0.f;
+  for (int i = 0; i < 8; ++i) sum += c[i].x + c[i].y + c[i].z + c[i].w;
+  out[t] = sum;
+  if (lane == 0) { clk[(t >> 6) * 2] = t1 - t0; clk[(t >> 6) * 2 + 1] = r1 - r0; }
+}
+"""
+MFMA_LOAD_MIXES = {"mfma": (0, 0), "mfma_lds": (6, 0), "mfma_dma": (0, 2), "mfma_lds_dma": (6, 2)}
+
+
+def mfma_clock_under_load(cp, be, iters=4096, reps=3):
+    """TFLOP/s and the engine clock of the register-only float16 MFMA loop
+    alone and with the large GEMM's LDS reads and global -> LDS copies
+    issued beside it at the GEMM's bytes per flop (2048 workgroups of four
+    waves; best of ``reps`` after one warm-up)."""
+    nwg = 2048
+    g = cp.array(np.random.default_rng(5).integers(0, 2 ** 16, (2 << 20) // 2, dtype=np.uint16)
+                 & np.uint16(0xbfff))
+    out = cp.zeros(nwg * 256, dtype=np.float32)
+    clk = cp.zeros(nwg * 4 * 2, dtype=np.uint64)
+    for x in (g, out, clk):
+        x._ensure_gpu()
+    res = {}
+    for name, (reads, dmas) in MFMA_LOAD_MIXES.items():
+        src = _MFMA_LOAD_SRC.replace("NAME", name).replace("READS", str(reads)).replace("DMAS", str(dmas))
+        k = cp.RawKernel(src, name)
+        args = lambda rep: (g, out, clk, np.int32(iters), np.uint32(2 + rep))  # noqa: E731
+        k((nwg * 256,), args(-1))
+        best = clock = None
+        for rep in range(reps):
+            s, e = be.event(), be.event()
+            be.record(s)
+            k((nwg * 256,), args(rep))
+            be.record(e)
+            cp.synchronize()
+            ms = be.elapsed_ms(s, e)
+            if best is None or ms < best:
+                c = clk.get().reshape(-1, 2).astype(np.float64)
+                best, clock = ms, float(np.mean(c[:, 0] / (c[:, 1] / 100.0)))
+        flops = nwg * 4 * iters * 16 * 16384
+        res[name] = {"ms": round(best, 3), "tflops": round(flops / best / 1e9, 1),
+                     "clock_mhz": round(clock), "lds_read_bytes_per_kflop": round(reads * 1024 * 1000 / 262144, 2),
+                     "dma_bytes_per_kflop": round(dmas * 1024 * 1000 / 262144, 2)}
+    return res
+
+
 def bench_c4(cp, be, reps=20, warm=10):
     from macmetalpy_amd.workloads import c4_inputs
     res = {}
@@ -554,6 +660,13 @@ def bench_c4(cp, be, reps=20, warm=10):
         res["fp16_mfma_practical_ceiling"] = mfma_ceiling(cp, be)
     except Exception as e:
         res["fp16_mfma_practical_ceiling"] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    try:
+        under = res["fp16_mfma_clock_under_gemm_traffic"] = mfma_clock_under_load(cp, be)
+        if "tflops" in res.get("f16", {}):
+            res["f16"]["frac_of_traffic_ceiling"] = round(
+                res["f16"]["tflops"] / under["mfma_lds_dma"]["tflops"], 4)
+    except Exception as e:
+        res["fp16_mfma_clock_under_gemm_traffic"] = {"error": f"{type(e).__name__}: {e}"[:300]}
     return res
 
 
@@ -1151,6 +1264,7 @@ CONFIG_SECTIONS = {
     "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
     "small_host_ops": bench_small_host_ops,
     "scan_shape_copy_2p28": scan_shape_copy,
+    "mfma_clock_under_load": mfma_clock_under_load,
     "c3_reduce_scan": bench_c3, "c4_matmul": bench_c4,
     "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
     "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,

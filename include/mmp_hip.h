@@ -207,6 +207,15 @@ int mmp_host_free(void *ptr);
  * (the flags live in pinned host memory, so the check costs no copy). */
 int mmp_sync(void);
 
+/* The library stream as an opaque hipStream_t (null before mmp_init), for
+ * callers that order their own work against the library's, or that record
+ * library calls into a HIP graph: hipStreamBeginCapture on this stream,
+ * the calls, hipStreamEndCapture, then replay with hipGraphLaunch on it.
+ * Only calls that neither allocate nor wait can be captured
+ * (mmp_reduce_noalloc is one).  The reference keeps metalgpu's command
+ * queue private (_metal_backend.py:197-221), so it has no counterpart. */
+int mmp_stream(void **stream);
+
 /* Stream-ordered timing events on the library stream (benchmarks). */
 int mmp_event_create(void **ev);
 int mmp_event_record(void *ev);

@@ -202,6 +202,7 @@ EXPORTS = (
     "mmp_init", "mmp_device_count", "mmp_device_info", "mmp_last_error",
     "mmp_alloc", "mmp_free", "mmp_empty_cache", "mmp_memory_stats",
     "mmp_h2d", "mmp_d2h", "mmp_d2d", "mmp_host_alloc", "mmp_host_free", "mmp_sync",
+    "mmp_stream",
     "mmp_event_create", "mmp_event_record", "mmp_event_elapsed_ms",
     "mmp_event_destroy",
     "mmp_unary", "mmp_binary", "mmp_binary_scalar", "mmp_copy",

@@ -88,6 +88,7 @@ _SIGNATURES = {
     "mmp_host_alloc": [_c_sz, ctypes.POINTER(_c_vp)],
     "mmp_host_free": [_c_vp],
     "mmp_sync": [],
+    "mmp_stream": [ctypes.POINTER(_c_vp)],
     "mmp_event_create": [ctypes.POINTER(_c_vp)],
     "mmp_event_record": [_c_vp],
     "mmp_event_elapsed_ms": [_c_vp, _c_vp, ctypes.POINTER(ctypes.c_float)],

@@ -616,6 +616,12 @@ int mmp_sync(void) {
   return check_waits();
 }
 
+int mmp_stream(void **stream) {
+  if (!stream) return mmpi::fail(MMP_E_ARG, "null stream pointer");
+  *stream = g_dev.ready ? static_cast<void *>(g_dev.stream) : nullptr;
+  return MMP_OK;
+}
+
 int mmp_event_create(void **ev) {
   if (int st = mmpi::ensure_init()) return st;
   if (!ev) return mmpi::fail(MMP_E_ARG, "null event");

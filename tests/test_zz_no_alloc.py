@@ -4,9 +4,12 @@ The allocation-free variant keeps its cross-workgroup partials in a static
 device array; it must give mmp_reduce's results (bit for bit where it
 splits the same way, within the float32 reduction tolerance of 1e-5
 relative where it lowers a strided split to fit) on two calls in a row,
-the second smaller, and must leave the allocator untouched.
+the second smaller, and must leave the allocator untouched.  Captured into
+a HIP graph on the library stream (mmp_stream), it must give the eager
+call's results on every replay.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -127,3 +130,104 @@ def test_noalloc_rejects_bad_arguments():
     assert lib.mmp_reduce_noalloc(_abi.REDUCE_SUM, F32, F32, 1, 0, 1, x.ptr, o.ptr) == _abi.MMP_E_ARG
     assert lib.mmp_reduce_noalloc(99, F32, F32, 1, 16, 1, x.ptr, o.ptr) == _abi.MMP_E_ARG
     assert lib.mmp_reduce_noalloc(_abi.REDUCE_SUM, F32, F32, 1, 16, 1, None, o.ptr) == _abi.MMP_E_ARG
+
+
+def _hip_runtime():
+    """The HIP runtime's graph-capture entry points through ctypes (the
+    process already has the library loaded through libmmp_hip.so)."""
+    path = "/opt/rocm/lib/libamdhip64.so"
+    hip = ctypes.CDLL(path if os.path.exists(path) else "libamdhip64.so")
+    vp = ctypes.c_void_p
+    sigs = {
+        "hipStreamBeginCapture": [vp, ctypes.c_int],
+        "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+        "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, ctypes.c_size_t],
+        "hipGraphLaunch": [vp, vp],
+        "hipGraphExecDestroy": [vp],
+        "hipGraphDestroy": [vp],
+    }
+    for name, argtypes in sigs.items():
+        fn = getattr(hip, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    return hip
+
+
+HIP_STREAM_CAPTURE_MODE_RELAXED = 2
+
+GRAPH_CASES = [
+    # (op, dtype, out dtype, (outer, len, inner)): split rows, then column partials
+    (_abi.REDUCE_SUM, np.float32, np.float32, (1, 1 << 22, 1)),
+    (_abi.REDUCE_SUM, np.int32, np.int64, (2, 1 << 20, 1)),
+    (_abi.REDUCE_MEAN, np.float32, np.float32, (1, 4096, 300)),
+]
+
+
+@pytest.mark.parametrize("op,dt,odt,shape", GRAPH_CASES)
+def test_noalloc_graph_replays_match_eager(op, dt, odt, shape):
+    """mmp_reduce_noalloc captured into a HIP graph on the library stream
+    and replayed four times.  Before each replay the input gets new values
+    and another no-alloc reduction (another tag, the same scratch words)
+    runs eagerly.  Every replay must give, bit for bit, what an eager
+    mmp_reduce_noalloc call on the same input gives afterwards, and the
+    float64 / exact reference of that input."""
+    be = HipBackend()
+    lib = load_library()
+    hip = _hip_runtime()
+    rng = np.random.default_rng(97 + op)
+    outer, length, inner = shape
+    n, n_out = outer * length * inner, outer * inner
+    dc, oc = _abi.DTYPE_CODES[np.dtype(dt)], _abi.DTYPE_CODES[np.dtype(odt)]
+
+    def draw():
+        if np.dtype(dt).kind == "f":
+            return rng.standard_normal(n).astype(dt)
+        return rng.integers(-1000, 1000, n).astype(dt)
+
+    x = be.create_buffer(n, dt)
+    out_graph = be.create_buffer(n_out, odt)
+    out_eager = be.create_buffer(n_out, odt)
+    other_x = _dev(be, rng.standard_normal(1 << 20).astype(np.float32))
+    other_out = be.create_buffer(1, np.float32)
+    be.write_buffer(x, 0, draw())
+    be.synchronize()
+
+    stream = ctypes.c_void_p()
+    assert lib.mmp_stream(ctypes.byref(stream)) == 0 and stream.value
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(stream, HIP_STREAM_CAPTURE_MODE_RELAXED) == 0
+    try:
+        st = lib.mmp_reduce_noalloc(op, dc, oc, outer, length, inner, x.ptr, out_graph.ptr)
+    finally:
+        end = hip.hipStreamEndCapture(stream, ctypes.byref(graph))
+    assert st == 0, lib.mmp_last_error().decode()
+    assert end == 0 and graph.value
+    try:
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep in range(4):
+            data = draw()
+            be.write_buffer(x, 0, data)
+            assert lib.mmp_reduce_noalloc(_abi.REDUCE_MAX, F32, F32, 1, 1 << 20, 1,
+                                          other_x.ptr, other_out.ptr) == 0
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            be.synchronize()
+            got = be.read_buffer(out_graph, 0, np.empty(n_out, odt))
+            assert lib.mmp_reduce_noalloc(op, dc, oc, outer, length, inner, x.ptr,
+                                          out_eager.ptr) == 0
+            be.synchronize()
+            want = be.read_buffer(out_eager, 0, np.empty(n_out, odt))
+            assert got.tobytes() == want.tobytes(), (rep, got[:4], want[:4])
+            v = data.reshape(outer, length, inner)
+            if np.dtype(dt).kind == "f":
+                ref = v.astype(np.float64).sum(axis=1).reshape(-1)
+                if op == _abi.REDUCE_MEAN:
+                    ref /= length
+                scale = np.abs(v).astype(np.float64).sum(axis=1).reshape(-1) / (
+                    length if op == _abi.REDUCE_MEAN else 1)
+                assert np.all(np.abs(got - ref) <= 1e-5 * scale), rep
+            else:
+                assert np.array_equal(got, v.sum(axis=1, dtype=np.int64).reshape(-1)), rep
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)

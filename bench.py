@@ -130,6 +130,40 @@ def _mat(r):
     return r
 
 
+def bench_c2_end_to_end(cp, be, reps=5):
+    """The C2 calls timed end to end from Python, as the reference's
+    bench_core.py:291-297 times `cp_func(data).get()`: ``call_sync_ms`` is a
+    call plus cp.synchronize() (host dispatch, kernel, wait),
+    ``call_get_ms`` a call plus .get() (the 1 GiB result copied into host
+    memory); medians of ``reps`` after one warm-up, inputs resident in HBM.
+    ``d2h_gbs`` is the result bytes over the difference of the two."""
+    from macmetalpy_amd.workloads import c2_float_inputs, c2_int_inputs
+    a, b = (cp.array(x) for x in c2_float_inputs(N28))
+    ai, bi = (cp.array(x) for x in c2_int_inputs(N28))
+    for x in (a, b, ai, bi):
+        x._ensure_gpu()
+    cp.synchronize()
+    ops = {"add_f32": lambda: a + b, "sin_f32": lambda: cp.sin(a),
+           "floor_divide_i32": lambda: cp.floor_divide(ai, bi), "mod_i32": lambda: cp.mod(ai, bi)}
+
+    def median_ms(f):
+        f()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            f()
+            ts.append((time.perf_counter() - t) * 1e3)
+        return statistics.median(ts)
+
+    res = {}
+    for name, fn in ops.items():
+        sync_ms = median_ms(lambda: (_mat(fn()), cp.synchronize()))
+        get_ms = median_ms(lambda: fn().get())
+        res[name] = {"call_sync_ms": round(sync_ms, 3), "call_get_ms": round(get_ms, 3),
+                     "d2h_gbs": round(4 * N28 / max(get_ms - sync_ms, 1e-6) / 1e6, 1)}
+    return res
+
+
 def _launch_ms(cp, be, f, reps):
     """Mean device time per call over ``reps`` back-to-back calls between
     one pair of events on the library stream: the queue stays ahead of the
@@ -1261,6 +1295,7 @@ def bench_routines(cp, be, reps=5):
 
 
 CONFIG_SECTIONS = {
+    "c2_end_to_end": bench_c2_end_to_end,
     "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
     "small_host_ops": bench_small_host_ops,
     "scan_shape_copy_2p28": scan_shape_copy,

@@ -180,9 +180,9 @@ from ._native import DeviceBuffer  # noqa: E402
 
 _U32x3 = ctypes.c_uint32 * 3
 
-# Results of 64 KiB .. 256 MiB come back into page-locked host blocks.
+# Results of 64 KiB .. 1 GiB come back into page-locked host blocks.
 _PINNED_MIN = 64 << 10
-_PINNED_MAX = 256 << 20
+_PINNED_MAX = 1 << 30
 
 
 class _PinnedBlock:

@@ -552,7 +552,7 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
 // pageable memory beyond that).
 namespace {
 constexpr size_t kHostRound = 64 << 10;
-constexpr size_t kHostCacheMax = 1ull << 30;
+constexpr size_t kHostCacheMax = 2ull << 30;
 constexpr size_t kHostLiveMax = 4ull << 30;
 std::multimap<size_t, void *> g_host_free;          // rounded size -> block
 std::unordered_map<void *, size_t> g_host_live;     // block -> rounded size

@@ -1,6 +1,6 @@
 """ndarray.get() into page-locked host blocks (the reference's get(),
 src/macmetalpy/ndarray.py:576-603, reads unified memory; here results of
-64 KiB .. 256 MiB come back by DMA into cached pinned blocks)."""
+64 KiB .. 1 GiB come back by DMA into cached pinned blocks)."""
 import gc
 
 import numpy as np
@@ -21,7 +21,8 @@ def _pinned(a):
 
 @pytest.mark.parametrize("n,dtype", [(1000, np.float32), (1 << 16, np.float32),
                                      (1 << 20, np.float64), ((1 << 20) + 3, np.int16),
-                                     (3 << 20, np.int32), (_PINNED_MAX // 4 + 1, np.float32)])
+                                     (3 << 20, np.int32), (_PINNED_MAX // 8, np.float64),
+                                     (_PINNED_MAX // 8 + 1, np.float64)])
 def test_get_values_and_backing(n, dtype):
     g = np.random.default_rng(n)
     h = (g.standard_normal(n) * 100).astype(dtype)

@@ -130,6 +130,77 @@ def _mat(r):
     return r
 
 
+# The reference's published "scaling story" (README.md:107-118: speedup of
+# macmetalpy over NumPy on an M4 Mac mini, float32, at 1K / 100K / 1M).
+REFERENCE_SCALING = {
+    "add": (0.40, 0.93, 0.98), "sin": (0.69, 0.98, 2.41), "exp": (0.72, 0.96, 2.12),
+    "cumsum": (0.59, 1.40, 1.39), "floor_divide": (0.79, 3.04, 11.12),
+    "mod": (0.76, 2.35, 7.57), "randn": (2.88, 3.71, 3.69), "normal": (2.02, 2.48, 2.47),
+    "sort": (0.84, 0.93, 1.57), "searchsorted": (0.01, 4.12, 32.50),
+}
+SCALING_SIZES = (1_000, 100_000, 1_000_000)
+
+
+def bench_scaling_vs_numpy(cp, be, warm=2, reps=15):
+    """The reference's scaling table re-measured here with its method
+    (bench_core.py:276-357, 368-402; bench_advanced.py:316-365, 550-608):
+    inputs made with np.random (rand + 0.1 for the ufuncs, rand for cumsum
+    and sort, a sorted base with size // 10 queries for searchsorted) and
+    put on the device once; a timed call is the op plus .get() of its
+    result (randn / normal: generation plus .get()); NumPy runs the same
+    call on the host copy.  Medians of ``reps`` after ``warm`` warm-ups
+    (the reference: 5 after 2).  ``speedup`` = NumPy time / this time;
+    ``reference_speedup`` is the README's M4 figure for the same cell."""
+    rng = np.random.default_rng(31)
+
+    def median_s(f):
+        for _ in range(warm):
+            f()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            f()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    res = {}
+    for si, n in enumerate(SCALING_SIZES):
+        a_np = (rng.random(n) + 0.1).astype(np.float32)
+        b_np = (rng.random(n) + 0.1).astype(np.float32)
+        r_np = rng.random(n).astype(np.float32)
+        base_np = np.sort(rng.random(n).astype(np.float32))
+        q_np = rng.random(max(n // 10, 1)).astype(np.float32)
+        a, b, r, base, q = (cp.array(x) for x in (a_np, b_np, r_np, base_np, q_np))
+        for x in (a, b, r, base, q):
+            x._ensure_gpu()
+        cases = {
+            "add": (lambda: cp.add(a, b).get(), lambda: np.add(a_np, b_np)),
+            "sin": (lambda: cp.sin(a).get(), lambda: np.sin(a_np)),
+            "exp": (lambda: cp.exp(a).get(), lambda: np.exp(a_np)),
+            "cumsum": (lambda: cp.cumsum(r).get(), lambda: np.cumsum(r_np)),
+            "floor_divide": (lambda: cp.floor_divide(a, b).get(),
+                             lambda: np.floor_divide(a_np, b_np)),
+            "mod": (lambda: cp.mod(a, b).get(), lambda: np.mod(a_np, b_np)),
+            "randn": (lambda: cp.random.randn(n).get(), lambda: np.random.randn(n)),
+            "normal": (lambda: cp.random.normal(0.0, 1.0, size=(n,)).get(),
+                       lambda: np.random.normal(0.0, 1.0, size=(n,))),
+            "sort": (lambda: cp.sort(r).get(), lambda: np.sort(r_np)),
+            "searchsorted": (lambda: cp.searchsorted(base, q).get(),
+                             lambda: np.searchsorted(base_np, q_np)),
+        }
+        label = {1_000: "1K", 100_000: "100K", 1_000_000: "1M"}[n]
+        sec = {}
+        for name, (dev, host) in cases.items():
+            t_dev = median_s(dev)
+            t_np = median_s(host)
+            sec[name] = {"us": round(t_dev * 1e6, 1), "numpy_us": round(t_np * 1e6, 1),
+                         "speedup": round(t_np / t_dev, 2),
+                         "reference_speedup": REFERENCE_SCALING[name][si]}
+        res[label] = sec
+        del a, b, r, base, q
+    return res
+
+
 def bench_c2_end_to_end(cp, be, reps=5):
     """The C2 calls timed end to end from Python, as the reference's
     bench_core.py:291-297 times `cp_func(data).get()`: ``call_sync_ms`` is a
@@ -1296,6 +1367,7 @@ def bench_routines(cp, be, reps=5):
 
 CONFIG_SECTIONS = {
     "c2_end_to_end": bench_c2_end_to_end,
+    "scaling_vs_numpy": bench_scaling_vs_numpy,
     "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
     "small_host_ops": bench_small_host_ops,
     "scan_shape_copy_2p28": scan_shape_copy,

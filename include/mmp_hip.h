@@ -181,11 +181,12 @@ int mmp_memory_stats(size_t *in_use, size_t *cached);
  * with respect to the host buffer (it may be reused as soon as they return);
  * d2d is stream-ordered.  mmp_h2d of at most 1 MiB copies the bytes into
  * page-locked staging memory and queues the transfer on the library stream
- * without waiting for it (work queued later sees the data; up to 64 KiB the
- * transfer is a small copy kernel reading the mapped staging memory, above
- * that a DMA); larger copies wait for the transfer.  mmp_d2h of at most
- * 64 KiB runs a copy kernel into mapped page-locked memory, synchronises
- * and copies out on the host.  mmp_d2h returns
+ * without waiting for it (work queued later sees the data; the transfer is
+ * a small copy kernel reading the mapped staging memory); larger copies
+ * wait for the transfer.  mmp_d2h of
+ * less than 32 KiB runs a copy kernel into mapped page-locked memory,
+ * synchronises and copies out on the host; larger ones are a DMA and a
+ * wait.  mmp_d2h returns
  * MMP_E_WAIT (after completing the copy) when a device-side bounded wait
  * ran out since the last check -- see mmp_wait_status. */
 int mmp_h2d(void *dst, const void *src, size_t bytes);

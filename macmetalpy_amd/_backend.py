@@ -180,8 +180,9 @@ from ._native import DeviceBuffer  # noqa: E402
 
 _U32x3 = ctypes.c_uint32 * 3
 
-# Results of 64 KiB .. 1 GiB come back into page-locked host blocks.
-_PINNED_MIN = 64 << 10
+# Results of 32 KiB .. 1 GiB come back into page-locked host blocks (below
+# 32 KiB the library copies through its own mapped block).
+_PINNED_MIN = 32 << 10
 _PINNED_MAX = 1 << 30
 
 

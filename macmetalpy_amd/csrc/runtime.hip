@@ -363,12 +363,20 @@ int mmp_memory_stats(size_t *in_use, size_t *cached) {
 // (in-order stream).  For small host arrays this turns each upload from a
 // blocking round trip into a host memcpy plus a queued copy.
 namespace {
-// Copies of at most kKernelCopyMax bytes between device memory and the
-// mapped, coherent staging memory below run as a small kernel on the
-// library stream instead of a DMA transfer: a launch on the stream the
-// consuming kernels use costs less than handing the copy to a DMA engine
-// and back.
-constexpr size_t kKernelCopyMax = 1 << 20;
+// Small copies between device memory and the mapped, coherent staging
+// memory below run as a kernel on the library stream instead of a DMA
+// transfer.  Measured on MI355X:
+//  * device -> host, copy plus stream wait: 4-24 KiB 13.0-14.3 us by kernel
+//    against 19-27 us by DMA; from 32 KiB on the DMA is faster (32 KiB 11.0
+//    against 14.5 us, 1 MiB 27.7 against 62.1 us: a kernel's writes to host
+//    memory reach ~15 GB/s), so downloads take the kernel below 32 KiB;
+//  * host -> device: the upload is followed by kernels on the same stream,
+//    and there a DMA costs its hand-over to the compute queue (a 64K-element
+//    float32 a + b of host arrays, two 256 KiB uploads: 66 us per call with
+//    DMA uploads, 55 with kernel copies), so uploads take the kernel up to
+//    the 1 MiB staging segment.
+constexpr size_t kDownloadKernelBelow = 32 << 10;
+constexpr size_t kUploadKernelMax = 1 << 20;
 
 __global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ dst,
                                                     const unsigned char *__restrict__ src,
@@ -470,7 +478,7 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
   char *slot = g_stage + at;
   std::memcpy(slot, src, bytes);
   g_stage_head += span;
-  if (bytes <= kKernelCopyMax) return launch_copy_small(dst, g_stage_dev + at, bytes);
+  if (bytes <= kUploadKernelMax) return launch_copy_small(dst, g_stage_dev + at, bytes);
   return mmpi::check_hip(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_dev.stream),
                          "hipMemcpyAsync(H2D, staged)");
 }
@@ -487,7 +495,7 @@ int small_download(void *dst, const void *src, size_t bytes) {
   if (g_back_off) return kNotStaged;
   if (!g_back) {
     void *p = nullptr;
-    if (hipHostMalloc(&p, kKernelCopyMax, hipHostMallocMapped | hipHostMallocCoherent) !=
+    if (hipHostMalloc(&p, kDownloadKernelBelow, hipHostMallocMapped | hipHostMallocCoherent) !=
             hipSuccess ||
         !p) {
       (void)hipGetLastError();
@@ -530,7 +538,7 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
-  if (bytes <= kKernelCopyMax && is_device_memory(src)) {
+  if (bytes < kDownloadKernelBelow && is_device_memory(src)) {
     const int st = small_download(dst, src, bytes);
     if (st == MMP_OK) return check_waits();
     if (st != kNotStaged) return st;

@@ -1,6 +1,6 @@
 """ndarray.get() into page-locked host blocks (the reference's get(),
 src/macmetalpy/ndarray.py:576-603, reads unified memory; here results of
-64 KiB .. 1 GiB come back by DMA into cached pinned blocks)."""
+32 KiB .. 1 GiB come back by DMA into cached pinned blocks)."""
 import gc
 
 import numpy as np

@@ -84,16 +84,18 @@ def test_uploads_wrapping_the_staging_ring_stay_intact():
 
 def test_uploads_of_changing_host_data_and_sizes():
     """One NumPy buffer rewritten between uploads (each upload must have
-    copied it at call time), sizes around the 1 MiB staging limit (staged
-    and direct copies interleaved), and set() of a host array."""
-    print("staging: rewritten source, sizes around 1 MiB", flush=True)
+    copied it at call time), sizes around the 32 KiB kernel-copy limit
+    (kernel and DMA transfers, up and down) and the 1 MiB staging limit
+    (staged and direct copies interleaved), and set() of a host array."""
+    print("staging: rewritten source, sizes around 32 KiB and 1 MiB", flush=True)
     src = np.zeros(1 << 18, dtype=np.float32)       # exactly 1 MiB
     arrs, wants = [], []
     for i in range(20):
         src[:] = i
         arrs.append(cp.array(src) * 1.0)
         wants.append(np.full(src.shape, i, np.float32))
-    for n in ((1 << 18) - 1, (1 << 18) + 1, 3, 1 << 19, 17):
+    for n in ((1 << 18) - 1, (1 << 18) + 1, 3, 1 << 19, 17, (1 << 13) - 1, 1 << 13,
+              (1 << 13) + 1, 8190, 8195):
         h = np.arange(n, dtype=np.float32)
         arrs.append(cp.array(h) + 0.0)
         wants.append(h)

@@ -185,8 +185,9 @@ int mmp_memory_stats(size_t *in_use, size_t *cached);
  * a small copy kernel reading the mapped staging memory); larger copies
  * wait for the transfer.  mmp_d2h of
  * less than 32 KiB runs a copy kernel into mapped page-locked memory,
- * synchronises and copies out on the host; larger ones are a DMA and a
- * wait.  mmp_d2h returns
+ * waits for the word the kernel writes after the bytes (the kernel runs
+ * after all work queued before it) and copies out on the host; larger ones
+ * are a DMA and a stream wait.  mmp_d2h returns
  * MMP_E_WAIT (after completing the copy) when a device-side bounded wait
  * ran out since the last check -- see mmp_wait_status. */
 int mmp_h2d(void *dst, const void *src, size_t bytes);

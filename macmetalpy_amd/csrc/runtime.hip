@@ -29,6 +29,7 @@
 #include "mmp_internal.h"
 
 #include <atomic>
+#include <chrono>
 
 namespace {
 
@@ -412,6 +413,29 @@ int launch_copy_small(void *dst, const void *src, size_t n) {
   return mmpi::check_hip(hipGetLastError(), "small copy launch");
 }
 
+// Download copy: one workgroup copies the bytes into the mapped block, then
+// publishes `seq` in the block's completion word with a system-scope
+// release once every lane's stores are ordered before it (each lane's
+// system fence, then the barrier).  The host waits for that word instead of
+// the end-of-kernel signal.
+__global__ __launch_bounds__(256) void k_copy_back(unsigned char *__restrict__ dst,
+                                                   const unsigned char *__restrict__ src, size_t n,
+                                                   unsigned *done, unsigned seq) {
+  const unsigned t = threadIdx.x;
+  size_t head = 0;
+  if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const size_t nv = n / 16;
+    for (size_t i = t; i < nv; i += 256)
+      reinterpret_cast<u4 *>(dst)[i] = reinterpret_cast<const u4 *>(src)[i];
+    head = nv * 16;
+  }
+  for (size_t i = head + t; i < n; i += 256) dst[i] = src[i];
+  __threadfence_system();
+  __syncthreads();
+  if (t == 0) __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 constexpr size_t kStageSeg = 1 << 20;
 constexpr int kStageSegs = 8;
 constexpr size_t kStageAlign = 256;
@@ -484,18 +508,24 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
 }
 
 // Small device -> host copies: a kernel writes the bytes into a mapped,
-// coherent page-locked block, the stream is synchronised, then the host
-// copies them out.
+// coherent page-locked block and then a completion word behind them; the
+// host polls that word (bounded: after kBackSpin it waits for the stream
+// instead, then the word must be there), then copies the bytes out.  Stream
+// order puts the copy after every kernel queued before it, and a word seen
+// means the bytes before it are visible.
 std::mutex g_back_mu;
 char *g_back = nullptr, *g_back_dev = nullptr;
 bool g_back_off = false;
+unsigned g_back_seq = 0;
+constexpr size_t kBackWord = kDownloadKernelBelow;  // offset of the completion word
+constexpr auto kBackSpin = std::chrono::microseconds(200);
 
 int small_download(void *dst, const void *src, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_back_mu);
   if (g_back_off) return kNotStaged;
   if (!g_back) {
     void *p = nullptr;
-    if (hipHostMalloc(&p, kDownloadKernelBelow, hipHostMallocMapped | hipHostMallocCoherent) !=
+    if (hipHostMalloc(&p, kBackWord + 256, hipHostMallocMapped | hipHostMallocCoherent) !=
             hipSuccess ||
         !p) {
       (void)hipGetLastError();
@@ -511,10 +541,31 @@ int small_download(void *dst, const void *src, size_t bytes) {
     }
     g_back = static_cast<char *>(p);
     g_back_dev = static_cast<char *>(dp);
+    *reinterpret_cast<volatile unsigned *>(g_back + kBackWord) = 0;
   }
-  if (int st = launch_copy_small(g_back_dev, src, bytes)) return st;
-  if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
-    return st;
+  if (++g_back_seq == 0) g_back_seq = 1;  // 0 is the word's initial value
+  const unsigned seq = g_back_seq;
+  hipLaunchKernelGGL(k_copy_back, dim3(1), dim3(256), 0, g_dev.stream,
+                     reinterpret_cast<unsigned char *>(g_back_dev),
+                     static_cast<const unsigned char *>(src), bytes,
+                     reinterpret_cast<unsigned *>(g_back_dev + kBackWord), seq);
+  if (int st = mmpi::check_hip(hipGetLastError(), "download copy launch")) return st;
+  const volatile unsigned *done = reinterpret_cast<volatile unsigned *>(g_back + kBackWord);
+  const auto t0 = std::chrono::steady_clock::now();
+  bool seen = false;
+  for (unsigned i = 1;; ++i) {
+    if (*done == seq) {
+      seen = true;
+      break;
+    }
+    if ((i & 63) == 0 && std::chrono::steady_clock::now() - t0 > kBackSpin) break;
+  }
+  if (!seen) {
+    if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
+      return st;
+    if (*done != seq) return mmpi::fail(MMP_E_HIP, "small download: completion word not written");
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
   std::memcpy(dst, g_back, bytes);
   return MMP_OK;
 }

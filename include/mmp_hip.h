@@ -184,7 +184,8 @@ int mmp_memory_stats(size_t *in_use, size_t *cached);
  * without waiting for it (work queued later sees the data; the transfer is
  * a small copy kernel reading the mapped staging memory); larger copies
  * wait for the transfer.  mmp_d2h of
- * less than 32 KiB runs a copy kernel into mapped page-locked memory,
+ * less than 32 KiB (48 KiB into pageable memory) runs a copy kernel into
+ * mapped page-locked memory,
  * waits for the word the kernel writes after the bytes (the kernel runs
  * after all work queued before it) and copies out on the host; larger ones
  * are a DMA and a stream wait.  mmp_d2h returns

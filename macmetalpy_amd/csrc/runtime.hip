@@ -371,12 +371,16 @@ namespace {
 //    against 19-27 us by DMA; from 32 KiB on the DMA is faster (32 KiB 11.0
 //    against 14.5 us, 1 MiB 27.7 against 62.1 us: a kernel's writes to host
 //    memory reach ~15 GB/s), so downloads take the kernel below 32 KiB;
+//    into pageable memory (which the runtime stages) a DMA stays slow up
+//    to 47 KiB (32 KiB 23.3 us, 48 KiB 11.7), so pageable destinations
+//    take the kernel below 48 KiB;
 //  * host -> device: the upload is followed by kernels on the same stream,
 //    and there a DMA costs its hand-over to the compute queue (a 64K-element
 //    float32 a + b of host arrays, two 256 KiB uploads: 66 us per call with
 //    DMA uploads, 55 with kernel copies), so uploads take the kernel up to
 //    the 1 MiB staging segment.
 constexpr size_t kDownloadKernelBelow = 32 << 10;
+constexpr size_t kDownloadPageableBelow = 48 << 10;
 constexpr size_t kUploadKernelMax = 1 << 20;
 
 __global__ __launch_bounds__(256) void k_copy_small(unsigned char *__restrict__ dst,
@@ -404,6 +408,17 @@ bool is_device_memory(const void *p) {
     return false;
   }
   return a.type == hipMemoryTypeDevice;
+}
+
+// Page-locked host memory the runtime knows (hipHostMalloc'd); pageable
+// memory is not.
+bool is_page_locked(const void *p) {
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return a.type == hipMemoryTypeHost;
 }
 
 int launch_copy_small(void *dst, const void *src, size_t n) {
@@ -507,17 +522,17 @@ int stage_upload(void *dst, const void *src, size_t bytes) {
                          "hipMemcpyAsync(H2D, staged)");
 }
 
-// Small device -> host copies: a kernel writes the bytes into a mapped,
-// coherent page-locked block and then a completion word behind them; the
-// host polls that word (bounded: after kBackSpin it waits for the stream
-// instead, then the word must be there), then copies the bytes out.  Stream
-// order puts the copy after every kernel queued before it, and a word seen
-// means the bytes before it are visible.
+// Small device -> host copies: one workgroup writes the bytes into a
+// mapped, coherent page-locked block and then a completion word behind
+// them; the host polls that word (bounded: after kBackSpin it waits for
+// the stream instead, then the word must be there), then copies the bytes
+// out.  Stream order puts the copy after every kernel queued before it,
+// and a word seen means the bytes before it are visible.
 std::mutex g_back_mu;
 char *g_back = nullptr, *g_back_dev = nullptr;
 bool g_back_off = false;
 unsigned g_back_seq = 0;
-constexpr size_t kBackWord = kDownloadKernelBelow;  // offset of the completion word
+constexpr size_t kBackWord = kDownloadPageableBelow;  // offset of the completion word
 constexpr auto kBackSpin = std::chrono::microseconds(200);
 
 int small_download(void *dst, const void *src, size_t bytes) {
@@ -589,7 +604,8 @@ int mmp_d2h(void *dst, const void *src, size_t bytes) {
   if (int st = mmpi::ensure_init()) return st;
   if (bytes == 0) return MMP_OK;
   if (!dst || !src) return mmpi::fail(MMP_E_ARG, "null pointer");
-  if (bytes < kDownloadKernelBelow && is_device_memory(src)) {
+  if (bytes < kDownloadPageableBelow && is_device_memory(src) &&
+      (bytes < kDownloadKernelBelow || !is_page_locked(dst))) {
     const int st = small_download(dst, src, bytes);
     if (st == MMP_OK) return check_waits();
     if (st != kNotStaged) return st;

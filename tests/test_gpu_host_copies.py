@@ -62,3 +62,27 @@ def test_strided_and_2d_views_come_back_contiguous():
     np.testing.assert_array_equal(d.T.get(), h.T)
     np.testing.assert_array_equal(d[::3, 1::2].get(), h[::3, 1::2])
     assert d.T.get().flags.c_contiguous
+
+
+@pytest.mark.parametrize("nbytes", [1, 15, 4096, (32 << 10) - 4, 32 << 10, (32 << 10) + 4,
+                                    (48 << 10) - 4, 48 << 10, (48 << 10) + 4, 200_000])
+@pytest.mark.parametrize("src_off", [0, 4, 3])
+def test_d2h_by_size_source_offset_and_destination(nbytes, src_off):
+    """mmp_d2h through the C ABI at the sizes where its route changes (the
+    polled copy kernel below 32 KiB, and below 48 KiB into pageable
+    memory; DMA above), from aligned and unaligned device addresses, into
+    pageable and page-locked host memory, twice in a row with new data."""
+    be = HipBackend()
+    lib = be._lib
+    g = np.random.default_rng(nbytes + src_off)
+    dev = be.create_buffer(nbytes + 16, np.uint8)
+    for rep in range(2):
+        h = g.integers(0, 256, nbytes + 16, dtype=np.uint8)
+        be.write_buffer(dev, 0, h)
+        pageable = np.zeros(nbytes, np.uint8)
+        assert lib.mmp_d2h(pageable.ctypes.data, dev.ptr + src_off, nbytes) == 0
+        np.testing.assert_array_equal(pageable, h[src_off:src_off + nbytes])
+        locked = be.host_empty((nbytes,), np.uint8)
+        locked[:] = 0
+        assert lib.mmp_d2h(locked.ctypes.data, dev.ptr + src_off, nbytes) == 0
+        np.testing.assert_array_equal(locked, h[src_off:src_off + nbytes])

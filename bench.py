@@ -884,6 +884,26 @@ def bench_sort(cp, be, reps=5):
                                                 "gqueries_s": round((1 << 20) / ms / 1e6, 2)}
             del a, q
         del x
+    # rows of at most one 4096-key tile: one workgroup sorts each row in LDS
+    # (8 B/key of HBM traffic for sort: read once, written once)
+    xr = cp.array(rng.standard_normal((65536, 1024), dtype=np.float32))
+    xr._ensure_gpu()
+    n = xr.size
+    for name, f in (("sort_rows_f32_65536x1024", lambda: cp.sort(xr, axis=-1)),
+                    ("argsort_rows_f32_65536x1024", lambda: cp.argsort(xr, axis=-1))):
+        try:
+            f()
+            cp.synchronize()
+            timer = EventTimer(be)
+            for _ in range(reps):
+                timer.run(name, f)
+            cp.synchronize()
+            ms, _ = timer.ms(name)
+            timer.close()
+            res[name] = {"kernel_ms": round(ms, 4), "gkeys_s": round(n / ms / 1e6, 2)}
+        except Exception as e:
+            res[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+    del xr
     return res
 
 

@@ -75,6 +75,54 @@ def test_sort_argsort_nd(shape, axis, dtype):
         _value_equal(cy.get(), y)
 
 
+@pytest.mark.parametrize("shape,dtype,lo,hi", [((300, 4096), np.int32, 0, 200),
+                                                ((1000, 37), np.int64, -3, 3),
+                                                ((64, 4096), np.uint16, 7, 7),
+                                                ((17, 2049), np.int32, -(2 ** 31), 2 ** 31 - 1)])
+def test_sort_tile_rows_uniform_digits(shape, dtype, lo, hi):
+    """Rows of at most one tile, whose keys share most digit bytes (passes
+    with one digit for the whole row are skipped) or are all equal: stable
+    argsort, sort and kind='stable' equal NumPy's along the last axis."""
+    rng = np.random.default_rng(shape[0])
+    x = rng.integers(lo, hi, shape, dtype=np.int64, endpoint=True).astype(dtype)
+    cx = cp.array(x)
+    assert np.array_equal(cp.argsort(cx, axis=-1).get(), ref.argsort_stable(x, axis=-1))
+    _value_equal(cp.sort(cx, axis=-1).get(), ref.sort(x, axis=-1))
+    f = np.full(shape, 1.5, np.float32)
+    assert np.array_equal(cp.argsort(cp.array(f), axis=-1).get(), ref.argsort_stable(f, axis=-1))
+
+
+@pytest.mark.parametrize("length", [1, 2, 3, 15, 16, 17, 100, 257, 1000, 2048, 2049, 4096])
+@pytest.mark.parametrize("dtype", [np.float32, np.int16, np.float64])
+def test_sort_rows_packed_per_tile(length, dtype):
+    """Whole rows packed into one 4096-key tile (min(256, 4096 // length)
+    rows, the last tile partly filled): stable argsort and sort along the
+    last axis equal NumPy's for every row length around the packing steps."""
+    rows = 1000 + 7 * length % 13
+    x = _data(rows * length, dtype, length).reshape(rows, length)
+    cx = cp.array(x)
+    assert np.array_equal(cp.argsort(cx, axis=-1).get(), ref.argsort_stable(x, axis=-1))
+    _value_equal(cp.sort(cx, axis=-1).get(), ref.sort(x, axis=-1))
+    got = cp.sort(cx, axis=-1, kind="stable").get()
+    want = ref.sort(x, axis=-1, kind="stable")
+    if got.dtype.kind == "f":
+        got, want = got.view(f"u{got.itemsize}"), want.view(f"u{want.itemsize}")
+    assert np.array_equal(got, want)
+
+
+def test_sort_more_rows_than_workgroups():
+    """(2^20 + 5) rows of 2, and 2^28 + 300 rows of 1 (2^20 + 2 tiles of 256
+    rows: more tiles than the one-tile kernel's 2^20 workgroups, so the
+    last two are taken grid-stride)."""
+    x = np.random.default_rng(11).standard_normal(((1 << 20) + 5, 2)).astype(np.float32)
+    cx = cp.array(x)
+    assert np.array_equal(cp.argsort(cx, axis=-1).get(), ref.argsort_stable(x, axis=-1))
+    _value_equal(cp.sort(cx, axis=-1).get(), ref.sort(x, axis=-1))
+    y = np.random.default_rng(12).integers(-30000, 30000, ((1 << 28) + 300, 1), dtype=np.int16)
+    got = cp.sort(cp.array(y), axis=-1).get()
+    assert np.array_equal(got, y)  # rows of one key are already sorted
+
+
 def test_sort_large_properties():
     """2^24 float32: the output is nondecreasing (NaN last), a permutation
     of the input (same multiset), and argsort reorders the input into it."""

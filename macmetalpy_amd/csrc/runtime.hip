@@ -556,7 +556,7 @@ int small_download(void *dst, const void *src, size_t bytes) {
     }
     g_back = static_cast<char *>(p);
     g_back_dev = static_cast<char *>(dp);
-    *reinterpret_cast<volatile unsigned *>(g_back + kBackWord) = 0;
+    __atomic_store_n(reinterpret_cast<unsigned *>(g_back + kBackWord), 0u, __ATOMIC_RELAXED);
   }
   if (++g_back_seq == 0) g_back_seq = 1;  // 0 is the word's initial value
   const unsigned seq = g_back_seq;
@@ -565,11 +565,12 @@ int small_download(void *dst, const void *src, size_t bytes) {
                      static_cast<const unsigned char *>(src), bytes,
                      reinterpret_cast<unsigned *>(g_back_dev + kBackWord), seq);
   if (int st = mmpi::check_hip(hipGetLastError(), "download copy launch")) return st;
-  const volatile unsigned *done = reinterpret_cast<volatile unsigned *>(g_back + kBackWord);
+  // acquire loads: the bytes read below are ordered after the word
+  unsigned *done = reinterpret_cast<unsigned *>(g_back + kBackWord);
   const auto t0 = std::chrono::steady_clock::now();
   bool seen = false;
   for (unsigned i = 1;; ++i) {
-    if (*done == seq) {
+    if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == seq) {
       seen = true;
       break;
     }
@@ -578,9 +579,9 @@ int small_download(void *dst, const void *src, size_t bytes) {
   if (!seen) {
     if (int st = mmpi::check_hip(hipStreamSynchronize(g_dev.stream), "hipStreamSynchronize"))
       return st;
-    if (*done != seq) return mmpi::fail(MMP_E_HIP, "small download: completion word not written");
+    if (__atomic_load_n(done, __ATOMIC_ACQUIRE) != seq)
+      return mmpi::fail(MMP_E_HIP, "small download: completion word not written");
   }
-  std::atomic_thread_fence(std::memory_order_acquire);
   std::memcpy(dst, g_back, bytes);
   return MMP_OK;
 }

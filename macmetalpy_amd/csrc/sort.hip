@@ -106,6 +106,13 @@ struct SegTile {
   unsigned count;  // elements in the tile
   unsigned row, j;
 };
+// Workgroup ids are dealt round-robin over the eight XCDs; tile numbers are
+// remapped so that each XCD takes a contiguous range of tiles.  Neighbouring
+// tiles' digit counts share cache lines (count_slot is tile-minor), which
+// then fill in one XCD's L2 instead of being written piecewise from eight.
+__device__ __forceinline__ unsigned xcd_tile(unsigned b, unsigned tiles) {
+  return (tiles & 7u) == 0 ? (b & 7u) * (tiles >> 3) + (b >> 3) : b;
+}
 __device__ __forceinline__ SegTile seg_tile(unsigned b, unsigned len, unsigned tpr) {
   SegTile t;
   t.row = b / tpr;
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ 
 #pragma unroll
   for (int k = 0; k < kBlock / 64; ++k) h[k][t] = 0;
   __syncthreads();
-  const SegTile tl = seg_tile(blockIdx.x, len, tpr);
+  const SegTile tl = seg_tile(xcd_tile(blockIdx.x, gridDim.x), len, tpr);
   const E *e = reinterpret_cast<const E *>(src) + tl.start;
   auto key_at = [&](E v) -> K {
     if constexpr (FIRST) return to_key<T, CANON>(v);
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(
   __shared__ unsigned lds4[kWaves];
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const SegTile tl = seg_tile(blockIdx.x, len, tpr);
+  const SegTile tl = seg_tile(xcd_tile(blockIdx.x, gridDim.x), len, tpr);
   {
     const size_t slot = count_slot(tl, t, tpr);
     const unsigned c = counts[slot];

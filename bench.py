@@ -201,6 +201,37 @@ def bench_scaling_vs_numpy(cp, be, warm=2, reps=15):
     return res
 
 
+def vendor_copy(cp, be, reps=20):
+    """The HIP runtime's own device-to-device copy (hipMemcpyAsync on the
+    library stream) of 2^28 float32 beside the library's copy kernel and
+    a + b over the same arrays: GB/s of the algorithmic bytes (copy 8 B,
+    a + b 12 B per element), mean of ``reps`` back-to-back calls."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    hip.hipMemcpyAsync.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    stream = vp()
+    if be._lib.mmp_stream(ctypes.byref(stream)) != 0:
+        raise RuntimeError("mmp_stream failed")
+    from macmetalpy_amd.workloads import c2_float_inputs
+    a, b = (cp.array(x) for x in c2_float_inputs(N28))
+    for x in (a, b):
+        x._ensure_gpu()
+    dst = be.create_buffer(N28, np.float32)
+
+    def d2d():
+        if hip.hipMemcpyAsync(dst.ptr, a._ptr, 4 * N28, 3, stream) != 0:  # DeviceToDevice
+            raise RuntimeError("hipMemcpyAsync failed")
+
+    res = {}
+    for name, f, bpe in (("hipMemcpy_d2d", d2d, 8), ("library_copy", lambda: _mat(a.copy()), 8),
+                         ("library_add", lambda: _mat(a + b), 12)):
+        ms = _launch_ms(cp, be, f, reps)
+        res[name] = {"ms": round(ms, 4), "gbs": round(bpe * N28 / ms / 1e6, 1)}
+    return res
+
+
 def bench_c2_end_to_end(cp, be, reps=5):
     """The C2 calls timed end to end from Python, as the reference's
     bench_core.py:291-297 times `cp_func(data).get()`: ``call_sync_ms`` is a
@@ -1387,6 +1418,7 @@ def bench_routines(cp, be, reps=5):
 
 CONFIG_SECTIONS = {
     "c2_end_to_end": bench_c2_end_to_end,
+    "vendor_copy_2p28": vendor_copy,
     "scaling_vs_numpy": bench_scaling_vs_numpy,
     "c1_fused_elementwise": bench_c1, "small_ops_2p20": bench_small_ops,
     "small_host_ops": bench_small_host_ops,

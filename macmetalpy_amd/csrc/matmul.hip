@@ -24,7 +24,9 @@
 //  * float32 / float64: v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64.  The
 //    k slot a lane feeds is permuted (MFMA step t, lane group g consumes
 //    k = KG*g + t), so a lane's A values for a whole slab are contiguous in
-//    LDS and B keeps its natural n-contiguous layout.
+//    LDS and B keeps its natural n-contiguous layout.  float32 products with
+//    128-divisible extents and 16-byte aligned rows use k_gemm4_dma
+//    (operands copied global -> LDS, swizzled stages).
 // Partial tiles and unaligned operands use guarded scalar loads (zero fill)
 // and guarded stores.  Integer matmul: LDS-tiled exact kernel with
 // wrap-around arithmetic (NumPy's integer matmul wraps).
@@ -33,6 +35,9 @@
 
 namespace {
 
+#ifndef GEMM4_WIDE
+#define GEMM4_WIDE 1
+#endif
 constexpr int kBlock = 256;
 constexpr int BM = 128, BN = 128;
 
@@ -542,6 +547,177 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm4(const T *__restrict__ A, co
       }
 }
 
+// ------------------------------------------- float32, global -> LDS DMA
+// (64 WM) x 128 output tile per workgroup of 2 WM waves (WM along M, two
+// along N, each 64 x 64 = 4 x 4 MFMA tiles of v_mfma_f32_16x16x4f32) for
+// operands whose extents divide the tile and the 32-float slab and whose
+// rows are 16-byte aligned: WM = 4 (256 x 128, eight waves, one workgroup
+// per CU) when M divides by 256, else WM = 2 (128 x 128, four waves, two
+// per CU).  Operands are copied HBM/L2 -> LDS with global_load_lds_dwordx4
+// (lane L of a wave's copy lands at 16 B x L of its destination): no
+// register staging, no ds_write.  Two LDS stages; waves 0 .. WM-1 copy A
+// (eight 1 KiB copies each per slab), the next two copy B, any others none.
+// The MFMA's k slot is permuted as in k_gemm4 (lane group g feeds
+// k = 8 g + t), so a lane's A values of a half-slab are one 16-byte chunk.
+//  * A stage: 128 rows x 32 floats (128 B, k-contiguous as in HBM); chunk c
+//    of row r sits at slot c ^ ((r >> 1) & 7), so the 16 rows of a fragment
+//    read spread over all 64 banks.
+//  * B stage: 32 k-rows x 128 floats (512 B, n-contiguous); chunk c of row
+//    k sits at slot c ^ (4 ((k >> 3) & 3)), so the four lane groups of a
+//    scalar fragment read (rows 8 apart) fall in different bank quarters.
+//  * Pipeline as in k_gemm16_dma: one barrier per slab (it waits for this
+//    wave's copies), the copy of the slab two ahead issued right after it
+//    into the stage just consumed, fragment reads half a slab ahead of the
+//    MFMAs.
+template <int WM>
+__global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void k_gemm4_dma(
+    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
+    int K, long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
+    int tiles_n) {
+  constexpr int BK = 32, TM = 64 * WM;  // tile rows: WM waves of 64 rows along M
+  __shared__ __attribute__((aligned(16))) float As0[TM * BK], As1[TM * BK];
+  __shared__ __attribute__((aligned(16))) float Bs0[BK * BN], Bs1[BK * BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const long long bz = blockIdx.y;
+  const int m0 = tm * TM, n0 = tn * BN;
+  const float *Ag = A + bz * sA + (long long)m0 * lda;
+  const float *Bg = B + bz * sB + n0;
+
+  // Copies.  Wave w copies q = 8 (w & 1) + p, p = 0-7.  A: copy q fills
+  // rows 8q .. 8q + 7, lane L row 8q + L/8, slot L % 8; its swizzle
+  // (r >> 1) & 7 = ((L >> 4) + 4q) & 7 depends on q only through p & 1.
+  // B: copy q fills k-rows 2q, 2q + 1, lane L row 2q + L/32, slot L % 32;
+  // swizzle 4 ((q >> 2) & 3) = 4 (2 (w & 1) + (p >> 2)).  A lane keeps the
+  // two offsets its copies use, indexed by the unrolled p (32-bit: the host
+  // keeps lda and ldb below 2^28).
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool a_role = wv < WM, b_role = wv >= WM && wv < WM + 2;  // the rest copy nothing
+  const int w2 = b_role ? wv - WM : wv;
+  unsigned loff[2];
+  if (b_role) {
+    const int h = lane >> 5, slot = lane & 31;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      loff[u] = (unsigned)h * (unsigned)ldb + (unsigned)((slot ^ (4 * (2 * w2 + u))) * 4);
+  } else {
+    const int r8 = lane >> 3, slot = lane & 7;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int sw = ((lane >> 4) + 4 * u) & 7;
+      loff[u] = (unsigned)r8 * (unsigned)lda + (unsigned)((slot ^ sw) * 4);
+    }
+  }
+  auto issue = [&](float *As_, float *Bs_, int k0) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int q = w2 * 8 + p;
+      if (b_role) {
+        const float *g = Bg + (long long)(k0 + 2 * q) * ldb + loff[p >> 2];
+        __builtin_amdgcn_global_load_lds(g, Bs_ + q * 256, 16, 0, 0);
+      } else if (a_role) {
+        const float *g = Ag + (long long)(8 * q) * lda + k0 + loff[p & 1];
+        __builtin_amdgcn_global_load_lds(g, As_ + q * 256, 16, 0, 0);
+      }
+    }
+  };
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, g = lane >> 4;
+  // Fragments of half-slab s (k = 8 g + 4 s .. + 3 of each lane group).
+  auto read_half = [&](const float *As_, const float *Bs_, int s, f4 (&af)[4], f4 (&bf)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 64 + i * 16 + fr;
+      af[i] = *reinterpret_cast<const f4 *>(As_ + r * BK + (((2 * g + s) ^ ((r >> 1) & 7)) * 4));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int k = g * 8 + s * 4 + t;
+      const int sw = 4 * ((k >> 3) & 3);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn * 64 + j * 16 + fr;
+        bf[j][t] = Bs_[k * BN + (((n >> 2) ^ sw) * 4) + (n & 3)];
+      }
+    }
+  };
+  auto mfma_half = [&](const f4 (&af)[4], const f4 (&bf)[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
+  };
+  // A half-slab's 64 MFMAs with the next half-slab's LDS reads placed one
+  // after each of the first 20 (4 A reads, 16 B reads).
+  auto sched_half = [&]() {
+#pragma unroll
+    for (int m = 0; m < 64; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
+      if (m < 20) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+  };
+
+  // As in k_gemm16_dma: before each slab's barrier the MFMAs of its first
+  // half and the reads of its second half; after it the copy of the slab
+  // two ahead, the MFMAs of the second half and the reads of the next
+  // slab's first half.  Copies past the last slab reload the last slab
+  // into a stage no longer read; reads past it are never used.
+  const int nk = K / BK;
+  f4 f0a[4], f0b[4], f1a[4], f1b[4];
+  issue(As0, Bs0, 0);
+  __syncthreads();
+  issue(As1, Bs1, min(1, nk - 1) * BK);
+  read_half(As0, Bs0, 0, f0a, f0b);
+  for (int kt = 0; kt < nk; kt += 2) {
+    mfma_half(f0a, f0b);
+    read_half(As0, Bs0, 1, f1a, f1b);
+    sched_half();
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    issue(As0, Bs0, min(kt + 2, nk - 1) * BK);
+    mfma_half(f1a, f1b);
+    read_half(As1, Bs1, 0, f0a, f0b);
+    sched_half();
+    asm volatile("" ::: "memory");
+    if (kt + 1 < nk) {
+      mfma_half(f0a, f0b);
+      read_half(As1, Bs1, 1, f1a, f1b);
+      sched_half();
+      asm volatile("" ::: "memory");
+      __syncthreads();
+      issue(As1, Bs1, min(kt + 3, nk - 1) * BK);
+      mfma_half(f1a, f1b);
+      read_half(As0, Bs0, 0, f0a, f0b);
+      sched_half();
+      asm volatile("" ::: "memory");
+    }
+  }
+  __syncthreads();  // no copy into LDS may be in flight when the workgroup ends
+
+  float *Cb = C + bz * sC;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
+        const int col = n0 + wn * 64 + j * 16 + fr;
+        Cb[(long long)row * ldc + col] = acc[i][j][r];
+      }
+}
+
 // ----------------------------------------------------------- integers
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_gemm_int(const T *__restrict__ A, const T *__restrict__ B,
@@ -612,6 +788,22 @@ int launch4(long long batch, int M, int N, int K, const void *A, long long lda, 
   const bool fast = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % V == 0 && ldb % V == 0 &&
                     sA % V == 0 && sB % V == 0 && al(A, 16) && al(B, 16);
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+  if constexpr (__is_same(T, float)) {
+    // the DMA kernel's per-lane copy offsets are 32-bit (7 lda + 28 floats)
+    if (fast && lda < (1LL << 28) && ldb < (1LL << 28)) {
+      if (M % 256 == 0 && GEMM4_WIDE) {  // 256 x 128 tiles, eight waves
+        const dim3 g2((unsigned)((M / 256) * tiles_n), (unsigned)batch);
+        hipLaunchKernelGGL((k_gemm4_dma<4>), g2, dim3(512), 0, mmpi::stream(), (const float *)A,
+                           (const float *)B, (float *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
+                           tiles_n);
+      } else {
+        hipLaunchKernelGGL((k_gemm4_dma<2>), grid, dim3(kBlock), 0, mmpi::stream(),
+                           (const float *)A, (const float *)B, (float *)C, M, N, K, lda, ldb, ldc,
+                           sA, sB, sC, tiles_n);
+      }
+      return mmpi::check_launch("mmp_matmul(mfma4 dma)");
+    }
+  }
   if (fast)
     hipLaunchKernelGGL((k_gemm4<T, false>), grid, dim3(kBlock), 0, mmpi::stream(), (const T *)A,
                        (const T *)B, (T *)C, M, N, K, lda, ldb, ldc, sA, sB, sC, tiles_n);

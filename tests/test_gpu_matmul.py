@@ -70,6 +70,19 @@ def test_matmul_f16_large_tile_exact(batch, m, n, k):
     assert got.dtype == np.float16 and np.array_equal(got.astype(np.float32), want)
 
 
+@pytest.mark.parametrize("batch,m,n,k", [(1, 128, 128, 32), (2, 256, 128, 96), (1, 384, 256, 160),
+                                         (3, 128, 384, 1024), (1, 512, 640, 224)])
+def test_matmul_f32_dma_exact(batch, m, n, k):
+    """Float32 products with 128-divisible extents and 32-divisible k take
+    the global -> LDS copy kernel (swizzled A and B stages, two copy roles,
+    odd and even numbers of 32-deep slabs, batches); integer-valued
+    operands make every product exact, so the result must equal NumPy's."""
+    g = np.random.default_rng(batch * 1000 + k)
+    a = g.integers(-3, 4, (batch, m, k)).astype(np.float32)
+    b = g.integers(-3, 4, (batch, k, n)).astype(np.float32)
+    got = (cp.array(a) @ cp.array(b)).get()
+    assert np.array_equal(got, np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32))
+
 @pytest.mark.parametrize("dtype", [np.int32, np.int64, np.int16, np.uint32])
 def test_matmul_integer_exact(dtype):
     g = np.random.default_rng(1)

@@ -718,6 +718,182 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void k_gemm4_dma(
       }
 }
 
+// 256 x 128 tiles with three LDS stages of 48 KiB (A's 256 x 32 floats,
+// then B's 32 x 128), same layouts and swizzles as k_gemm4_dma.  A slab's
+// 48 one-KiB copies (32 of A, 16 of B) are split six per wave, so every
+// wave copies and none branches on its role inside the loop.  The copy of
+// slab kt + 3 is issued after the barrier that ends the reads of slab kt,
+// into that slab's stage, and waited for two slabs later: each barrier
+// waits until at most this wave's six newest copies (slab kt + 2) are in
+// flight (vmcnt(6)), not for all of them.  Copies past the last slab reload
+// the last slab into a stage never read again, so every wave always has
+// six copies per slab in flight and the count stays exact.
+#ifndef GEMM4_STAGES
+#define GEMM4_STAGES 3
+#endif
+__global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
+    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
+    int K, long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
+    int tiles_n) {
+  constexpr int BK = 32, TM = 256, AS = TM * BK, ST = AS + BK * BN;  // floats per stage
+  __shared__ __attribute__((aligned(16))) float S0[ST], S1[ST], S2[ST];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const long long bz = blockIdx.y;
+  const int m0 = tm * TM, n0 = tn * BN;
+  const float *Ag = A + bz * sA + (long long)m0 * lda;
+  const float *Bg = B + bz * sB + n0;
+
+  // Copy c = 6 w + p lands at 1 KiB x c of a stage.  c < 32: rows 8c .. 8c
+  // + 7 of A, lane L row 8c + L/8, slot L % 8 holding chunk slot ^ sw with
+  // sw = ((L >> 4) + 4c) & 7.  c >= 32, q = c - 32: k-rows 2q, 2q + 1 of B,
+  // lane L row 2q + L/32, slot L % 32 holding chunk slot ^ 4 ((q >> 2) & 3).
+  // The wave-uniform part of each source (a row pointer and the step of one
+  // k) stays scalar; the lane part is a 32-bit byte offset (the host keeps
+  // lda and ldb below 2^27, so 7 lda + 32 floats fit).
+  //
+  // The copies are written as instructions (scalar base + lane offset form;
+  // M0 holds the LDS destination, and an LDS copy may not read M0 in the
+  // cycle after it is written, hence the s_nop) rather than through the
+  // compiler's builtin: the compiler cannot tell which stage an in-flight copy writes
+  // across the loop's back edge and would wait for every copy before the
+  // first LDS read of each pass.  The waits here are the explicit ones.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const float *sb[6];
+  long long ks[6];
+  unsigned vo[6];
+#pragma unroll
+  for (int p = 0; p < 6; ++p) {
+    const int c = wv * 6 + p;
+    if (c < 32) {
+      sb[p] = Ag + (long long)(8 * c) * lda;
+      ks[p] = 1;
+      const int sw = ((lane >> 4) + 4 * c) & 7;
+      vo[p] = ((unsigned)(lane >> 3) * (unsigned)lda + (unsigned)(((lane & 7) ^ sw) * 4)) * 4u;
+    } else {
+      const int q = c - 32;
+      sb[p] = Bg + (long long)(2 * q) * ldb;
+      ks[p] = ldb;
+      const int sw = 4 * ((q >> 2) & 3);
+      vo[p] = ((unsigned)(lane >> 5) * (unsigned)ldb + (unsigned)(((lane & 31) ^ sw) * 4)) * 4u;
+    }
+  }
+  // Sources of a slab's copies, computed ahead of the barrier they follow.
+  auto sources = [&](int k0, const float *(&src)[6]) {
+#pragma unroll
+    for (int p = 0; p < 6; ++p) src[p] = sb[p] + (long long)k0 * ks[p];
+  };
+  auto issue = [&](float *S, const float *(&src)[6]) {
+#pragma unroll
+    for (int p = 0; p < 6; ++p) {
+      const unsigned dst =
+          (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(S + (wv * 6 + p) * 256);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :
+                   : "s"(dst), "v"(vo[p]), "s"(src[p])
+                   : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+  };
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, g = lane >> 4;
+  auto read_half = [&](const float *S, int s, f4 (&af)[4], f4 (&bf)[4]) {
+    const float *Bs_ = S + AS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 64 + i * 16 + fr;
+      af[i] = *reinterpret_cast<const f4 *>(S + r * BK + (((2 * g + s) ^ ((r >> 1) & 7)) * 4));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int k = g * 8 + s * 4 + t;
+      const int sw = 4 * ((k >> 3) & 3);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn * 64 + j * 16 + fr;
+        bf[j][t] = Bs_[k * BN + (((n >> 2) ^ sw) * 4) + (n & 3)];
+      }
+    }
+  };
+  auto mfma_half = [&](const f4 (&af)[4], const f4 (&bf)[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
+  };
+  auto sched_half = [&]() {
+#pragma unroll
+    for (int m = 0; m < 64; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
+      if (m < 20) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+  };
+
+  const int nk = K / BK;
+  f4 f0a[4], f0b[4], f1a[4], f1b[4];
+  const float *src[6];
+  sources(0, src);
+  issue(S0, src);
+  sources(min(1, nk - 1) * BK, src);
+  issue(S1, src);
+  sources(min(2, nk - 1) * BK, src);
+  issue(S2, src);
+  asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");  // slab 0 landed everywhere
+  read_half(S0, 0, f0a, f0b);
+  // One slab: the MFMAs of its first half with the reads of its second; a
+  // barrier once slab kt + 1 has landed and every wave has read slab kt; the
+  // copy of slab kt + 3 into slab kt's stage; the second half's MFMAs with
+  // the reads of the first half of slab kt + 1.
+  auto slab = [&](float *cur, const float *nxt, int kt) {
+    mfma_half(f0a, f0b);
+    read_half(cur, 1, f1a, f1b);
+    sources(min(kt + 3, nk - 1) * BK, src);
+    sched_half();
+    __builtin_amdgcn_sched_barrier(0);  // the half's MFMAs stay ahead of the barrier
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(cur, src);
+    mfma_half(f1a, f1b);
+    read_half(nxt, 0, f0a, f0b);
+    sched_half();
+    asm volatile("" ::: "memory");
+  };
+  for (int kt = 0; kt < nk; kt += 3) {
+    slab(S0, S1, kt);
+    if (kt + 1 < nk) {
+      slab(S1, S2, kt + 1);
+      if (kt + 2 < nk) slab(S2, S0, kt + 2);
+    }
+  }
+  // no copy into LDS may be in flight when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+  float *Cb = C + bz * sC;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
+        const int col = n0 + wn * 64 + j * 16 + fr;
+        Cb[(long long)row * ldc + col] = acc[i][j][r];
+      }
+}
+
 // ----------------------------------------------------------- integers
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_gemm_int(const T *__restrict__ A, const T *__restrict__ B,
@@ -793,9 +969,14 @@ int launch4(long long batch, int M, int N, int K, const void *A, long long lda, 
     if (fast && lda < (1LL << 28) && ldb < (1LL << 28)) {
       if (M % 256 == 0 && GEMM4_WIDE) {  // 256 x 128 tiles, eight waves
         const dim3 g2((unsigned)((M / 256) * tiles_n), (unsigned)batch);
-        hipLaunchKernelGGL((k_gemm4_dma<4>), g2, dim3(512), 0, mmpi::stream(), (const float *)A,
-                           (const float *)B, (float *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
-                           tiles_n);
+        if (GEMM4_STAGES == 3 && lda < (1LL << 27) && ldb < (1LL << 27))
+          hipLaunchKernelGGL(k_gemm4_dma3, g2, dim3(512), 0, mmpi::stream(), (const float *)A,
+                             (const float *)B, (float *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
+                             tiles_n);
+        else
+          hipLaunchKernelGGL((k_gemm4_dma<4>), g2, dim3(512), 0, mmpi::stream(),
+                             (const float *)A, (const float *)B, (float *)C, M, N, K, lda, ldb,
+                             ldc, sA, sB, sC, tiles_n);
       } else {
         hipLaunchKernelGGL((k_gemm4_dma<2>), grid, dim3(kBlock), 0, mmpi::stream(),
                            (const float *)A, (const float *)B, (float *)C, M, N, K, lda, ldb, ldc,

@@ -71,17 +71,42 @@ def test_matmul_f16_large_tile_exact(batch, m, n, k):
 
 
 @pytest.mark.parametrize("batch,m,n,k", [(1, 128, 128, 32), (2, 256, 128, 96), (1, 384, 256, 160),
-                                         (3, 128, 384, 1024), (1, 512, 640, 224)])
+                                         (3, 128, 384, 1024), (1, 512, 640, 224), (1, 256, 128, 32),
+                                         (2, 256, 256, 64), (1, 256, 384, 160), (1, 768, 128, 320)])
 def test_matmul_f32_dma_exact(batch, m, n, k):
     """Float32 products with 128-divisible extents and 32-divisible k take
-    the global -> LDS copy kernel (swizzled A and B stages, two copy roles,
-    odd and even numbers of 32-deep slabs, batches); integer-valued
-    operands make every product exact, so the result must equal NumPy's."""
+    the global -> LDS copy kernels: 128-row tiles with two stages, and
+    256-row tiles with three stages, where one to ten 32-deep slabs leave
+    every remainder of the three-slab loop.  Integer-valued operands make
+    every product exact, so the result must equal NumPy's."""
     g = np.random.default_rng(batch * 1000 + k)
     a = g.integers(-3, 4, (batch, m, k)).astype(np.float32)
     b = g.integers(-3, 4, (batch, k, n)).astype(np.float32)
     got = (cp.array(a) @ cp.array(b)).get()
     assert np.array_equal(got, np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("batch,m,n,k,pad", [(1, 256, 128, 96, 32), (2, 512, 256, 128, 4),
+                                             (1, 256, 384, 64, 128), (2, 128, 128, 64, 36)])
+def test_matmul_f32_dma_row_strides(batch, m, n, k, pad):
+    """mmp_matmul with row strides wider than the product (lda = k + pad,
+    ldb = n + pad, ldc = n + 4) and batch strides of whole padded matrices:
+    the copy kernels address every row from the row stride, not from k or
+    n, and leave the padding of C untouched."""
+    from macmetalpy_amd._backend import HipBackend
+    from macmetalpy_amd._dtypes import dtype_code
+    g = np.random.default_rng(m + n + k + pad)
+    af = g.integers(-3, 4, (batch, m, k + pad)).astype(np.float32)
+    bf = g.integers(-3, 4, (batch, k, n + pad)).astype(np.float32)
+    cf = np.full((batch, m, n + 4), 7.0, np.float32)
+    da, db, dc = (cp.array(x)._ensure_gpu() for x in (af, bf, cf))  # device-resident
+    HipBackend().matmul(dtype_code(np.dtype(np.float32)), batch, m, n, k,
+                        da._ptr, k + pad, m * (k + pad), db._ptr, n + pad, k * (n + pad),
+                        dc._ptr, n + 4, m * (n + 4))
+    got = dc.get()
+    want = np.matmul(af[:, :, :k].astype(np.float64), bf[:, :, :n].astype(np.float64))
+    assert np.array_equal(got[:, :, :n], want.astype(np.float32))
+    assert np.all(got[:, :, n:] == 7.0)
 
 @pytest.mark.parametrize("dtype", [np.int32, np.int64, np.int16, np.uint32])
 def test_matmul_integer_exact(dtype):

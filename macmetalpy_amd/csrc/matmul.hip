@@ -25,8 +25,10 @@
 //    k slot a lane feeds is permuted (MFMA step t, lane group g consumes
 //    k = KG*g + t), so a lane's A values for a whole slab are contiguous in
 //    LDS and B keeps its natural n-contiguous layout.  float32 products with
-//    128-divisible extents and 16-byte aligned rows use k_gemm4_dma
-//    (operands copied global -> LDS, swizzled stages).
+//    128-divisible extents and 16-byte aligned rows copy operands global ->
+//    LDS into swizzled stages: k_gemm4_dma3 (256 x 128 tiles, persistent,
+//    three stages) when the tiles fill whole rounds of the CUs, else
+//    k_gemm4_dma (128 x 128 tiles).
 // Partial tiles and unaligned operands use guarded scalar loads (zero fill)
 // and guarded stores.  Integer matmul: LDS-tiled exact kernel with
 // wrap-around arithmetic (NumPy's integer matmul wraps).
@@ -548,15 +550,14 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm4(const T *__restrict__ A, co
 }
 
 // ------------------------------------------- float32, global -> LDS DMA
-// (64 WM) x 128 output tile per workgroup of 2 WM waves (WM along M, two
-// along N, each 64 x 64 = 4 x 4 MFMA tiles of v_mfma_f32_16x16x4f32) for
-// operands whose extents divide the tile and the 32-float slab and whose
-// rows are 16-byte aligned: WM = 4 (256 x 128, eight waves, one workgroup
-// per CU) when M divides by 256, else WM = 2 (128 x 128, four waves, two
-// per CU).  Operands are copied HBM/L2 -> LDS with global_load_lds_dwordx4
-// (lane L of a wave's copy lands at 16 B x L of its destination): no
-// register staging, no ds_write.  Two LDS stages; waves 0 .. WM-1 copy A
-// (eight 1 KiB copies each per slab), the next two copy B, any others none.
+// 128 x 128 output tile per workgroup of four waves (two along M, two
+// along N, each 64 x 64 = 4 x 4 MFMA tiles of v_mfma_f32_16x16x4f32; two
+// workgroups per CU) for operands whose extents divide the tile and the
+// 32-float slab and whose rows are 16-byte aligned, where the 256 x 128
+// kernel below does not fill the CUs.  Operands are copied HBM/L2 -> LDS
+// with global_load_lds_dwordx4 (lane L of a wave's copy lands at 16 B x L
+// of its destination): no register staging, no ds_write.  Two LDS stages;
+// waves 0-1 copy A (eight 1 KiB copies each per slab), waves 2-3 copy B.
 // The MFMA's k slot is permuted as in k_gemm4 (lane group g feeds
 // k = 8 g + t), so a lane's A values of a half-slab are one 16-byte chunk.
 //  * A stage: 128 rows x 32 floats (128 B, k-contiguous as in HBM); chunk c
@@ -569,12 +570,11 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm4(const T *__restrict__ A, co
 //    wave's copies), the copy of the slab two ahead issued right after it
 //    into the stage just consumed, fragment reads half a slab ahead of the
 //    MFMAs.
-template <int WM>
-__global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void k_gemm4_dma(
+__global__ __launch_bounds__(256, 2) void k_gemm4_dma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
     int K, long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
     int tiles_n) {
-  constexpr int BK = 32, TM = 64 * WM;  // tile rows: WM waves of 64 rows along M
+  constexpr int WM = 2, BK = 32, TM = 64 * WM;  // tile rows: WM waves of 64 rows along M
   __shared__ __attribute__((aligned(16))) float As0[TM * BK], As1[TM * BK];
   __shared__ __attribute__((aligned(16))) float Bs0[BK * BN], Bs1[BK * BN];
 
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void k_gemm4_dma(
   // two offsets its copies use, indexed by the unrolled p (32-bit: the host
   // keeps lda and ldb below 2^28).
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const bool a_role = wv < WM, b_role = wv >= WM && wv < WM + 2;  // the rest copy nothing
+  const bool a_role = wv < WM, b_role = wv >= WM;
   const int w2 = b_role ? wv - WM : wv;
   unsigned loff[2];
   if (b_role) {
@@ -721,69 +721,130 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void k_gemm4_dma(
 // 256 x 128 tiles with three LDS stages of 48 KiB (A's 256 x 32 floats,
 // then B's 32 x 128), same layouts and swizzles as k_gemm4_dma.  A slab's
 // 48 one-KiB copies (32 of A, 16 of B) are split six per wave, so every
-// wave copies and none branches on its role inside the loop.  The copy of
-// slab kt + 3 is issued after the barrier that ends the reads of slab kt,
-// into that slab's stage, and waited for two slabs later: each barrier
-// waits until at most this wave's six newest copies (slab kt + 2) are in
-// flight (vmcnt(6)), not for all of them.  Copies past the last slab reload
-// the last slab into a stage never read again, so every wave always has
-// six copies per slab in flight and the count stays exact.
-#ifndef GEMM4_STAGES
-#define GEMM4_STAGES 3
+// wave copies and none branches on its role inside the loop.
+//
+// Persistent: one workgroup per CU walks a list of tiles, and its slabs
+// form one stream across them.  The copy of stream slab s + 3 is issued
+// after the barrier that ends the reads of slab s, into that slab's stage,
+// and waited for two slabs later: each barrier waits until at most this
+// wave's six newest copies (slab s + 2) are in flight (vmcnt(6)), not for
+// all of them.  So the next tile's first slabs are in flight while the
+// current tile finishes, and a tile's C stores overlap the next tile's
+// MFMAs; the barrier after a tile's stores waits for everything (vmcnt(0):
+// stores and copies need not complete in issue order).  Copies past the
+// last slab reload the last slab into a stage never read again, so every
+// wave always has six copies per slab in flight and the count stays exact.
+#ifndef GEMM4_XCD
+#define GEMM4_XCD 1
+#endif
+#ifndef GEMM4_PERSIST
+#define GEMM4_PERSIST 1
 #endif
 __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
-    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
-    int K, long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
-    int tiles_n) {
+    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int K,
+    long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
+    int tiles_n, int per_b, int T) {
   constexpr int BK = 32, TM = 256, AS = TM * BK, ST = AS + BK * BN;  // floats per stage
   __shared__ __attribute__((aligned(16))) float S0[ST], S1[ST], S2[ST];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
-  const long long bz = blockIdx.y;
-  const int m0 = tm * TM, n0 = tn * BN;
-  const float *Ag = A + bz * sA + (long long)m0 * lda;
-  const float *Bg = B + bz * sB + n0;
+
+  // Tile order.  Workgroups are dispatched to the eight XCDs round-robin
+  // (workgroup w to XCD w % 8); when the tile count and the grid divide by
+  // 8, the workgroups of XCD x share the contiguous range x T/8 .. (x + 1)
+  // T/8 - 1 of the order below, in turn, instead of every eighth tile.  The
+  // order runs batch by batch and, within a batch, over groups of four tile
+  // rows, column by column, so the 32 workgroups an XCD runs at a time
+  // share their operand slabs in its L2 (a 4 x 8 block of one product, or
+  // one whole product of a batch of small ones).
+  const int P = gridDim.x, w = blockIdx.x;
+  int tfirst, tstep, nt;
+  if (GEMM4_XCD && (T & 7) == 0 && (P & 7) == 0) {
+    const int q = T >> 3, ps = P >> 3, s = w >> 3;
+    tfirst = (w & 7) * q + s;
+    tstep = ps;
+    nt = s < q ? (q - 1 - s) / ps + 1 : 0;
+  } else {
+    tfirst = w;
+    tstep = P;
+    nt = w < T ? (T - 1 - w) / P + 1 : 0;
+  }
+  if (nt == 0) return;  // the whole workgroup, before any barrier
+  auto decode = [&](int i, long long &bz, int &m0, int &n0) {
+    const int t = tfirst + i * tstep;
+    bz = t / per_b;
+    const int r = t - (int)bz * per_b;
+    const int tiles_m = per_b / tiles_n;
+    const int rows = GEMM4_XCD ? 4 : 1;  // tile rows per group (1: row-major order)
+    const int first = (r / (rows * tiles_n)) * rows, gsize = min(rows, tiles_m - first);
+    const int local = r - first * tiles_n;
+    m0 = (first + local % gsize) * TM;
+    n0 = (local / gsize) * BN;
+  };
 
   // Copy c = 6 w + p lands at 1 KiB x c of a stage.  c < 32: rows 8c .. 8c
   // + 7 of A, lane L row 8c + L/8, slot L % 8 holding chunk slot ^ sw with
   // sw = ((L >> 4) + 4c) & 7.  c >= 32, q = c - 32: k-rows 2q, 2q + 1 of B,
   // lane L row 2q + L/32, slot L % 32 holding chunk slot ^ 4 ((q >> 2) & 3).
-  // The wave-uniform part of each source (a row pointer and the step of one
-  // k) stays scalar; the lane part is a 32-bit byte offset (the host keeps
-  // lda and ldb below 2^27, so 7 lda + 32 floats fit).
+  // The wave-uniform part of each source (panel, row and slab offsets)
+  // stays scalar; the lane part is a 32-bit byte offset (the host keeps lda
+  // and ldb below 2^27, so 7 lda + 32 floats fit).
   //
   // The copies are written as instructions (scalar base + lane offset form;
   // M0 holds the LDS destination, and an LDS copy may not read M0 in the
   // cycle after it is written, hence the s_nop) rather than through the
-  // compiler's builtin: the compiler cannot tell which stage an in-flight copy writes
-  // across the loop's back edge and would wait for every copy before the
-  // first LDS read of each pass.  The waits here are the explicit ones.
+  // compiler's builtin: the compiler cannot tell which stage an in-flight
+  // copy writes across the loop's back edge and would wait for every copy
+  // before the first LDS read of each pass.  The waits here are the
+  // explicit ones.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const float *sb[6];
-  long long ks[6];
+  bool isA[6];
+  long long off[6], ks[6];
   unsigned vo[6];
 #pragma unroll
   for (int p = 0; p < 6; ++p) {
     const int c = wv * 6 + p;
+    isA[p] = c < 32;
     if (c < 32) {
-      sb[p] = Ag + (long long)(8 * c) * lda;
+      off[p] = (long long)(8 * c) * lda;
       ks[p] = 1;
       const int sw = ((lane >> 4) + 4 * c) & 7;
       vo[p] = ((unsigned)(lane >> 3) * (unsigned)lda + (unsigned)(((lane & 7) ^ sw) * 4)) * 4u;
     } else {
       const int q = c - 32;
-      sb[p] = Bg + (long long)(2 * q) * ldb;
+      off[p] = (long long)(2 * q) * ldb;
       ks[p] = ldb;
       const int sw = 4 * ((q >> 2) & 3);
       vo[p] = ((unsigned)(lane >> 5) * (unsigned)ldb + (unsigned)(((lane & 31) ^ sw) * 4)) * 4u;
     }
   }
-  // Sources of a slab's copies, computed ahead of the barrier they follow.
-  auto sources = [&](int k0, const float *(&src)[6]) {
+  const int nk = K / BK;
+  // The copy stream: tile ci of the list, its slab ck, and that tile's
+  // operand panels.
+  int ci = 0, ck = 0;
+  const float *cA, *cB;
+  auto copy_tile = [&]() {
+    long long bz;
+    int m0, n0;
+    decode(ci, bz, m0, n0);
+    cA = A + bz * sA + (long long)m0 * lda;
+    cB = B + bz * sB + n0;
+  };
+  copy_tile();
+  // Sources of the next slab of the copy stream (computed ahead of the
+  // barrier they follow), then advance; after the last slab of the last
+  // tile the stream stays on it.
+  auto next_sources = [&](const float *(&src)[6]) {
 #pragma unroll
-    for (int p = 0; p < 6; ++p) src[p] = sb[p] + (long long)k0 * ks[p];
+    for (int p = 0; p < 6; ++p) src[p] = (isA[p] ? cA : cB) + off[p] + (long long)(ck * BK) * ks[p];
+    if (ck + 1 < nk) {
+      ++ck;
+    } else if (ci + 1 < nt) {
+      ++ci;
+      ck = 0;
+      copy_tile();
+    }
   };
   auto issue = [&](float *S, const float *(&src)[6]) {
 #pragma unroll
@@ -842,56 +903,74 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
     }
   };
 
-  const int nk = K / BK;
   f4 f0a[4], f0b[4], f1a[4], f1b[4];
   const float *src[6];
-  sources(0, src);
+  next_sources(src);
   issue(S0, src);
-  sources(min(1, nk - 1) * BK, src);
+  next_sources(src);
   issue(S1, src);
-  sources(min(2, nk - 1) * BK, src);
+  next_sources(src);
   issue(S2, src);
   asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");  // slab 0 landed everywhere
   read_half(S0, 0, f0a, f0b);
+  int kt = 0, ti = 0;  // the compute stream: slab kt of tile ti
+  bool stored = false;  // C stores issued since the last barrier
   // One slab: the MFMAs of its first half with the reads of its second; a
-  // barrier once slab kt + 1 has landed and every wave has read slab kt; the
-  // copy of slab kt + 3 into slab kt's stage; the second half's MFMAs with
-  // the reads of the first half of slab kt + 1.
-  auto slab = [&](float *cur, const float *nxt, int kt) {
+  // barrier once the next slab has landed and every wave has read this one;
+  // the copy three slabs ahead into this slab's stage; the second half's
+  // MFMAs with the reads of the first half of the next slab; after a tile's
+  // last slab, its C stores.
+  auto slab = [&](float *cur, const float *nxt) {
     mfma_half(f0a, f0b);
     read_half(cur, 1, f1a, f1b);
-    sources(min(kt + 3, nk - 1) * BK, src);
+    next_sources(src);
     sched_half();
     __builtin_amdgcn_sched_barrier(0);  // the half's MFMAs stay ahead of the barrier
-    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (stored)
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+    stored = false;
     issue(cur, src);
     mfma_half(f1a, f1b);
     read_half(nxt, 0, f0a, f0b);
     sched_half();
     asm volatile("" ::: "memory");
-  };
-  for (int kt = 0; kt < nk; kt += 3) {
-    slab(S0, S1, kt);
     if (kt + 1 < nk) {
-      slab(S1, S2, kt + 1);
-      if (kt + 2 < nk) slab(S2, S0, kt + 2);
+      ++kt;
+    } else {
+      long long bz;
+      int m0, n0;
+      decode(ti, bz, m0, n0);
+      float *Cb = C + bz * sC;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
+            const int col = n0 + wn * 64 + j * 16 + fr;
+            Cb[(long long)row * ldc + col] = acc[i][j][r];
+          }
+          acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+      ++ti;
+      kt = 0;
+      stored = true;
+    }
+  };
+  const int total = nt * nk;
+  for (int s = 0; s < total; s += 3) {
+    slab(S0, S1);
+    if (s + 1 < total) {
+      slab(S1, S2);
+      if (s + 2 < total) slab(S2, S0);
     }
   }
   // no copy into LDS may be in flight when the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-
-  float *Cb = C + bz * sC;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
-        const int col = n0 + wn * 64 + j * 16 + fr;
-        Cb[(long long)row * ldc + col] = acc[i][j][r];
-      }
 }
 
 // ----------------------------------------------------------- integers
@@ -967,18 +1046,21 @@ int launch4(long long batch, int M, int N, int K, const void *A, long long lda, 
   if constexpr (__is_same(T, float)) {
     // the DMA kernel's per-lane copy offsets are 32-bit (7 lda + 28 floats)
     if (fast && lda < (1LL << 28) && ldb < (1LL << 28)) {
-      if (M % 256 == 0 && GEMM4_WIDE) {  // 256 x 128 tiles, eight waves
-        const dim3 g2((unsigned)((M / 256) * tiles_n), (unsigned)batch);
-        if (GEMM4_STAGES == 3 && lda < (1LL << 27) && ldb < (1LL << 27))
-          hipLaunchKernelGGL(k_gemm4_dma3, g2, dim3(512), 0, mmpi::stream(), (const float *)A,
-                             (const float *)B, (float *)C, M, N, K, lda, ldb, ldc, sA, sB, sC,
-                             tiles_n);
-        else
-          hipLaunchKernelGGL((k_gemm4_dma<4>), g2, dim3(512), 0, mmpi::stream(),
-                             (const float *)A, (const float *)B, (float *)C, M, N, K, lda, ldb,
-                             ldc, sA, sB, sC, tiles_n);
+      // 256 x 128 tiles (one persistent workgroup per CU) when the tiles fill
+      // whole rounds of the CUs, or nearly; otherwise 128 x 128 tiles, whose
+      // finer grain leaves fewer CUs idle in the last round (2048^2: 128
+      // wide tiles for 256 CUs; 6144^2: 4.5 rounds).
+      const long long cus = mmpi::cu_count() > 0 ? mmpi::cu_count() : 256;
+      const long long wide_tiles = M % 256 == 0 ? (long long)(M / 256) * tiles_n * batch : 0;
+      const long long rounds = (wide_tiles + cus - 1) / cus;
+      if (GEMM4_WIDE && wide_tiles > 0 && wide_tiles < (1LL << 30) && lda < (1LL << 27) &&
+          ldb < (1LL << 27) && wide_tiles * 100 >= rounds * cus * 97) {
+        const long long P = GEMM4_PERSIST && wide_tiles > cus ? cus : wide_tiles;
+        hipLaunchKernelGGL(k_gemm4_dma3, dim3((unsigned)P), dim3(512), 0, mmpi::stream(),
+                           (const float *)A, (const float *)B, (float *)C, K, lda, ldb, ldc, sA,
+                           sB, sC, tiles_n, (int)((M / 256) * tiles_n), (int)wide_tiles);
       } else {
-        hipLaunchKernelGGL((k_gemm4_dma<2>), grid, dim3(kBlock), 0, mmpi::stream(),
+        hipLaunchKernelGGL(k_gemm4_dma, grid, dim3(kBlock), 0, mmpi::stream(),
                            (const float *)A, (const float *)B, (float *)C, M, N, K, lda, ldb, ldc,
                            sA, sB, sC, tiles_n);
       }

@@ -70,20 +70,44 @@ def test_matmul_f16_large_tile_exact(batch, m, n, k):
     assert got.dtype == np.float16 and np.array_equal(got.astype(np.float32), want)
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(1, 128, 128, 32), (2, 256, 128, 96), (1, 384, 256, 160),
-                                         (3, 128, 384, 1024), (1, 512, 640, 224), (1, 256, 128, 32),
-                                         (2, 256, 256, 64), (1, 256, 384, 160), (1, 768, 128, 320)])
-def test_matmul_f32_dma_exact(batch, m, n, k):
-    """Float32 products with 128-divisible extents and 32-divisible k take
-    the global -> LDS copy kernels: 128-row tiles with two stages, and
-    256-row tiles with three stages, where one to ten 32-deep slabs leave
-    every remainder of the three-slab loop.  Integer-valued operands make
-    every product exact, so the result must equal NumPy's."""
-    g = np.random.default_rng(batch * 1000 + k)
+def _exact_f32_product(batch, m, n, k, seed):
+    g = np.random.default_rng(seed)
     a = g.integers(-3, 4, (batch, m, k)).astype(np.float32)
     b = g.integers(-3, 4, (batch, k, n)).astype(np.float32)
     got = (cp.array(a) @ cp.array(b)).get()
     assert np.array_equal(got, np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("batch,m,n,k", [(1, 128, 128, 32), (2, 256, 128, 96), (1, 384, 256, 160),
+                                         (3, 128, 384, 1024), (1, 512, 640, 224), (1, 256, 128, 32),
+                                         (2, 256, 256, 64), (1, 768, 128, 320), (300, 256, 128, 64)])
+def test_matmul_f32_dma_exact(batch, m, n, k):
+    """Float32 products with 128-divisible extents and 32-divisible k whose
+    256-row tiles would leave CUs idle take the 128 x 128 global -> LDS copy
+    kernel (one to 32 slabs of 32, batches).  Integer-valued operands make
+    every product exact, so the result must equal NumPy's."""
+    _exact_f32_product(batch, m, n, k, batch * 1000 + k)
+
+
+# (tiles per CU, tile rows of 256, tile columns of 128, k): the batch is set
+# so the 256 x 128 tiles fill whole rounds of the device's CUs.
+@pytest.mark.parametrize("rounds,tm,tn,k", [(1, 1, 1, 32), (2, 1, 1, 32), (3, 1, 1, 64), (2, 1, 2, 96),
+                                            (2, 2, 2, 160), (3, 3, 4, 320), (3, 6, 4, 96)])
+def test_matmul_f32_persistent_exact(rounds, tm, tn, k):
+    """Products whose 256 x 128 tiles fill whole rounds of the CUs take the
+    persistent three-stage kernel: one workgroup per CU runs `rounds` tiles
+    in one slab stream, so tile ends fall at every position of the
+    three-slab loop (tiles of 1, 2, 3, 5 and 10 slabs; C stored after every
+    slab with 1), tile counts divisible by 8 take the XCD ranges, and the
+    four-row tile groups end with a group of two or three rows.
+    Integer-valued operands make every product exact, so the result must
+    equal NumPy's."""
+    from macmetalpy_amd._backend import HipBackend
+    cus = HipBackend().device_info()["cu_count"]
+    per_b = tm * tn
+    if (rounds * cus) % per_b:
+        pytest.skip(f"{cus} CUs do not divide into whole products of {per_b} tiles")
+    _exact_f32_product(rounds * cus // per_b, 256 * tm, 128 * tn, k, rounds * 100 + k)
 
 
 @pytest.mark.parametrize("batch,m,n,k,pad", [(1, 256, 128, 96, 32), (2, 512, 256, 128, 4),

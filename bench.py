@@ -232,6 +232,46 @@ def vendor_copy(cp, be, reps=20):
     return res
 
 
+_VENDOR_GEMM = r"""
+import json, torch
+torch.backends.cuda.matmul.allow_tf32 = False
+out = {}
+for name, (m, n, k, b), dt in (("f32", (4096, 4096, 4096, 1), torch.float32),
+                               ("f16", (8192, 8192, 8192, 1), torch.float16),
+                               ("batched", (1024, 1024, 1024, 64), torch.float32)):
+    g = torch.Generator(device="cuda").manual_seed(1)
+    a = torch.randn((b, m, k) if b > 1 else (m, k), device="cuda", dtype=dt, generator=g)
+    c = torch.randn((b, k, n) if b > 1 else (k, n), device="cuda", dtype=dt, generator=g)
+    for _ in range(10):
+        r = a @ c
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(REPS):
+        r = a @ c
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / REPS
+    out[name] = {"kernel_ms": round(ms, 4), "tflops": round(2.0 * m * n * k * b / ms / 1e9, 2)}
+    del a, c, r
+print(json.dumps(out))
+"""
+
+
+def vendor_gemm(cp, be, reps=20):
+    """torch.matmul (hipBLASLt; TF32 off) on the C4 shapes, for scale: float32
+    4096^3, float16 8192^3 and batched float32 64 x 1024^3, ``reps``
+    back-to-back calls between two torch events after 10 warm-up calls.  It
+    runs in a child process (torch does not share the device with this
+    process's HIP context) and is opt-in: ``--config vendor_gemm``."""
+    import subprocess
+    p = subprocess.run([sys.executable, "-c", _VENDOR_GEMM.replace("REPS", str(int(reps)))],
+                       capture_output=True, text=True, timeout=900)
+    if p.returncode != 0:
+        raise RuntimeError(f"torch child exited {p.returncode}: {p.stderr[-300:]}")
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def bench_c2_end_to_end(cp, be, reps=5):
     """The C2 calls timed end to end from Python, as the reference's
     bench_core.py:291-297 times `cp_func(data).get()`: ``call_sync_ms`` is a
@@ -1430,6 +1470,8 @@ CONFIG_SECTIONS = {
     "indexing_manipulation": bench_indexing, "linalg": bench_linalg,
     "routines": bench_routines,
 }
+# sections that only run when named with --config
+OPT_IN_SECTIONS = {"vendor_gemm": vendor_gemm}
 
 
 def main():
@@ -1442,7 +1484,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=ONLY_OPS, default=None,
                     help="run one headline op `--steps` times and exit (profiling)")
-    ap.add_argument("--config", choices=sorted(CONFIG_SECTIONS), default=None,
+    ap.add_argument("--config", choices=sorted({**CONFIG_SECTIONS, **OPT_IN_SECTIONS}), default=None,
                     help="run one configuration section, print its JSON and exit (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -1457,7 +1499,8 @@ def main():
         run_only(cp, be, args.only, args.steps)
         return
     if args.config:
-        print(json.dumps({args.config: CONFIG_SECTIONS[args.config](cp, be)}), flush=True)
+        fn = {**CONFIG_SECTIONS, **OPT_IN_SECTIONS}[args.config]
+        print(json.dumps({args.config: fn(cp, be)}), flush=True)
         return
 
     c2 = bench_c2(cp, be, args.steps, args.warmup)

@@ -232,41 +232,58 @@ def vendor_copy(cp, be, reps=20):
     return res
 
 
-_VENDOR_GEMM = r"""
+_VENDOR_TORCH = r"""
 import json, torch
 torch.backends.cuda.matmul.allow_tf32 = False
-out = {}
-for name, (m, n, k, b), dt in (("f32", (4096, 4096, 4096, 1), torch.float32),
-                               ("f16", (8192, 8192, 8192, 1), torch.float16),
-                               ("batched", (1024, 1024, 1024, 64), torch.float32)):
-    g = torch.Generator(device="cuda").manual_seed(1)
-    a = torch.randn((b, m, k) if b > 1 else (m, k), device="cuda", dtype=dt, generator=g)
-    c = torch.randn((b, k, n) if b > 1 else (k, n), device="cuda", dtype=dt, generator=g)
-    for _ in range(10):
-        r = a @ c
+out = {"torch": torch.__version__, "elementwise_2p28": {}, "gemm": {}}
+
+
+def timed(f, warm, reps):
+    for _ in range(warm):
+        f()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(REPS):
-        r = a @ c
+    for _ in range(reps):
+        f()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / REPS
-    out[name] = {"kernel_ms": round(ms, 4), "tflops": round(2.0 * m * n * k * b / ms / 1e9, 2)}
-    del a, c, r
+    return e0.elapsed_time(e1) / reps
+
+
+n = 1 << 28
+g = torch.Generator(device="cuda").manual_seed(2)
+a = torch.randn(n, device="cuda", generator=g)
+b = torch.randn(n, device="cuda", generator=g)
+c = torch.empty_like(a)
+for name, f, bpe in (("copy", lambda: c.copy_(a), 8), ("add", lambda: torch.add(a, b, out=c), 12),
+                     ("sin", lambda: torch.sin(a, out=c), 8)):
+    ms = timed(f, 3, REPS)
+    out["elementwise_2p28"][name] = {"ms": round(ms, 4), "gbs": round(bpe * n / ms / 1e6, 1)}
+del a, b, c
+for name, (m, nn, k, bt), dt in (("f32", (4096, 4096, 4096, 1), torch.float32),
+                                 ("f16", (8192, 8192, 8192, 1), torch.float16),
+                                 ("batched", (1024, 1024, 1024, 64), torch.float32)):
+    a = torch.randn((bt, m, k) if bt > 1 else (m, k), device="cuda", dtype=dt, generator=g)
+    c = torch.randn((bt, k, nn) if bt > 1 else (k, nn), device="cuda", dtype=dt, generator=g)
+    ms = timed(lambda: a @ c, 10, REPS)
+    out["gemm"][name] = {"kernel_ms": round(ms, 4), "tflops": round(2.0 * m * nn * k * bt / ms / 1e9, 2)}
+    del a, c
 print(json.dumps(out))
 """
 
 
-def vendor_gemm(cp, be, reps=20):
-    """torch.matmul (hipBLASLt; TF32 off) on the C4 shapes, for scale: float32
-    4096^3, float16 8192^3 and batched float32 64 x 1024^3, ``reps``
-    back-to-back calls between two torch events after 10 warm-up calls.  It
-    runs in a child process (torch does not share the device with this
-    process's HIP context) and is opt-in: ``--config vendor_gemm``."""
+def vendor_torch(cp, be, reps=20):
+    """The vendor's own paths on the same device, for scale: torch's copy_,
+    add and sin over 2^28 float32 (GB/s of the algorithmic bytes, as C2) and
+    torch.matmul (hipBLASLt; TF32 off) on the C4 shapes -- float32 4096^3,
+    float16 8192^3, batched float32 64 x 1024^3 -- each ``reps`` back-to-back
+    calls between two torch events after a warm-up (3 calls elementwise, 10
+    matmul, as c4_matmul).  It runs in a child process: torch does not
+    share the device with this process's HIP context."""
     import subprocess
-    p = subprocess.run([sys.executable, "-c", _VENDOR_GEMM.replace("REPS", str(int(reps)))],
-                       capture_output=True, text=True, timeout=900)
+    p = subprocess.run([sys.executable, "-c", _VENDOR_TORCH.replace("REPS", str(int(reps)))],
+                       capture_output=True, text=True, timeout=600)
     if p.returncode != 0:
         raise RuntimeError(f"torch child exited {p.returncode}: {p.stderr[-300:]}")
     return json.loads(p.stdout.strip().splitlines()[-1])
@@ -1468,10 +1485,27 @@ CONFIG_SECTIONS = {
     "c5_fusion_chain": bench_c5, "logic_where_clip_2p28": bench_logic,
     "nan_reductions_16384sq": bench_nan, "sort_searchsorted": bench_sort,
     "indexing_manipulation": bench_indexing, "linalg": bench_linalg,
-    "routines": bench_routines,
+    "routines": bench_routines, "vendor_torch": vendor_torch,
 }
-# sections that only run when named with --config
-OPT_IN_SECTIONS = {"vendor_gemm": vendor_gemm}
+
+
+def _vendor_ratios(out, cfgs):
+    """Beside each C2 op and C4 product, the same run's vendor rate and
+    this library's rate over it (vendor_torch: torch / hipBLASLt)."""
+    v = cfgs.get("vendor_torch")
+    if not isinstance(v, dict) or "gemm" not in v:
+        return
+    for op, name in (("add_f32", "add"), ("sin_f32", "sin")):
+        t = v["elementwise_2p28"].get(name)
+        if t and op in out.get("per_op", {}):
+            d = out["per_op"][op]
+            d["torch_gbs"] = t["gbs"]
+            d["vs_torch"] = round(d["gbs"] / t["gbs"], 3)
+    c4 = cfgs.get("c4_matmul", {})
+    for kind, t in v["gemm"].items():
+        if isinstance(c4.get(kind), dict) and "tflops" in c4[kind]:
+            c4[kind]["hipblaslt_tflops"] = t["tflops"]
+            c4[kind]["vs_hipblaslt"] = round(c4[kind]["tflops"] / t["tflops"], 3)
 
 
 def main():
@@ -1484,7 +1518,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=ONLY_OPS, default=None,
                     help="run one headline op `--steps` times and exit (profiling)")
-    ap.add_argument("--config", choices=sorted({**CONFIG_SECTIONS, **OPT_IN_SECTIONS}), default=None,
+    ap.add_argument("--config", choices=sorted(CONFIG_SECTIONS), default=None,
                     help="run one configuration section, print its JSON and exit (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -1499,8 +1533,7 @@ def main():
         run_only(cp, be, args.only, args.steps)
         return
     if args.config:
-        fn = {**CONFIG_SECTIONS, **OPT_IN_SECTIONS}[args.config]
-        print(json.dumps({args.config: fn(cp, be)}), flush=True)
+        print(json.dumps({args.config: CONFIG_SECTIONS[args.config](cp, be)}), flush=True)
         return
 
     c2 = bench_c2(cp, be, args.steps, args.warmup)
@@ -1548,6 +1581,7 @@ def main():
                 cfgs[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
             _log(f"{name} done in {time.time() - t:.1f}s")
         out["configs"] = cfgs
+        _vendor_ratios(out, cfgs)
     if not args.no_cpu:
         t = time.time()
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_log2)

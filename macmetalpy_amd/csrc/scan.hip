@@ -154,12 +154,10 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 // itself (64 KiB for a float32 tile, a few microseconds), and goes on.
 // Forward progress needs no other workgroup, and no atomic ticket is
 // drawn (a same-address ticket per workgroup cost 6 % of the float32 scan).
-// Integer prefixes are exact.  A floating prefix is the nearest inclusive
-// prefix combined with the aggregates after it, so which predecessor had
-// published its inclusive prefix decides the association of those float64
-// additions: the last bit of the accumulator can differ between runs
-// (float32 outputs rounded from it almost never do); every form is within
-// the accumulator's error bound.
+// Integer prefixes are exact in any association.  A floating scan folds
+// the values read in tile order, oldest first, so that every prefix is the
+// same sequential fold whichever inclusive prefix a tile found: floating
+// scans are bit-for-bit repeatable.
 // Window per type, measured at 2^28 elements with the ticket-free look-back:
 // int32 -> int64 (8-byte outputs) 4 (6.0 TB/s; 8: 5.9, 16: 5.8), float32 8
 // (5.6; 4: 5.1, 16: 5.6).
@@ -167,6 +165,7 @@ template <typename Ti, typename To> constexpr int scan_look() {
   return (sizeof(Ti) == 4 && sizeof(To) == 8) ? 4 : 8;
 }
 constexpr int kLookMax = 8;
+constexpr int kMaxWin = 64;  // look-back reads kept for the fold (kMaxWin x kLook tiles)
 constexpr long long kPollsBeforeSum = 256;
 
 // Aggregate of a whole tile (Q sub-tiles of kSubTile elements at p) by one
@@ -207,37 +206,47 @@ __device__ typename S::A wave_aggregate(const Ti *__restrict__ p, int lane) {
 template <typename S, int kLook, int Q, typename Ti>
 __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long long t,
                                    typename S::A total, unsigned gen, int lane,
-                                   const Ti *__restrict__ xrow, typename S::A *own_val) {
+                                   const Ti *__restrict__ xrow, typename S::A *own_val,
+                                   typename S::A *win) {
   constexpr long long tile_len = (long long)Q * kSubTile;
   typedef typename S::A A;
+  constexpr bool kOrdered = __is_same(A, double);  // floating: fold in tile order
   A prefix = S::ident();
   unsigned long long *d = sc.desc;
   if (t > 0) {
     if (lane == 0) publish(d + 2 * tile, total, (gen << 2) | 1u);
     const long long first = tile - t;  // first tile of this row
     const unsigned long long in_window = kLook >= 64 ? ~0ull : ((1ull << kLook) - 1);
-    long long top = tile - 1;
-    long long spins = 0;
-    // lanes whose predecessor was summed here (wave-uniform), values in LDS
-    unsigned long long own = 0;
-    while (true) {
-      const long long j = top - lane;
-      unsigned state = 2u;
-      A val = S::ident();
-      if (lane < kLook && j >= first) {
+    // One descriptor: state 0 missing / stale, 1 aggregate, 2 inclusive
+    // prefix; tiles before the row count as an inclusive identity.
+    auto read = [&](long long j, bool want, unsigned &state, A &val) {
+      state = 2u;
+      val = S::ident();
+      if (want && j >= first) {
         const unsigned long long w0 = __hip_atomic_load(d + 2 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long w1 = __hip_atomic_load(d + 2 * j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned t0 = (unsigned)(w0 >> 32), t1 = (unsigned)(w1 >> 32);
         state = (t0 == t1 && (t0 >> 2) == sc.read_gen) ? (t0 & 3u) : 0u;
         val = __builtin_bit_cast(A, (w0 & 0xffffffffull) | (w1 << 32));
-        if (state == 0u && ((own >> lane) & 1ull)) {
-          state = 1u;
-          val = own_val[lane];
-        }
+      }
+    };
+    long long top = tile - 1;
+    long long spins = 0;
+    int nwin = 0;  // windows read before this one (the first kMaxWin are kept in `win`)
+    // lanes whose predecessor was summed here (wave-uniform), values in LDS
+    unsigned long long own = 0;
+    unsigned state;
+    A val;
+    int p;
+    while (true) {
+      read(top - lane, lane < kLook, state, val);
+      if (lane < kLook && state == 0u && ((own >> lane) & 1ull)) {
+        state = 1u;
+        val = own_val[lane];
       }
       const unsigned long long incl = __ballot(state == 2u) & in_window;
       const unsigned long long bad = __ballot(state == 0u) & in_window;
-      const int p = incl ? __ffsll((long long)incl) - 1 : kLook;  // nearest inclusive lane
+      p = incl ? __ffsll((long long)incl) - 1 : kLook;  // nearest inclusive lane
       const unsigned long long nearer = p >= 63 ? ~0ull : ((1ull << (p + 1)) - 1);
       if (bad & nearer) {
         if (++spins <= sc.spin_limit) {
@@ -251,14 +260,80 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
         own |= 1ull << b;
         continue;
       }
-      A part = lane <= p && lane < kLook ? val : S::ident();
+      if constexpr (!kOrdered) {  // integers: any association is exact
+        A part = lane <= p && lane < kLook ? val : S::ident();
 #pragma unroll
-      for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
-      prefix = S::comb(part, prefix);
+        for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
+        prefix = S::comb(part, prefix);
+      } else if (nwin < kMaxWin && lane < kLook) {
+        win[nwin * kLook + lane] = val;
+      }
       if (p < kLook) break;
       top -= kLook;
+      ++nwin;
       own = 0;
       spins = 0;
+    }
+    if constexpr (kOrdered) {
+      // Fold oldest first: the inclusive prefix (lane p of the last window),
+      // then every later tile's aggregate in tile order.  Each inclusive
+      // prefix is then the sequential fold of the row's tile aggregates from
+      // its start, whichever predecessor's prefix a tile started from, so a
+      // floating scan rounds the same way in every run.
+      A s = S::ident();
+      if (nwin < kMaxWin) {
+        if (lane == 0) {
+          s = win[nwin * kLook + p];
+          for (int L = p - 1; L >= 0; --L) s = S::comb(s, win[nwin * kLook + L]);
+          for (int w = nwin - 1; w >= 0; --w)
+#pragma unroll
+            for (int L = kLook - 1; L >= 0; --L) s = S::comb(s, win[w * kLook + L]);
+        }
+        s = shfl64(s, 0);
+      } else {
+        // More than kMaxWin windows back (rare): re-read the tiles after the
+        // inclusive prefix, 64 at a time, folding as above; the newest
+        // inclusive prefix in a read replaces the base, a missing aggregate is
+        // summed here in the tile's own order (so its bits are the tile's).
+        s = shfl64(val, p);
+        long long k0 = top - p + 1;
+        spins = 0;
+        own = 0;
+        A own_v = S::ident();
+        while (k0 < tile) {
+          const int cnt = tile - k0 < 64 ? (int)(tile - k0) : 64;
+          unsigned st;
+          A v;
+          read(k0 + lane, lane < cnt, st, v);
+          if ((own >> lane) & 1ull) {
+            st = 1u;
+            v = own_v;
+          }
+          const unsigned long long live = cnt >= 64 ? ~0ull : ((1ull << cnt) - 1);
+          const unsigned long long incl = __ballot(st == 2u) & live;
+          const int q = incl ? 63 - __clzll((long long)incl) : -1;  // newest inclusive lane
+          const unsigned long long after =
+              q < 0 ? live : (q >= 63 ? 0ull : (live & ~((2ull << q) - 1)));  // lanes after q
+          const unsigned long long miss = __ballot(st == 0u) & after;
+          if (miss) {
+            if (++spins <= sc.spin_limit) {
+              __builtin_amdgcn_s_sleep(1);
+              continue;
+            }
+            const int b = __ffsll((long long)miss) - 1;
+            const A agg = wave_aggregate<S, Q>(xrow + (k0 + b - first) * tile_len, lane);
+            if (lane == b) own_v = agg;
+            own |= 1ull << b;
+            continue;
+          }
+          if (q >= 0) s = shfl64(v, q);
+          for (int L = q + 1; L < cnt; ++L) s = S::comb(s, shfl64(v, L));
+          k0 += cnt;
+          own = 0;
+          spins = 0;
+        }
+      }
+      prefix = s;
     }
   }
   if (lane == 0) publish(d + 2 * tile, S::comb(prefix, total), (gen << 2) | 2u);
@@ -300,6 +375,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
   __shared__ A wsum[Q][kBlock / 64];
   __shared__ A s_prefix;
   __shared__ A s_own[kLookMax];  // predecessor aggregates the look-back summed itself
+  __shared__ A s_win[kMaxWin * kLookMax];  // the look-back's reads, folded oldest first
   __shared__ A s_excl[Q][kBlock];
   Ti *sx = reinterpret_cast<Ti *>(stage);
   To *sy = reinterpret_cast<To *>(stage);
@@ -409,7 +485,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
       if (tid == 0) s_prefix = t > 0 ? tail_prefix<S>(sc, tile - 1, gen) : S::ident();
     } else if (wave == 0) {
       const A prefix = look_back<S, scan_look<Ti, To>(), Q>(sc, tile, t, total, gen, lane,
-                                                            x + row * len, s_own);
+                                                            x + row * len, s_own, s_win);
       if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();

@@ -64,10 +64,9 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
     expects a tag no writer produces) sums each missing predecessor's input
     itself: the result is exact and no wait is reported.  The fallback
     combines a predecessor's elements in the order that tile's own
-    workgroup does; float prefixes still meet the accumulator's error bound
-    (the look-back's association of tile aggregates depends on where it
-    finds an inclusive prefix, so float64 bits may differ between runs in
-    the last place)."""
+    workgroup does, and a floating scan's prefixes have an association
+    fixed by tile position, so float results are bit-identical to a run
+    that found every descriptor."""
     g = np.random.default_rng(42)
     x_np = g.integers(-100, 100, n, dtype=np.int32)
     x = cp.array(x_np)
@@ -88,6 +87,7 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
         ref = np.cumsum(f_np, dtype=np.float64)
         got = cf.get()
         assert np.all(np.abs(got - ref) <= 1e-5 * ref + 1e-6)
+        assert np.array_equal(got, cp.cumsum(f).get())  # the same bits as a normal run
         assert be.wait_status() == 0
         d_np = g.random(n)                              # float64: 8192-element tiles
         d = cp.array(d_np)
@@ -95,6 +95,7 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
         got = cp.cumsum(d).get()
         want = np.cumsum(d_np)
         assert np.all(np.abs(got - want) <= 1e-12 * want)
+        assert np.array_equal(got, cp.cumsum(d).get())
         h_np = (g.random(3 * 16384) + 0.5).astype(np.float32)
         h = cp.array(h_np)
         be.debug_fail_next(4, 1)
@@ -102,6 +103,7 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
         want = np.cumprod(h_np.astype(np.float64))
         ok = (want > 1e-30) & (want < 1e30)          # float32 normal range
         assert np.all(np.abs(got[ok] - want[ok]) <= 1e-5 * want[ok])
+        assert np.array_equal(got, cp.cumprod(h).get())
     else:
         with pytest.raises(HipWaitTimeoutError, match="scan"):
             cf.get()

@@ -267,6 +267,26 @@ def test_scan_repeated_generations():
         assert np.array_equal(cp.cumsum(X).get(), want)
 
 
+@pytest.mark.parametrize("dtype,shape,op", [(np.float32, (1 << 24,), "cumsum"),
+                                            (np.float32, (3, (1 << 22) + 1000), "cumsum"),
+                                            (np.float64, (1 << 23,), "cumsum"),
+                                            (np.float16, (1 << 22,), "cumsum"),
+                                            (np.float32, (1 << 22,), "cumprod")])
+def test_float_scan_bits_repeat(dtype, shape, op):
+    """A floating scan's tile prefixes are folded in an order fixed by tile
+    position, not by which predecessor happened to publish first, so
+    repeated runs over hundreds of tiles give the same bits."""
+    g = np.random.default_rng(77)
+    x = (g.random(shape) + (0.5 if op == "cumprod" else 0.0))
+    if op == "cumprod":
+        x = 1.0 + (x - 1.0) * 1e-6
+    X = cp.array(x.astype(dtype))
+    f = getattr(cp, op)
+    first = f(X, axis=-1).get()
+    for _ in range(3):
+        assert np.array_equal(f(X, axis=-1).get(), first, equal_nan=True)
+
+
 # ------------------------------------------------------ fused reductions
 def test_fused_sum_matches_unfused():
     x_np = np.random.default_rng(10).standard_normal((300, 7001)).astype(np.float32)
@@ -312,6 +332,8 @@ def test_c3_scan_full_size():
     assert got.dtype == np.int64
     assert np.array_equal(got, np.cumsum(ci))
     del got
-    gf = cp.cumsum(cp.array(cf)).get()
+    CF = cp.array(cf)
+    gf = cp.cumsum(CF).get()
     want = np.cumsum(cf.astype(np.float64))
     assert _rel_err(gf, want) <= RTOL
+    assert np.array_equal(cp.cumsum(CF).get(), gf)  # the same bits on a second run

@@ -318,8 +318,10 @@ int mmp_argreduce(int op, int dtype, int64_t outer, int64_t len,
 
 /* Inclusive scan along the middle axis of (outer, len, inner).
  * MMP_S_CUMSUM / MMP_S_CUMPROD.  out_dtype follows numpy (int32 -> int64,
- * float32 -> float32); floating scans carry a float64 running value.  out
- * must not overlap x (MMP_E_ARG): a tile may read its predecessors' input. */
+ * float32 -> float32); floating scans carry a float64 running value whose
+ * additions run in one fixed order, so repeated calls on the same input
+ * give the same bits.  out must not overlap x (MMP_E_ARG): a tile may read
+ * its predecessors' input. */
 int mmp_scan(int op, int dtype, int out_dtype, int64_t outer, int64_t len,
              int64_t inner, const void *x, void *out);
 

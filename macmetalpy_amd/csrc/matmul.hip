@@ -37,9 +37,6 @@
 
 namespace {
 
-#ifndef GEMM4_WIDE
-#define GEMM4_WIDE 1
-#endif
 constexpr int kBlock = 256;
 constexpr int BM = 128, BN = 128;
 
@@ -734,15 +731,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm4_dma(
 // stores and copies need not complete in issue order).  Copies past the
 // last slab reload the last slab into a stage never read again, so every
 // wave always has six copies per slab in flight and the count stays exact.
-#ifndef GEMM4_XCD
-#define GEMM4_XCD 1
-#endif
-#ifndef GEMM4_PERSIST
-#define GEMM4_PERSIST 1
-#endif
-#ifndef GEMM4_BCOL
-#define GEMM4_BCOL 1
-#endif
 __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int K,
     long long lda, long long ldb, long long ldc, long long sA, long long sB, long long sC,
@@ -763,7 +751,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
   // one whole product of a batch of small ones).
   const int P = gridDim.x, w = blockIdx.x;
   int tfirst, tstep, nt;
-  if (GEMM4_XCD && (T & 7) == 0 && (P & 7) == 0) {
+  if ((T & 7) == 0 && (P & 7) == 0) {
     const int q = T >> 3, ps = P >> 3, s = w >> 3;
     tfirst = (w & 7) * q + s;
     tstep = ps;
@@ -779,8 +767,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
     bz = t / per_b;
     const int r = t - (int)bz * per_b;
     const int tiles_m = per_b / tiles_n;
-    const int rows = GEMM4_XCD ? 4 : 1;  // tile rows per group (1: row-major order)
-    const int first = (r / (rows * tiles_n)) * rows, gsize = min(rows, tiles_m - first);
+    const int first = (r / (4 * tiles_n)) * 4, gsize = min(4, tiles_m - first);
     const int local = r - first * tiles_n;
     m0 = (first + local % gsize) * TM;
     n0 = (local / gsize) * BN;
@@ -882,17 +869,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
     for (int t = 0; t < 4; ++t) {
       const int k = g * 8 + s * 4 + t;
       const int sw = 4 * ((k >> 3) & 3);
-      if (GEMM4_BCOL) {  // columns 4 fr .. 4 fr + 3 of the wave's 64: one 16-byte chunk
-        const f4 v = *reinterpret_cast<const f4 *>(Bs_ + k * BN + (((wn * 16 + fr) ^ sw) * 4));
+      // columns 4 fr .. 4 fr + 3 of the wave's 64: one 16-byte chunk
+      const f4 v = *reinterpret_cast<const f4 *>(Bs_ + k * BN + (((wn * 16 + fr) ^ sw) * 4));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j][t] = v[j];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = wn * 64 + j * 16 + fr;
-          bf[j][t] = Bs_[k * BN + (((n >> 2) ^ sw) * 4) + (n & 3)];
-        }
-      }
+      for (int j = 0; j < 4; ++j) bf[j][t] = v[j];
     }
   };
   auto mfma_half = [&](const f4 (&af)[4], const f4 (&bf)[4]) {
@@ -904,7 +884,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
   };
-  constexpr int kReads = GEMM4_BCOL ? 8 : 20;  // LDS reads of a half-slab's fragments
+  constexpr int kReads = 8;  // LDS reads of a half-slab's fragments (4 of A, 4 of B)
   auto sched_half = [&]() {
 #pragma unroll
     for (int m = 0; m < 64; ++m) {
@@ -954,27 +934,15 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
       int m0, n0;
       decode(ti, bz, m0, n0);
       float *Cb = C + bz * sC;
-      if (GEMM4_BCOL) {  // lane fr holds columns 4 fr .. 4 fr + 3: one 16-byte store per row
+      // lane fr holds columns 4 fr .. 4 fr + 3: one 16-byte store per row
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
-            *reinterpret_cast<f4 *>(Cb + (long long)row * ldc + n0 + wn * 64 + 4 * fr) =
-                f4{acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
-          }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
-              const int col = n0 + wn * 64 + j * 16 + fr;
-              Cb[(long long)row * ldc + col] = acc[i][j][r];
-            }
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * 64 + i * 16 + 4 * g + r;
+          *reinterpret_cast<f4 *>(Cb + (long long)row * ldc + n0 + wn * 64 + 4 * fr) =
+              f4{acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1077,9 +1045,9 @@ int launch4(long long batch, int M, int N, int K, const void *A, long long lda, 
       const long long wide_tiles = M % 256 == 0 ? (long long)(M / 256) * tiles_n * batch : 0;
       const long long rounds = (wide_tiles + cus - 1) / cus;
       const bool c16 = al(C, 16) && ldc % 4 == 0 && sC % 4 == 0;  // 16-byte C rows
-      if (GEMM4_WIDE && wide_tiles > 0 && wide_tiles < (1LL << 30) && lda < (1LL << 27) &&
-          ldb < (1LL << 27) && (c16 || !GEMM4_BCOL) && wide_tiles * 100 >= rounds * cus * 97) {
-        const long long P = GEMM4_PERSIST && wide_tiles > cus ? cus : wide_tiles;
+      if (wide_tiles > 0 && wide_tiles < (1LL << 30) && lda < (1LL << 27) && ldb < (1LL << 27) &&
+          c16 && wide_tiles * 100 >= rounds * cus * 97) {
+        const long long P = wide_tiles > cus ? cus : wide_tiles;
         hipLaunchKernelGGL(k_gemm4_dma3, dim3((unsigned)P), dim3(512), 0, mmpi::stream(),
                            (const float *)A, (const float *)B, (float *)C, K, lda, ldb, ldc, sA,
                            sB, sC, tiles_n, (int)((M / 256) * tiles_n), (int)wide_tiles);

@@ -86,6 +86,14 @@ template <typename A> __device__ __forceinline__ A shfl64(A v, int src) {
   return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
 }
 
+// Lane `src` (wave-uniform) of v, read into scalar registers.
+template <typename A> __device__ __forceinline__ A readlane64(A v, int src) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = __builtin_amdgcn_readlane((unsigned)u, src);
+  const unsigned hi = __builtin_amdgcn_readlane((unsigned)(u >> 32), src);
+  return __builtin_bit_cast(A, ((unsigned long long)hi << 32) | lo);
+}
+
 template <typename A> __device__ __forceinline__ A shfl_up64(A v, int d) {
   unsigned long long u = __builtin_bit_cast(unsigned long long, v);
   unsigned lo = __shfl_up((unsigned)u, d, 64), hi = __shfl_up((unsigned)(u >> 32), d, 64);
@@ -265,10 +273,10 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
 #pragma unroll
         for (int m = 32; m > 0; m >>= 1) part = S::comb(part, shfl_xor64(part, m));
         prefix = S::comb(part, prefix);
-      } else if (nwin < kMaxWin && lane < kLook) {
-        win[nwin * kLook + lane] = val;
       }
       if (p < kLook) break;
+      // a window walked past: kept for the fold (the last one stays in registers)
+      if (kOrdered && nwin < kMaxWin && lane < kLook) win[nwin * kLook + lane] = val;
       top -= kLook;
       ++nwin;
       own = 0;
@@ -282,14 +290,13 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
       // floating scan rounds the same way in every run.
       A s = S::ident();
       if (nwin < kMaxWin) {
-        if (lane == 0) {
-          s = win[nwin * kLook + p];
-          for (int L = p - 1; L >= 0; --L) s = S::comb(s, win[nwin * kLook + L]);
-          for (int w = nwin - 1; w >= 0; --w)
+        // the window just read from registers (lane index uniform: readlane),
+        // the newer ones from LDS
+        s = readlane64(val, p);
+        for (int L = p - 1; L >= 0; --L) s = S::comb(s, readlane64(val, L));
+        for (int w = nwin - 1; w >= 0; --w)
 #pragma unroll
-            for (int L = kLook - 1; L >= 0; --L) s = S::comb(s, win[w * kLook + L]);
-        }
-        s = shfl64(s, 0);
+          for (int L = kLook - 1; L >= 0; --L) s = S::comb(s, win[w * kLook + L]);
       } else {
         // More than kMaxWin windows back (rare): re-read the tiles after the
         // inclusive prefix, 64 at a time, folding as above; the newest

@@ -167,13 +167,17 @@ template <typename T> __device__ __forceinline__ T opaque(T v) {
 // same sequential fold whichever inclusive prefix a tile found: floating
 // scans are bit-for-bit repeatable.
 // Window per type, measured at 2^28 elements with the ticket-free look-back:
-// int32 -> int64 (8-byte outputs) 4 (6.0 TB/s; 8: 5.9, 16: 5.8), float32 8
-// (5.6; 4: 5.1, 16: 5.6).
+// int32 -> int64 (8-byte outputs) 4 (6.0 TB/s; 8: 5.9, 16: 5.8).  Floating
+// scans fold in tile order (below), which lengthens the walk: a tile's
+// look-back goes back 128 tiles on average against 58 with a tree over
+// each read (per-tile counts at 2^28 float32); 16 per read then beats 8
+// (0.398-0.405 ms against 0.409-0.414; 32: 0.42, 64: 0.51).
 template <typename Ti, typename To> constexpr int scan_look() {
+  if (mmp_t<Ti>::is_float) return 16;
   return (sizeof(Ti) == 4 && sizeof(To) == 8) ? 4 : 8;
 }
-constexpr int kLookMax = 8;
-constexpr int kMaxWin = 64;  // look-back reads kept for the fold (kMaxWin x kLook tiles)
+constexpr int kLookMax = 16;
+constexpr int kMaxWinTiles = 512;  // look-back reads kept for the fold
 constexpr long long kPollsBeforeSum = 256;
 
 // Aggregate of a whole tile (Q sub-tiles of kSubTile elements at p) by one
@@ -219,6 +223,7 @@ __device__ typename S::A look_back(const ScanScratch &sc, long long tile, long l
   constexpr long long tile_len = (long long)Q * kSubTile;
   typedef typename S::A A;
   constexpr bool kOrdered = __is_same(A, double);  // floating: fold in tile order
+  constexpr int kMaxWin = kMaxWinTiles / kLook;
   A prefix = S::ident();
   unsigned long long *d = sc.desc;
   if (t > 0) {
@@ -382,7 +387,7 @@ __global__ __launch_bounds__(kBlock, MODE == 0 ? 2 : 1) void k_scan_rows(
   __shared__ A wsum[Q][kBlock / 64];
   __shared__ A s_prefix;
   __shared__ A s_own[kLookMax];  // predecessor aggregates the look-back summed itself
-  __shared__ A s_win[kMaxWin * kLookMax];  // the look-back's reads, folded oldest first
+  __shared__ A s_win[kMaxWinTiles];  // the look-back's reads, folded oldest first
   __shared__ A s_excl[Q][kBlock];
   Ti *sx = reinterpret_cast<Ti *>(stage);
   To *sy = reinterpret_cast<To *>(stage);

@@ -110,6 +110,26 @@ def test_scan_without_predecessor_descriptors_sums_them_itself(be, n):
     assert be.wait_status() == 0
 
 
+def test_float_scan_walk_beyond_kept_windows_same_bits(be):
+    """A floating scan tile keeps the last 512 predecessors it walked past
+    for its tile-ordered fold.  With every descriptor withheld, the tiles
+    of a 528-tile float32 row walk back to the row start, so the last ones
+    walk past more than that and take the other branch: re-read the tiles
+    after the inclusive prefix in order, summing each missing one itself.
+    The bits must equal a normal run's (which walks a few windows)."""
+    n = 528 * 16384
+    g = np.random.default_rng(44)
+    f_np = g.random(n, dtype=np.float32)
+    f = cp.array(f_np)
+    normal = cp.cumsum(f).get()
+    be.debug_fail_next(4, 1)
+    got = cp.cumsum(f).get()
+    assert be.wait_status() == 0
+    assert np.array_equal(got, normal)
+    ref = np.cumsum(f_np, dtype=np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * ref + 1e-6)
+
+
 def test_injected_allocation_failure_leaks_nothing(be):
     a = cp.array(np.ones(1 << 20, np.float32))
     b = cp.array(np.full(1 << 20, 2.0, np.float32))

@@ -110,6 +110,24 @@ def test_matmul_f32_persistent_exact(rounds, tm, tn, k):
     _exact_f32_product(rounds * cus // per_b, 256 * tm, 128 * tn, k, rounds * 100 + k)
 
 
+# (tiles short of whole rounds, rounds, tile rows of 256, k)
+@pytest.mark.parametrize("short,rounds,tm,k", [(6, 1, 1, 96), (2, 2, 1, 32), (8, 2, 1, 64),
+                                               (8, 3, 1, 160), (6, 1, 2, 32)])
+def test_matmul_f32_persistent_partial_round_exact(short, rounds, tm, k):
+    """Tile counts a few short of whole rounds of the CUs (at least 97 % of
+    the last round) also take the persistent kernel.  A count not divisible
+    by 8 (250, 510 tiles on 256 CUs) is taken grid-stride by workgroup id;
+    one divisible by 8 (504, 760) is cut into eight XCD ranges whose
+    workgroups run uneven numbers of tiles (2 or 1, 3 or 2).  Integer-valued
+    operands make every product exact, so the result must equal NumPy's."""
+    from macmetalpy_amd._backend import HipBackend
+    cus = HipBackend().device_info()["cu_count"]
+    tiles = rounds * cus - short
+    if tiles % tm or tiles * 100 < rounds * cus * 97:
+        pytest.skip(f"{tiles} tiles on {cus} CUs do not make this case")
+    _exact_f32_product(tiles // tm, 256 * tm, 128, k, tiles + k)
+
+
 @pytest.mark.parametrize("batch,m,n,k,pad", [(1, 256, 128, 96, 32), (2, 512, 256, 128, 4),
                                              (1, 256, 384, 64, 128), (2, 128, 128, 64, 36)])
 def test_matmul_f32_dma_row_strides(batch, m, n, k, pad):

@@ -822,18 +822,30 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
     cB = B + bz * sB + n0;
   };
   copy_tile();
-  // Sources of the next slab of the copy stream (computed ahead of the
-  // barrier they follow), then advance; after the last slab of the last
-  // tile the stream stays on it.
-  auto next_sources = [&](const float *(&src)[6]) {
+  // src: this wave's six sources in the copy stream's next slab.  advance()
+  // steps them one slab along k, or to the next tile's panels; after the
+  // last slab of the last tile the stream stays on it.  It runs at the end
+  // of a slab, beside the compute stream's tile-end branch: a branch inside
+  // a half-slab splits its block, and the scheduler then cannot interleave
+  // that half's LDS reads with its MFMAs (the first half's reads went after
+  // all 64 of its MFMAs, then waited out their latency before the barrier:
+  // 2-2.5 % of the kernel).
+  const float *src[6];
+  auto panel_sources = [&]() {
 #pragma unroll
-    for (int p = 0; p < 6; ++p) src[p] = (isA[p] ? cA : cB) + off[p] + (long long)(ck * BK) * ks[p];
+    for (int p = 0; p < 6; ++p) src[p] = (isA[p] ? cA : cB) + off[p];
+  };
+  panel_sources();
+  auto advance = [&]() {
     if (ck + 1 < nk) {
       ++ck;
+#pragma unroll
+      for (int p = 0; p < 6; ++p) src[p] += BK * ks[p];
     } else if (ci + 1 < nt) {
       ++ci;
       ck = 0;
       copy_tile();
+      panel_sources();
     }
   };
   auto issue = [&](float *S, const float *(&src)[6]) {
@@ -894,13 +906,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
   };
 
   f4 f0a[4], f0b[4], f1a[4], f1b[4];
-  const float *src[6];
-  next_sources(src);
   issue(S0, src);
-  next_sources(src);
+  advance();
   issue(S1, src);
-  next_sources(src);
+  advance();
   issue(S2, src);
+  advance();
   asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");  // slab 0 landed everywhere
   read_half(S0, 0, f0a, f0b);
   int kt = 0, ti = 0;  // the compute stream: slab kt of tile ti
@@ -909,11 +920,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
   // barrier once the next slab has landed and every wave has read this one;
   // the copy three slabs ahead into this slab's stage; the second half's
   // MFMAs with the reads of the first half of the next slab; after a tile's
-  // last slab, its C stores.
+  // last slab, its C stores; the copy stream's next sources.
   auto slab = [&](float *cur, const float *nxt) {
     mfma_half(f0a, f0b);
     read_half(cur, 1, f1a, f1b);
-    next_sources(src);
     sched_half();
     __builtin_amdgcn_sched_barrier(0);  // the half's MFMAs stay ahead of the barrier
     if (stored)
@@ -951,6 +961,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm4_dma3(
       kt = 0;
       stored = true;
     }
+    advance();
   };
   const int total = nt * nk;
   for (int s = 0; s < total; s += 3) {

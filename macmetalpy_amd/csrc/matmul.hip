@@ -591,7 +591,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm4_dma(
   // two offsets its copies use, indexed by the unrolled p (32-bit: the host
   // keeps lda and ldb below 2^28).
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const bool a_role = wv < WM, b_role = wv >= WM;
+  const bool b_role = wv >= WM;  // the first WM waves copy A, the rest B
   const int w2 = b_role ? wv - WM : wv;
   unsigned loff[2];
   if (b_role) {
@@ -607,17 +607,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm4_dma(
       loff[u] = (unsigned)r8 * (unsigned)lda + (unsigned)((slot ^ sw) * 4);
     }
   }
+  // The role is selected, not branched on: a branch per copy splits the
+  // block the copies and MFMAs share.
   auto issue = [&](float *As_, float *Bs_, int k0) {
+    const float *base = b_role ? Bg + (long long)k0 * ldb : Ag + k0;
+    const long long step = b_role ? 2 * ldb : 8 * lda;  // rows per copy
+    float *dst = b_role ? Bs_ : As_;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       const int q = w2 * 8 + p;
-      if (b_role) {
-        const float *g = Bg + (long long)(k0 + 2 * q) * ldb + loff[p >> 2];
-        __builtin_amdgcn_global_load_lds(g, Bs_ + q * 256, 16, 0, 0);
-      } else if (a_role) {
-        const float *g = Ag + (long long)(8 * q) * lda + k0 + loff[p & 1];
-        __builtin_amdgcn_global_load_lds(g, As_ + q * 256, 16, 0, 0);
-      }
+      const unsigned lo = b_role ? loff[p >> 2] : loff[p & 1];
+      __builtin_amdgcn_global_load_lds(base + q * step + lo, dst + q * 256, 16, 0, 0);
     }
   };
 

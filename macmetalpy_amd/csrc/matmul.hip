@@ -287,7 +287,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm16_dma(
     }
   }
   auto issue = [&](unsigned short *As_, unsigned short *Bs_, int k0) {
-    const unsigned short *g = b_role ? Bg + (long long)k0 * ldb : Ag + k0;
+    // operands selected, one product: hipcc branches on the role when each
+    // side has its own multiply, and the branch splits the copies' block
+    const unsigned short *g = (b_role ? Bg : Ag) + (long long)k0 * (b_role ? ldb : 1LL);
     unsigned short *dst = b_role ? Bs_ : As_;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {

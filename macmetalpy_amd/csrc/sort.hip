@@ -8,8 +8,9 @@
 //
 // Sort: least-significant-digit radix sort with 8-bit digits over
 // order-preserving unsigned keys, stable, three launches per digit:
-//  * k_radix_hist: one 256-bin histogram per 4096-key tile (LDS atomics,
-//    one histogram per wave), written digit-major: counts[d * tiles + b];
+//  * k_radix_hist: one 256-bin histogram per 4096-key tile (LDS atomics
+//    into 16 padded sub-histograms), written digit-major:
+//    counts[d * tiles + b];
 //  * one inclusive scan of the counts (mmp_scan), so that the global
 //    offset of digit d in tile b is incl[d * tiles + b] - counts[...];
 //  * k_radix_scatter: each wave ranks a contiguous quarter of the tile in
@@ -135,10 +136,15 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ 
                                                        unsigned *__restrict__ counts) {
   typedef typename KeyOf<T>::K K;
   typedef typename std::conditional<FIRST, T, K>::type E;  // element type read
-  __shared__ unsigned h[kBlock / 64][kRadix];
-  const int t = threadIdx.x, w = t >> 6;
-#pragma unroll
-  for (int k = 0; k < kBlock / 64; ++k) h[k][t] = 0;
+  // kSub sub-histograms, lane l counting into l % kSub, each padded by one
+  // word: lanes with equal digits (the sign and exponent byte of floats
+  // takes a handful of values) then hit kSub different banks instead of
+  // queueing on one LDS word.
+  constexpr int kSub = 16, kStride = kRadix + 1;
+  __shared__ unsigned h[kSub * kStride];
+  const int t = threadIdx.x;
+  unsigned *hs = h + (t & (kSub - 1)) * kStride;
+  for (int k = t; k < kSub * kStride; k += kBlock) h[k] = 0;
   __syncthreads();
   const SegTile tl = seg_tile(xcd_tile(blockIdx.x, gridDim.x), len, tpr);
   const E *e = reinterpret_cast<const E *>(src) + tl.start;
@@ -158,14 +164,17 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const void *__restrict__ 
       } q;
       q.v = __builtin_nontemporal_load(pv + j);
 #pragma unroll
-      for (int i = 0; i < V; ++i) atomicAdd(&h[w][digit_of<K>(key_at(q.x[i]), shift)], 1u);
+      for (int i = 0; i < V; ++i) atomicAdd(&hs[digit_of<K>(key_at(q.x[i]), shift)], 1u);
     }
   } else {
     for (unsigned i = t; i < tl.count; i += kBlock)
-      atomicAdd(&h[w][digit_of<K>(key_at(e[i]), shift)], 1u);
+      atomicAdd(&hs[digit_of<K>(key_at(e[i]), shift)], 1u);
   }
   __syncthreads();
-  counts[count_slot(tl, t, tpr)] = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+  unsigned c = 0;
+#pragma unroll
+  for (int k = 0; k < kSub; ++k) c += h[k * kStride + t];
+  counts[count_slot(tl, t, tpr)] = c;
 }
 
 // exclusive prefix over the 256 threads of a block (value per thread)

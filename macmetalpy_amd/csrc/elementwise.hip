@@ -278,10 +278,19 @@ __global__ __launch_bounds__(kBlock) void k_copy_rows(const Ti *__restrict__ x,
     }
     return;
   }
+  // Other strides: all loads first as well (a column past the row's end
+  // reads column c0, which exists); a guarded load-convert-store per
+  // element had each load waited for before the next was issued.
+  Ti v[kRowItems];
 #pragma unroll
   for (int u = 0; u < kRowItems; ++u) {
     const long long c = c0 + u * kBlock + threadIdx.x;
-    if (c < len) y[dof + c * ds] = mmp_convert<To, Ti>(x[so + c * ss]);
+    v[u] = x[so + (c < len ? c : c0) * ss];
+  }
+#pragma unroll
+  for (int u = 0; u < kRowItems; ++u) {
+    const long long c = c0 + u * kBlock + threadIdx.x;
+    if (c < len) y[dof + c * ds] = mmp_convert<To, Ti>(v[u]);
   }
 }
 
@@ -369,11 +378,21 @@ __global__ __launch_bounds__(kBlock) void k_copy_transpose(const Ti *__restrict_
   }
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const long long p0 = jp * 64, q0 = jq * 64;
+  // All 16 loads first (an element outside the array reads the tile's
+  // corner (p0, q0), which exists), then the guarded LDS writes: a guarded
+  // load per element had each load waited for before the next was issued.
+  Ti v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = ty + 4 * i;  // q within the tile
     const long long pp = p0 + tx, qq = q0 + r;
-    if (pp < t.np && qq < t.nq) tile[r][tx] = x[so + pp * t.sp + qq * t.sq];
+    const bool in = pp < t.np && qq < t.nq;
+    v[i] = x[so + (in ? pp : p0) * t.sp + (in ? qq : q0) * t.sq];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;
+    if (p0 + tx < t.np && q0 + r < t.nq) tile[r][tx] = v[i];
   }
   __syncthreads();
 #pragma unroll
